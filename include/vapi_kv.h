@@ -1,0 +1,268 @@
+/*
+ * vapi_kv.h — C ABI of the MI355X (gfx950) paged KV-cache library.
+ *
+ * This is the drop-in boundary for vapi's paged KV hot path: the KV append
+ * (slot_mapping scatter), the block-table gather, paged attention (decode and
+ * chunked prefill in one varlen call), the copy-on-write block copy and the
+ * spill-tier export/import/swap. Every entry point:
+ *   - is `extern "C"` with plain pointers, sizes and a hipStream_t;
+ *   - returns 0 on success and a negative VAPI_KV_E* code on error, with a
+ *     thread-local message in vapi_kv_last_error();
+ *   - never allocates device or host memory (the "vapi_cache_*" host object
+ *     at the bottom of this file is the exception: it owns the pool, like the
+ *     reference's PagedKvCache);
+ *   - takes every device argument by value/pointer, so a call can be recorded
+ *     into a HIP graph.
+ *
+ * Reference interfaces replaced (paths relative to the vapi repository):
+ *   crates/vapi-backend-candle/src/cache.rs:12-118   PagedKvCache
+ *   crates/vapi-backend-candle/src/cache.rs:136-278  write_kv_to_cache/write_rows
+ *   crates/vapi-backend-candle/src/rows.rs:22-33     rows::scatter (CUDA append)
+ *   crates/vapi-backend-candle/src/cache.rs:283-290  gather_kv
+ *   crates/vapi-backend-candle/src/attention.rs:42-71,170-288 paged attention
+ *   crates/vapi-backend-candle/src/backend.rs:695-797 block_bytes/export/import/copy
+ *   crates/vapi-engine/src/backend.rs:96-204          ForwardBatch::validate
+ */
+#ifndef VAPI_KV_H
+#define VAPI_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t without pulling in the HIP headers. */
+typedef struct ihipStream_t* vapi_stream_t;
+
+/* ---- status codes ------------------------------------------------------ */
+#define VAPI_KV_OK 0
+#define VAPI_KV_EINVAL (-1)   /* bad argument, shape, dtype or range */
+#define VAPI_KV_EUNSUP (-2)   /* valid but unsupported configuration */
+#define VAPI_KV_EHIP (-3)     /* a HIP runtime call failed */
+#define VAPI_KV_ESPACE (-4)   /* a caller-provided buffer is too small */
+
+/* ---- pool description -------------------------------------------------- */
+typedef enum {
+  VAPI_KV_F32 = 0,
+  VAPI_KV_F16 = 1,
+  VAPI_KV_BF16 = 2
+} vapi_kv_dtype;
+
+typedef enum {
+  /* [num_blocks, num_kv_heads, block_size, head_dim]: each (block, head) is
+   * one contiguous block_size*head_dim tile. The default on MI355X. */
+  VAPI_KV_LAYOUT_HND = 0,
+  /* [num_blocks, block_size, num_kv_heads, head_dim]: the reference's own
+   * layout (cache.rs:7-11), for byte-for-byte interchange. */
+  VAPI_KV_LAYOUT_NHD = 1
+} vapi_kv_layout;
+
+/* A padded token in slot_mapping: written nowhere (vLLM's -1 as u32). */
+#define VAPI_KV_SLOT_SKIP 0xFFFFFFFFu
+
+/*
+ * One paged K/V pool for `num_layers` layers. Layer l's K buffer starts at
+ * (char*)k + l*layer_stride_bytes and its V buffer at (char*)v +
+ * l*layer_stride_bytes; each is num_blocks blocks in `layout`. A slot is
+ * block*block_size + offset, the addressing of ForwardBatch::slot_mapping
+ * (crates/vapi-engine/src/backend.rs:62-64).
+ */
+typedef struct vapi_kv_pool {
+  void* k;
+  void* v;
+  uint64_t layer_stride_bytes;
+  uint32_t num_layers;
+  uint32_t num_blocks;
+  uint32_t block_size;
+  uint32_t num_kv_heads;
+  uint32_t head_dim;
+  uint32_t dtype;  /* vapi_kv_dtype */
+  uint32_t layout; /* vapi_kv_layout */
+} vapi_kv_pool;
+
+/* Thread-local message for the last failing call on this thread ("" if none). */
+const char* vapi_kv_last_error(void);
+
+/* Library version string. */
+const char* vapi_kv_version(void);
+
+/* Bytes of one block across every layer, K then V (backend.rs:695-708):
+ * num_layers * 2 * block_size * num_kv_heads * head_dim * sizeof(dtype). */
+size_t vapi_kv_block_bytes(const vapi_kv_pool* pool);
+
+/* Bytes of one layer's K (or V) buffer: num_blocks * block elements. */
+size_t vapi_kv_layer_bytes(const vapi_kv_pool* pool);
+
+/*
+ * KV append (reshape_and_cache). Replaces write_kv_to_cache/write_rows
+ * (cache.rs:136-148, 217-273) and the CUDA rows::scatter kernel
+ * (rows.rs:22-33, 60-72; call site models/qwen.rs:372-382).
+ *
+ * k_src, v_src: device [n_tokens, num_kv_heads, head_dim] in pool dtype.
+ * slot_mapping: device u32[n_tokens]; token i lands in flat slot
+ * slot_mapping[i]. VAPI_KV_SLOT_SKIP skips the token. A slot past the end of
+ * the pool is never written (the device guard drops it); the host-side
+ * vapi_cache_write_kv() reports it as an error as the reference does.
+ * Duplicate slots are undefined (ForwardBatch::validate rejects them).
+ * K and V are written in one launch.
+ */
+int vapi_kv_append(const vapi_kv_pool* pool, uint32_t layer, const void* k_src,
+                   const void* v_src, const uint32_t* slot_mapping,
+                   uint32_t n_tokens, vapi_stream_t stream);
+
+/*
+ * Block-table gather into logical order. Replaces gather_kv (cache.rs:283-290).
+ * block_table: device u32[n_table]; out: device [len_k, num_kv_heads,
+ * head_dim] for K and for V (either may be NULL). len_k <= n_table*block_size.
+ */
+int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
+                   const uint32_t* block_table, uint32_t n_table,
+                   uint32_t len_k, void* k_out, void* v_out,
+                   vapi_stream_t stream);
+
+/*
+ * Paged attention over a varlen batch: decode rows (len_q == 1) and prefill
+ * chunks (len_q > 1) in one call, dispatched inside. Replaces
+ * paged_attention_cuda/_windowed/_prepared (attention.rs:170-288) with
+ * paged_attention_cpu (attention.rs:90-163) as the numerical contract.
+ *
+ * q:   device [cu_seqlens_q[batch], num_heads, head_dim], pool dtype.
+ * out: device, same shape and dtype as q.
+ * cu_seqlens_q, cu_seqlens_k: device u32[batch+1]; len_k includes the cached
+ *   prefix and len_q <= len_k. Query j of a sequence sits at absolute
+ *   position p = len_k - len_q + j (bottom-right aligned).
+ * block_table: device u32[batch, max_blocks] (pack_block_tables layout,
+ *   attention.rs:42-62).
+ * max_seqlen_q, max_seqlen_k: upper bounds of len_q and len_k.
+ * window_left: keys k < p - window_left are hidden; -1 = unlimited. A sliding
+ *   window of w (HF q - k < w) is window_left = w - 1 (attention.rs:179-194).
+ * window_right: keys k > p + window_right are hidden; 0 = causal, -1 =
+ *   unlimited (bidirectional).
+ * workspace: device scratch of at least vapi_paged_attention_workspace_size()
+ *   bytes (split-K partials); may be NULL when that size is 0.
+ */
+size_t vapi_paged_attention_workspace_size(const vapi_kv_pool* pool,
+                                           uint32_t batch, uint32_t num_heads,
+                                           uint32_t max_seqlen_q,
+                                           uint32_t max_seqlen_k);
+
+int vapi_paged_attention(const vapi_kv_pool* pool, uint32_t layer,
+                         const void* q, void* out,
+                         const uint32_t* cu_seqlens_q,
+                         const uint32_t* cu_seqlens_k,
+                         const uint32_t* block_table, uint32_t batch,
+                         uint32_t max_blocks, uint32_t max_seqlen_q,
+                         uint32_t max_seqlen_k, uint32_t num_heads, float scale,
+                         int32_t window_left, int32_t window_right,
+                         void* workspace, size_t workspace_bytes,
+                         vapi_stream_t stream);
+
+/*
+ * Copy-on-write block copy over every layer, K and V, in one launch.
+ * Replaces CandleBackend::copy_blocks (backend.rs:781-797), which the
+ * engine calls with Scheduler::fork's pairs (scheduler.rs:217-281).
+ * pairs: device u32[n_pairs][2] = (src, dst). A dst must not also be a src
+ * or another pair's dst in the same call.
+ */
+int vapi_kv_copy_blocks(const vapi_kv_pool* pool, const uint32_t* pairs,
+                        uint32_t n_pairs, vapi_stream_t stream);
+
+/*
+ * Spill export / import. Block i's blob (vapi_kv_block_bytes bytes) is the
+ * reference's byte order (backend.rs:718-734, 738-773): K of layers
+ * 0..L-1, then V of layers 0..L-1, each [block_size, num_kv_heads, head_dim]
+ * in native little-endian element bytes, whatever the pool layout.
+ * ids: device u32[n]. dst/src: n blobs back to back; device memory or
+ * host-mapped pinned memory (hipHostMalloc), either is read/written directly
+ * by the kernel.
+ */
+int vapi_kv_export_blocks(const vapi_kv_pool* pool, const uint32_t* ids,
+                          uint32_t n, void* dst, vapi_stream_t stream);
+int vapi_kv_import_blocks(const vapi_kv_pool* pool, const uint32_t* ids,
+                          uint32_t n, const void* src, vapi_stream_t stream);
+
+/*
+ * Swap between HBM and pinned host memory through a device staging buffer:
+ * swap_out packs blocks into staging and hipMemcpyAsync's them device→host;
+ * swap_in copies host→staging and unpacks. Work is chunked to fit
+ * staging_bytes (at least one block). All work is enqueued on `stream`
+ * (typically a side stream, so a decode launch on another stream overlaps
+ * the DMA). host buffers: n * vapi_kv_block_bytes bytes, pinned.
+ */
+int vapi_kv_swap_out(const vapi_kv_pool* pool, const uint32_t* ids, uint32_t n,
+                     void* host_dst, void* staging, size_t staging_bytes,
+                     vapi_stream_t stream);
+int vapi_kv_swap_in(const vapi_kv_pool* pool, const uint32_t* ids, uint32_t n,
+                    const void* host_src, void* staging, size_t staging_bytes,
+                    vapi_stream_t stream);
+
+/*
+ * Host-side check of a step descriptor: ForwardBatch::validate
+ * (crates/vapi-engine/src/backend.rs:96-204). All arrays are host memory.
+ * block_tables is ragged: row i is table_data[table_offsets[i] ..
+ * table_offsets[i+1]] (table_offsets has batch+1 entries). Returns
+ * VAPI_KV_EINVAL with the reference's message on the first violation.
+ */
+int vapi_forward_batch_validate(uint32_t n_tokens, const uint32_t* positions,
+                                const uint32_t* slot_mapping,
+                                const uint32_t* cu_seqlens_q,
+                                const uint32_t* cu_seqlens_k, uint32_t batch,
+                                const uint32_t* table_offsets,
+                                const uint32_t* table_data,
+                                const uint32_t* logits_indices,
+                                uint32_t n_logits, uint32_t num_blocks,
+                                uint32_t block_size);
+
+/*
+ * Host packing of ragged block tables into [batch, width] (pack_block_tables,
+ * attention.rs:42-62): width = max(max row length, 1); each row is padded
+ * with its own last block (0 for an empty row). out holds batch*width u32;
+ * returns width, or a negative code if out_capacity is too small.
+ */
+int64_t vapi_pack_block_tables(uint32_t batch, const uint32_t* table_offsets,
+                               const uint32_t* table_data, uint32_t* out,
+                               size_t out_capacity);
+
+/* ---- host-side cache object (PagedKvCache + the backend block methods) -- */
+
+typedef struct vapi_cache vapi_cache;
+
+/* PagedKvCache::new (cache.rs:48-68): zeroed K and V for every layer, in one
+ * device allocation. */
+int vapi_cache_new(uint32_t num_layers, uint32_t num_blocks,
+                   uint32_t block_size, uint32_t num_kv_heads,
+                   uint32_t head_dim, uint32_t dtype, uint32_t layout,
+                   vapi_cache** out);
+void vapi_cache_free(vapi_cache* cache);
+/* The pool descriptor the low-level calls take. */
+int vapi_cache_pool(const vapi_cache* cache, vapi_kv_pool* out);
+/* PagedKvCache::num_slots (cache.rs:115-117). */
+uint64_t vapi_cache_num_slots(const vapi_cache* cache);
+
+/* write_kv_to_cache (cache.rs:136-148): k, v device [n_tokens, kvh, d] of
+ * src_dtype; slot_mapping is host u32[n_slots]. Errors as the reference:
+ * n_tokens != n_slots, src dtype != cache dtype, a slot past the end. */
+int vapi_cache_write_kv(vapi_cache* cache, uint32_t layer, const void* k,
+                        const void* v, uint32_t n_tokens, uint32_t src_dtype,
+                        const uint32_t* slot_mapping, uint32_t n_slots,
+                        vapi_stream_t stream);
+
+/* ExecutionBackend::block_bytes / export_block / import_block / copy_blocks
+ * (crates/vapi-engine/src/backend.rs:344-367, implementation
+ * crates/vapi-backend-candle/src/backend.rs:695-797). Synchronous on the
+ * null stream; host buffers may be pageable. */
+size_t vapi_cache_block_bytes(const vapi_cache* cache);
+int vapi_cache_export_block(vapi_cache* cache, uint32_t id, void* out,
+                            size_t out_len);
+int vapi_cache_import_block(vapi_cache* cache, uint32_t id, const void* bytes,
+                            size_t len);
+int vapi_cache_copy_blocks(vapi_cache* cache, const uint32_t* pairs_host,
+                           uint32_t n_pairs);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VAPI_KV_H */

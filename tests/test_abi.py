@@ -1,0 +1,152 @@
+"""CPU-side checks of the C ABI: the library loads, exports every symbol the
+header declares, and its host-only entry points (argument checks,
+ForwardBatch::validate, pack_block_tables, block sizing) behave like the
+reference. No GPU work is launched here."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from vapi_amd import _lib, workload
+from vapi_amd.attention import ForwardBatch
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def header_functions():
+    text = (ROOT / "include" / "vapi_kv.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vapi_\w+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    L = _lib.lib()
+    names = header_functions()
+    assert len(names) >= 20
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) == set(_lib.EXPORTS)
+    assert L.vapi_kv_version().startswith(b"vapi_kv")
+
+
+def pool(**kw):
+    p = dict(k=1, v=2, layer_stride_bytes=1 << 20, num_layers=1, num_blocks=8, block_size=16,
+             num_kv_heads=2, head_dim=64, dtype=_lib.BF16, layout=_lib.LAYOUT_HND)
+    p.update(kw)
+    return _lib.Pool(**p)
+
+
+def test_bad_arguments_are_errors_not_crashes():
+    L = _lib.lib()
+    assert L.vapi_kv_append(pool(dtype=9), 0, 1, 1, 1, 1, None) == _lib.EINVAL
+    assert b"dtype" in L.vapi_kv_last_error()
+    assert L.vapi_kv_append(pool(layout=5), 0, 1, 1, 1, 1, None) == _lib.EINVAL
+    assert L.vapi_kv_append(pool(), 1, 1, 1, 1, 1, None) == _lib.EINVAL
+    assert L.vapi_kv_append(pool(), 0, None, 1, 1, 1, None) == _lib.EINVAL
+    assert L.vapi_kv_append(pool(), 0, 1, 1, 1, 0, None) == _lib.OK  # nothing to do
+    assert L.vapi_kv_gather(pool(), 0, 1, 2, 33, 1, 1, None) == _lib.EINVAL
+    assert b"exceeds" in L.vapi_kv_last_error()
+    args = [1, 1, 1, 1, 1, 2, 4, 1, 100, 5, 0.1, -1, 0, None, 0, None]
+    assert L.vapi_paged_attention(pool(), 0, *args) == _lib.EINVAL
+    assert b"multiple" in L.vapi_kv_last_error()
+    # Workspace too small for a split-K decode.
+    need = L.vapi_paged_attention_workspace_size(pool(), 2, 8, 1, 5000)
+    assert need > 0
+    args = [1, 1, 1, 1, 1, 2, 320, 1, 5000, 8, 0.1, -1, 0, None, 0, None]
+    assert L.vapi_paged_attention(pool(), 0, *args) == _lib.ESPACE
+    assert L.vapi_kv_copy_blocks(pool(num_layers=2, layer_stride_bytes=16), 1, 1, None) == _lib.EINVAL
+    assert L.vapi_kv_swap_out(pool(), 1, 1, 1, 1, 10, None) == _lib.ESPACE
+
+
+def test_block_bytes_is_layers_times_kv_times_block():
+    L = _lib.lib()
+    p = pool(num_layers=28, num_kv_heads=4, head_dim=128)
+    assert L.vapi_kv_block_bytes(p) == 917504  # BASELINE config 4's block
+    assert L.vapi_kv_block_bytes(p) == oracle.block_bytes(28, 16, 4, 128, 2)
+    # lib.rs:143-157: 1 GiB holds 1024 blocks of 16 layers x 8 x 64 bf16, BS 32.
+    assert (1 << 30) // L.vapi_kv_block_bytes(
+        pool(num_layers=16, num_kv_heads=8, head_dim=64, block_size=32)) == 1024
+
+
+def test_pack_block_tables_matches_the_reference():
+    L = _lib.lib()
+    for tables in ([[0, 1, 2], [7]], [[], [3, 4]], [[5]], []):
+        offs, data = oracle.ragged(tables)
+        width = max([len(t) for t in tables] + [1])
+        out = np.zeros(max(len(tables), 1) * width, np.uint32)
+        u32p = ctypes.POINTER(ctypes.c_uint32)
+        w = L.vapi_pack_block_tables(len(tables), offs.ctypes.data_as(u32p),
+                                     data.ctypes.data_as(u32p), out.ctypes.data_as(u32p),
+                                     out.size)
+        assert w == width
+        if tables:
+            np.testing.assert_array_equal(out[:len(tables) * w].reshape(len(tables), w),
+                                          oracle.pack_block_tables(tables))
+    out = np.zeros(2, np.uint32)
+    offs, data = oracle.ragged([[0, 1, 2]])
+    u32p = ctypes.POINTER(ctypes.c_uint32)
+    assert L.vapi_pack_block_tables(1, offs.ctypes.data_as(u32p), data.ctypes.data_as(u32p),
+                                    out.ctypes.data_as(u32p), 2) == _lib.ESPACE
+
+
+def good_batch():
+    # Two sequences over 4-slot blocks: a 3-token prefill on 5 cached keys and a decode.
+    return ForwardBatch(tokens=[1, 2, 3, 4], positions=[5, 6, 7, 5],
+                        cu_seqlens_q=[0, 3, 4], cu_seqlens_k=[0, 8, 14],
+                        slot_mapping=[21, 22, 23, 1], block_tables=[[4, 5], [7, 0]],
+                        logits_indices=[2, 3], max_seqlen_q=3, max_seqlen_k=8)
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda b: b.slot_mapping.__setitem__(3, 22), "two tokens both write KV cache slot 22"),
+    (lambda b: b.block_tables.__setitem__(0, [4]), "needs 2 blocks to cover 8 keys"),
+    (lambda b: b.positions.__setitem__(1, 9), "non-contiguous positions"),
+    (lambda b: b.cu_seqlens_k.__setitem__(2, 7), "not monotonic"),
+    (lambda b: b.cu_seqlens_k.__setitem__(1, 2), "3 query tokens but only 2 key tokens"),
+    (lambda b: b.block_tables.__setitem__(1, [7, 8]), "references block 8 of 8"),
+    (lambda b: b.slot_mapping.__setitem__(3, 40), "past the end of the cache"),
+    (lambda b: b.logits_indices.append(4), "logits index 4"),
+    (lambda b: b.cu_seqlens_q.__setitem__(0, 1), "must start at 0"),
+])
+def test_validate_rejects_what_the_reference_rejects(mutate, msg):
+    b = good_batch()
+    b.validate(8, 4)
+    mutate(b)
+    with pytest.raises((_lib.VapiKvError, ValueError), match=msg):
+        b.validate(8, 4)
+
+
+def test_validate_checks_the_host_side_lengths_too():
+    b = good_batch()
+    b.positions.pop()
+    with pytest.raises(ValueError, match="positions"):
+        b.validate(8, 4)
+    b = good_batch()
+    b.block_tables.pop()
+    with pytest.raises(ValueError, match="block tables"):
+        b.validate(8, 4)
+
+
+def test_the_workloads_have_the_baseline_shapes():
+    w0 = workload.config0_decode_small()
+    assert w0.batch == 8 and 64 <= w0.lens.min() and w0.lens.max() <= 512
+    assert len({b for t in w0.tables for b in t}) == sum(len(t) for t in w0.tables)
+    w1 = workload.config1_append()
+    assert w1.n_tokens == 4096 and w1.n_tokens - w1.n_valid == 205
+    valid = w1.slots[w1.slots != workload.SKIP]
+    assert len(np.unique(valid)) == len(valid) and valid.max() < 65536 * 16
+    w2 = workload.config2_decode()
+    assert w2.batch == 64 and w2.lens.min() >= 256 and w2.lens.max() <= 8192
+    assert 1e5 < w2.lens.sum() < 3e5
+    assert sum(len(t) for t in w2.tables) <= 32768
+    w3 = workload.config3_prefill()
+    assert w3.batch == 32 and w3.num_blocks == 4608
+    assert all(np.array_equal(w3.tables[0][:128], w3.tables[7][:128]) for _ in [0])
+    assert not np.array_equal(w3.tables[0][:128], w3.tables[8][:128])
+    assert abs(w3.flops() - 1.031e12) / 1.031e12 < 1e-3
+    w4 = workload.config4_block_ops()
+    assert w4.pairs.shape == (2048, 2) and len(w4.swap_ids) == 4096
+    assert not set(w4.pairs[:, 1]) & set(w4.pairs[:, 0])

@@ -1,0 +1,281 @@
+"""GPU parity of vapi_paged_attention against the oracle.
+
+Tolerances (written here, per dtype):
+  f32:  max-abs <= 1e-5 against the f32 oracle (the reference's own CPU bar,
+        attention.rs:400-404).
+  bf16: max-abs <= 2e-2 * max|reference| (relative) and the reference's own
+        CUDA-vs-CPU bound max-abs < 1e-2 on its test shapes (attention.rs:661-664).
+  f16:  max-abs < 1e-3 on the reference's test shape (attention.rs:666-669).
+The oracle output is cast to the input dtype before comparing, as
+paged_attention_cpu does (attention.rs:162).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from vapi_amd import workload
+from vapi_amd.attention import (ForwardBatch, PreparedAttention, paged_attention,
+                                paged_attention_prepared, paged_attention_windowed)
+from vapi_amd.cache import PagedKvCache, write_kv_to_cache
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def host_f32(t):
+    return t.detach().float().cpu().numpy()
+
+
+def oracle_out(q, cache, layer, batch: ForwardBatch, scale, window=None, wr=0):
+    kc = host_f32(cache.reference_view(layer, "k").contiguous())
+    vc = host_f32(cache.reference_view(layer, "v").contiguous())
+    out = oracle.paged_attention(host_f32(q), kc, vc, batch.cu_seqlens_q, batch.cu_seqlens_k,
+                                 batch.block_tables, scale, window, wr, threads=8)
+    return torch.from_numpy(out).to(q.dtype).float()
+
+
+def max_abs(a, b):
+    return float((a.float().cpu() - b.float().cpu()).abs().max())
+
+
+# ---- the reference's CUDA tests (attention.rs:441-714), same shapes ----------
+
+HEADS, KV_HEADS, HEAD_DIM, BLOCK = 4, 2, 64, 32
+
+
+def ref_rows(n, seed, heads, d, dtype, mul):
+    i = torch.arange(n * heads * d, dtype=torch.float32)
+    data = (torch.sin(i * mul + seed) if mul == 0.173 else torch.cos(i * mul + seed)) * 0.5
+    return data.reshape(n, heads, d).to(dtype).to(DEV)
+
+
+def slots(table, positions, bs=BLOCK):
+    return [table[p // bs] * bs + p % bs for p in positions]
+
+
+def mixed(dtype, layout="HND"):
+    """attention.rs:476-514: A = 70 cached + 20-token chunk, B = decode over 40."""
+    c = PagedKvCache(1, 8, BLOCK, KV_HEADS, HEAD_DIM, dtype, layout)
+    ta, tb = [5, 1, 6], [7, 2]
+    len_a, chunk_a, len_b = 90, 20, 40
+    write_kv_to_cache(c, 0, ref_rows(len_a, 0.1, KV_HEADS, HEAD_DIM, dtype, 0.173),
+                      ref_rows(len_a, 0.2, KV_HEADS, HEAD_DIM, dtype, 0.173), slots(ta, range(len_a)))
+    write_kv_to_cache(c, 0, ref_rows(len_b, 0.3, KV_HEADS, HEAD_DIM, dtype, 0.173),
+                      ref_rows(len_b, 0.4, KV_HEADS, HEAD_DIM, dtype, 0.173), slots(tb, range(len_b)))
+    q = ref_rows(chunk_a + 1, 0.5, HEADS, HEAD_DIM, dtype, 0.131)
+    batch = ForwardBatch(cu_seqlens_q=[0, chunk_a, chunk_a + 1],
+                         cu_seqlens_k=[0, len_a, len_a + len_b], block_tables=[ta, tb],
+                         max_seqlen_q=chunk_a, max_seqlen_k=len_a)
+    return c, q, batch
+
+
+@pytest.mark.parametrize("layout", ["HND", "NHD"])
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 1e-2), (torch.float16, 1e-3)])
+def test_the_kernel_matches_the_cpu_reference(dtype, tol, layout):
+    c, q, batch = mixed(dtype, layout)
+    scale = 1.0 / HEAD_DIM ** 0.5
+    want = oracle_out(q, c, 0, batch, scale)
+    got = paged_attention(q, c, 0, batch, scale)
+    assert got.shape == want.shape
+    d = max_abs(got, want)
+    assert d < tol, f"{dtype}: max abs diff {d}"
+
+
+def test_laguna_shapes_match_the_cpu_reference():
+    """attention.rs:558-625: head_dim 16, GQA 3:1 and 4:1, window 6."""
+    for heads, window in [(6, None), (8, 6), (6, 6)]:
+        kvh, hd = 2, 16
+        c = PagedKvCache(1, 8, BLOCK, kvh, hd, torch.bfloat16)
+
+        def mk(n, h, seed):
+            i = torch.arange(n * h * hd, dtype=torch.float32)
+            return (torch.sin(i * 0.173 + seed) * 0.5).reshape(n, h, hd).to(torch.bfloat16).to(DEV)
+
+        ta, tb = [4], [6, 1]
+        la, lb = 18, 40
+        write_kv_to_cache(c, 0, mk(la, kvh, 0.1), mk(la, kvh, 0.2), slots(ta, range(la)))
+        write_kv_to_cache(c, 0, mk(lb, kvh, 0.3), mk(lb, kvh, 0.4), slots(tb, range(lb)))
+        q = mk(la + 1, heads, 0.5)
+        batch = ForwardBatch(cu_seqlens_q=[0, la, la + 1], cu_seqlens_k=[0, la, la + lb],
+                             block_tables=[ta, tb], max_seqlen_q=la, max_seqlen_k=lb)
+        scale = 1.0 / hd ** 0.5
+        want = oracle_out(q, c, 0, batch, scale, window)
+        got = paged_attention(q, c, 0, batch, scale, window)
+        d = max_abs(got, want)
+        assert d < 1e-2, f"heads {heads} window {window}: max abs diff {d}"
+
+
+def test_a_sliding_window_matches_the_cpu_reference_and_differs_from_full():
+    c, q, batch = mixed(torch.bfloat16)
+    scale = 1.0 / HEAD_DIM ** 0.5
+    want = oracle_out(q, c, 0, batch, scale, 16)
+    got = paged_attention(q, c, 0, batch, scale, 16)
+    assert max_abs(got, want) < 1e-2
+    full = oracle_out(q, c, 0, batch, scale)
+    assert max_abs(full, want) > 1e-2, "the window must hide something"
+
+
+def test_a_bidirectional_window_is_not_causal():
+    c, q, batch = mixed(torch.bfloat16)
+    scale = 1.0 / HEAD_DIM ** 0.5
+    causal = paged_attention_windowed(q, c, 0, batch, scale, None, 0)
+    bidir = paged_attention_windowed(q, c, 0, batch, scale, None, None)
+    want = oracle_out(q, c, 0, batch, scale)
+    assert max_abs(causal, want) < 1e-2
+    assert max_abs(bidir[:20], want[:20]) > 1e-2
+    assert max_abs(bidir, oracle_out(q, c, 0, batch, scale, None, -1)) < 1e-2
+
+
+def test_the_sliding_window_closed_form_on_the_device():
+    """attention.rs:323-353 with Q = 0: output[1] is the mean visible key index."""
+    c = PagedKvCache(1, 2, 4, 1, 2, torch.float32)
+    k = torch.tensor([[i, 0.0] for i in range(6)]).reshape(6, 1, 2).to(DEV)
+    v = torch.tensor([[1.0, i] for i in range(6)]).reshape(6, 1, 2).to(DEV)
+    write_kv_to_cache(c, 0, k, v, list(range(6)))
+    q = torch.zeros(6, 1, 2, device=DEV)
+    batch = ForwardBatch(cu_seqlens_q=[0, 6], cu_seqlens_k=[0, 6], block_tables=[[0, 1]],
+                         max_seqlen_q=6, max_seqlen_k=6)
+    out = paged_attention(q, c, 0, batch, 1.0, 3)
+    assert out[:, 0, 1].cpu().tolist() == [0.0, 0.5, 1.0, 2.0, 3.0, 4.0]
+
+
+# ---- random mixed batches over every kernel path --------------------------------
+
+def random_case(rng, dtype, heads, kvh, d, bs, lens_q, lens_k, layout, nb=None):
+    nb = nb or sum(-(-l // bs) for l in lens_k) + 3
+    c = PagedKvCache(1, nb, bs, kvh, d, dtype, layout)
+    workload.fill_normal(c._slab, int(rng.integers(1 << 30)))
+    perm = rng.permutation(nb)
+    tables, at = [], 0
+    for lk in lens_k:
+        n = -(-lk // bs)
+        tables.append(perm[at:at + n].tolist())
+        at += n
+    g = torch.Generator(device=DEV).manual_seed(int(rng.integers(1 << 30)))
+    q = torch.randn(sum(lens_q), heads, d, generator=g, device=DEV).to(dtype)
+    batch = ForwardBatch(cu_seqlens_q=np.concatenate([[0], np.cumsum(lens_q)]).tolist(),
+                         cu_seqlens_k=np.concatenate([[0], np.cumsum(lens_k)]).tolist(),
+                         block_tables=tables, max_seqlen_q=max(lens_q),
+                         max_seqlen_k=max(lens_k))
+    return c, q, batch
+
+
+CASES = [
+    # dtype, heads, kvh, d, bs, lens_q, lens_k, window, layout
+    (torch.bfloat16, 32, 8, 128, 16, [1, 1, 1, 1], [1, 17, 600, 1500], None, "HND"),
+    (torch.bfloat16, 32, 8, 128, 16, [1, 37, 1, 64], [700, 37, 33, 300], None, "NHD"),
+    (torch.float16, 16, 8, 128, 32, [1, 5, 1], [1100, 40, 513], None, "HND"),
+    (torch.bfloat16, 28, 4, 128, 16, [1, 19], [2000, 300], 100, "HND"),
+    (torch.bfloat16, 8, 8, 64, 16, [1, 100], [900, 100], None, "HND"),
+    (torch.bfloat16, 64, 4, 64, 32, [2, 1], [70, 64], 9, "NHD"),
+    (torch.float32, 16, 8, 128, 16, [1, 1, 9], [64, 512, 200], None, "HND"),
+    (torch.float32, 6, 2, 80, 8, [3, 1], [10, 50], 4, "NHD"),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"{str(c[0])[6:]}-h{c[1]}-kv{c[2]}-d{c[3]}-bs{c[4]}-w{c[7]}-{c[8]}")
+def test_random_mixed_batches_match_the_oracle(case):
+    dtype, heads, kvh, d, bs, lens_q, lens_k, window, layout = case
+    rng = np.random.default_rng(abs(hash(str(case))) % (1 << 32))
+    c, q, batch = random_case(rng, dtype, heads, kvh, d, bs, lens_q, lens_k, layout)
+    scale = d ** -0.5
+    want = oracle_out(q, c, 0, batch, scale, window)
+    got = paged_attention(q, c, 0, batch, scale, window)
+    d_abs = max_abs(got, want)
+    if dtype == torch.float32:
+        assert d_abs <= 1e-5, d_abs
+    else:
+        assert d_abs <= 2e-2 * float(want.abs().max()), d_abs
+
+
+def test_config0_decode_f32_matches_within_1e_5():
+    """Qwen3-0.6B-shaped f32 decode; prior context and the
+    new token appended through slot_mapping, then attend."""
+    w = workload.config0_decode_small()
+    c = PagedKvCache(1, w.num_blocks, w.block_size, w.num_kv_heads, w.head_dim, torch.float32)
+    g = torch.Generator(device=DEV).manual_seed(workload.seed_for(0))
+    for t, l in zip(w.tables, w.lens):
+        prev = int(l) - 1
+        k = torch.randn(prev, 8, 128, generator=g, device=DEV)
+        v = torch.randn(prev, 8, 128, generator=g, device=DEV)
+        write_kv_to_cache(c, 0, k, v, workload.slots_for(t, np.arange(prev), 16))
+    knew = torch.randn(w.batch, 8, 128, generator=g, device=DEV)
+    vnew = torch.randn(w.batch, 8, 128, generator=g, device=DEV)
+    write_kv_to_cache(c, 0, knew, vnew, w.new_token_slots())
+    q = torch.randn(w.batch, 16, 128, generator=g, device=DEV)
+    batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
+                         block_tables=[t.tolist() for t in w.tables], max_seqlen_q=1,
+                         max_seqlen_k=int(w.lens.max()))
+    scale = 128 ** -0.5
+    want = oracle_out(q, c, 0, batch, scale)
+    got = paged_attention(q, c, 0, batch, scale)
+    assert max_abs(got, want) <= 1e-5
+
+
+def test_config2_decode_full_size_matches_the_oracle():
+    """BASELINE config 2 at full size (64 sequences, log-normal contexts up to
+    8k, 32k-block pool); every sequence checked against the oracle."""
+    w = workload.config2_decode()
+    c = PagedKvCache(1, w.num_blocks, w.block_size, 8, 128, torch.bfloat16)
+    workload.fill_normal(c._slab, workload.seed_for(2))
+    g = torch.Generator(device=DEV).manual_seed(7)
+    q = torch.randn(w.batch, 32, 128, generator=g, device=DEV).to(torch.bfloat16)
+    batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
+                         block_tables=[t.tolist() for t in w.tables], max_seqlen_q=1,
+                         max_seqlen_k=int(w.lens.max()))
+    scale = 128 ** -0.5
+    got = paged_attention(q, c, 0, batch, scale)
+    want = oracle_out(q, c, 0, batch, scale)
+    assert max_abs(got, want) <= 2e-2 * float(want.abs().max())
+    # Determinism: the same launch gives the same bits.
+    assert torch.equal(paged_attention(q, c, 0, batch, scale), got)
+
+
+def test_config3_prefill_rows_match_the_oracle():
+    """BASELINE config 3 (32 x 512-token chunks over 4,096 keys, shared
+    prefixes): the whole batch runs in one call; rows at the start, middle and
+    end of four sequences are checked against the oracle run on those rows."""
+    w = workload.config3_prefill()
+    c = PagedKvCache(1, w.num_blocks, w.block_size, 8, 128, torch.bfloat16)
+    workload.fill_normal(c._slab, workload.seed_for(3))
+    g = torch.Generator(device=DEV).manual_seed(8)
+    q = torch.randn(w.batch * w.len_q, 32, 128, generator=g, device=DEV).to(torch.bfloat16)
+    batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
+                         block_tables=[t.tolist() for t in w.tables], max_seqlen_q=w.len_q,
+                         max_seqlen_k=w.len_k)
+    scale = 128 ** -0.5
+    got = paged_attention(q, c, 0, batch, scale)
+    kc = host_f32(c.reference_view(0, "k").contiguous())
+    vc = host_f32(c.reference_view(0, "v").contiguous())
+    for s in (0, 9, 18, 31):
+        for j0 in (0, 250, w.len_q - 16):
+            rows_q = q[s * w.len_q + j0: s * w.len_q + j0 + 16]
+            lk = w.len_k - w.len_q + j0 + 16
+            want = oracle.paged_attention(host_f32(rows_q), kc, vc, [0, 16], [0, lk],
+                                          [w.tables[s].tolist()], scale, threads=8)
+            want = torch.from_numpy(want).to(torch.bfloat16).float()
+            gr = got[s * w.len_q + j0: s * w.len_q + j0 + 16]
+            assert max_abs(gr, want) <= 2e-2 * float(want.abs().max()), (s, j0)
+
+
+def test_prepared_inputs_are_reusable_across_layers():
+    rng = np.random.default_rng(9)
+    L = 3
+    c = PagedKvCache(L, 64, 16, 8, 128, torch.bfloat16)
+    workload.fill_normal(c._slab, 9)
+    lens_k = [300, 1, 520]
+    perm = rng.permutation(64)
+    tables, at = [], 0
+    for lk in lens_k:
+        n = -(-lk // 16)
+        tables.append(perm[at:at + n].tolist())
+        at += n
+    q = torch.randn(3, 32, 128, device=DEV).to(torch.bfloat16)
+    batch = ForwardBatch(cu_seqlens_q=[0, 1, 2, 3], cu_seqlens_k=np.concatenate([[0], np.cumsum(lens_k)]).tolist(),
+                         block_tables=tables, max_seqlen_q=1, max_seqlen_k=520)
+    prep = PreparedAttention.from_batch(batch, DEV)
+    for layer in range(L):
+        got = paged_attention_prepared(q, c, layer, prep, 128 ** -0.5)
+        want = oracle_out(q, c, layer, batch, 128 ** -0.5)
+        assert max_abs(got, want) <= 2e-2 * float(want.abs().max())

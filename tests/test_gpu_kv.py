@@ -1,0 +1,254 @@
+"""GPU parity of the data-movement kernels against the oracle: append,
+gather, copy-on-write, export/import and swap — all bit-exact.
+
+Mirrors the reference's cache.rs tests (:308-445) on the device, then runs
+the BASELINE configurations' shapes.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from vapi_amd import _lib
+from vapi_amd.backend import KvBlockBackend
+from vapi_amd.cache import PagedKvCache, gather_kv, write_kv_to_cache
+from vapi_amd import workload
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+BS = 4
+LAYOUTS = ["HND", "NHD"]
+
+
+def rows(n, base, heads=2, width=3, dtype=torch.float32):
+    return (base + torch.arange(n * heads * width, dtype=torch.float32)).reshape(
+        n, heads, width).to(dtype).to(DEV)
+
+
+def ref_pool(cache, layer, which="k"):
+    """Layer buffer in the reference layout [nb, bs, kvh, d] on the host."""
+    return cache.reference_view(layer, which).contiguous().cpu()
+
+
+def as_np(t: torch.Tensor) -> np.ndarray:
+    """Host copy with 16-bit floats kept as raw bits."""
+    t = t.detach().cpu().contiguous()
+    if t.dtype in (torch.bfloat16, torch.float16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_a_write_spanning_non_adjacent_blocks_lands_in_exactly_those_slots(layout):
+    c = PagedKvCache(2, 8, BS, 2, 3, torch.float32, layout)
+    slots = [24, 25, 26, 27, 4, 5, 6, 7, 12]
+    k, v = rows(9, 100.0), rows(9, 1000.0)
+    write_kv_to_cache(c, 1, k, v, slots)
+    assert torch.equal(gather_kv(c, 1, [6, 1, 3], 9, "k"), k)
+    assert torch.equal(gather_kv(c, 1, [6, 1, 3], 9, "v"), v)
+    assert float(c.k[0].abs().sum()) == 0.0
+    flat = ref_pool(c, 1).reshape(32, 2, 3)
+    for slot in range(32):
+        assert bool((flat[slot] != 0).any()) == (slot in slots), slot
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_slot_5_is_block_1_offset_1(layout):
+    c = PagedKvCache(2, 2, BS, 2, 3, torch.float32, layout)
+    write_kv_to_cache(c, 0, rows(1, 7.0), rows(1, 9.0), [5])
+    assert ref_pool(c, 0)[1][1].tolist() == [[7, 8, 9], [10, 11, 12]]
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_a_decode_batch_and_an_overwrite(layout):
+    c = PagedKvCache(2, 4, BS, 2, 3, torch.float32, layout)
+    slots = [3, 9, 0, 14, 6, 11]
+    k = rows(6, 1.0)
+    write_kv_to_cache(c, 0, k, k, slots)
+    flat = ref_pool(c, 0).reshape(16, 2, 3)
+    for i, s in enumerate(slots):
+        assert torch.equal(flat[s], k[i].cpu())
+    write_kv_to_cache(c, 0, rows(1, 50.0), rows(1, 50.0), [2])
+    assert ref_pool(c, 0).reshape(16, 2, 3)[2][0][0] == 50.0
+
+
+def test_mismatched_shapes_and_out_of_range_slots_are_errors():
+    c = PagedKvCache(2, 2, BS, 2, 3, torch.float32)
+    with pytest.raises(ValueError):
+        write_kv_to_cache(c, 0, rows(2, 0.0), rows(2, 0.0), [0])
+    with pytest.raises(ValueError):
+        write_kv_to_cache(c, 0, rows(1, 0.0), rows(1, 0.0), [8])
+    with pytest.raises(ValueError):
+        write_kv_to_cache(c, 0, rows(1, 0.0, dtype=torch.float16),
+                          rows(1, 0.0, dtype=torch.float16), [0])
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("dtype,kvh,d", [(torch.bfloat16, 8, 128), (torch.float16, 2, 64),
+                                         (torch.float32, 3, 5), (torch.bfloat16, 1, 3)])
+def test_append_matches_the_oracle_bit_exactly(layout, dtype, kvh, d):
+    rng = np.random.default_rng(11)
+    bs, nb, n = 16, 64, 300
+    c = PagedKvCache(1, nb, bs, kvh, d, dtype, layout)
+    init = torch.randn(c._slab.shape, device=DEV).to(dtype)
+    c._slab.copy_(init)
+    slots = rng.permutation(nb * bs)[:n].astype(np.uint32)
+    slots[rng.choice(n, 15, replace=False)] = _lib.SLOT_SKIP
+    k = torch.randn(n, kvh, d, device=DEV).to(dtype)
+    v = torch.randn(n, kvh, d, device=DEV).to(dtype)
+    want_k, want_v = as_np(ref_pool(c, 0, "k")), as_np(ref_pool(c, 0, "v"))
+    oracle.write_rows(want_k, as_np(k), slots)
+    oracle.write_rows(want_v, as_np(v), slots)
+    write_kv_to_cache(c, 0, k, v, slots)
+    np.testing.assert_array_equal(as_np(ref_pool(c, 0, "k")), want_k)
+    np.testing.assert_array_equal(as_np(ref_pool(c, 0, "v")), want_v)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_config1_append_full_size_is_bit_exact(layout):
+    """BASELINE config 1 at full size: 4,096 tokens (5% padded) into a
+    65,536-block bf16 pool pre-filled with noise; the whole pool (4 GiB) must
+    equal the oracle's scatter applied to the same starting bytes."""
+    w = workload.config1_append()
+    c = PagedKvCache(1, w.num_blocks, w.block_size, w.num_kv_heads, w.head_dim,
+                     torch.bfloat16, layout)
+    workload.fill_normal(c._slab, 1)
+    g = torch.Generator(device=DEV).manual_seed(101)
+    k = torch.randn(w.n_tokens, 8, 128, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(w.n_tokens, 8, 128, generator=g, device=DEV).to(torch.bfloat16)
+    want = {"k": as_np(ref_pool(c, 0, "k")), "v": as_np(ref_pool(c, 0, "v"))}
+    write_kv_to_cache(c, 0, k, v, w.slots)
+    torch.cuda.synchronize()
+    for which, src in (("k", k), ("v", v)):
+        runs = oracle.write_rows(want[which], as_np(src), w.slots)
+        assert runs > 4  # the reference would take its scatter branch
+        np.testing.assert_array_equal(as_np(ref_pool(c, 0, which)), want[which])
+        del want[which]
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_gather_matches_the_oracle(layout):
+    rng = np.random.default_rng(2)
+    c = PagedKvCache(2, 40, 16, 4, 64, torch.bfloat16, layout)
+    workload.fill_normal(c._slab, 2)
+    table = rng.permutation(40)[:9].astype(np.uint32)
+    for len_k in (1, 17, 130, 144):
+        got = gather_kv(c, 1, table, len_k, "v")
+        want = oracle.gather_kv(as_np(ref_pool(c, 1, "v")), table, len_k)
+        np.testing.assert_array_equal(as_np(got), want)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_copy_blocks_matches_the_oracle(layout):
+    rng = np.random.default_rng(3)
+    L, nb = 5, 96
+    c = PagedKvCache(L, nb, 16, 4, 128, torch.bfloat16, layout)
+    workload.fill_normal(c._slab, 3)
+    perm = rng.permutation(nb)
+    pairs = np.stack([perm[:20], perm[20:40]], 1)
+    ks = [as_np(ref_pool(c, l, "k")) for l in range(L)]
+    vs = [as_np(ref_pool(c, l, "v")) for l in range(L)]
+    oracle.copy_blocks(ks, vs, pairs)
+    KvBlockBackend(c).copy_blocks(pairs.tolist())
+    for l in range(L):
+        np.testing.assert_array_equal(as_np(ref_pool(c, l, "k")), ks[l])
+        np.testing.assert_array_equal(as_np(ref_pool(c, l, "v")), vs[l])
+
+
+def test_copy_blocks_rejects_overlapping_pairs():
+    c = PagedKvCache(1, 8, 16, 1, 64, torch.bfloat16)
+    with pytest.raises(ValueError):
+        KvBlockBackend(c).copy_blocks([(1, 2), (2, 3)])
+    with pytest.raises(ValueError):
+        KvBlockBackend(c).copy_blocks([(1, 8)])
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("dtype,kvh,d", [(torch.bfloat16, 4, 128), (torch.float32, 2, 3)])
+def test_export_matches_the_reference_byte_order_and_import_inverts_it(layout, dtype, kvh, d):
+    L, nb = 3, 12
+    c = PagedKvCache(L, nb, 16, kvh, d, dtype, layout)
+    workload.fill_normal(c._slab, 4)
+    be = KvBlockBackend(c)
+    ks = [as_np(ref_pool(c, l, "k")) for l in range(L)]
+    vs = [as_np(ref_pool(c, l, "v")) for l in range(L)]
+    assert be.block_bytes() == oracle.block_bytes(L, 16, kvh, d, c._slab.element_size())
+    for bid in (0, 5, 11):
+        assert be.export_block(bid) == oracle.export_block(ks, vs, bid)
+    blob = be.export_blocks([3, 7])
+    c2 = PagedKvCache(L, nb, 16, kvh, d, dtype, layout)
+    be2 = KvBlockBackend(c2)
+    be2.import_blocks([9, 1], blob)
+    assert be2.export_block(9) == be.export_block(3)
+    assert be2.export_block(1) == be.export_block(7)
+    be2.import_block(4, be.export_block(11))
+    assert be2.export_block(4) == be.export_block(11)
+    with pytest.raises(ValueError):
+        be2.import_block(0, be.export_block(0)[:-2])
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_swap_round_trip_through_pinned_host_is_bit_exact(layout):
+    L, nb, n = 4, 64, 20
+    c = PagedKvCache(L, nb, 16, 4, 128, torch.bfloat16, layout)
+    workload.fill_normal(c._slab, 5)
+    be = KvBlockBackend(c)
+    bb = be.block_bytes()
+    rng = np.random.default_rng(6)
+    perm = rng.permutation(nb)
+    out_ids, in_ids = perm[:n], perm[n:2 * n]
+    host = torch.empty(n * bb, dtype=torch.uint8, pin_memory=True)
+    staging = torch.empty(3 * bb + 5, dtype=torch.uint8, device=DEV)  # forces chunking
+    side = torch.cuda.Stream()
+    ids_out = torch.from_numpy(out_ids.astype(np.int32)).to(DEV)
+    ids_in = torch.from_numpy(in_ids.astype(np.int32)).to(DEV)
+    want = be.export_blocks(out_ids.tolist()).cpu()
+    torch.cuda.synchronize()
+    be.swap_out(ids_out, host, staging, stream=side)
+    side.synchronize()
+    assert torch.equal(host, want)
+    be.swap_in(ids_in, host, staging, stream=side)
+    side.synchronize()
+    for a, b in zip(out_ids, in_ids):
+        assert be.export_block(int(b)) == be.export_block(int(a))
+
+
+def test_the_native_cache_object_mirrors_the_backend_block_methods():
+    L = _lib.lib()
+    h = ctypes.c_void_p()
+    _lib.check(L.vapi_cache_new(2, 8, 4, 2, 3, _lib.F32, _lib.LAYOUT_HND, ctypes.byref(h)))
+    try:
+        assert L.vapi_cache_num_slots(h) == 32
+        assert L.vapi_cache_block_bytes(h) == 2 * 2 * 4 * 2 * 3 * 4
+        k = rows(9, 100.0)
+        v = rows(9, 1000.0)
+        slots = (ctypes.c_uint32 * 9)(24, 25, 26, 27, 4, 5, 6, 7, 12)
+        _lib.check(L.vapi_cache_write_kv(h, 1, k.data_ptr(), v.data_ptr(), 9, _lib.F32,
+                                         slots, 9, None))
+        torch.cuda.synchronize()
+        bad = (ctypes.c_uint32 * 1)(32)
+        assert L.vapi_cache_write_kv(h, 1, k.data_ptr(), v.data_ptr(), 1, _lib.F32, bad, 1,
+                                     None) == _lib.EINVAL
+        assert b"past the end" in L.vapi_kv_last_error()
+        assert L.vapi_cache_write_kv(h, 1, k.data_ptr(), v.data_ptr(), 2, _lib.F32, bad, 1,
+                                     None) == _lib.EINVAL
+        bb = L.vapi_cache_block_bytes(h)
+        buf = (ctypes.c_uint8 * bb)()
+        _lib.check(L.vapi_cache_export_block(h, 6, buf, bb))
+        blob = np.frombuffer(bytes(buf), np.float32)
+        seg = 4 * 2 * 3
+        # Layer 1 K of block 6 holds tokens 0..3 (slots 24..27): k rows 0..3.
+        np.testing.assert_array_equal(blob[seg:2 * seg], k[:4].cpu().numpy().reshape(-1))
+        np.testing.assert_array_equal(blob[3 * seg:4 * seg], v[:4].cpu().numpy().reshape(-1))
+        _lib.check(L.vapi_cache_import_block(h, 2, buf, bb))
+        assert L.vapi_cache_import_block(h, 2, buf, bb - 4) == _lib.EINVAL
+        pairs = (ctypes.c_uint32 * 2)(2, 5)
+        _lib.check(L.vapi_cache_copy_blocks(h, pairs, 1))
+        buf2 = (ctypes.c_uint8 * bb)()
+        _lib.check(L.vapi_cache_export_block(h, 5, buf2, bb))
+        assert bytes(buf2) == bytes(buf)
+    finally:
+        L.vapi_cache_free(h)

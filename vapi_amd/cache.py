@@ -1,0 +1,166 @@
+"""The paged KV pool and the KV append, host side.
+
+Mirrors vapi's crates/vapi-backend-candle/src/cache.rs:
+  PagedKvCache (:12-118), write_kv_to_cache (:136-148) with write_rows's
+  checks (:217-240), scatter_index/write_rows_indexed (:165-215) and
+  gather_kv (:283-290).
+Device memory comes from torch; every byte the pool sees is moved by
+libvapi_kv.so kernels.
+"""
+from __future__ import annotations
+
+from typing import Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import Pool, check, lib
+
+_DTYPES = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}
+_LAYOUTS = {"HND": _lib.LAYOUT_HND, "NHD": _lib.LAYOUT_NHD}
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPES[dt]
+    except KeyError:
+        raise TypeError(f"unsupported KV dtype {dt}") from None
+
+
+def stream_handle(stream=None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+class PagedKvCache:
+    """Per-layer K and V block pools in one device slab.
+
+    layout "HND": each layer buffer is [num_blocks, num_kv_heads, block_size,
+    head_dim] (a (block, head) tile is contiguous, the MI355X default);
+    "NHD": [num_blocks, block_size, num_kv_heads, head_dim], the reference's
+    own layout (cache.rs:7-11). Both are addressed by the same flat slot
+    block*block_size + offset (cache.rs:113-117).
+    """
+
+    def __init__(self, num_layers: int, num_blocks: int, block_size: int,
+                 num_kv_heads: int, head_dim: int, dtype: torch.dtype = torch.bfloat16,
+                 layout: str = "HND", device: str | torch.device = "cuda"):
+        if layout not in _LAYOUTS:
+            raise ValueError(f"layout must be HND or NHD, not {layout!r}")
+        self.num_layers = num_layers
+        self.num_blocks = num_blocks
+        self.block_size = block_size
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.dtype = dtype
+        self.layout = layout
+        self.device = torch.device(device)
+        layer_elems = num_blocks * block_size * num_kv_heads * head_dim
+        elt = torch.tensor([], dtype=dtype).element_size()
+        # Pad each layer to a multiple of 256 bytes so every layer is aligned.
+        pad_elems = (-(layer_elems * elt) % 256) // elt
+        self._stride_elems = layer_elems + pad_elems
+        self._slab = torch.zeros((2, num_layers, self._stride_elems), dtype=dtype,
+                                 device=self.device)
+        shape = ((num_blocks, num_kv_heads, block_size, head_dim) if layout == "HND"
+                 else (num_blocks, block_size, num_kv_heads, head_dim))
+        self.k = [self._slab[0, i, :layer_elems].view(shape) for i in range(num_layers)]
+        self.v = [self._slab[1, i, :layer_elems].view(shape) for i in range(num_layers)]
+        self.pool = Pool(
+            k=self._slab[0, 0].data_ptr() if num_layers else None,
+            v=self._slab[1, 0].data_ptr() if num_layers else None,
+            layer_stride_bytes=self._stride_elems * elt,
+            num_layers=num_layers, num_blocks=num_blocks, block_size=block_size,
+            num_kv_heads=num_kv_heads, head_dim=head_dim, dtype=dtype_code(dtype),
+            layout=_LAYOUTS[layout])
+
+    def num_slots(self) -> int:
+        return self.num_blocks * self.block_size
+
+    def reference_view(self, layer: int, which: str = "k") -> torch.Tensor:
+        """Layer buffer as the reference's [nb, bs, kvh, d] (a permuted view
+        for HND; call .contiguous() for bytes)."""
+        t = (self.k if which == "k" else self.v)[layer]
+        return t.permute(0, 2, 1, 3) if self.layout == "HND" else t
+
+    def block_bytes(self) -> int:
+        return lib().vapi_kv_block_bytes(self.pool)
+
+
+def _slots_host(slot_mapping) -> np.ndarray:
+    if isinstance(slot_mapping, torch.Tensor):
+        slot_mapping = slot_mapping.cpu().numpy()
+    return np.ascontiguousarray(np.asarray(slot_mapping, dtype=np.int64).astype(np.uint32))
+
+
+def write_kv_to_cache(cache: PagedKvCache, layer: int, k: torch.Tensor, v: torch.Tensor,
+                      slot_mapping: Sequence[int] | np.ndarray | torch.Tensor,
+                      stream=None) -> None:
+    """Write a step's K/V at `slot_mapping` in place (cache.rs:136-148).
+
+    k, v: [n, num_kv_heads, head_dim] device tensors in the cache dtype.
+    slot_mapping: host sequence of u32 slots (SLOT_SKIP = padded, skipped).
+    Raises ValueError for the reference's error cases (cache.rs:143-145,
+    223-240): k/v shape mismatch, token/slot count mismatch, dtype mismatch,
+    a slot past the end.
+    """
+    if tuple(k.shape) != tuple(v.shape):
+        raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} differ in shape")
+    if k.dim() != 3:
+        raise ValueError(f"rows must be (n, heads, width), got {tuple(k.shape)}")
+    slots = _slots_host(slot_mapping)
+    n = k.shape[0]
+    if n != slots.shape[0]:
+        raise ValueError(f"{n} tokens but {slots.shape[0]} cache slots")
+    if k.dtype != cache.dtype or v.dtype != cache.dtype:
+        raise ValueError(f"cache is {cache.dtype} but the rows are {k.dtype}")
+    if tuple(k.shape[1:]) != (cache.num_kv_heads, cache.head_dim):
+        raise ValueError(f"rows {tuple(k.shape)} do not match the cache's "
+                         f"({cache.num_kv_heads}, {cache.head_dim})")
+    real = slots[slots != _lib.SLOT_SKIP]
+    if real.size and int(real.max()) >= cache.num_slots():
+        raise ValueError(f"slot {int(real.max())} is past the end of the cache")
+    if n == 0:
+        return
+    dev_slots = torch.from_numpy(slots.view(np.int32)).to(k.device, non_blocking=False)
+    write_rows_indexed(cache, layer, k, v, dev_slots, stream=stream)
+
+
+def scatter_index(slot_mapping, device) -> torch.Tensor:
+    """The step's slot index on the device, built once and reused by every
+    layer (cache.rs:165-174; one u32 per token here, no broadcast needed)."""
+    return torch.from_numpy(_slots_host(slot_mapping).view(np.int32)).to(device)
+
+
+def write_rows_indexed(cache: PagedKvCache, layer: int, k: torch.Tensor, v: torch.Tensor,
+                       idx: torch.Tensor, stream=None) -> None:
+    """Append with a prebuilt device slot index (cache.rs:178-215): one
+    launch for K and V. Out-of-range slots are dropped on the device."""
+    if idx.dim() != 1 or idx.shape[0] != k.shape[0]:
+        raise ValueError(f"scatter index {tuple(idx.shape)} does not match rows "
+                         f"{tuple(k.shape)}")
+    if idx.dtype not in (torch.int32, torch.uint32):
+        raise TypeError("scatter index must be 32-bit")
+    k = k.contiguous()
+    v = v.contiguous()
+    check(lib().vapi_kv_append(cache.pool, layer, k.data_ptr(), v.data_ptr(),
+                               idx.data_ptr(), k.shape[0], stream_handle(stream)))
+
+
+def gather_kv(cache: PagedKvCache, layer: int, block_table, len_k: int,
+              which: str = "k", stream=None) -> torch.Tensor:
+    """One sequence's K (or V) rows in logical order, [len_k, kvh, d]
+    (cache.rs:283-290)."""
+    table = torch.from_numpy(_slots_host(block_table).view(np.int32)).to(cache.device)
+    if len_k > table.shape[0] * cache.block_size:
+        raise ValueError(f"len_k {len_k} exceeds {table.shape[0]} blocks")
+    out = torch.empty((len_k, cache.num_kv_heads, cache.head_dim), dtype=cache.dtype,
+                      device=cache.device)
+    if len_k == 0:
+        return out
+    kp = out.data_ptr() if which == "k" else None
+    vp = out.data_ptr() if which == "v" else None
+    check(lib().vapi_kv_gather(cache.pool, layer, table.data_ptr(), table.shape[0],
+                               len_k, kp, vp, stream_handle(stream)))
+    return out

@@ -1,0 +1,164 @@
+// Shared helpers for the gfx950 paged KV kernels: error reporting, pool
+// geometry, element types and 16-byte vector access.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/vapi_kv.h"
+
+namespace vk {
+
+// ---- error reporting ------------------------------------------------------
+
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define VK_FAIL(code, ...)        \
+  do {                            \
+    ::vk::set_error(__VA_ARGS__); \
+    return (code);                \
+  } while (0)
+
+#define VK_HIP(call)                                                      \
+  do {                                                                    \
+    hipError_t e_ = (call);                                               \
+    if (e_ != hipSuccess)                                                 \
+      VK_FAIL(VAPI_KV_EHIP, "%s failed: %s", #call, hipGetErrorString(e_)); \
+  } while (0)
+
+// Check the launch that was just enqueued.
+#define VK_LAUNCHED(name)                                                   \
+  do {                                                                      \
+    hipError_t e_ = hipGetLastError();                                      \
+    if (e_ != hipSuccess)                                                   \
+      VK_FAIL(VAPI_KV_EHIP, "launch of %s failed: %s", name,                \
+              hipGetErrorString(e_));                                       \
+  } while (0)
+
+inline size_t dtype_size(uint32_t dt) {
+  switch (dt) {
+    case VAPI_KV_F32: return 4;
+    case VAPI_KV_F16: return 2;
+    case VAPI_KV_BF16: return 2;
+    default: return 0;
+  }
+}
+
+// Validates a pool descriptor; returns 0 or an error code with a message.
+int check_pool(const vapi_kv_pool* p, const char* who);
+
+// ---- geometry -------------------------------------------------------------
+
+// Element strides of one layer buffer, for either layout.
+struct Geom {
+  uint32_t num_blocks, block_size, kvh, d;
+  uint64_t blk;   // elements per block
+  uint64_t head;  // stride between kv heads
+  uint64_t tok;   // stride between token offsets within a block
+};
+
+inline Geom make_geom(const vapi_kv_pool* p) {
+  Geom g;
+  g.num_blocks = p->num_blocks;
+  g.block_size = p->block_size;
+  g.kvh = p->num_kv_heads;
+  g.d = p->head_dim;
+  g.blk = (uint64_t)p->block_size * p->num_kv_heads * p->head_dim;
+  if (p->layout == VAPI_KV_LAYOUT_HND) {
+    g.head = (uint64_t)p->block_size * p->head_dim;
+    g.tok = p->head_dim;
+  } else {
+    g.head = p->head_dim;
+    g.tok = (uint64_t)p->num_kv_heads * p->head_dim;
+  }
+  return g;
+}
+
+// Largest power-of-two chunk (16, 8, 4, 2 or 1 bytes) dividing `bytes`.
+inline int chunk_bytes_for(uint64_t bytes) {
+  for (int c = 16; c > 1; c >>= 1)
+    if (bytes % c == 0) return c;
+  return 1;
+}
+
+// Unsigned division by a runtime constant via a precomputed multiplier
+// (round-up method, exact for n < 2^31 and 1 <= d < 2^31).
+struct FastDiv {
+  uint32_t d, mul, shift;
+  FastDiv() : d(1), mul(0), shift(0) {}
+  explicit FastDiv(uint32_t div) : d(div) {
+    shift = 0;
+    while ((1u << shift) < div) ++shift;
+    uint64_t m = ((1ull << 32) * ((1ull << shift) - div)) / div + 1;
+    mul = (uint32_t)m;
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    uint32_t t = __umulhi(n, mul);
+    return (t + n) >> shift;
+  }
+};
+
+// ---- element types ----------------------------------------------------------
+
+template <int N>
+struct Chunk;
+template <> struct Chunk<16> { using T = uint4; };
+template <> struct Chunk<8> { using T = uint2; };
+template <> struct Chunk<4> { using T = uint32_t; };
+template <> struct Chunk<2> { using T = uint16_t; };
+template <> struct Chunk<1> { using T = uint8_t; };
+
+// 16-bit float storage types as raw bits.
+struct bf16_t { uint16_t x; };
+struct f16_t { uint16_t x; };
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16_t v) {
+  return __uint_as_float(((uint32_t)v.x) << 16);
+}
+__device__ __forceinline__ float to_f32(f16_t v) {
+  return (float)__builtin_bit_cast(_Float16, v.x);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);  // RNE
+}
+
+// Round-to-nearest-even f32 -> bf16 (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float f);
+template <> __device__ __forceinline__ float from_f32<float>(float f) { return f; }
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float f) {
+  return bf16_t{f32_to_bf16_bits(f)};
+}
+template <> __device__ __forceinline__ f16_t from_f32<f16_t>(float f) {
+  return f16_t{__builtin_bit_cast(uint16_t, (_Float16)f)};
+}
+
+// Host-side unpack of the pool descriptor into a Geom plus layer base pointers.
+struct LayerPtrs {
+  char* k;
+  char* v;
+};
+inline LayerPtrs layer_ptrs(const vapi_kv_pool* p, uint32_t layer) {
+  LayerPtrs r;
+  r.k = (char*)p->k + (uint64_t)layer * p->layer_stride_bytes;
+  r.v = (char*)p->v + (uint64_t)layer * p->layer_stride_bytes;
+  return r;
+}
+
+inline hipStream_t hs(vapi_stream_t s) { return (hipStream_t)s; }
+
+}  // namespace vk

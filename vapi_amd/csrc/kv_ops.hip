@@ -1,0 +1,532 @@
+// Data-movement kernels of the paged KV pool: append (slot_mapping scatter),
+// block-table gather, copy-on-write block copy and spill export/import/swap.
+//
+// All of them are HBM-bound byte movers. Each thread moves ITEMS chunks of C
+// bytes (C = 16 whenever the row size allows it, so every lane issues
+// dwordx4 loads and stores); item indices are laid out so that consecutive
+// lanes touch consecutive bytes of the contiguous side (source rows for
+// append, destination blobs for export) and full head_dim rows of the paged
+// side. Loads for all ITEMS are issued before any store.
+#include <mutex>
+
+#include "common.hpp"
+
+namespace vk {
+
+static thread_local std::string g_err;
+
+void set_error(const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+}
+void clear_error() { g_err.clear(); }
+
+int check_pool(const vapi_kv_pool* p, const char* who) {
+  if (!p) VK_FAIL(VAPI_KV_EINVAL, "%s: null pool", who);
+  if (dtype_size(p->dtype) == 0)
+    VK_FAIL(VAPI_KV_EINVAL, "%s: unknown dtype %u", who, p->dtype);
+  if (p->layout != VAPI_KV_LAYOUT_HND && p->layout != VAPI_KV_LAYOUT_NHD)
+    VK_FAIL(VAPI_KV_EINVAL, "%s: unknown layout %u", who, p->layout);
+  if (p->num_layers == 0 || p->block_size == 0 || p->num_kv_heads == 0 ||
+      p->head_dim == 0)
+    VK_FAIL(VAPI_KV_EINVAL,
+            "%s: empty pool geometry (layers %u, block_size %u, kv_heads %u, "
+            "head_dim %u)",
+            who, p->num_layers, p->block_size, p->num_kv_heads, p->head_dim);
+  if ((uint64_t)p->num_blocks * p->block_size >= 0xFFFFFFFFull)
+    VK_FAIL(VAPI_KV_EINVAL, "%s: %u blocks of %u slots overflow u32 slots", who,
+            p->num_blocks, p->block_size);
+  uint64_t layer_bytes = (uint64_t)p->num_blocks * p->block_size *
+                         p->num_kv_heads * p->head_dim * dtype_size(p->dtype);
+  if (p->num_layers > 1 && p->layer_stride_bytes < layer_bytes)
+    VK_FAIL(VAPI_KV_EINVAL, "%s: layer stride %llu < layer size %llu", who,
+            (unsigned long long)p->layer_stride_bytes,
+            (unsigned long long)layer_bytes);
+  if (p->num_blocks > 0 && (!p->k || !p->v))
+    VK_FAIL(VAPI_KV_EINVAL, "%s: null K or V base pointer", who);
+  return 0;
+}
+
+// ---- append ---------------------------------------------------------------
+
+struct AppendArgs {
+  const char* k_src;
+  const char* v_src;
+  char* k_dst;
+  char* v_dst;
+  const uint32_t* slots;
+  uint32_t total;  // n_tokens * 2 * kvh * upr
+  uint32_t num_slots;
+  FastDiv upr, kvh, bs;
+  uint32_t row_bytes;  // head_dim * elt
+  uint64_t blk_b, head_b, tok_b;  // byte strides
+};
+
+template <int C, int ITEMS>
+__global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
+  using V = typename Chunk<C>::T;
+  const uint32_t base = blockIdx.x * (256u * ITEMS) + threadIdx.x;
+  V val[ITEMS];
+  char* dst[ITEMS];
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) {
+    const uint32_t i = base + j * 256u;
+    dst[j] = nullptr;
+    if (i < a.total) {
+      const uint32_t r = a.upr.div(i);
+      const uint32_t u = i - r * a.upr.d;
+      const uint32_t r2 = a.kvh.div(r);
+      const uint32_t h = r - r2 * a.kvh.d;
+      const uint32_t kv = r2 & 1u, t = r2 >> 1;
+      const uint32_t slot = a.slots[t];
+      if (slot < a.num_slots) {  // VAPI_KV_SLOT_SKIP and out-of-range drop
+        const uint32_t blk = a.bs.div(slot);
+        const uint32_t off = slot - blk * a.bs.d;
+        const uint64_t src_off =
+            ((uint64_t)t * a.kvh.d + h) * a.row_bytes + (uint64_t)u * C;
+        val[j] = *(const V*)((kv ? a.v_src : a.k_src) + src_off);
+        dst[j] = (kv ? a.v_dst : a.k_dst) + blk * a.blk_b + h * a.head_b +
+                 off * a.tok_b + (uint64_t)u * C;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j)
+    if (dst[j]) *(V*)dst[j] = val[j];
+}
+
+template <int C>
+static void launch_append(const AppendArgs& a, hipStream_t s) {
+  constexpr int ITEMS = 4;
+  uint32_t grid = (a.total + 256 * ITEMS - 1) / (256 * ITEMS);
+  hipLaunchKernelGGL((kv_append_kernel<C, ITEMS>), dim3(grid), dim3(256), 0, s,
+                     a);
+}
+
+// ---- gather -----------------------------------------------------------------
+
+struct GatherArgs {
+  const char* k_src;
+  const char* v_src;
+  char* k_out;
+  char* v_out;
+  const uint32_t* table;
+  uint32_t total;  // 2 * len_k * kvh * upr
+  uint32_t len_k;
+  FastDiv upr, kvh, bs, len;
+  uint32_t row_bytes;
+  uint64_t blk_b, head_b, tok_b;
+};
+
+template <int C, int ITEMS>
+__global__ __launch_bounds__(256) void kv_gather_kernel(GatherArgs a) {
+  using V = typename Chunk<C>::T;
+  const uint32_t base = blockIdx.x * (256u * ITEMS) + threadIdx.x;
+  V val[ITEMS];
+  char* dst[ITEMS];
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) {
+    const uint32_t i = base + j * 256u;
+    dst[j] = nullptr;
+    if (i < a.total) {
+      const uint32_t r = a.upr.div(i);
+      const uint32_t u = i - r * a.upr.d;
+      const uint32_t r2 = a.kvh.div(r);
+      const uint32_t h = r - r2 * a.kvh.d;
+      const uint32_t kv = a.len.div(r2);
+      const uint32_t t = r2 - kv * a.len.d;
+      char* out = kv ? a.v_out : a.k_out;
+      if (out) {
+        const uint32_t bi = a.bs.div(t);
+        const uint32_t off = t - bi * a.bs.d;
+        const uint32_t blk = a.table[bi];
+        const char* src = (kv ? a.v_src : a.k_src) + blk * a.blk_b +
+                          h * a.head_b + off * a.tok_b + (uint64_t)u * C;
+        val[j] = *(const V*)src;
+        dst[j] = out + ((uint64_t)t * a.kvh.d + h) * a.row_bytes +
+                 (uint64_t)u * C;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j)
+    if (dst[j]) *(V*)dst[j] = val[j];
+}
+
+// ---- block copy ---------------------------------------------------------------
+
+struct CopyArgs {
+  char* k;
+  char* v;
+  const uint32_t* pairs;
+  uint64_t layer_b, blk_b;
+  uint32_t total;  // n_pairs * L * 2 * upb
+  FastDiv upb, two_l;
+  uint32_t num_layers;
+};
+
+template <int C, int ITEMS>
+__global__ __launch_bounds__(256) void kv_copy_kernel(CopyArgs a) {
+  using V = typename Chunk<C>::T;
+  const uint32_t base = blockIdx.x * (256u * ITEMS) + threadIdx.x;
+  V val[ITEMS];
+  char* dst[ITEMS];
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) {
+    const uint32_t i = base + j * 256u;
+    dst[j] = nullptr;
+    if (i < a.total) {
+      const uint32_t r = a.upb.div(i);
+      const uint32_t u = i - r * a.upb.d;
+      const uint32_t p = a.two_l.div(r);
+      const uint32_t s = r - p * a.two_l.d;  // 0..2L-1: K layers then V layers
+      const uint32_t kv = s >= a.num_layers;
+      const uint32_t layer = kv ? s - a.num_layers : s;
+      const uint32_t src_blk = a.pairs[2 * p], dst_blk = a.pairs[2 * p + 1];
+      char* buf = (kv ? a.v : a.k) + layer * a.layer_b;
+      const uint64_t o = (uint64_t)u * C;
+      val[j] = *(const V*)(buf + src_blk * a.blk_b + o);
+      dst[j] = buf + dst_blk * a.blk_b + o;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j)
+    if (dst[j]) *(V*)dst[j] = val[j];
+}
+
+// ---- export / import (reference blob order) ----------------------------------
+
+// Blob of block i: segments s = 0..2L-1 (K layers then V layers), each NHD
+// [bs, kvh, d]. Item index = (((i*2L + s)*bs + t)*kvh + h)*upr + u, so the
+// blob side is walked contiguously.
+struct BlobArgs {
+  char* k;
+  char* v;
+  char* blob;
+  const uint32_t* ids;
+  uint64_t layer_b, blk_b, head_b, tok_b;
+  uint64_t block_bytes;
+  uint32_t total;
+  FastDiv upr, kvh, bs, two_l;
+  uint32_t num_layers, row_bytes, seg_bytes;
+};
+
+template <int C, int ITEMS, bool EXPORT>
+__global__ __launch_bounds__(256) void kv_blob_kernel(BlobArgs a) {
+  using V = typename Chunk<C>::T;
+  const uint32_t base = blockIdx.x * (256u * ITEMS) + threadIdx.x;
+  V val[ITEMS];
+  char* dst[ITEMS];
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) {
+    const uint32_t i = base + j * 256u;
+    dst[j] = nullptr;
+    if (i < a.total) {
+      const uint32_t r = a.upr.div(i);
+      const uint32_t u = i - r * a.upr.d;
+      const uint32_t r2 = a.kvh.div(r);
+      const uint32_t h = r - r2 * a.kvh.d;
+      const uint32_t r3 = a.bs.div(r2);
+      const uint32_t t = r2 - r3 * a.bs.d;
+      const uint32_t bi = a.two_l.div(r3);
+      const uint32_t s = r3 - bi * a.two_l.d;
+      const uint32_t kv = s >= a.num_layers;
+      const uint32_t layer = kv ? s - a.num_layers : s;
+      const uint32_t blk = a.ids[bi];
+      char* pool = (kv ? a.v : a.k) + layer * a.layer_b + blk * a.blk_b +
+                   h * a.head_b + t * a.tok_b + (uint64_t)u * C;
+      char* blob = a.blob + bi * a.block_bytes + (uint64_t)s * a.seg_bytes +
+                   ((uint64_t)t * a.kvh.d + h) * a.row_bytes + (uint64_t)u * C;
+      if (EXPORT) {
+        val[j] = *(const V*)pool;
+        dst[j] = blob;
+      } else {
+        val[j] = *(const V*)blob;
+        dst[j] = pool;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j)
+    if (dst[j]) *(V*)dst[j] = val[j];
+}
+
+// Dispatch a kernel template over the chunk size chosen at runtime.
+#define VK_DISPATCH_CHUNK(c, LAUNCH) \
+  switch (c) {                       \
+    case 16: LAUNCH(16); break;      \
+    case 8: LAUNCH(8); break;        \
+    case 4: LAUNCH(4); break;        \
+    case 2: LAUNCH(2); break;        \
+    default: LAUNCH(1); break;       \
+  }
+
+}  // namespace vk
+
+using namespace vk;
+
+extern "C" {
+
+const char* vapi_kv_last_error(void) { return g_err.c_str(); }
+
+const char* vapi_kv_version(void) { return "vapi_kv 0.1.0 gfx950"; }
+
+size_t vapi_kv_block_bytes(const vapi_kv_pool* p) {
+  if (!p) return 0;
+  return (size_t)p->num_layers * 2 * p->block_size * p->num_kv_heads *
+         p->head_dim * dtype_size(p->dtype);
+}
+
+size_t vapi_kv_layer_bytes(const vapi_kv_pool* p) {
+  if (!p) return 0;
+  return (size_t)p->num_blocks * p->block_size * p->num_kv_heads *
+         p->head_dim * dtype_size(p->dtype);
+}
+
+int vapi_kv_append(const vapi_kv_pool* pool, uint32_t layer, const void* k_src,
+                   const void* v_src, const uint32_t* slot_mapping,
+                   uint32_t n_tokens, vapi_stream_t stream) {
+  if (int rc = check_pool(pool, "vapi_kv_append")) return rc;
+  if (layer >= pool->num_layers)
+    VK_FAIL(VAPI_KV_EINVAL, "vapi_kv_append: layer %u of %u", layer,
+            pool->num_layers);
+  if (n_tokens == 0) return 0;
+  if (!k_src || !v_src || !slot_mapping)
+    VK_FAIL(VAPI_KV_EINVAL, "vapi_kv_append: null source or slot_mapping");
+  const Geom g = make_geom(pool);
+  const uint32_t elt = dtype_size(pool->dtype);
+  const uint32_t row_bytes = g.d * elt;
+  const int c = chunk_bytes_for(row_bytes);
+  const uint64_t total = (uint64_t)n_tokens * 2 * g.kvh * (row_bytes / c);
+  if (total >= (1ull << 31))
+    VK_FAIL(VAPI_KV_EUNSUP, "vapi_kv_append: %u tokens is too many for one call",
+            n_tokens);
+  LayerPtrs lp = layer_ptrs(pool, layer);
+  AppendArgs a;
+  a.k_src = (const char*)k_src;
+  a.v_src = (const char*)v_src;
+  a.k_dst = lp.k;
+  a.v_dst = lp.v;
+  a.slots = slot_mapping;
+  a.total = (uint32_t)total;
+  a.num_slots = g.num_blocks * g.block_size;
+  a.upr = FastDiv(row_bytes / c);
+  a.kvh = FastDiv(g.kvh);
+  a.bs = FastDiv(g.block_size);
+  a.row_bytes = row_bytes;
+  a.blk_b = g.blk * elt;
+  a.head_b = g.head * elt;
+  a.tok_b = g.tok * elt;
+#define L_APPEND(C) launch_append<C>(a, hs(stream))
+  VK_DISPATCH_CHUNK(c, L_APPEND)
+#undef L_APPEND
+  VK_LAUNCHED("kv_append");
+  return 0;
+}
+
+int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
+                   const uint32_t* block_table, uint32_t n_table,
+                   uint32_t len_k, void* k_out, void* v_out,
+                   vapi_stream_t stream) {
+  if (int rc = check_pool(pool, "vapi_kv_gather")) return rc;
+  if (layer >= pool->num_layers)
+    VK_FAIL(VAPI_KV_EINVAL, "vapi_kv_gather: layer %u of %u", layer,
+            pool->num_layers);
+  if ((uint64_t)len_k > (uint64_t)n_table * pool->block_size)
+    VK_FAIL(VAPI_KV_EINVAL,
+            "vapi_kv_gather: len_k %u exceeds %u blocks of %u slots", len_k,
+            n_table, pool->block_size);
+  if (len_k == 0 || (!k_out && !v_out)) return 0;
+  if (!block_table)
+    VK_FAIL(VAPI_KV_EINVAL, "vapi_kv_gather: null block_table");
+  const Geom g = make_geom(pool);
+  const uint32_t elt = dtype_size(pool->dtype);
+  const uint32_t row_bytes = g.d * elt;
+  const int c = chunk_bytes_for(row_bytes);
+  const uint64_t total = (uint64_t)2 * len_k * g.kvh * (row_bytes / c);
+  if (total >= (1ull << 31))
+    VK_FAIL(VAPI_KV_EUNSUP, "vapi_kv_gather: len_k %u too large", len_k);
+  LayerPtrs lp = layer_ptrs(pool, layer);
+  GatherArgs a;
+  a.k_src = lp.k;
+  a.v_src = lp.v;
+  a.k_out = (char*)k_out;
+  a.v_out = (char*)v_out;
+  a.table = block_table;
+  a.total = (uint32_t)total;
+  a.len_k = len_k;
+  a.upr = FastDiv(row_bytes / c);
+  a.kvh = FastDiv(g.kvh);
+  a.bs = FastDiv(g.block_size);
+  a.len = FastDiv(len_k);
+  a.row_bytes = row_bytes;
+  a.blk_b = g.blk * elt;
+  a.head_b = g.head * elt;
+  a.tok_b = g.tok * elt;
+  constexpr int ITEMS = 4;
+  const uint32_t grid = (a.total + 256 * ITEMS - 1) / (256 * ITEMS);
+#define L_GATHER(C)                                                        \
+  hipLaunchKernelGGL((kv_gather_kernel<C, ITEMS>), dim3(grid), dim3(256), 0, \
+                     hs(stream), a)
+  VK_DISPATCH_CHUNK(c, L_GATHER)
+#undef L_GATHER
+  VK_LAUNCHED("kv_gather");
+  return 0;
+}
+
+int vapi_kv_copy_blocks(const vapi_kv_pool* pool, const uint32_t* pairs,
+                        uint32_t n_pairs, vapi_stream_t stream) {
+  if (int rc = check_pool(pool, "vapi_kv_copy_blocks")) return rc;
+  if (n_pairs == 0) return 0;
+  if (!pairs) VK_FAIL(VAPI_KV_EINVAL, "vapi_kv_copy_blocks: null pairs");
+  const Geom g = make_geom(pool);
+  const uint32_t elt = dtype_size(pool->dtype);
+  const uint64_t blk_b = g.blk * elt;
+  const int c = chunk_bytes_for(blk_b);
+  const uint64_t upb = blk_b / c;
+  const uint64_t per_pair = (uint64_t)pool->num_layers * 2 * upb;
+  if (per_pair >= (1ull << 31))
+    VK_FAIL(VAPI_KV_EUNSUP, "vapi_kv_copy_blocks: block too large");
+  const uint32_t pairs_per_launch =
+      (uint32_t)std::min<uint64_t>(n_pairs, ((1ull << 31) - 1) / per_pair);
+  CopyArgs a;
+  a.k = (char*)pool->k;
+  a.v = (char*)pool->v;
+  a.layer_b = pool->layer_stride_bytes;
+  a.blk_b = blk_b;
+  a.upb = FastDiv((uint32_t)upb);
+  a.two_l = FastDiv(2 * pool->num_layers);
+  a.num_layers = pool->num_layers;
+  constexpr int ITEMS = 4;
+  for (uint32_t p0 = 0; p0 < n_pairs; p0 += pairs_per_launch) {
+    const uint32_t np = std::min(pairs_per_launch, n_pairs - p0);
+    a.pairs = pairs + 2ull * p0;
+    a.total = (uint32_t)(np * per_pair);
+    const uint32_t grid = (a.total + 256 * ITEMS - 1) / (256 * ITEMS);
+#define L_COPY(C)                                                        \
+  hipLaunchKernelGGL((kv_copy_kernel<C, ITEMS>), dim3(grid), dim3(256), 0, \
+                     hs(stream), a)
+    VK_DISPATCH_CHUNK(c, L_COPY)
+#undef L_COPY
+    VK_LAUNCHED("kv_copy_blocks");
+  }
+  return 0;
+}
+
+static int blob_move(const vapi_kv_pool* pool, const uint32_t* ids, uint32_t n,
+                     char* blob, bool do_export, hipStream_t stream,
+                     const char* who) {
+  if (int rc = check_pool(pool, who)) return rc;
+  if (n == 0) return 0;
+  if (!ids || !blob) VK_FAIL(VAPI_KV_EINVAL, "%s: null ids or buffer", who);
+  const Geom g = make_geom(pool);
+  const uint32_t elt = dtype_size(pool->dtype);
+  const uint32_t row_bytes = g.d * elt;
+  const int c = chunk_bytes_for(row_bytes);
+  const uint64_t per_block = (uint64_t)2 * pool->num_layers * g.block_size *
+                             g.kvh * (row_bytes / c);
+  if (per_block >= (1ull << 31))
+    VK_FAIL(VAPI_KV_EUNSUP, "%s: block too large", who);
+  const uint32_t blocks_per_launch =
+      (uint32_t)std::min<uint64_t>(n, ((1ull << 31) - 1) / per_block);
+  BlobArgs a;
+  a.k = (char*)pool->k;
+  a.v = (char*)pool->v;
+  a.layer_b = pool->layer_stride_bytes;
+  a.blk_b = g.blk * elt;
+  a.head_b = g.head * elt;
+  a.tok_b = g.tok * elt;
+  a.block_bytes = vapi_kv_block_bytes(pool);
+  a.upr = FastDiv(row_bytes / c);
+  a.kvh = FastDiv(g.kvh);
+  a.bs = FastDiv(g.block_size);
+  a.two_l = FastDiv(2 * pool->num_layers);
+  a.num_layers = pool->num_layers;
+  a.row_bytes = row_bytes;
+  a.seg_bytes = (uint32_t)(g.blk * elt);
+  constexpr int ITEMS = 4;
+  for (uint32_t b0 = 0; b0 < n; b0 += blocks_per_launch) {
+    const uint32_t nb = std::min(blocks_per_launch, n - b0);
+    a.ids = ids + b0;
+    a.blob = blob + (uint64_t)b0 * a.block_bytes;
+    a.total = (uint32_t)(nb * per_block);
+    const uint32_t grid = (a.total + 256 * ITEMS - 1) / (256 * ITEMS);
+    if (do_export) {
+#define L_EXP(C)                                                               \
+  hipLaunchKernelGGL((kv_blob_kernel<C, ITEMS, true>), dim3(grid), dim3(256), \
+                     0, stream, a)
+      VK_DISPATCH_CHUNK(c, L_EXP)
+#undef L_EXP
+    } else {
+#define L_IMP(C)                                                                \
+  hipLaunchKernelGGL((kv_blob_kernel<C, ITEMS, false>), dim3(grid), dim3(256), \
+                     0, stream, a)
+      VK_DISPATCH_CHUNK(c, L_IMP)
+#undef L_IMP
+    }
+    VK_LAUNCHED(who);
+  }
+  return 0;
+}
+
+int vapi_kv_export_blocks(const vapi_kv_pool* pool, const uint32_t* ids,
+                          uint32_t n, void* dst, vapi_stream_t stream) {
+  return blob_move(pool, ids, n, (char*)dst, true, hs(stream),
+                   "vapi_kv_export_blocks");
+}
+
+int vapi_kv_import_blocks(const vapi_kv_pool* pool, const uint32_t* ids,
+                          uint32_t n, const void* src, vapi_stream_t stream) {
+  return blob_move(pool, ids, n, (char*)src, false, hs(stream),
+                   "vapi_kv_import_blocks");
+}
+
+int vapi_kv_swap_out(const vapi_kv_pool* pool, const uint32_t* ids, uint32_t n,
+                     void* host_dst, void* staging, size_t staging_bytes,
+                     vapi_stream_t stream) {
+  if (int rc = check_pool(pool, "vapi_kv_swap_out")) return rc;
+  const size_t bb = vapi_kv_block_bytes(pool);
+  if (n == 0) return 0;
+  if (!host_dst || !staging)
+    VK_FAIL(VAPI_KV_EINVAL, "vapi_kv_swap_out: null host or staging buffer");
+  const size_t per = staging_bytes / bb;
+  if (per == 0)
+    VK_FAIL(VAPI_KV_ESPACE, "vapi_kv_swap_out: staging %zu bytes < one block (%zu)",
+            staging_bytes, bb);
+  for (uint32_t b0 = 0; b0 < n; b0 += (uint32_t)per) {
+    const uint32_t nb = (uint32_t)std::min<size_t>(per, n - b0);
+    if (int rc = vapi_kv_export_blocks(pool, ids + b0, nb, staging, stream))
+      return rc;
+    VK_HIP(hipMemcpyAsync((char*)host_dst + (size_t)b0 * bb, staging,
+                          (size_t)nb * bb, hipMemcpyDeviceToHost, hs(stream)));
+  }
+  return 0;
+}
+
+int vapi_kv_swap_in(const vapi_kv_pool* pool, const uint32_t* ids, uint32_t n,
+                    const void* host_src, void* staging, size_t staging_bytes,
+                    vapi_stream_t stream) {
+  if (int rc = check_pool(pool, "vapi_kv_swap_in")) return rc;
+  const size_t bb = vapi_kv_block_bytes(pool);
+  if (n == 0) return 0;
+  if (!host_src || !staging)
+    VK_FAIL(VAPI_KV_EINVAL, "vapi_kv_swap_in: null host or staging buffer");
+  const size_t per = staging_bytes / bb;
+  if (per == 0)
+    VK_FAIL(VAPI_KV_ESPACE, "vapi_kv_swap_in: staging %zu bytes < one block (%zu)",
+            staging_bytes, bb);
+  for (uint32_t b0 = 0; b0 < n; b0 += (uint32_t)per) {
+    const uint32_t nb = (uint32_t)std::min<size_t>(per, n - b0);
+    VK_HIP(hipMemcpyAsync(staging, (const char*)host_src + (size_t)b0 * bb,
+                          (size_t)nb * bb, hipMemcpyHostToDevice, hs(stream)));
+    if (int rc = vapi_kv_import_blocks(pool, ids + b0, nb, staging, stream))
+      return rc;
+  }
+  return 0;
+}
+
+}  // extern "C"
