@@ -1,0 +1,352 @@
+"""Benchmark of the paged KV hot path on one MI355X.
+
+Headline (the JSON line's value): paged decode attention at Llama-3-8B GQA
+shape, batch 64, log-normal contexts up to 8k, as
+algorithmic HBM GB/s. A step is one vapi_paged_attention call over that
+batch (the split-K decode kernel plus its partial-merge kernel), with every
+input already resident in HBM.
+
+Also measured in the same run (under "extras"): KV append GB/s (config 1),
+chunked-prefill TFLOP/s (config 3), copy-on-write GB/s (config 4a), swap
+GB/s per direction overlapped with a decode launch (config 4b), and the
+device-copy / pinned-copy probes. The CPU baseline is the C oracle
+(a restatement of vapi's candle CPU path) timed on this box's host cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from vapi_amd import workload  # noqa: E402
+from vapi_amd.attention import ForwardBatch, PreparedAttention, paged_attention_prepared  # noqa: E402
+from vapi_amd.backend import KvBlockBackend  # noqa: E402
+from vapi_amd.cache import PagedKvCache, write_rows_indexed, scatter_index  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+DEV = "cuda"
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def timed(fn, steps, warmup):
+    """Run fn warmup times, then time `steps` runs with one pair of events per
+    run on the current stream. Returns (mean ms per run, total ms)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3
+    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return float(np.mean(per)), wall, per
+
+
+# ---- config 2: decode (headline) ---------------------------------------------
+
+def setup_decode():
+    w = workload.config2_decode()
+    cache = PagedKvCache(1, w.num_blocks, w.block_size, w.num_kv_heads, w.head_dim,
+                         torch.bfloat16, "HND")
+    workload.fill_normal(cache._slab, workload.seed_for(2))
+    g = torch.Generator(device=DEV).manual_seed(workload.seed_for(2) + 1)
+    q = torch.randn(w.batch, w.num_heads, w.head_dim, generator=g, device=DEV).to(torch.bfloat16)
+    batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
+                         block_tables=[t.tolist() for t in w.tables], max_seqlen_q=1,
+                         max_seqlen_k=int(w.lens.max()))
+    prep = PreparedAttention.from_batch(batch, DEV)
+    out = torch.empty_like(q)
+    scale = w.head_dim ** -0.5
+    sum_len = int(w.lens.sum())
+    n_blocks = sum(len(t) for t in w.tables)
+    kv_bytes = sum_len * 2 * w.num_kv_heads * w.head_dim * 2
+    alg_bytes = (kv_bytes + 2 * w.batch * w.num_heads * w.head_dim * 2 + n_blocks * 4
+                 + 2 * (w.batch + 1) * 4)
+
+    def step():
+        paged_attention_prepared(q, cache, 0, prep, scale, out=out)
+
+    return dict(w=w, cache=cache, q=q, batch=batch, prep=prep, step=step, scale=scale,
+                sum_len=sum_len, alg_bytes=alg_bytes, flops=4.0 * w.num_heads * w.head_dim * sum_len)
+
+
+def bench_decode(steps, warmup):
+    d = setup_decode()
+    ms, wall, _ = timed(d["step"], steps, warmup)
+    gbs = d["alg_bytes"] / (ms * 1e-3) / 1e9
+    log(f"decode cfg2: sum_len {d['sum_len']}, {d['alg_bytes'] / 1e6:.1f} MB/step, "
+        f"{ms * 1e3:.1f} us/step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+    d.update(ms=ms, wall=wall, gbs=gbs)
+    return d
+
+
+# ---- config 1: append --------------------------------------------------------------
+
+def bench_append(steps, warmup):
+    w = workload.config1_append()
+    cache = PagedKvCache(1, w.num_blocks, w.block_size, w.num_kv_heads, w.head_dim,
+                         torch.bfloat16, "HND")
+    g = torch.Generator(device=DEV).manual_seed(workload.seed_for(1))
+    k = torch.randn(w.n_tokens, 8, 128, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(w.n_tokens, 8, 128, generator=g, device=DEV).to(torch.bfloat16)
+    idx = scatter_index(w.slots, DEV)
+    ms, _, _ = timed(lambda: write_rows_indexed(cache, 0, k, v, idx), steps, warmup)
+    alg = w.n_valid * 2 * 8 * 128 * 2 * 2 + w.n_tokens * 4
+    gbs = alg / (ms * 1e-3) / 1e9
+    log(f"append cfg1: {alg / 1e6:.1f} MB, {ms * 1e3:.1f} us, {gbs:.0f} GB/s")
+    del cache
+    return dict(us=ms * 1e3, gbs=gbs, frac=gbs / HBM_PEAK_GBS, bytes=alg)
+
+
+# ---- config 3: chunked prefill ----------------------------------------------------
+
+def bench_prefill(steps, warmup):
+    w = workload.config3_prefill()
+    cache = PagedKvCache(1, w.num_blocks, w.block_size, 8, 128, torch.bfloat16, "HND")
+    workload.fill_normal(cache._slab, workload.seed_for(3))
+    g = torch.Generator(device=DEV).manual_seed(workload.seed_for(3) + 1)
+    q = torch.randn(w.batch * w.len_q, 32, 128, generator=g, device=DEV).to(torch.bfloat16)
+    batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
+                         block_tables=[t.tolist() for t in w.tables], max_seqlen_q=w.len_q,
+                         max_seqlen_k=w.len_k)
+    prep = PreparedAttention.from_batch(batch, DEV)
+    out = torch.empty_like(q)
+    ms, _, _ = timed(lambda: paged_attention_prepared(q, cache, 0, prep, 128 ** -0.5, out=out),
+                     steps, warmup)
+    tf = w.flops() / (ms * 1e-3) / 1e12
+    log(f"prefill cfg3: {w.flops() / 1e12:.3f} TFLOP, {ms:.2f} ms, {tf:.1f} TFLOP/s "
+        f"({tf / BF16_MFMA_PEAK_TFLOPS:.1%} of 2.5 PF)")
+    del cache
+    return dict(ms=ms, tflops=tf, frac=tf / BF16_MFMA_PEAK_TFLOPS, flops=w.flops())
+
+
+# ---- config 4: copy-on-write and swap ---------------------------------------------
+
+def bench_blocks(steps, warmup, decode):
+    w = workload.config4_block_ops()
+    cache = PagedKvCache(w.num_layers, w.num_blocks, w.block_size, w.num_kv_heads,
+                         w.head_dim, torch.bfloat16, "HND")
+    workload.fill_normal(cache._slab, workload.seed_for(4))
+    be = KvBlockBackend(cache)
+    bb = be.block_bytes()
+    pairs_dev = torch.from_numpy(w.pairs.astype(np.int32).reshape(-1)).to(DEV)
+    from vapi_amd._lib import check, lib
+    from vapi_amd.cache import stream_handle
+
+    def copy():
+        check(lib().vapi_kv_copy_blocks(cache.pool, pairs_dev.data_ptr(), w.pairs.shape[0],
+                                        stream_handle()))
+
+    ms, _, _ = timed(copy, steps, warmup)
+    alg = w.pairs.shape[0] * bb * 2
+    copy_gbs = alg / (ms * 1e-3) / 1e9
+    log(f"copy cfg4a: {alg / 1e9:.2f} GB moved, {ms:.3f} ms, {copy_gbs:.0f} GB/s")
+    # Bit-exactness at full size: every pair's destination equals its source.
+    src = torch.from_numpy(w.pairs[:, 0].astype(np.int64)).to(DEV)
+    dst = torch.from_numpy(w.pairs[:, 1].astype(np.int64)).to(DEV)
+    copy_ok = all(torch.equal(t[src], t[dst]) for t in cache.k + cache.v)
+
+    # Swap: 4,096 blocks out to pinned host and back into other blocks.
+    n = len(w.swap_ids)
+    host = torch.empty(n * bb, dtype=torch.uint8, pin_memory=True)
+    staging = torch.empty(256 * bb, dtype=torch.uint8, device=DEV)
+    ids_out = torch.from_numpy(w.swap_ids.astype(np.int32)).to(DEV)
+    ids_in = torch.from_numpy(w.swap_in_ids.astype(np.int32)).to(DEV)
+    side = torch.cuda.Stream()
+
+    def on_side(fn):
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record(side)
+        fn()
+        ev1.record(side)
+        side.synchronize()
+        return ev0.elapsed_time(ev1)
+
+    torch.cuda.synchronize()
+    out_ms = on_side(lambda: be.swap_out(ids_out, host, staging, stream=side))
+    in_ms = on_side(lambda: be.swap_in(ids_in, host, staging, stream=side))
+    swap_ok = True
+    for a, b in ((0, 0), (n // 2, n // 2), (n - 1, n - 1)):
+        swap_ok &= be.export_block(int(w.swap_ids[a])) == be.export_block(int(w.swap_in_ids[b]))
+    # Overlap: swap-out on the side stream while decode steps run on the main stream.
+    dec_alone, _, _ = timed(decode["step"], 10, 2)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(side)
+    be.swap_out(ids_out, host, staging, stream=side)
+    ev1.record(side)
+    dec_ms = []
+    while not ev1.query():
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        decode["step"]()
+        e1.record()
+        e1.synchronize()
+        dec_ms.append(e0.elapsed_time(e1))
+        if len(dec_ms) > 5000:
+            break
+    side.synchronize()
+    overlap_out_ms = ev0.elapsed_time(ev1)
+    # Pinned-copy probe (host-link peak).
+    probe = torch.empty(1 << 30, dtype=torch.uint8, device=DEV)
+    ph = torch.empty(1 << 30, dtype=torch.uint8, pin_memory=True)
+    torch.cuda.synchronize()
+    d2h = on_side(lambda: _copy_on(side, ph, probe))
+    h2d = on_side(lambda: _copy_on(side, probe, ph))
+    link = dict(d2h_gbs=(1 << 30) / (d2h * 1e-3) / 1e9, h2d_gbs=(1 << 30) / (h2d * 1e-3) / 1e9)
+    gb = n * bb / 1e9
+    res = dict(copy_ms=ms, copy_gbs=copy_gbs, copy_frac=copy_gbs / HBM_PEAK_GBS,
+               copy_bit_exact=bool(copy_ok),
+               swap_out_gbs=gb / (out_ms * 1e-3), swap_in_gbs=gb / (in_ms * 1e-3),
+               swap_round_trip_bit_exact=bool(swap_ok),
+               swap_out_overlapped_gbs=gb / (overlap_out_ms * 1e-3),
+               decode_us_alone=dec_alone * 1e3,
+               decode_us_during_swap=float(np.median(dec_ms)) * 1e3 if dec_ms else None,
+               pinned_probe=link, swap_bytes_per_direction=n * bb)
+    log(f"swap cfg4b: out {res['swap_out_gbs']:.1f} GB/s, in {res['swap_in_gbs']:.1f} GB/s, "
+        f"pinned probe d2h {link['d2h_gbs']:.1f} h2d {link['h2d_gbs']:.1f}; decode "
+        f"{res['decode_us_alone']:.0f} us alone, {res['decode_us_during_swap']} us during swap")
+    del cache, host, ph, probe
+    return res
+
+
+def _copy_on(stream, dst, src):
+    with torch.cuda.stream(stream):
+        dst.copy_(src, non_blocking=True)
+
+
+def hbm_probe():
+    a = torch.empty(4 << 30, dtype=torch.uint8, device=DEV)
+    b = torch.empty_like(a)
+    ms, _, _ = timed(lambda: b.copy_(a), 10, 3)
+    return 2 * a.numel() / (ms * 1e-3) / 1e9
+
+
+# ---- CPU baseline ------------------------------------------------------------------
+
+def cpu_baseline(decode, budget_s=12.0):
+    """The C oracle (candle CPU path restated) on the same config-2 batch,
+    repeated until ~budget_s of CPU time; OpenMP over sequences."""
+    import oracle  # checker/baseline only
+    w = decode["w"]
+    cache = decode["cache"]
+    # Host copy of just the blocks the batch uses, renumbered densely.
+    used = np.concatenate(w.tables).astype(np.int64)
+    remap = {int(b): i for i, b in enumerate(used)}
+    idx = torch.from_numpy(used).to(DEV)
+    kc = cache.reference_view(0, "k")[idx].float().cpu().numpy()
+    vc = cache.reference_view(0, "v")[idx].float().cpu().numpy()
+    tables = [[remap[int(b)] for b in t] for t in w.tables]
+    q = decode["q"].float().cpu().numpy()
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    cu_q, cu_k = w.cu_q(), w.cu_k()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.paged_attention(q, kc, vc, cu_q, cu_k, tables, decode["scale"], threads=threads)
+        reps += 1
+        if time.perf_counter() - t0 > budget_s or reps >= 50:
+            break
+    sec = (time.perf_counter() - t0) / reps
+    gbs = decode["alg_bytes"] / sec / 1e9
+    log(f"cpu baseline: {sec * 1e3:.1f} ms per config-2 step on {threads} threads, {gbs:.2f} GB/s")
+    return dict(value=gbs, unit="GB/s", cores=threads, kind="port",
+                sample=f"full config-2 decode batch (64 seqs, sum_len {w.lens.sum()}), "
+                       f"{reps} passes, C oracle with OpenMP over sequences, f32 math on "
+                       f"bf16-valued K/V", ms_per_step=sec * 1e3)
+
+
+def load_traffic():
+    p = ROOT / "profiles" / "decode_cfg2_traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text())
+        except Exception:
+            return None
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--only", choices=["decode", "append", "prefill", "blocks"], default=None)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build's paged-KV path runs on a single "
+              "MI355X (see DESIGN.md for how it would shard); run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    torch.cuda.init()
+    if args.only == "append":
+        bench_append(args.steps, args.warmup)
+        return
+    if args.only == "prefill":
+        bench_prefill(args.steps, args.warmup)
+        return
+    dec = bench_decode(args.steps, args.warmup)
+    if args.only == "decode":
+        return
+    extras = {}
+    if args.only in (None,):
+        extras["append_cfg1"] = bench_append(args.steps, args.warmup)
+        extras["prefill_cfg3"] = bench_prefill(max(args.steps // 5, 3), 2)
+    extras["blocks_cfg4"] = bench_blocks(max(args.steps // 5, 3), 2, dec)
+    if args.only == "blocks":
+        return
+    extras["hbm_copy_probe_gbs"] = hbm_probe()
+    traffic = load_traffic()
+    cpu = None if args.no_cpu else cpu_baseline(dec)
+    alg = dec["alg_bytes"]
+    line = {
+        "metric": "decode paged-attn HBM GB/s & % of peak (B=64, 8B GQA); KV append GB/s",
+        "value": round(dec["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) K/V/Q, seeded log-normal context lengths)",
+        "config": {"workload": "paged decode attention, BASELINE config 2: 32 q / 8 kv heads, "
+                               "head_dim 128, block_size 16, batch 64, log-normal contexts "
+                               "median 2k in [256, 8192], 32k-block pool",
+                   "sum_context_tokens": dec["sum_len"], "global_batch": 64,
+                   "algorithmic_bytes_per_step": alg, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": traffic.get("bytes_per_launch") if traffic else None,
+                     "kernel": "paged_decode_mfma + paged_decode_reduce (one call)"},
+        "cpu_baseline": cpu,
+        "kv_append_gbs": round(extras["append_cfg1"]["gbs"], 1) if "append_cfg1" in extras else None,
+        "extras": extras,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
