@@ -137,7 +137,9 @@ def paged_attention_prepared(q: torch.Tensor, cache: PagedKvCache, layer: int,
     need = workspace_bytes(cache, b, num_heads, max_q, max_k)
     ws = prepared.workspace
     if need and (ws is None or ws.numel() < need):
-        ws = torch.empty(need, dtype=torch.uint8, device=q.device)
+        # Zero-filled once: the split-K arrival counters must start at 0 (the
+        # kernels leave them at 0 when they finish).
+        ws = torch.zeros(need, dtype=torch.uint8, device=q.device)
         prepared.workspace = ws
     check(lib().vapi_paged_attention(
         cache.pool, layer, q.data_ptr(), out.data_ptr(), prepared.seqlens_q.data_ptr(),

@@ -34,7 +34,8 @@ COMMON_FLAGS = [
     f"-I{ROOT / 'include'}",
 ]
 
-SOURCES = ["kv_ops.hip", "attention.hip", "host.cpp"]
+SOURCES = ["kv_ops.hip", "attention.hip", "attn_decode.hip", "attn_prefill.hip",
+           "attn_generic.hip", "host.cpp"]
 
 
 def _compile(src: Path, obj: Path) -> None:

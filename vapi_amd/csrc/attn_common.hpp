@@ -1,0 +1,268 @@
+// Shared pieces of the gfx950 paged-attention kernels: argument block, MFMA
+// operand helpers and the 32-key online-softmax step used by both the decode
+// and the prefill kernels.
+//
+// Numerical contract: paged_attention_cpu (vapi
+// crates/vapi-backend-candle/src/attention.rs:90-163): f32 scores
+// q.k*scale, bottom-right-aligned causal mask (query j of a sequence sits at
+// p = len_k - len_q + j), optional left window, softmax, times V, output cast
+// to the input dtype. Masking follows the flash convention the reference's
+// CUDA path passes (attention.rs:179-194): key k is visible iff
+//   (window_right < 0 || k <= p + window_right) &&
+//   (window_left  < 0 || k >= p - window_left).
+//
+// MFMA scheme (v_mfma_f32_16x16x32_{bf16,f16}; lane l: row/col = l%16,
+// k-group g = l/16 holding 8 consecutive k):
+//  * S^T = K Q^T: A = K tile (16 keys x 32 d, a lane loads 16 B of one key
+//    row straight from HBM), B = Q^T (16 query rows). Result: lane holds
+//    keys 4g..4g+3 of one query row (column l%16).
+//  * O = P V: A = P, which is exactly the S^T lane layout reinterpreted with
+//    the k-slots ordered as the 8 keys that lane already holds (4 from each
+//    of two 16-key tiles). B = V: lane (g, n) loads the V rows of those same
+//    8 keys at d = n*DPL .. n*DPL+DPL-1 and transposes the 8 x DPL tile in
+//    registers (v_perm_b32), giving DPL B fragments; MFMA number k produces
+//    output column n <-> d = n*DPL + k. No LDS round trip and no cross-lane
+//    moves are needed for either operand.
+#pragma once
+
+#include "common.hpp"
+
+namespace vk {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegBig = -1e30f;  // running-max start: finite, so exp2 never sees inf-inf
+constexpr float kRescaleSlack = 8.0f;  // log2 units the running max may lag by
+
+struct AttnArgs {
+  const char* k;  // layer K base
+  const char* v;  // layer V base
+  const char* q;
+  char* out;
+  const uint32_t* cu_q;
+  const uint32_t* cu_k;
+  const uint32_t* table;
+  uint32_t* plan;  // decode: per-sequence step prefix sums (batch + 1)
+  float* ws_ml;    // decode: partial (m, l) per slot and head
+  float* ws_o;     // decode: partial outputs per slot and head
+  uint64_t blk_e, head_e;  // element strides in the pool
+  uint32_t tok_e;
+  uint32_t max_blocks, batch, num_heads, kvh, group, block_size, bs_shift;
+  uint32_t num_waves;  // decode: persistent waves in the grid
+  float scale_log2;    // scale * log2(e)
+  float scale;
+  int32_t wl, wr;
+};
+
+__device__ __forceinline__ void key_range(int32_t p, int32_t len_k, int32_t wl,
+                                          int32_t wr, int32_t& lo, int32_t& hi) {
+  lo = wl >= 0 ? max(0, p - wl) : 0;
+  hi = wr >= 0 ? min(len_k - 1, p + wr) : len_k - 1;
+}
+
+// ---------------------------------------------------------------------------
+// MFMA helpers
+// ---------------------------------------------------------------------------
+
+template <typename T>
+__device__ __forceinline__ floatx4 mfma16x16x32(uint4 a, uint4 b, floatx4 c);
+template <>
+__device__ __forceinline__ floatx4 mfma16x16x32<bf16_t>(uint4 a, uint4 b,
+                                                        floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+      __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ floatx4 mfma16x16x32<f16_t>(uint4 a, uint4 b,
+                                                       floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(
+      __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+typedef float float2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Pack two f32 into one dword of 16-bit values (lo first), round to nearest
+// even (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 style conversions).
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi);
+template <>
+__device__ __forceinline__ uint32_t pack2<bf16_t>(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{lo, hi}, bf16x2));
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<f16_t>(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{lo, hi}, f16x2));
+}
+
+template <typename T>
+__device__ __forceinline__ uint4 pack8(const float (&p)[8]) {
+  return make_uint4(pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3]), pack2<T>(p[4], p[5]),
+                    pack2<T>(p[6], p[7]));
+}
+
+// DPL 16-bit elements (DPL*2 bytes) of one row, as dwords.
+template <int DPL>
+struct VRow {
+  uint32_t w[DPL / 2];
+};
+template <int DPL>
+__device__ __forceinline__ VRow<DPL> load_vrow(const void* p) {
+  VRow<DPL> r;
+  if constexpr (DPL == 4) {
+    const uint2 x = *(const uint2*)p;
+    r.w[0] = x.x; r.w[1] = x.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < DPL / 8; ++i) {
+      const uint4 x = ((const uint4*)p)[i];
+      r.w[4 * i] = x.x; r.w[4 * i + 1] = x.y; r.w[4 * i + 2] = x.z; r.w[4 * i + 3] = x.w;
+    }
+  }
+  return r;
+}
+
+// Column k (0..DPL-1) of the 8 x DPL tile held as 8 rows: 8 16-bit values,
+// row j in slot j. One v_perm_b32 per output dword.
+template <int DPL>
+__device__ __forceinline__ uint4 vcol(const VRow<DPL> (&rows)[8], int k) {
+  const uint32_t sel = (k & 1) ? 0x07060302u : 0x05040100u;
+  uint32_t w[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    w[m] = __builtin_amdgcn_perm(rows[2 * m + 1].w[k >> 1], rows[2 * m].w[k >> 1], sel);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+__device__ __forceinline__ float wave_max_g(float x) {  // over lanes l, l^16, l^32, l^48
+  x = fmaxf(x, __shfl_xor(x, 16));
+  x = fmaxf(x, __shfl_xor(x, 32));
+  return x;
+}
+__device__ __forceinline__ float wave_sum_g(float x) {
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// K and V of one 32-key step (two 16-key tiles) in MFMA operand order.
+//  k[tt][c]: this lane's key row (tile tt, key col) at d = 32c + 8g .. +8.
+//  v[j]: the V row of key slot j (tile j/4, key 4g + j%4) at d = DPL*col ..
+template <int D>
+struct KVStep {
+  uint4 k[2][D / 32];
+  VRow<D / 16> v[8];
+};
+
+// Load a step whose first key s0 is a multiple of 32. Tiles at or past `pend`
+// are zero-filled without touching memory; keys past `last` (the sequence's
+// final key) read the final key instead, so every load stays inside a block
+// the table names. The block id of a 16-key tile is wave-uniform (block_size
+// is a power of two >= 16), so it comes through the scalar cache.
+template <typename T, int D>
+__device__ __forceinline__ void load_kv_step(KVStep<D>& st, const uint32_t* __restrict__ tab,
+                                             const T* kb, const T* vb, const AttnArgs& a,
+                                             int32_t s0, int32_t pend, int32_t last,
+                                             uint32_t col, uint32_t g) {
+  constexpr int KC = D / 32, DPL = D / 16;
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const int32_t ts = s0 + 16 * tt;
+    if (ts < pend) {
+      const uint32_t blk = tab[(uint32_t)ts >> a.bs_shift];
+      const uint32_t off0 = (uint32_t)ts & (a.block_size - 1);
+      const int32_t lim = last - ts;
+      const uint64_t base = (uint64_t)blk * a.blk_e + (uint64_t)off0 * a.tok_e;
+      const T* kt = kb + base;
+      const T* vt = vb + base;
+      const uint32_t kr = (uint32_t)min((int32_t)col, lim) * a.tok_e + 8 * g;
+#pragma unroll
+      for (int c = 0; c < KC; ++c) st.k[tt][c] = *(const uint4*)(kt + kr + 32 * c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t vr = (uint32_t)min((int32_t)(4 * g + i), lim) * a.tok_e + DPL * col;
+        st.v[4 * tt + i] = load_vrow<DPL>(vt + vr);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < KC; ++c) st.k[tt][c] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int w = 0; w < DPL / 2; ++w) st.v[4 * tt + i].w[w] = 0;
+    }
+  }
+}
+
+// One online-softmax step for 16 query rows (the MFMA columns): scores
+// S^T = K Q^T, lazy rescale of the running max, P in the input dtype, O += P V.
+// `visible(i_tile, i)` masks key slot (tt, 4g+i).
+template <typename T, int D, typename Mask>
+__device__ __forceinline__ void attend_step(const KVStep<D>& st, const uint4 (&qf)[D / 32],
+                                            floatx4 (&o)[D / 16], float& m_run, float& l_run,
+                                            float scale_log2, uint32_t g, Mask visible) {
+  constexpr int KC = D / 32, DPL = D / 16;
+  float s[8];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < KC; ++c) acc = mfma16x16x32<T>(st.k[tt][c], qf[c], acc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[4 * tt + i] = visible(tt, i) ? acc[i] * scale_log2 : -INFINITY;
+  }
+  float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])),
+                   fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+  mx = wave_max_g(mx);
+  // Rescale only when some row's max grew by more than 2^kRescaleSlack: the
+  // result is the same softmax, and P stays below 2^kRescaleSlack.
+  if (__any(mx > m_run + kRescaleSlack)) {
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    l_run *= alpha;
+    float al[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * g + i);
+#pragma unroll
+    for (int k = 0; k < DPL; ++k)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[k][i] *= al[i];
+  }
+  float p[8];
+  float ps = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    p[j] = fast_exp2(s[j] - m_run);
+    ps += p[j];
+  }
+  l_run += ps;
+  const uint4 pf = pack8<T>(p);
+#pragma unroll
+  for (int k = 0; k < DPL; ++k) o[k] = mfma16x16x32<T>(pf, vcol<DPL>(st.v, k), o[k]);
+}
+
+
+// ---- launchers (one per translation unit) ----------------------------------
+
+// Decode rows (len_q == 1) of the batch; bf16/f16, head_dim 64 or 128.
+size_t decode_workspace_bytes(uint32_t batch, uint32_t kvh, uint32_t group,
+                              uint32_t head_dim, uint32_t num_waves);
+void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, bool bf16,
+                   hipStream_t s);
+// Prefill rows (len_q > 1); same dtypes and head dims.
+void launch_prefill(const AttnArgs& a, uint32_t max_q, uint32_t head_dim, bool bf16,
+                    hipStream_t s);
+// Any row, any dtype, head_dim <= 256 (VALU).
+void launch_generic(const AttnArgs& a, uint32_t max_q, uint32_t head_dim,
+                    uint32_t dtype, hipStream_t s);
+// Persistent decode waves for the current device (CUs x 8).
+uint32_t decode_num_waves();
+
+}  // namespace vk
