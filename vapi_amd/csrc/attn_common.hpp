@@ -48,10 +48,12 @@ struct AttnArgs {
   uint32_t* plan;  // decode: per-sequence step prefix sums (batch + 1)
   float* ws_ml;    // decode: partial (m, l) per slot and head
   float* ws_o;     // decode: partial outputs per slot and head
+  uint64_t* trace;  // decode timing probes (VK_DECODE_TRACE builds only)
   uint64_t blk_e, head_e;  // element strides in the pool
   uint32_t tok_e;
   uint32_t max_blocks, batch, num_heads, kvh, group, block_size, bs_shift;
   uint32_t num_waves;  // decode: persistent waves in the grid
+  uint32_t static_num, static_den, chunk_steps;  // decode: static share, chunk size
   float scale_log2;    // scale * log2(e)
   float scale;
   int32_t wl, wr;
@@ -152,68 +154,97 @@ __device__ __forceinline__ float wave_sum_g(float x) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // K and V of one 32-key step (two 16-key tiles) in MFMA operand order.
-//  k[tt][c]: this lane's key row (tile tt, key col) at d = 32c + 8g .. +8.
-//  v[j]: the V row of key slot j (tile j/4, key 4g + j%4) at d = DPL*col ..
+//  KTile::k[tt][c]: this lane's key row (tile tt, key col) at d = 32c + 8g .. +8.
+//  VTile::v[j]: the V row of key slot j (tile j/4, key 4g + j%4) at
+//  d = DPL*col .. +DPL.
 template <int D>
-struct KVStep {
+struct KTile {
   uint4 k[2][D / 32];
+};
+template <int D>
+struct VTile {
   VRow<D / 16> v[8];
 };
+template <int D>
+struct KVStep {
+  KTile<D> k;
+  VTile<D> v;
+};
 
-// Load a step whose first key s0 is a multiple of 32. Tiles at or past `pend`
-// are zero-filled without touching memory; keys past `last` (the sequence's
-// final key) read the final key instead, so every load stays inside a block
-// the table names. The block id of a 16-key tile is wave-uniform (block_size
-// is a power of two >= 16), so it comes through the scalar cache.
+// Loads of a step whose first key s0 is a multiple of 32. Every load stays
+// inside a block the table names: a tile past the sequence's final key
+// `last` re-reads the tile holding `last`, and keys past `last` read `last`
+// itself (all of them are masked out of the softmax, and V rows are finite
+// data, so p = 0 removes them exactly). Loads are unconditional, so the
+// tiles need no zero-fill. The block id of a 16-key tile is wave-uniform
+// (block_size is a power of two >= 16) and comes through the scalar cache;
+// per-lane addresses are 32-bit byte offsets from that uniform base.
+template <typename T>
+__device__ __forceinline__ const char* tile_base(const uint32_t* __restrict__ tab, const T* base,
+                                                 const AttnArgs& a, int32_t ts) {
+  const uint32_t blk = tab[(uint32_t)ts >> a.bs_shift];
+  const uint32_t off0 = (uint32_t)ts & (a.block_size - 1);
+  return (const char*)(base + (uint64_t)blk * a.blk_e + (uint64_t)off0 * a.tok_e);
+}
+
 template <typename T, int D>
-__device__ __forceinline__ void load_kv_step(KVStep<D>& st, const uint32_t* __restrict__ tab,
-                                             const T* kb, const T* vb, const AttnArgs& a,
-                                             int32_t s0, int32_t pend, int32_t last,
-                                             uint32_t col, uint32_t g) {
-  constexpr int KC = D / 32, DPL = D / 16;
+__device__ __forceinline__ void load_k(KTile<D>& st, const uint32_t* __restrict__ tab,
+                                       const T* kb, const AttnArgs& a, int32_t s0, int32_t last,
+                                       uint32_t col, uint32_t g) {
+  constexpr int KC = D / 32;
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
-    const int32_t ts = s0 + 16 * tt;
-    if (ts < pend) {
-      const uint32_t blk = tab[(uint32_t)ts >> a.bs_shift];
-      const uint32_t off0 = (uint32_t)ts & (a.block_size - 1);
-      const int32_t lim = last - ts;
-      const uint64_t base = (uint64_t)blk * a.blk_e + (uint64_t)off0 * a.tok_e;
-      const T* kt = kb + base;
-      const T* vt = vb + base;
-      const uint32_t kr = (uint32_t)min((int32_t)col, lim) * a.tok_e + 8 * g;
+    const int32_t ts = min(s0 + 16 * tt, last & ~15);
+    const char* kt = tile_base(tab, kb, a, ts);
+    const uint32_t kr = ((uint32_t)min((int32_t)col, last - ts) * a.tok_e + 8 * g) * sizeof(T);
 #pragma unroll
-      for (int c = 0; c < KC; ++c) st.k[tt][c] = *(const uint4*)(kt + kr + 32 * c);
+    for (int c = 0; c < KC; ++c) st.k[tt][c] = *(const uint4*)(kt + (kr + 64u * c));
+  }
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void load_v(VTile<D>& st, const uint32_t* __restrict__ tab,
+                                       const T* vb, const AttnArgs& a, int32_t s0, int32_t last,
+                                       uint32_t col, uint32_t g) {
+  constexpr int DPL = D / 16;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t vr = (uint32_t)min((int32_t)(4 * g + i), lim) * a.tok_e + DPL * col;
-        st.v[4 * tt + i] = load_vrow<DPL>(vt + vr);
-      }
-    } else {
+  for (int tt = 0; tt < 2; ++tt) {
+    const int32_t ts = min(s0 + 16 * tt, last & ~15);
+    const char* vt = tile_base(tab, vb, a, ts);
+    const int32_t lim = last - ts;
 #pragma unroll
-      for (int c = 0; c < KC; ++c) st.k[tt][c] = make_uint4(0, 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int w = 0; w < DPL / 2; ++w) st.v[4 * tt + i].w[w] = 0;
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t vr =
+          ((uint32_t)min((int32_t)(4 * g + i), lim) * a.tok_e + DPL * col) * sizeof(T);
+      st.v[4 * tt + i] = load_vrow<DPL>(vt + vr);
     }
   }
 }
 
-// One online-softmax step for 16 query rows (the MFMA columns): scores
-// S^T = K Q^T, lazy rescale of the running max, P in the input dtype, O += P V.
+template <typename T, int D>
+__device__ __forceinline__ void load_kv_step(KVStep<D>& st, const uint32_t* __restrict__ tab,
+                                             const T* kb, const T* vb, const AttnArgs& a,
+                                             int32_t s0, int32_t last, uint32_t col,
+                                             uint32_t g) {
+  load_k<T, D>(st.k, tab, kb, a, s0, last, col, g);
+  load_v<T, D>(st.v, tab, vb, a, s0, last, col, g);
+}
+
+// First half of an online-softmax step for 16 query rows (the MFMA
+// columns): scores S^T = K Q^T, lazy rescale of the running max (and of O),
+// returns P packed in the input dtype as the PV A operand.
 // `visible(i_tile, i)` masks key slot (tt, 4g+i).
 template <typename T, int D, typename Mask>
-__device__ __forceinline__ void attend_step(const KVStep<D>& st, const uint4 (&qf)[D / 32],
-                                            floatx4 (&o)[D / 16], float& m_run, float& l_run,
-                                            float scale_log2, uint32_t g, Mask visible) {
+__device__ __forceinline__ uint4 attend_qk(const KTile<D>& kt, const uint4 (&qf)[D / 32],
+                                           floatx4 (&o)[D / 16], float& m_run, float& l_run,
+                                           float scale_log2, uint32_t g, Mask visible) {
   constexpr int KC = D / 32, DPL = D / 16;
   float s[8];
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < KC; ++c) acc = mfma16x16x32<T>(st.k[tt][c], qf[c], acc);
+    for (int c = 0; c < KC; ++c) acc = mfma16x16x32<T>(kt.k[tt][c], qf[c], acc);
 #pragma unroll
     for (int i = 0; i < 4; ++i) s[4 * tt + i] = visible(tt, i) ? acc[i] * scale_log2 : -INFINITY;
   }
@@ -227,13 +258,10 @@ __device__ __forceinline__ void attend_step(const KVStep<D>& st, const uint4 (&q
     const float alpha = fast_exp2(m_run - m_new);
     m_run = m_new;
     l_run *= alpha;
-    float al[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * g + i);
 #pragma unroll
     for (int k = 0; k < DPL; ++k)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[k][i] *= al[i];
+      for (int i = 0; i < 4; ++i) o[k][i] *= alpha;
   }
   float p[8];
   float ps = 0.f;
@@ -243,19 +271,59 @@ __device__ __forceinline__ void attend_step(const KVStep<D>& st, const uint4 (&q
     ps += p[j];
   }
   l_run += ps;
-  const uint4 pf = pack8<T>(p);
-#pragma unroll
-  for (int k = 0; k < DPL; ++k) o[k] = mfma16x16x32<T>(pf, vcol<DPL>(st.v, k), o[k]);
+  return pack8<T>(p);
 }
 
+// Second half: O^T += V^T P^T. The V fragments are the A operand (MFMA k's
+// row m <-> d = DPL*m + k) and P^T is the B operand exactly as the score
+// layout left it, so the result lands as lane (g, col) holding query row col
+// at d = DPL*(4g + i) + k (i = 0..3, k = 0..DPL-1): every lane's accumulators
+// belong to its own row, and rescaling needs no cross-lane traffic.
+template <typename T, int D>
+__device__ __forceinline__ void attend_pv(const VTile<D>& vt, uint4 pf, floatx4 (&o)[D / 16]) {
+  constexpr int DPL = D / 16;
+#pragma unroll
+  for (int k = 0; k < DPL; ++k) o[k] = mfma16x16x32<T>(vcol<DPL>(vt.v, k), pf, o[k]);
+}
+
+// Store row `col`'s DPL-wide runs d = DPL*(4g + i) .. +DPL of o, scaled, to
+// `row` (16-bit output).
+template <typename T, int D>
+__device__ __forceinline__ void store_row(T* row, const floatx4 (&o)[D / 16], float scale,
+                                          uint32_t g) {
+  constexpr int DPL = D / 16;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t w[DPL / 2];
+#pragma unroll
+    for (int k = 0; k < DPL / 2; ++k)
+      w[k] = pack2<T>(o[2 * k][i] * scale, o[2 * k + 1][i] * scale);
+    T* dst = row + DPL * (4 * g + i);
+    if constexpr (DPL == 4) {
+      *(uint2*)dst = make_uint2(w[0], w[1]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < DPL / 8; ++k)
+        ((uint4*)dst)[k] = make_uint4(w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]);
+    }
+  }
+}
+
+template <typename T, int D, typename Mask>
+__device__ __forceinline__ void attend_step(const KVStep<D>& st, const uint4 (&qf)[D / 32],
+                                            floatx4 (&o)[D / 16], float& m_run, float& l_run,
+                                            float scale_log2, uint32_t g, Mask visible) {
+  const uint4 pf = attend_qk<T, D>(st.k, qf, o, m_run, l_run, scale_log2, g, visible);
+  attend_pv<T, D>(st.v, pf, o);
+}
 
 // ---- launchers (one per translation unit) ----------------------------------
 
 // Decode rows (len_q == 1) of the batch; bf16/f16, head_dim 64 or 128.
 size_t decode_workspace_bytes(uint32_t batch, uint32_t kvh, uint32_t group,
-                              uint32_t head_dim, uint32_t num_waves);
-void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, bool bf16,
-                   hipStream_t s);
+                              uint32_t head_dim, uint32_t max_k, uint32_t num_waves);
+void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t max_k,
+                   bool bf16, hipStream_t s);
 // Prefill rows (len_q > 1); same dtypes and head dims.
 void launch_prefill(const AttnArgs& a, uint32_t max_q, uint32_t head_dim, bool bf16,
                     hipStream_t s);

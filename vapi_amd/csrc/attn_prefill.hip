@@ -65,7 +65,7 @@ __global__ __launch_bounds__(64 * NW) void paged_prefill_mfma(AttnArgs a) {
 
   KVStep<D> st;
   for (int32_t s0 = klo & ~31; s0 <= khi; s0 += 32) {
-    load_kv_step<T, D>(st, tab, kb, vb, a, s0, khi + 1, len_k - 1, col, g);
+    load_kv_step<T, D>(st, tab, kb, vb, a, s0, len_k - 1, col, g);
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
       const int32_t pt = pos[t];
@@ -81,31 +81,11 @@ __global__ __launch_bounds__(64 * NW) void paged_prefill_mfma(AttnArgs a) {
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
     const float lt = wave_sum_g(l_run[t]);
-    float inv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float li = __shfl(lt, 4 * g + i);
-      inv[i] = li > 0.f ? 1.f / li : 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t r = row0 + 16 * t + 4 * g + i;
-      if (r >= nrows) continue;
-      const uint32_t j = r / G, hl = r % G;
-      T* orow = (T*)a.out + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * D;
-      uint32_t w[DPL / 2];
-#pragma unroll
-      for (int k = 0; k < DPL / 2; ++k)
-        w[k] = pack2<T>(o[t][2 * k][i] * inv[i], o[t][2 * k + 1][i] * inv[i]);
-      if constexpr (DPL == 4) {
-        *(uint2*)(orow + DPL * col) = make_uint2(w[0], w[1]);
-      } else {
-#pragma unroll
-        for (int k = 0; k < DPL / 8; ++k)
-          ((uint4*)(orow + DPL * col))[k] =
-              make_uint4(w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]);
-      }
-    }
+    const uint32_t r = row0 + 16 * t + col;  // this lane's query row
+    if (r >= nrows) continue;
+    const uint32_t j = r / G, hl = r % G;
+    T* orow = (T*)a.out + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * D;
+    store_row<T, D>(orow, o[t], lt > 0.f ? 1.f / lt : 0.f, g);
   }
 }
 
