@@ -230,6 +230,19 @@ def bench_blocks(steps, warmup, decode):
     return res
 
 
+def bench_copy(steps, warmup):
+    """Copy-on-write alone (config 4a), for profiling."""
+    w = workload.config4_block_ops()
+    cache = PagedKvCache(w.num_layers, w.num_blocks, w.block_size, w.num_kv_heads,
+                         w.head_dim, torch.bfloat16, "HND")
+    workload.fill_normal(cache._slab, workload.seed_for(4))
+    pairs = w.pairs.tolist()
+    be = KvBlockBackend(cache)
+    ms, _, _ = timed(lambda: be.copy_blocks(pairs), steps, warmup)
+    alg = len(pairs) * be.block_bytes() * 2
+    log(f"copy cfg4a: {alg / 1e9:.2f} GB moved, {ms:.3f} ms, {alg / (ms * 1e-3) / 1e9:.0f} GB/s")
+
+
 def _copy_on(stream, dst, src):
     with torch.cuda.stream(stream):
         dst.copy_(src, non_blocking=True)
@@ -290,8 +303,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["decode", "append", "prefill", "blocks"], default=None)
+    ap.add_argument("--only", choices=["decode", "append", "prefill", "copy", "blocks"],
+                    default=None)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="first run one plain 256 MiB device copy, whose FETCH_SIZE/WRITE_SIZE "
+                         "counters scale the hot kernels' counters to bytes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build's paged-KV path runs on a single "
@@ -299,8 +316,18 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     torch.cuda.init()
+    if args.calibrate:
+        # A plain conversion kernel of known traffic: reads 256 MiB of f32,
+        # writes 128 MiB of f16 (the only f32->f16 copy in the run).
+        src = torch.ones(64 << 20, dtype=torch.float32, device=DEV)
+        dst = src.to(torch.float16)
+        torch.cuda.synchronize()
+        del src, dst
     if args.only == "append":
         bench_append(args.steps, args.warmup)
+        return
+    if args.only == "copy":
+        bench_copy(args.steps, args.warmup)
         return
     if args.only == "prefill":
         bench_prefill(args.steps, args.warmup)

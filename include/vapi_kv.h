@@ -141,7 +141,12 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
  * window_right: keys k > p + window_right are hidden; 0 = causal, -1 =
  *   unlimited (bidirectional).
  * workspace: device scratch of at least vapi_paged_attention_workspace_size()
- *   bytes (split-K partials); may be NULL when that size is 0.
+ *   bytes (decode plan, a work counter and split-context partials); may be
+ *   NULL when that size is 0. Zero-fill it once before its first use; every
+ *   call leaves it ready for the next. Calls sharing one workspace must not
+ *   overlap (same stream, or ordered streams).
+ * max_seqlen_q/k must bound every sequence's len_q/len_k (as in
+ *   flash-attention); they size the grid and the workspace.
  */
 size_t vapi_paged_attention_workspace_size(const vapi_kv_pool* pool,
                                            uint32_t batch, uint32_t num_heads,

@@ -82,13 +82,15 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
       const uint32_t r2 = a.kvh.div(r);
       const uint32_t h = r - r2 * a.kvh.d;
       const uint32_t kv = r2 & 1u, t = r2 >> 1;
+      // The source row and the slot are loaded together (the source address
+      // does not depend on the slot), so one memory round trip precedes the
+      // store.
+      const uint64_t src_off = ((uint64_t)t * a.kvh.d + h) * a.row_bytes + (uint64_t)u * C;
+      val[j] = *(const V*)((kv ? a.v_src : a.k_src) + src_off);
       const uint32_t slot = a.slots[t];
       if (slot < a.num_slots) {  // VAPI_KV_SLOT_SKIP and out-of-range drop
         const uint32_t blk = a.bs.div(slot);
         const uint32_t off = slot - blk * a.bs.d;
-        const uint64_t src_off =
-            ((uint64_t)t * a.kvh.d + h) * a.row_bytes + (uint64_t)u * C;
-        val[j] = *(const V*)((kv ? a.v_src : a.k_src) + src_off);
         dst[j] = (kv ? a.v_dst : a.k_dst) + blk * a.blk_b + h * a.head_b +
                  off * a.tok_b + (uint64_t)u * C;
       }
