@@ -96,7 +96,9 @@ int vapi_paged_attention(const vapi_kv_pool* pool, uint32_t layer,
   while ((1u << a.bs_shift) < g.block_size) ++a.bs_shift;
   a.num_waves = 0;
   a.scale = scale;
-  a.scale_log2 = scale * kLog2e;
+  // A zero scale is kept positive so that masked scores (-inf) times it stay -inf.
+  a.scale_log2 = fmaxf(fabsf(scale) * kLog2e, 1e-30f);
+  a.q_sign = scale < 0.f ? 0x80008000u : 0u;
   a.wl = window_left < 0 ? -1 : window_left;
   a.wr = window_right < 0 ? -1 : window_right;
   const hipStream_t s = hs(stream);

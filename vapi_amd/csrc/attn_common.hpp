@@ -54,8 +54,9 @@ struct AttnArgs {
   uint32_t max_blocks, batch, num_heads, kvh, group, block_size, bs_shift;
   uint32_t num_waves;  // decode: persistent waves in the grid
   uint32_t static_num, static_den, chunk_steps;  // decode: static share, chunk size
-  float scale_log2;    // scale * log2(e)
+  float scale_log2;    // |scale| * log2(e) (MFMA paths: Q is negated when scale < 0)
   float scale;
+  uint32_t q_sign;     // 0x80008000 when scale < 0: XOR into packed 16-bit Q words
   int32_t wl, wr;
 };
 
@@ -140,15 +141,27 @@ __device__ __forceinline__ uint4 vcol(const VRow<DPL> (&rows)[8], int k) {
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-__device__ __forceinline__ float wave_max_g(float x) {  // over lanes l, l^16, l^32, l^48
-  x = fmaxf(x, __shfl_xor(x, 16));
-  x = fmaxf(x, __shfl_xor(x, 32));
-  return x;
+// Reductions over the four lane groups l, l^16, l^32, l^48 with the gfx950
+// lane-swap instructions (no LDS round trip): permlane32_swap of x with
+// itself leaves (lower half, lower half) in one result and (upper, upper)
+// in the other, permlane16_swap does the same for odd/even 16-lane rows.
+// Kernels run with the IEEE mode bit clear and no NaN inputs, so fmaxf
+// needs no quieting of its operands (see the build flags).
+__device__ __forceinline__ float max_nc(float a, float b) { return fmaxf(a, b); }
+__device__ __forceinline__ float max3_nc(float a, float b, float c) {
+  return fmaxf(fmaxf(a, b), c);
+}
+__device__ __forceinline__ float wave_max_g(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = max_nc(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return max_nc(__uint_as_float(q[0]), __uint_as_float(q[1]));
 }
 __device__ __forceinline__ float wave_sum_g(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -182,7 +195,11 @@ struct KVStep {
 template <typename T>
 __device__ __forceinline__ const char* tile_base(const uint32_t* __restrict__ tab, const T* base,
                                                  const AttnArgs& a, int32_t ts) {
-  const uint32_t blk = tab[(uint32_t)ts >> a.bs_shift];
+  // Read through the constant address space: the block table is never
+  // written by a kernel, and this keeps the load scalar wherever it is
+  // inlined (a restrict qualifier does not survive every inlining).
+  using ConstU32 = const __attribute__((address_space(4))) uint32_t;
+  const uint32_t blk = ((ConstU32*)tab)[(uint32_t)ts >> a.bs_shift];
   const uint32_t off0 = (uint32_t)ts & (a.block_size - 1);
   return (const char*)(base + (uint64_t)blk * a.blk_e + (uint64_t)off0 * a.tok_e);
 }
@@ -233,7 +250,9 @@ __device__ __forceinline__ void load_kv_step(KVStep<D>& st, const uint32_t* __re
 // First half of an online-softmax step for 16 query rows (the MFMA
 // columns): scores S^T = K Q^T, lazy rescale of the running max (and of O),
 // returns P packed in the input dtype as the PV A operand.
-// `visible(i_tile, i)` masks key slot (tt, 4g+i).
+// `visible(i_tile, i)` masks key slot (tt, 4g+i). m_run is kept in scaled
+// log2 units; scale_log2 >= 0, so the max is taken on the raw scores and the
+// scale folds into one FMA per score: p = exp2(s * c - m).
 template <typename T, int D, typename Mask>
 __device__ __forceinline__ uint4 attend_qk(const KTile<D>& kt, const uint4 (&qf)[D / 32],
                                            floatx4 (&o)[D / 16], float& m_run, float& l_run,
@@ -246,11 +265,10 @@ __device__ __forceinline__ uint4 attend_qk(const KTile<D>& kt, const uint4 (&qf)
 #pragma unroll
     for (int c = 0; c < KC; ++c) acc = mfma16x16x32<T>(kt.k[tt][c], qf[c], acc);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s[4 * tt + i] = visible(tt, i) ? acc[i] * scale_log2 : -INFINITY;
+    for (int i = 0; i < 4; ++i) s[4 * tt + i] = visible(tt, i) ? acc[i] : -INFINITY;
   }
-  float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])),
-                   fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-  mx = wave_max_g(mx);
+  float mx = max3_nc(max3_nc(s[0], s[1], s[2]), max3_nc(s[3], s[4], s[5]), max_nc(s[6], s[7]));
+  mx = wave_max_g(mx) * scale_log2;
   // Rescale only when some row's max grew by more than 2^kRescaleSlack: the
   // result is the same softmax, and P stays below 2^kRescaleSlack.
   if (__any(mx > m_run + kRescaleSlack)) {
@@ -267,7 +285,7 @@ __device__ __forceinline__ uint4 attend_qk(const KTile<D>& kt, const uint4 (&qf)
   float ps = 0.f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    p[j] = fast_exp2(s[j] - m_run);
+    p[j] = fast_exp2(__builtin_fmaf(s[j], scale_log2, -m_run));
     ps += p[j];
   }
   l_run += ps;

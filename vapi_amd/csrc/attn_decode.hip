@@ -62,7 +62,7 @@ struct Split {
 struct DecodePos {
   uint32_t seq, kh, q0;
   int32_t key0, len_k, lo;
-  bool seg_first;  // key0 is the segment's first step
+  uint32_t seg_first;  // key0 is the segment's first step (a word, not a bool: no stack copy)
 };
 
 __device__ __forceinline__ DecodePos locate(const AttnArgs& a, const uint32_t* __restrict__ cu_q,
@@ -98,7 +98,11 @@ __device__ __forceinline__ void load_q(uint4* qs, const AttnArgs& a, const Decod
   const uint32_t h = col < a.group ? col : 0;
   const T* qrow = (const T*)a.q + ((uint64_t)p.q0 * a.num_heads + p.kh * a.group + h) * D;
 #pragma unroll
-  for (int c = 0; c < D / 32; ++c) qs[c * 64 + lane] = *(const uint4*)(qrow + 32 * c + 8 * g);
+  for (int c = 0; c < D / 32; ++c) {
+    uint4 x = *(const uint4*)(qrow + 32 * c + 8 * g);
+    x.x ^= a.q_sign, x.y ^= a.q_sign, x.z ^= a.q_sign, x.w ^= a.q_sign;
+    qs[c * 64 + lane] = x;
+  }
 }
 
 template <typename T, int D>
