@@ -141,10 +141,14 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
  * window_right: keys k > p + window_right are hidden; 0 = causal, -1 =
  *   unlimited (bidirectional).
  * workspace: device scratch of at least vapi_paged_attention_workspace_size()
- *   bytes (decode plan, a work counter and split-context partials); may be
- *   NULL when that size is 0. Zero-fill it once before its first use; every
- *   call leaves it ready for the next. Calls sharing one workspace must not
- *   overlap (same stream, or ordered streams).
+ *   bytes (the decode's per-XCD work shares, its plan and split-context
+ *   partials); may be NULL when that size is 0. Zero-fill it once before its
+ *   first use. Keep one workspace per stream across calls and layers: each
+ *   call measures how fast each XCD streamed and moves the shares the next
+ *   call on that workspace uses (a fresh workspace starts from equal
+ *   shares). Results do not depend on the shares beyond f32 rounding of the
+ *   split merge. Calls sharing one workspace must not overlap (same stream,
+ *   or ordered streams).
  * max_seqlen_q/k must bound every sequence's len_q/len_k (as in
  *   flash-attention); they size the grid and the workspace.
  */

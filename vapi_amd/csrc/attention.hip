@@ -82,6 +82,7 @@ int vapi_paged_attention(const vapi_kv_pool* pool, uint32_t layer,
   a.plan = nullptr;
   a.ws_ml = nullptr;
   a.ws_o = nullptr;
+  a.bal = nullptr;
   a.trace = nullptr;
   a.blk_e = g.blk;
   a.head_e = g.head;

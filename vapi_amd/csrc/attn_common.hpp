@@ -45,15 +45,15 @@ struct AttnArgs {
   const uint32_t* cu_q;
   const uint32_t* cu_k;
   const uint32_t* table;
-  uint32_t* plan;  // decode: per-sequence step prefix sums (batch + 1)
-  float* ws_ml;    // decode: partial (m, l) per slot and head
-  float* ws_o;     // decode: partial outputs per slot and head
+  uint32_t* plan;      // decode: step prefix sums (batch + 1), then group bounds (9)
+  float* ws_ml;        // decode: partial (m, l) per slot and head
+  float* ws_o;         // decode: partial outputs per slot and head
+  uint32_t* bal;       // decode: XCD shares and per-wave timings, kept across launches
   uint64_t* trace;  // decode timing probes (VK_DECODE_TRACE builds only)
   uint64_t blk_e, head_e;  // element strides in the pool
   uint32_t tok_e;
   uint32_t max_blocks, batch, num_heads, kvh, group, block_size, bs_shift;
   uint32_t num_waves;  // decode: persistent waves in the grid
-  uint32_t static_num, static_den, chunk_steps;  // decode: static share, chunk size
   float scale_log2;    // |scale| * log2(e) (MFMA paths: Q is negated when scale < 0)
   float scale;
   uint32_t q_sign;     // 0x80008000 when scale < 0: XOR into packed 16-bit Q words
@@ -336,6 +336,7 @@ __device__ __forceinline__ void attend_step(const KVStep<D>& st, const uint4 (&q
 }
 
 // ---- launchers (one per translation unit) ----------------------------------
+
 
 // Decode rows (len_q == 1) of the batch; bf16/f16, head_dim 64 or 128.
 size_t decode_workspace_bytes(uint32_t batch, uint32_t kvh, uint32_t group,

@@ -1,25 +1,34 @@
-// Decode (len_q == 1) paged attention as one persistent stream with guided
-// self-scheduling.
+// Decode (len_q == 1) paged attention as one persistent stream, one launch.
 //
 // The work of a decode batch is the sequence of 32-key steps over every
 // (sequence, kv head) segment: segment (s, h) has ceil((len_k - lo32)/32)
 // steps, where lo32 is the window start rounded down to 32. The grid holds
-// exactly as many waves as the chip runs at once (CUs x 8). The first
-// fraction of the S steps is split statically, wave w taking the contiguous
-// slice [w*S1/W, (w+1)*S1/W); the rest is cut into chunks of a few steps that
-// waves take from an atomic counter as they finish, so waves on faster
-// CUs/XCDs (measured: +-25% spread in per-wave throughput) can absorb the
-// tail. The static share defaults to 100% (see static_pct()).
-// A wave keeps the next step's K/V in flight while it computes the current
-// one, across segment and range boundaries, and asks for its next chunk one
-// range ahead so the request latency is hidden too. Only the counter value is
-// shared between waves, so no memory fence is needed (agent-scope fences on
-// gfx950 write back the XCD-private L2s).
+// one workgroup of 4 waves per CU, one wave per SIMD: two waves sharing a
+// SIMD do not share it fairly on gfx950 (the older one issues first and
+// streams about 3x faster), so equal shares would not finish together. Each
+// wave keeps a whole step (K and V, 16 KiB) in flight while it computes the
+// current one, which keeps HBM saturated with 4 waves per CU.
 //
-// Ranges (static slices r < W, chunks r = W + c) are increasing in step
-// order, as are segments, so piece slot r + segment is unique. A range that
-// covers a whole segment writes the normalised output directly; otherwise
-// it writes the piece's (m, l, o) and paged_decode_merge combines the pieces.
+// The XCDs differ in per-wave bandwidth (by up to ~15% on one box, and which
+// XCD is slow differs between boxes), so the steps are split into 8 group
+// ranges, one per XCD (workgroup b runs on XCD b % 8), in proportion to
+// shares that each launch measures for the next: every wave records its
+// steps and elapsed time, and the merge kernel moves the shares halfway to
+// the measured per-group rates. Within a group each wave takes an
+// equal contiguous slice. Any shares give the same results up to the f32
+// merge order; the shares only move where the pieces split.
+//
+// A wave's run of steps within one segment is a piece. A piece covering a
+// whole segment writes the normalised output; the first and last piece of a
+// slice may be partial and write (m, l, o) to slot range + segment (ranges
+// and segments are both numbered in step order, so slots are unique), and
+// paged_decode_merge, one wave per split segment, combines them. The merge
+// kernel's extra workgroup turns the stream's per-wave timings into the
+// next launch's shares. (Merging inside the stream, by the wave that
+// completes a segment, needs write-through stores, L2-bypassing loads and
+// counters across XCDs; measured, it costs more at the tail than the
+// second launch.)
+//
 // All G query heads of a kv head ride one MFMA tile, so K/V bytes are read
 // exactly once.
 #include <cstdlib>
@@ -29,7 +38,13 @@
 namespace vk {
 
 constexpr int kDecodeWavesPerWG = 4;
+constexpr int kDecodeWGsPerCU = 1;
+constexpr uint32_t kGroups = 8;          // XCDs; workgroup b runs on XCD b % 8
 constexpr uint32_t kMaxPlanSeqs = 4096;  // sequences per launch (host chunks beyond)
+
+// Balance block (u32 words, kept across launches at the start of the
+// workspace): shares f32[8] at 0, per-wave (steps, ticks) from kBalStats.
+constexpr uint32_t kBalStats = 64;
 
 // Steps of sequence s (0 for rows that are not decode rows).
 __device__ __forceinline__ uint32_t decode_steps(const AttnArgs& a,
@@ -42,21 +57,68 @@ __device__ __forceinline__ uint32_t decode_steps(const AttnArgs& a,
   return (uint32_t)(len_k - (lo & ~31) + 31) >> 5;
 }
 
-// Static/dynamic split of the S steps (identical in both kernels).
-struct Split {
-  uint32_t S, S1, C, K, W;
-  __device__ __forceinline__ Split(const AttnArgs& a, uint32_t S_) : S(S_) {
-    W = a.num_waves;
-    K = a.chunk_steps;
-    S1 = (uint32_t)(((uint64_t)S * a.static_num) / a.static_den);
-    C = (S - S1 + K - 1) / K;
+// Waves in group x and the number of waves in groups before it.
+__device__ __forceinline__ uint32_t group_waves(uint32_t nwg, uint32_t x) {
+  return nwg > x ? ((nwg - 1 - x) / kGroups + 1) * kDecodeWavesPerWG : 0u;
+}
+__device__ __forceinline__ uint32_t group_offset(uint32_t nwg, uint32_t x) {
+  uint32_t off = 0;
+  for (uint32_t y = 0; y < x; ++y) off += group_waves(nwg, y);
+  return off;
+}
+
+// The shares of this launch: 8 positive f32, uniform when the workspace
+// holds none yet (all zero) or anything unusable; 0 for groups without waves.
+__device__ __forceinline__ void load_shares(const AttnArgs& a, uint32_t nwg, float (&w)[kGroups]) {
+  bool ok = true;
+#pragma unroll
+  for (uint32_t x = 0; x < kGroups; ++x) {
+    w[x] = __uint_as_float(a.bal[x]);
+    ok = ok && w[x] > 0.f && w[x] < 1e6f;
   }
-  // Range holding step t.
-  __device__ __forceinline__ uint32_t range_of(uint32_t t) const {
-    if (t < S1) return (uint32_t)((((uint64_t)t + 1) * W - 1) / S1);
-    return W + (t - S1) / K;
+#pragma unroll
+  for (uint32_t x = 0; x < kGroups; ++x) {
+    if (!ok) w[x] = 1.f;
+    if (!group_waves(nwg, x)) w[x] = 0.f;
   }
-};
+}
+
+// Group x covers steps [F[x], F[x + 1]) of S.
+__device__ __forceinline__ void group_bounds(const float (&w)[kGroups], uint32_t S,
+                                             uint32_t (&F)[kGroups + 1]) {
+  float tot = 0.f;
+#pragma unroll
+  for (uint32_t x = 0; x < kGroups; ++x) tot += w[x];
+  float run = 0.f;
+  F[0] = 0;
+#pragma unroll
+  for (uint32_t x = 1; x < kGroups; ++x) {
+    run += w[x - 1];
+    const uint32_t f = (uint32_t)fminf((float)S, floorf((float)S * (run / tot)));
+    F[x] = max(F[x - 1], f);
+  }
+  F[kGroups] = S;
+}
+
+// Whether range r (wave slice) holds no steps: empty slices exist whenever a
+// group has more waves than steps, and their partial slots hold stale data.
+__device__ __forceinline__ bool range_empty(const uint32_t (&F)[kGroups + 1], uint32_t nwg,
+                                            uint32_t r) {
+  uint32_t x = 0, off = 0;
+  while (x + 1 < kGroups && off + group_waves(nwg, x) <= r) off += group_waves(nwg, x++);
+  const uint64_t j = r - off, len = F[x + 1] - F[x], nw = group_waves(nwg, x);
+  return j * len / nw == (j + 1) * len / nw;
+}
+
+// Range (wave slice) holding step t, given the group bounds.
+__device__ __forceinline__ uint32_t range_of(const uint32_t (&F)[kGroups + 1], uint32_t nwg,
+                                             uint32_t t) {
+  uint32_t x = 0;
+  while (x + 1 < kGroups && F[x + 1] <= t) ++x;
+  const uint32_t len = F[x + 1] - F[x], nw = group_waves(nwg, x);
+  const uint32_t j = (uint32_t)((((uint64_t)(t - F[x]) + 1) * nw - 1) / len);
+  return group_offset(nwg, x) + j;
+}
 
 // Where global step t lives.
 struct DecodePos {
@@ -123,6 +185,7 @@ __device__ __forceinline__ void load_step_v(VTile<D>& st, const AttnArgs& a,
   load_v<T, D>(st, tab, vb, a, p.key0, p.len_k - 1, col, g);
 }
 
+
 // Write a finished piece of segment (p.seq, p.kh): the final output if the
 // piece is the whole segment, else a partial in slot `slot`.
 template <typename T, int D>
@@ -148,16 +211,12 @@ __device__ __forceinline__ void flush_piece(const AttnArgs& a, const DecodePos& 
       for (int k = 0; k < DPL; k += 4)
         *(float4*)(po + DPL * (4 * g + i) + k) =
             make_float4(o[k][i], o[k + 1][i], o[k + 2][i], o[k + 3][i]);
-    if (g == 0) {
-      float* ml = a.ws_ml + ((uint64_t)slot * G + col) * 2;
-      ml[0] = m_run;
-      ml[1] = l_tot;
-    }
+    if (g == 0) *(float2*)(a.ws_ml + ((uint64_t)slot * G + col) * 2) = make_float2(m_run, l_tot);
   }
 }
 
 template <typename T, int D>
-__global__ __launch_bounds__(64 * kDecodeWavesPerWG, 2) void paged_decode_stream(
+__global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged_decode_stream(
     AttnArgs a, const uint32_t* __restrict__ cu_q, const uint32_t* __restrict__ cu_k,
     const uint32_t* __restrict__ table) {
   constexpr int DPL = D / 16;
@@ -167,7 +226,7 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, 2) void paged_decode_stream
   const uint32_t lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t B = a.batch;
-  uint32_t* counter = a.plan + B + 1;
+  const uint32_t nwg = gridDim.x;
 
   // Step prefix sums over sequences (each sequence contributes kvh segments).
   {
@@ -192,46 +251,37 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, 2) void paged_decode_stream
     }
     if (tid == NT - 1) P[B] = run;
     __syncthreads();
-    if (blockIdx.x == 0)
-      for (uint32_t s = tid; s <= B; s += NT) a.plan[s] = P[s];
   }
 
-  const Split sp(a, __builtin_amdgcn_readfirstlane(P[B]));
+  const uint32_t S = __builtin_amdgcn_readfirstlane(P[B]);
+  float w[kGroups];
+  load_shares(a, nwg, w);
+  uint32_t F[kGroups + 1];
+  group_bounds(w, S, F);
+  if (blockIdx.x == 0) {  // the merge kernel reads the plan back
+    for (uint32_t s = tid; s <= B; s += 64 * kDecodeWavesPerWG) a.plan[s] = P[s];
+    if (tid == 0)
+      for (uint32_t y = 0; y <= kGroups; ++y) a.plan[B + 1 + y] = F[y];
+  }
+  const uint32_t x = blockIdx.x % kGroups;
+  const uint32_t j = (blockIdx.x / kGroups) * kDecodeWavesPerWG + wave;
+  const uint32_t len = F[x + 1] - F[x], nw = group_waves(nwg, x);
+  const uint32_t t_begin = F[x] + (uint32_t)(((uint64_t)j * len) / nw);
+  const uint32_t t_end = F[x] + (uint32_t)(((uint64_t)(j + 1) * len) / nw);
+  const uint32_t r = group_offset(nwg, x) + j;
   const uint32_t gw = blockIdx.x * kDecodeWavesPerWG + wave;
-  // Next chunk id: requested when the wave starts the second-to-last step of
-  // its range (so requests from different waves spread out in time instead
-  // of all hitting the counter at once), read at the last step; lane 0 holds
-  // it until then.
-  // (atomicInc, not atomicAdd: the compiler's atomic optimizer rewrites a
-  // uniform-address add into a wave-aggregated form that broadcasts the
-  // result at once, i.e. waits for it and for every load in flight.)
-  auto request = [&]() -> uint32_t {
-    uint32_t v = 0;
-    if (lane == 0) v = atomicInc(counter, 0xFFFFFFFFu);
-    return v;
-  };
-
-  uint32_t t = sp.S1 ? (uint32_t)(((uint64_t)gw * sp.S1) / sp.W) : 0;
-  uint32_t t_end = sp.S1 ? (uint32_t)(((uint64_t)(gw + 1) * sp.S1) / sp.W) : 0;
-  uint32_t r = gw;
-  uint32_t nc_v = 0;
-  bool asked = false;
-  if (t >= t_end) {  // empty static slice: start on a chunk
-    const uint32_t nc = __builtin_amdgcn_readfirstlane(request());
-    if (nc >= sp.C) return;
-    t = sp.S1 + nc * sp.K;
-    t_end = min(t + sp.K, sp.S);
-    r = sp.W + nc;
+  uint32_t* stat = a.bal + kBalStats + 2 * gw;
+  if (t_begin >= t_end) {
+    if (lane == 0) stat[0] = 0u, stat[1] = 0u;
+    return;
   }
-#ifdef VK_DECODE_TRACE
   const uint64_t tr0 = __builtin_amdgcn_s_memrealtime();
-  uint32_t nsteps = 0;
-#endif
 
+  uint32_t t = t_begin;
   const uint32_t col = lane & 15, g = lane >> 4;
   DecodePos pos = locate(a, cu_q, cu_k, P, t);
   // The Q^T operand of the current segment lives in LDS (read back every
-  // step) to keep the two K/V buffers in registers without spilling.
+  // step) to keep the K/V buffers in registers.
   __shared__ uint4 q_lds[kDecodeWavesPerWG][D / 32 * 64];
   uint4* qs = q_lds[wave];
   load_q<T, D>(qs, a, pos, lane, col, g);
@@ -246,39 +296,26 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, 2) void paged_decode_stream
   load_step_k<T, D>(kA, a, table, pos, col, g);
   load_step_v<T, D>(vA, a, table, pos, col, g);
 
-  // One step: find the next step, prefetch its K before QK^T and its V
-  // before PV (so at most three of the four tiles are live), flush when the
-  // piece ends (segment or range boundary). Returns false when the wave has
-  // no more work.
+  // One step: find the next step, issue its K and V, attend over the current
+  // one, flush when the piece ends (segment or slice boundary). Returns
+  // false when the slice is done.
   auto step = [&](KTile<D>& kc, VTile<D>& vc, KTile<D>& kn, VTile<D>& vn) -> bool {
-    const bool in_range = t + 1 < t_end;
-    if (!asked && t + 2 >= t_end) {
-      nc_v = request();
-      asked = true;
-    }
-    bool more = in_range;
-    uint32_t tn = t + 1, nc = 0;
-    if (!in_range) {
-      nc = __builtin_amdgcn_readfirstlane(nc_v);
-      more = nc < sp.C;
-      tn = sp.S1 + nc * sp.K;
-    }
+    const bool more = t + 1 < t_end;
     const bool seg_ends = pos.key0 + 32 >= pos.len_k;
-    const bool same_piece = in_range && !seg_ends;
+    const bool same_piece = more && !seg_ends;
     // The next step's loads are issued unconditionally (the final step of a
     // wave re-reads its own tiles, which hit in L2): a load inside a branch
     // makes the waitcnt pass assume it may be the newest and wait for the
     // prefetch before this step's MFMAs.
     DecodePos nxt = pos;
-    if (more) {
-      if (same_piece) {
-        nxt.key0 += 32;
-        nxt.seg_first = false;
-      } else {
-        nxt = locate(a, cu_q, cu_k, P, tn);
-      }
+    if (same_piece) {
+      nxt.key0 += 32;
+      nxt.seg_first = false;
+    } else if (more) {
+      nxt = locate(a, cu_q, cu_k, P, t + 1);
     }
     load_step_k<T, D>(kn, a, table, nxt, col, g);
+    load_step_v<T, D>(vn, a, table, nxt, col, g);
     const int32_t lo = pos.lo, len_k = pos.len_k, key0 = pos.key0;
     uint4 qf[D / 32];
 #pragma unroll
@@ -287,11 +324,7 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, 2) void paged_decode_stream
       const int32_t key = key0 + 16 * tt + 4 * (int32_t)g + i;
       return key >= lo && key < len_k;
     });
-    load_step_v<T, D>(vn, a, table, nxt, col, g);
     attend_pv<T, D>(vc, pf, o);
-#ifdef VK_DECODE_TRACE
-    ++nsteps;
-#endif
     if (!same_piece) {
       const uint32_t seg = pos.seq * a.kvh + pos.kh;
       flush_piece<T, D>(a, pos, piece_first && seg_ends, r + seg, o, m_run, l_run, col, g);
@@ -303,75 +336,139 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, 2) void paged_decode_stream
       load_q<T, D>(qs, a, nxt, lane, col, g);
       piece_first = nxt.seg_first;
     }
-    if (!in_range) {
-      r = sp.W + nc;
-      t_end = min(tn + sp.K, sp.S);
-      asked = false;
-    }
     pos = nxt;
-    t = tn;
+    ++t;
     return true;
   };
   while (step(kA, vA, kB, vB) && step(kB, vB, kA, vA)) {
   }
+  const uint64_t tr1 = __builtin_amdgcn_s_memrealtime();
+  if (lane == 0) {
+    stat[0] = t_end - t_begin;
+    stat[1] = (uint32_t)min(tr1 - tr0, (uint64_t)0xFFFFFFFFu);
+  }
 #ifdef VK_DECODE_TRACE
-  // Per wave: start/end (100 MHz ticks), steps done, last sequence.
+  // Per wave: start/end (100 MHz ticks), steps done, HW_ID | XCC_ID << 32.
   if (lane == 0) {
     uint64_t* tr = a.trace + 4ull * gw;
     tr[0] = tr0;
-    tr[1] = __builtin_amdgcn_s_memrealtime();
-    tr[2] = nsteps;
-    tr[3] = pos.seq;
+    tr[1] = tr1;
+    tr[2] = t_end - t_begin;
+    tr[3] = (uint64_t)__builtin_amdgcn_s_getreg((31 << 11) | 4) |
+            ((uint64_t)__builtin_amdgcn_s_getreg((3 << 11) | 20) << 32);
   }
 #endif
 }
 
-// Combine the pieces of each split (sequence, kv head) segment; reset the
-// chunk counter for the next launch.
+// The next launch's shares from this launch's per-wave timings: groups that
+// ran keep their total and move halfway to their measured rates (steps per
+// tick per wave); groups without steps keep their share.
+__device__ __forceinline__ void update_shares(const AttnArgs& a, uint32_t nwg, uint32_t lane) {
+  float steps[kGroups], ticks[kGroups];
+  const uint32_t W = nwg * kDecodeWavesPerWG;
+  // Wave gw belongs to group (gw / 4) % 8, so the waves lane l reads (l,
+  // l + 64, ...) all belong to group (l / 4) % 8.
+  float st = 0.f, tk = 0.f;
+  for (uint32_t gw = lane; gw < W; gw += 64) {
+    const uint2 v = *(const uint2*)(a.bal + kBalStats + 2 * gw);
+    if (v.x) st += (float)v.x, tk += (float)v.y;
+  }
+  // Sum over the lanes of each group: lanes with equal (l / 4) % 8 are
+  // l ^ 32 and l ^ 1, l ^ 2 (same l / 4).
+  st += __shfl_xor(st, 1), tk += __shfl_xor(tk, 1);
+  st += __shfl_xor(st, 2), tk += __shfl_xor(tk, 2);
+  st += __shfl_xor(st, 32), tk += __shfl_xor(tk, 32);
+#pragma unroll
+  for (uint32_t y = 0; y < kGroups; ++y) {
+    steps[y] = __shfl(st, (int)(y * kDecodeWavesPerWG));
+    ticks[y] = __shfl(tk, (int)(y * kDecodeWavesPerWG));
+  }
+  if (lane != 0) return;
+  float w[kGroups], rate[kGroups], w_tot = 0.f, r_tot = 0.f;
+  load_shares(a, nwg, w);
+  for (uint32_t y = 0; y < kGroups; ++y) {
+    rate[y] = steps[y] > 0.f && ticks[y] > 0.f ? steps[y] / ticks[y] : 0.f;
+    if (rate[y] > 0.f) w_tot += w[y], r_tot += rate[y];
+  }
+  for (uint32_t y = 0; y < kGroups; ++y) {
+    const float nw = rate[y] > 0.f ? 0.5f * w[y] + 0.5f * w_tot * rate[y] / r_tot : w[y];
+    a.bal[y] = __float_as_uint(group_waves(nwg, y) ? fmaxf(nw, 1e-3f) : 0.f);
+  }
+}
+
+// One wave per (sequence, kv head) segment combines the segment's partials
+// if it was split; the extra last wave updates the shares. Lane l owns the
+// E = G*D/64 contiguous outputs from l*E (at most two heads), merged 8 at a
+// time over batches of 8 ranges.
 template <typename T, int D>
-__global__ __launch_bounds__(256) void paged_decode_merge(AttnArgs a) {
-  const uint32_t seq = blockIdx.y, kh = blockIdx.x;
-  const uint32_t* P = a.plan;
-  if (seq == 0 && kh == 0 && threadIdx.x == 0) a.plan[a.batch + 1] = 0;
-  const uint32_t p0 = P[seq], p1 = P[seq + 1];
+__global__ __launch_bounds__(64) void paged_decode_merge(AttnArgs a, uint32_t nwg) {
+  const uint32_t lane = threadIdx.x;
+  const uint32_t nseg = a.batch * a.kvh;
+  if (blockIdx.x == nseg) {
+    update_shares(a, nwg, lane);
+    return;
+  }
+  const uint32_t seq = blockIdx.x / a.kvh, kh = blockIdx.x - seq * a.kvh;
+  const uint32_t p0 = a.plan[seq], p1 = a.plan[seq + 1];
   if (p0 == p1) return;  // not a decode row
-  const Split sp(a, P[a.batch]);
+  uint32_t F[kGroups + 1];
+#pragma unroll
+  for (uint32_t y = 0; y <= kGroups; ++y) F[y] = a.plan[a.batch + 1 + y];
   const uint32_t nst = (p1 - p0) / a.kvh;
   const uint32_t t0 = p0 + kh * nst, t1 = t0 + nst - 1;
-  const uint32_t r0 = sp.range_of(t0), r1 = sp.range_of(t1);
+  const uint32_t r0 = range_of(F, nwg, t0), r1 = range_of(F, nwg, t1);
   if (r0 == r1) return;  // one range held the whole segment and wrote the output
-  const uint32_t G = a.group, seg = seq * a.kvh + kh;
-  const uint32_t q0 = a.cu_q[seq];
-  // One pass per output: an online merge of the pieces, four at a time so
-  // their loads are in flight together.
-  for (uint32_t idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
-    const uint32_t hh = idx / D, d = idx % D;
-    float M = kNegBig, L = 0.f, O = 0.f;
-    for (uint32_t w = r0; w <= r1; w += 4) {
-      float m[4], l[4], o[4];
+  const uint32_t G = a.group, seg = blockIdx.x;
+  const uint32_t E = G * D / 64;
+  const uint32_t e_lane = lane * E;
+  const uint32_t h0 = e_lane / D, h1 = (e_lane + E - 1) / D;
+  T* orow = (T*)a.out + ((uint64_t)a.cu_q[seq] * a.num_heads + kh * G) * D;
+  // Up to 8 ranges per round trip; E is a multiple of 4 for G*D >= 256
+  // (D is 64 or 128), so outputs move as float4.
+  constexpr int R = 8;
+  for (uint32_t j0 = 0; j0 < E; j0 += 8) {
+    const uint32_t n = min(8u, E - j0);
+    float M[8], L[8], O[8];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint32_t ww = min(w + u, r1);
-        const uint64_t sl = (uint64_t)(ww + seg) * G + hh;
-        const float2 x = *(const float2*)(a.ws_ml + sl * 2);
-        m[u] = w + u <= r1 ? x.x : kNegBig;
-        l[u] = x.y;
-        o[u] = a.ws_o[sl * D + d];
-      }
-      const float Mn = fmaxf(fmaxf(M, fmaxf(m[0], m[1])), fmaxf(m[2], m[3]));
-      const float f = fast_exp2(M - Mn);
-      L *= f;
-      O *= f;
+    for (int j = 0; j < 8; ++j) M[j] = kNegBig, L[j] = 0.f, O[j] = 0.f;
+    for (uint32_t w = r0; w <= r1; w += R) {
+      float om[R][8], mm[R][2], ll[R][2];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float e = fast_exp2(m[u] - Mn);
-        L += l[u] * e;
-        O += o[u] * e;
+      for (int u = 0; u < R; ++u) {
+        const bool valid = w + u <= r1 && !range_empty(F, nwg, w + u);
+        const uint64_t sl = (uint64_t)(w + u + seg) * G;
+        const float* po = a.ws_o + sl * D + e_lane + j0;
+        if (valid && n == 8) {
+          const float4 v0 = *(const float4*)po, v1 = *(const float4*)(po + 4);
+          om[u][0] = v0.x, om[u][1] = v0.y, om[u][2] = v0.z, om[u][3] = v0.w;
+          om[u][4] = v1.x, om[u][5] = v1.y, om[u][6] = v1.z, om[u][7] = v1.w;
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) om[u][j] = valid && j < (int)n ? po[j] : 0.f;
+        }
+        const float2 x0 = valid ? *(const float2*)(a.ws_ml + (sl + h0) * 2) : make_float2(kNegBig, 0.f);
+        const float2 x1 = valid ? *(const float2*)(a.ws_ml + (sl + h1) * 2) : make_float2(kNegBig, 0.f);
+        mm[u][0] = x0.x, ll[u][0] = x0.y, mm[u][1] = x1.x, ll[u][1] = x1.y;
       }
-      M = Mn;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int hw = e_lane + j0 + j >= (h0 + 1) * D;  // the lane's second head
+        float Mn = M[j];
+#pragma unroll
+        for (int u = 0; u < R; ++u) Mn = fmaxf(Mn, mm[u][hw]);
+        const float f = fast_exp2(M[j] - Mn);
+        float Lj = L[j] * f, Oj = O[j] * f;
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+          const float e = fast_exp2(mm[u][hw] - Mn);
+          Lj += ll[u][hw] * e;
+          Oj += om[u][j] * e;
+        }
+        M[j] = Mn, L[j] = Lj, O[j] = Oj;
+      }
     }
-    T* orow = (T*)a.out + ((uint64_t)q0 * a.num_heads + kh * G + hh) * D;
-    orow[d] = from_f32<T>(L > 0.f ? O / L : 0.f);
+    for (uint32_t j = 0; j < n; ++j)
+      orow[e_lane + j0 + j] = from_f32<T>(L[j] > 0.f ? O[j] / L[j] : 0.f);
   }
 }
 
@@ -384,50 +481,28 @@ uint32_t decode_num_waves() {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus <= 0)
       cus = 256;
-    cache[dev] = (uint32_t)cus * 2 * kDecodeWavesPerWG;  // 2 workgroups of 4 waves per CU
+    cache[dev] = (uint32_t)cus * kDecodeWGsPerCU * kDecodeWavesPerWG;
   }
   return cache[dev];
 }
 
-// Scheduling knobs: static fraction (percent) and chunk size (steps).
-// VAPI_KV_DECODE_STATIC_PCT / VAPI_KV_DECODE_CHUNK override them, for tuning.
-static uint32_t env_u32(const char* name, uint32_t def, uint32_t lo, uint32_t hi) {
-  const char* e = getenv(name);
-  if (!e) return def;
-  const long v = atol(e);
-  return (v < (long)lo || v > (long)hi) ? def : (uint32_t)v;
-}
-// Default: all static. Measured on config 2 (64 sequences, 2k median
-// context), chunked tails cost more in piece switches and merge work than
-// they recover in balance (150 us all-static vs 158-182 us at 70-30% static).
-static uint32_t static_pct() {
-  static const uint32_t v = env_u32("VAPI_KV_DECODE_STATIC_PCT", 100, 0, 100);
-  return v;
-}
-static uint32_t chunk_steps() {
-  static const uint32_t v = env_u32("VAPI_KV_DECODE_CHUNK", 8, 1, 1024);
-  return v;
-}
-
 static size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Slots: static ranges (W) + chunks (upper bound from max_seqlen_k) + one per
-// segment.
-static size_t decode_slots(uint32_t b, uint32_t kvh, uint32_t max_k, uint32_t num_waves) {
-  const uint64_t s_max = (uint64_t)b * kvh * ((max_k + 31) / 32 + 1);
-  const uint64_t chunks = (s_max * (100 - static_pct()) / 100 + chunk_steps()) / chunk_steps() + 1;
-  return (size_t)num_waves + chunks + (size_t)b * kvh;
-}
-
+// Workspace: the balance block (shares and per-wave timings; the shares
+// carry over between launches, so the block leads the workspace whatever
+// the batch), the plan, and the partials: one slot per range plus one per
+// segment. Only the shares persist; everything else is rewritten by each
+// launch before it is read. A zeroed workspace starts from uniform shares.
 struct DecodeWs {
-  size_t plan, ml, o, trace, total;
+  size_t bal, plan, ml, o, trace, total;
 };
 static DecodeWs decode_ws(uint32_t b, uint32_t kvh, uint32_t group, uint32_t head_dim,
-                          uint32_t max_k, uint32_t num_waves) {
-  const size_t slots = decode_slots(b, kvh, max_k, num_waves);
+                          uint32_t num_waves) {
+  const size_t slots = (size_t)num_waves + (size_t)b * kvh;
   DecodeWs w;
-  w.plan = 0;
-  w.ml = up256((b + 2) * sizeof(uint32_t));
+  w.bal = 0;
+  w.plan = up256((kBalStats + 2 * (size_t)num_waves) * sizeof(uint32_t));
+  w.ml = w.plan + up256((b + 2 + kGroups) * sizeof(uint32_t));
   w.o = w.ml + up256(slots * group * 2 * sizeof(float));
   w.trace = w.o + up256(slots * group * head_dim * sizeof(float));
   w.total = w.trace;
@@ -439,16 +514,16 @@ static DecodeWs decode_ws(uint32_t b, uint32_t kvh, uint32_t group, uint32_t hea
 
 size_t decode_workspace_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t head_dim,
                               uint32_t max_k, uint32_t num_waves) {
-  return decode_ws(std::min(batch, kMaxPlanSeqs), kvh, group, head_dim, max_k, num_waves).total;
+  (void)max_k;
+  return decode_ws(std::min(batch, kMaxPlanSeqs), kvh, group, head_dim, num_waves).total;
 }
 
 void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t max_k, bool bf16,
                    hipStream_t s) {
+  (void)max_k;
   const uint32_t W = a.num_waves;
+  const uint32_t nwg = W / kDecodeWavesPerWG;
   const uint32_t total = a.batch;
-  a.static_num = static_pct();
-  a.static_den = 100;
-  a.chunk_steps = chunk_steps();
   for (uint32_t b0 = 0; b0 < total; b0 += kMaxPlanSeqs) {
     const uint32_t nb = std::min(kMaxPlanSeqs, total - b0);
     AttnArgs c = a;
@@ -456,22 +531,21 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t max_
     c.cu_q = a.cu_q + b0;
     c.cu_k = a.cu_k + b0;
     c.table = a.table + (uint64_t)b0 * a.max_blocks;
-    const DecodeWs w = decode_ws(nb, a.kvh, a.group, head_dim, max_k, W);
+    const DecodeWs w = decode_ws(nb, a.kvh, a.group, head_dim, W);
     char* ws = (char*)workspace;
+    c.bal = (uint32_t*)(ws + w.bal);
     c.plan = (uint32_t*)(ws + w.plan);
     c.ws_ml = (float*)(ws + w.ml);
     c.ws_o = (float*)(ws + w.o);
 #ifdef VK_DECODE_TRACE
     c.trace = (uint64_t*)(ws + w.trace);
 #endif
-    const dim3 grid(W / kDecodeWavesPerWG), block(64 * kDecodeWavesPerWG);
-    const dim3 mgrid(a.kvh, nb);
-#define VK_DEC(T, DD)                                                                        \
-  do {                                                                                       \
-    hipLaunchKernelGGL((paged_decode_stream<T, DD>), grid, block, (nb + 1) * sizeof(uint32_t), \
-                       s, c, c.cu_q, c.cu_k,                                                 \
-                       c.table);                                                             \
-    hipLaunchKernelGGL((paged_decode_merge<T, DD>), mgrid, dim3(256), 0, s, c);              \
+#define VK_DEC(T, DD)                                                                           \
+  do {                                                                                          \
+    hipLaunchKernelGGL((paged_decode_stream<T, DD>), dim3(nwg), dim3(64 * kDecodeWavesPerWG), \
+                       (nb + 1) * sizeof(uint32_t), s, c, c.cu_q, c.cu_k, c.table);            \
+    hipLaunchKernelGGL((paged_decode_merge<T, DD>), dim3(nb * a.kvh + 1), dim3(64), 0, s, c,   \
+                       nwg);                                                                    \
   } while (0)
     if (bf16) {
       if (head_dim == 128) VK_DEC(bf16_t, 128);
