@@ -44,22 +44,43 @@ def log(msg):
 
 
 def timed(fn, steps, warmup):
-    """Run fn warmup times, then time `steps` runs with one pair of events per
-    run on the current stream. Returns (mean ms per run, total ms)."""
+    """Run fn warmup times, then time `steps` back-to-back runs between one
+    pair of HIP events on the current stream (the stream every kernel here
+    launches on), synchronized on both sides. Returns (ms per run, wall ms
+    for the timed region)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    for i in range(steps):
-        starts[i].record()
+    start.record()
+    for _ in range(steps):
         fn()
-        ends[i].record()
+    end.record()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3
-    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    return float(np.mean(per)), wall, per
+    return start.elapsed_time(end) / steps, wall
+
+
+def timed_graph(fn, steps, warmup, per_graph=20):
+    """Capture per_graph back-to-back calls of fn into one HIP graph, replay
+    it warmup times, then time ceil(steps / per_graph) replays between one
+    pair of events. Returns ms per call."""
+    fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for _ in range(per_graph):
+                fn()
+    torch.cuda.current_stream().wait_stream(side)
+    for _ in range(max(warmup // per_graph, 1)):
+        graph.replay()
+    reps = max(-(-steps // per_graph), 1)
+    ms, _ = timed(graph.replay, reps, 1)
+    return ms / per_graph
 
 
 # ---- config 2: decode (headline) ---------------------------------------------
@@ -92,7 +113,7 @@ def setup_decode():
 
 def bench_decode(steps, warmup):
     d = setup_decode()
-    ms, wall, _ = timed(d["step"], steps, warmup)
+    ms, wall = timed(d["step"], steps, warmup)
     gbs = d["alg_bytes"] / (ms * 1e-3) / 1e9
     log(f"decode cfg2: sum_len {d['sum_len']}, {d['alg_bytes'] / 1e6:.1f} MB/step, "
         f"{ms * 1e3:.1f} us/step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of 8 TB/s)")
@@ -110,12 +131,24 @@ def bench_append(steps, warmup):
     k = torch.randn(w.n_tokens, 8, 128, generator=g, device=DEV).to(torch.bfloat16)
     v = torch.randn(w.n_tokens, 8, 128, generator=g, device=DEV).to(torch.bfloat16)
     idx = scatter_index(w.slots, DEV)
-    ms, _, _ = timed(lambda: write_rows_indexed(cache, 0, k, v, idx), steps, warmup)
+
+    def append():
+        write_rows_indexed(cache, 0, k, v, idx)
+
+    # Host-launched calls: one Python + ctypes call per append (the host
+    # overhead is about the kernel's own duration at this size).
+    ms_host, _ = timed(append, steps, warmup)
+    # The same appends captured in one HIP graph and replayed, as a serving
+    # step would issue its per-layer appends: per-append device time.
+    ms = timed_graph(append, steps, warmup)
     alg = w.n_valid * 2 * 8 * 128 * 2 * 2 + w.n_tokens * 4
     gbs = alg / (ms * 1e-3) / 1e9
-    log(f"append cfg1: {alg / 1e6:.1f} MB, {ms * 1e3:.1f} us, {gbs:.0f} GB/s")
+    log(f"append cfg1: {alg / 1e6:.1f} MB, {ms * 1e3:.2f} us/append in a graph "
+        f"({gbs:.0f} GB/s), {ms_host * 1e3:.1f} us/append host-launched")
     del cache
-    return dict(us=ms * 1e3, gbs=gbs, frac=gbs / HBM_PEAK_GBS, bytes=alg)
+    return dict(us=ms * 1e3, gbs=gbs, frac=gbs / HBM_PEAK_GBS, bytes=alg,
+                us_host_launched=ms_host * 1e3,
+                gbs_host_launched=alg / (ms_host * 1e-3) / 1e9)
 
 
 # ---- config 3: chunked prefill ----------------------------------------------------
@@ -131,7 +164,7 @@ def bench_prefill(steps, warmup):
                          max_seqlen_k=w.len_k)
     prep = PreparedAttention.from_batch(batch, DEV)
     out = torch.empty_like(q)
-    ms, _, _ = timed(lambda: paged_attention_prepared(q, cache, 0, prep, 128 ** -0.5, out=out),
+    ms, _ = timed(lambda: paged_attention_prepared(q, cache, 0, prep, 128 ** -0.5, out=out),
                      steps, warmup)
     tf = w.flops() / (ms * 1e-3) / 1e12
     log(f"prefill cfg3: {w.flops() / 1e12:.3f} TFLOP, {ms:.2f} ms, {tf:.1f} TFLOP/s "
@@ -157,7 +190,7 @@ def bench_blocks(steps, warmup, decode):
         check(lib().vapi_kv_copy_blocks(cache.pool, pairs_dev.data_ptr(), w.pairs.shape[0],
                                         stream_handle()))
 
-    ms, _, _ = timed(copy, steps, warmup)
+    ms, _ = timed(copy, steps, warmup)
     alg = w.pairs.shape[0] * bb * 2
     copy_gbs = alg / (ms * 1e-3) / 1e9
     log(f"copy cfg4a: {alg / 1e9:.2f} GB moved, {ms:.3f} ms, {copy_gbs:.0f} GB/s")
@@ -189,7 +222,7 @@ def bench_blocks(steps, warmup, decode):
     for a, b in ((0, 0), (n // 2, n // 2), (n - 1, n - 1)):
         swap_ok &= be.export_block(int(w.swap_ids[a])) == be.export_block(int(w.swap_in_ids[b]))
     # Overlap: swap-out on the side stream while decode steps run on the main stream.
-    dec_alone, _, _ = timed(decode["step"], 10, 2)
+    dec_alone, _ = timed(decode["step"], 10, 2)
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record(side)
@@ -238,7 +271,7 @@ def bench_copy(steps, warmup):
     workload.fill_normal(cache._slab, workload.seed_for(4))
     pairs = w.pairs.tolist()
     be = KvBlockBackend(cache)
-    ms, _, _ = timed(lambda: be.copy_blocks(pairs), steps, warmup)
+    ms, _ = timed(lambda: be.copy_blocks(pairs), steps, warmup)
     alg = len(pairs) * be.block_bytes() * 2
     log(f"copy cfg4a: {alg / 1e9:.2f} GB moved, {ms:.3f} ms, {alg / (ms * 1e-3) / 1e9:.0f} GB/s")
 
@@ -251,7 +284,7 @@ def _copy_on(stream, dst, src):
 def hbm_probe():
     a = torch.empty(4 << 30, dtype=torch.uint8, device=DEV)
     b = torch.empty_like(a)
-    ms, _, _ = timed(lambda: b.copy_(a), 10, 3)
+    ms, _ = timed(lambda: b.copy_(a), 10, 3)
     return 2 * a.numel() / (ms * 1e-3) / 1e9
 
 
@@ -289,7 +322,7 @@ def cpu_baseline(decode, budget_s=12.0):
 
 
 def load_traffic():
-    p = ROOT / "profiles" / "decode_cfg2_traffic.json"
+    p = ROOT / "profiles" / "paged_decode_config2_traffic.json"
     if p.exists():
         try:
             return json.loads(p.read_text())
@@ -366,8 +399,8 @@ def main():
                    "algorithmic_bytes_per_step": alg, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": traffic.get("bytes_per_launch") if traffic else None,
-                     "kernel": "paged_decode_mfma + paged_decode_reduce (one call)"},
+                     "traffic": traffic.get("bytes_per_call") if traffic else None,
+                     "kernel": "paged_decode_stream + paged_decode_merge (one vapi_paged_attention call)"},
         "cpu_baseline": cpu,
         "kv_append_gbs": round(extras["append_cfg1"]["gbs"], 1) if "append_cfg1" in extras else None,
         "extras": extras,
