@@ -252,3 +252,39 @@ def test_the_native_cache_object_mirrors_the_backend_block_methods():
         assert bytes(buf2) == bytes(buf)
     finally:
         L.vapi_cache_free(h)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_a_fork_executed_through_copy_blocks_gives_every_child_the_parent_kv(layout):
+    """a12 + a13 end to end: the parent's prompt K/V is appended, fork's copy
+    pairs run through copy_blocks (every layer, K and V, one launch), and each
+    child's table gathers exactly the parent's rows, bit for bit; a write to
+    one child's private block leaves the parent and the sibling untouched."""
+    from vapi_amd.backend import fork_copy_pairs
+    L, nb, bs, kvh, d = 3, 64, 16, 4, 64
+    cache = PagedKvCache(L, nb, bs, kvh, d, torch.bfloat16, layout)
+    be = KvBlockBackend(cache)
+    computed = 43  # two full blocks and 11 rows of a third
+    parent = [17, 5, 40]
+    slots = [parent[p // bs] * bs + p % bs for p in range(computed)]
+    for layer in range(L):
+        k = torch.randn(computed, kvh, d, device=DEV).to(torch.bfloat16)
+        v = torch.randn(computed, kvh, d, device=DEV).to(torch.bfloat16)
+        write_kv_to_cache(cache, layer, k, v, slots)
+    free = iter([50, 51, 52])
+    children, pairs = fork_copy_pairs(parent, computed, bs, extra=3, allocate=lambda: next(free))
+    be.copy_blocks(pairs)
+    for layer in range(L):
+        for which in ("k", "v"):
+            want = as_np(gather_kv(cache, layer, parent, computed, which))
+            for child in children:
+                assert np.array_equal(as_np(gather_kv(cache, layer, child, computed, which)), want)
+    # The children diverge: child 0 rewrites position 40 (its private copy of
+    # the partial block); the parent and the sibling keep theirs.
+    before = [as_np(gather_kv(cache, 0, t, computed, "k")) for t in (parent, children[1])]
+    row = torch.full((1, kvh, d), 3.0, device=DEV).to(torch.bfloat16)
+    write_kv_to_cache(cache, 0, row, row, [children[0][2] * bs + 40 % bs])
+    after = [as_np(gather_kv(cache, 0, t, computed, "k")) for t in (parent, children[1])]
+    assert all(np.array_equal(a, b) for a, b in zip(before, after))
+    mine = gather_kv(cache, 0, children[0], computed, "k")
+    assert torch.equal(mine[40], row[0]) and not torch.equal(mine[40], gather_kv(cache, 0, parent, computed, "k")[40])
