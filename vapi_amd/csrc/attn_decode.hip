@@ -40,6 +40,10 @@ namespace vk {
 constexpr int kDecodeWavesPerWG = 4;
 constexpr int kDecodeWGsPerCU = 1;
 constexpr uint32_t kGroups = 8;          // XCDs; workgroup b runs on XCD b % 8
+#ifndef VK_MERGE_WAVES
+#define VK_MERGE_WAVES 4
+#endif
+constexpr uint32_t kMergeWaves = VK_MERGE_WAVES;  // merge: segments (waves) per workgroup
 constexpr uint32_t kMaxPlanSeqs = 4096;  // sequences per launch (host chunks beyond)
 
 // Balance block (u32 words, kept across launches at the start of the
@@ -401,14 +405,17 @@ __device__ __forceinline__ void update_shares(const AttnArgs& a, uint32_t nwg, u
 // E = G*D/64 contiguous outputs from l*E (at most two heads), merged 8 at a
 // time over batches of 8 ranges.
 template <typename T, int D>
-__global__ __launch_bounds__(64) void paged_decode_merge(AttnArgs a, uint32_t nwg) {
-  const uint32_t lane = threadIdx.x;
+__global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_merge(AttnArgs a, uint32_t nwg) {
+  const uint32_t lane = threadIdx.x & 63;
   const uint32_t nseg = a.batch * a.kvh;
-  if (blockIdx.x == nseg) {
+  const uint32_t segi =
+      blockIdx.x * kMergeWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (segi == nseg) {
     update_shares(a, nwg, lane);
     return;
   }
-  const uint32_t seq = blockIdx.x / a.kvh, kh = blockIdx.x - seq * a.kvh;
+  if (segi > nseg) return;
+  const uint32_t seq = segi / a.kvh, kh = segi - seq * a.kvh;
   const uint32_t p0 = a.plan[seq], p1 = a.plan[seq + 1];
   if (p0 == p1) return;  // not a decode row
   uint32_t F[kGroups + 1];
@@ -418,7 +425,7 @@ __global__ __launch_bounds__(64) void paged_decode_merge(AttnArgs a, uint32_t nw
   const uint32_t t0 = p0 + kh * nst, t1 = t0 + nst - 1;
   const uint32_t r0 = range_of(F, nwg, t0), r1 = range_of(F, nwg, t1);
   if (r0 == r1) return;  // one range held the whole segment and wrote the output
-  const uint32_t G = a.group, seg = blockIdx.x;
+  const uint32_t G = a.group, seg = segi;
   const uint32_t E = G * D / 64;
   const uint32_t e_lane = lane * E;
   const uint32_t h0 = e_lane / D, h1 = (e_lane + E - 1) / D;
@@ -544,7 +551,8 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t max_
   do {                                                                                          \
     hipLaunchKernelGGL((paged_decode_stream<T, DD>), dim3(nwg), dim3(64 * kDecodeWavesPerWG), \
                        (nb + 1) * sizeof(uint32_t), s, c, c.cu_q, c.cu_k, c.table);            \
-    hipLaunchKernelGGL((paged_decode_merge<T, DD>), dim3(nb * a.kvh + 1), dim3(64), 0, s, c,   \
+    hipLaunchKernelGGL((paged_decode_merge<T, DD>), dim3((nb * a.kvh + kMergeWaves) / kMergeWaves), \
+                       dim3(64 * kMergeWaves), 0, s, c,                                         \
                        nwg);                                                                    \
   } while (0)
     if (bf16) {
