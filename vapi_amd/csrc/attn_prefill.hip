@@ -71,31 +71,39 @@ __device__ __forceinline__ void pf_load(PfStage<D>& st, const uint32_t* __restri
                                         const T* kb, const T* vb, const AttnArgs& a, int32_t s0,
                                         int32_t last, uint32_t tid) {
   constexpr uint32_t CPK = D / 8;  // 16-byte chunks per key row
+  // The step's two 16-key tiles (a tile past the last key re-reads the
+  // tile holding it): both block-table entries are read once, back to back,
+  // for K and V alike, through the scalar cache (the table is never written
+  // by a kernel).
+  using ConstU32 = const __attribute__((address_space(4))) uint32_t;
+  const int32_t ts0 = min(s0, last & ~15), ts1 = min(s0 + 16, last & ~15);
+  const uint32_t blk0 = ((ConstU32*)tab)[(uint32_t)ts0 >> a.bs_shift];
+  const uint32_t blk1 = ((ConstU32*)tab)[(uint32_t)ts1 >> a.bs_shift];
+  const uint64_t off0 = (uint64_t)blk0 * a.blk_e + (uint64_t)((uint32_t)ts0 & (a.block_size - 1)) * a.tok_e;
+  const uint64_t off1 = (uint64_t)blk1 * a.blk_e + (uint64_t)((uint32_t)ts1 & (a.block_size - 1)) * a.tok_e;
 #pragma unroll
   for (int j = 0; j < D / 64; ++j) {
     const uint32_t ci = tid + kPfThreads * j;
     const uint32_t key = ci / CPK, part = ci % CPK;
-    const uint32_t tile = __builtin_amdgcn_readfirstlane(key >> 4);
-    const int32_t ts = min(s0 + 16 * (int32_t)tile, last & ~15);
-    const char* base = tile_base(tab, kb, a, ts);
-    const uint32_t kk = (uint32_t)min((int32_t)(key & 15), last - ts);
-    const uint4 x = *(const uint4*)(base + (kk * a.tok_e + 8 * part) * sizeof(T));
+    // Uniform per wave: the 64 lanes cover 64 / CPK keys of one tile.
+    const bool second = __builtin_amdgcn_readfirstlane(key >> 4) != 0;
+    const T* base = kb + (second ? off1 : off0);
+    const int32_t lim = last - (second ? ts1 : ts0);
+    const uint32_t kk = (uint32_t)min((int32_t)(key & 15), lim);
+    const uint4 x = *(const uint4*)(base + kk * a.tok_e + 8 * part);
     if (j == 0) st.k0 = x; else st.k1 = x;
   }
   if (tid < 2 * D) {
     const uint32_t kp = vkp(tid, CPK), c = vchunk(tid, CPK);
-    // Key pairs 0..7 sit in the step's first 16-key tile, 8..15 in the
-    // second; both tiles' blocks are scalar lookups, selected per lane.
-    const int32_t ts0 = min(s0, last & ~15), ts1 = min(s0 + 16, last & ~15);
-    const char* base0 = tile_base(tab, vb, a, ts0);
-    const char* base1 = tile_base(tab, vb, a, ts1);
+    // Key pairs 0..7 sit in the first tile, 8..15 in the second: selected
+    // per lane.
     const bool second = kp >= 8;
-    const char* base = second ? base1 : base0;
+    const T* base = vb + (second ? off1 : off0);
     const int32_t lim = last - (second ? ts1 : ts0);
     const uint32_t k0 = (uint32_t)min((int32_t)((2 * kp) & 15), lim);
     const uint32_t k1 = (uint32_t)min((int32_t)((2 * kp + 1) & 15), lim);
-    st.v0 = *(const uint4*)(base + (k0 * a.tok_e + 8 * c) * sizeof(T));
-    st.v1 = *(const uint4*)(base + (k1 * a.tok_e + 8 * c) * sizeof(T));
+    st.v0 = *(const uint4*)(base + k0 * a.tok_e + 8 * c);
+    st.v1 = *(const uint4*)(base + k1 * a.tok_e + 8 * c);
   }
 }
 
