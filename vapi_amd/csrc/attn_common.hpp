@@ -267,12 +267,15 @@ __device__ __forceinline__ uint4 attend_qk(const KTile<D>& kt, const uint4 (&qf)
 #pragma unroll
     for (int i = 0; i < 4; ++i) s[4 * tt + i] = visible(tt, i) ? acc[i] : -INFINITY;
   }
-  float mx = max3_nc(max3_nc(s[0], s[1], s[2]), max3_nc(s[3], s[4], s[5]), max_nc(s[6], s[7]));
-  mx = wave_max_g(mx) * scale_log2;
-  // Rescale only when some row's max grew by more than 2^kRescaleSlack: the
-  // result is the same softmax, and P stays below 2^kRescaleSlack.
+  // This lane's max over its 8 keys. m_run is the same in the four lane
+  // groups that hold a row, so comparing each lane's own max with it finds
+  // every row whose max grew by more than 2^kRescaleSlack; only then is the
+  // row max reduced across the groups and the row rescaled (the same
+  // softmax; P stays below 2^kRescaleSlack).
+  const float mx = max3_nc(max3_nc(s[0], s[1], s[2]), max3_nc(s[3], s[4], s[5]),
+                           max_nc(s[6], s[7])) * scale_log2;
   if (__any(mx > m_run + kRescaleSlack)) {
-    const float m_new = fmaxf(m_run, mx);
+    const float m_new = fmaxf(m_run, wave_max_g(mx));
     const float alpha = fast_exp2(m_run - m_new);
     m_run = m_new;
     l_run *= alpha;
