@@ -21,8 +21,14 @@
 
 namespace vk {
 
-constexpr int kPfWaves = 4;
+#ifndef VK_PF_WAVES
+#define VK_PF_WAVES 4
+#endif
+constexpr int kPfWaves = VK_PF_WAVES;
 constexpr int kPfThreads = 64 * kPfWaves;
+// 16-byte K chunks of one 32-key step per thread.
+template <int D>
+constexpr int kKIter = (32 * D / 8 + kPfThreads - 1) / kPfThreads;
 constexpr int kKPad = 8;  // elements of padding per K row in LDS
 constexpr int kVPad = 8;  // elements of padding per V^T row in LDS
 
@@ -82,8 +88,8 @@ __device__ __forceinline__ void pf_load(PfStage<D>& st, const uint32_t* __restri
   const uint64_t off0 = (uint64_t)blk0 * a.blk_e + (uint64_t)((uint32_t)ts0 & (a.block_size - 1)) * a.tok_e;
   const uint64_t off1 = (uint64_t)blk1 * a.blk_e + (uint64_t)((uint32_t)ts1 & (a.block_size - 1)) * a.tok_e;
 #pragma unroll
-  for (int j = 0; j < D / 64; ++j) {
-    const uint32_t ci = tid + kPfThreads * j;
+  for (int j = 0; j < kKIter<D>; ++j) {
+    const uint32_t ci = min(tid + kPfThreads * j, 32 * CPK - 1);
     const uint32_t key = ci / CPK, part = ci % CPK;
     // Uniform per wave: the 64 lanes cover 64 / CPK keys of one tile.
     const bool second = __builtin_amdgcn_readfirstlane(key >> 4) != 0;
@@ -112,9 +118,9 @@ __device__ __forceinline__ void pf_store(PfSmem<D>& sm, int buf, const PfStage<D
                                          uint32_t tid) {
   constexpr uint32_t CPK = D / 8;
 #pragma unroll
-  for (int j = 0; j < D / 64; ++j) {
+  for (int j = 0; j < kKIter<D>; ++j) {
     const uint32_t ci = tid + kPfThreads * j;
-    *(uint4*)&sm.k[buf][ci / CPK][8 * (ci % CPK)] = j == 0 ? st.k0 : st.k1;
+    if (ci < 32 * CPK) *(uint4*)&sm.k[buf][ci / CPK][8 * (ci % CPK)] = j == 0 ? st.k0 : st.k1;
   }
   if (tid < 2 * D) {
     const uint32_t kp = vkp(tid, CPK), c = vchunk(tid, CPK);
