@@ -173,6 +173,8 @@ CASES = [
     (torch.bfloat16, 64, 4, 64, 32, [2, 1], [70, 64], 9, "NHD"),
     (torch.float32, 16, 8, 128, 16, [1, 1, 9], [64, 512, 200], None, "HND"),
     (torch.float32, 6, 2, 80, 8, [3, 1], [10, 50], 4, "NHD"),
+    # Sequences with no new query rows (attention.rs:104-106 skips them).
+    (torch.bfloat16, 32, 8, 128, 16, [0, 1, 3, 0, 1], [5, 100, 40, 7, 1], None, "HND"),
 ]
 
 
@@ -337,3 +339,16 @@ def test_a_workspace_reused_across_batches_and_launches_stays_correct():
 def paged_ws_bytes(cache, batch):
     from vapi_amd.attention import workspace_bytes
     return workspace_bytes(cache, batch.batch_size(), 32, 1, batch.max_seqlen_k)
+
+
+def test_more_decode_rows_than_one_launch_plans_for():
+    """5,000 decode rows: the host splits the batch into launches of at most
+    4,096 sequences that share one workspace; every row against the oracle."""
+    rng = np.random.default_rng(5000)
+    lens_k = rng.integers(1, 80, size=5000).tolist()
+    nb = sum(-(-lk // 16) for lk in lens_k)
+    c, q, batch = random_case(rng, torch.bfloat16, 8, 2, 128, 16, [1] * 5000, lens_k, "HND")
+    assert c.num_blocks >= nb
+    want = oracle_out(q, c, 0, batch, 128 ** -0.5)
+    got = paged_attention(q, c, 0, batch, 128 ** -0.5)
+    assert max_abs(got, want) <= 2e-2 * float(want.abs().max())
