@@ -247,6 +247,55 @@ __device__ __forceinline__ void load_kv_step(KVStep<D>& st, const uint32_t* __re
   load_v<T, D>(st.v, tab, vb, a, s0, last, col, g);
 }
 
+// Scores S^T = K Q^T of a 32-key step for 16 query rows: acc[tt][i] is key
+// 16 tt + 4 g + i of this lane's row.
+template <typename T, int D>
+__device__ __forceinline__ void qk_scores(const KTile<D>& kt, const uint4 (&qf)[D / 32],
+                                          floatx4 (&acc)[2]) {
+  constexpr int KC = D / 32;
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    acc[tt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < KC; ++c) acc[tt] = mfma16x16x32<T>(kt.k[tt][c], qf[c], acc[tt]);
+  }
+}
+
+// Lazy rescale of 16 rows given each lane's max mx over its keys (scaled
+// log2 units): rows whose max grew by more than 2^kRescaleSlack take the row
+// max across the four lane groups and rescale O and l to it.
+template <int D>
+__device__ __forceinline__ void rescale_rows(float mx, floatx4 (&o)[D / 16], float& m_run,
+                                             float& l_run) {
+  constexpr int DPL = D / 16;
+  if (__any(mx > m_run + kRescaleSlack)) {
+    const float m_new = fmaxf(m_run, wave_max_g(mx));
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    l_run *= alpha;
+#pragma unroll
+    for (int k = 0; k < DPL; ++k)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[k][i] *= alpha;
+  }
+}
+
+// P = exp2(s * c - m) for a lane's 8 scores, added to l and packed in the
+// input dtype.
+template <typename T>
+__device__ __forceinline__ uint4 exp_pack(const float (&s)[8], float m_run, float& l_run,
+                                          float scale_log2) {
+  float p[8];
+  float ps = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    p[j] = fast_exp2(__builtin_fmaf(s[j], scale_log2, -m_run));
+    ps += p[j];
+  }
+  l_run += ps;
+  return pack8<T>(p);
+}
+
 // First half of an online-softmax step for 16 query rows (the MFMA
 // columns): scores S^T = K Q^T, lazy rescale of the running max (and of O),
 // returns P packed in the input dtype as the PV A operand.

@@ -249,19 +249,42 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
       for (int c = 0; c < KC; ++c)
         kt.k[tt][c] = *(const uint4*)&sm.k[buf][16 * tt + col][32 * c + 8 * g];
     // Every row tile runs every step: a tile whose rows see no key of the
-    // step gets P = 0 (all scores -inf).
-    uint4 pf[kPfRT];
+    // step gets P = 0 (all scores -inf). The scores of all row tiles are
+    // issued first (independent MFMA chains), then their maxima share one
+    // rescale branch, so no branch sits between a tile's MFMAs and the
+    // next tile's.
+    float sc[kPfRT][8];
+    {
+      floatx4 acc[kPfRT][2];
 #pragma unroll
-    for (int t = 0; t < kPfRT; ++t) {
-      if constexpr (decltype(masked)::value) {
+      for (int t = 0; t < kPfRT; ++t) qk_scores<T, D>(kt, qf[t], acc[t]);
+#pragma unroll
+      for (int t = 0; t < kPfRT; ++t) {
         const uint32_t base = (uint32_t)(s0 + 4 * (int32_t)g - lo[t]), n = (uint32_t)cnt[t];
-        pf[t] = attend_qk<T, D>(kt, qf[t], o[t], m_run[t], l_run[t], a.scale_log2, g,
-                                [&](int tt, int i) { return base + 16 * tt + i < n; });
-      } else {
-        pf[t] = attend_qk<T, D>(kt, qf[t], o[t], m_run[t], l_run[t], a.scale_log2, g,
-                                [](int, int) { return true; });
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool vis = !decltype(masked)::value || base + 16 * tt + i < n;
+            sc[t][4 * tt + i] = vis ? acc[t][tt][i] : -INFINITY;
+          }
       }
     }
+    float mx[kPfRT];
+    bool grow = false;
+#pragma unroll
+    for (int t = 0; t < kPfRT; ++t) {
+      mx[t] = max3_nc(max3_nc(sc[t][0], sc[t][1], sc[t][2]), max3_nc(sc[t][3], sc[t][4], sc[t][5]),
+                      max_nc(sc[t][6], sc[t][7])) * a.scale_log2;
+      grow |= mx[t] > m_run[t] + kRescaleSlack;
+    }
+    if (__any(grow)) {
+#pragma unroll
+      for (int t = 0; t < kPfRT; ++t) rescale_rows<D>(mx[t], o[t], m_run[t], l_run[t]);
+    }
+    uint4 pf[kPfRT];
+#pragma unroll
+    for (int t = 0; t < kPfRT; ++t) pf[t] = exp_pack<T>(sc[t], m_run[t], l_run[t], a.scale_log2);
 #pragma unroll
     for (int k = 0; k < DPL; ++k) {
       const uint4 vf = *(const uint4*)&sm.vt[buf][vrow<D>(DPL * col + k)][8 * g];
