@@ -79,7 +79,7 @@ int vapi_paged_attention(const vapi_kv_pool* pool, uint32_t layer,
   a.cu_q = cu_seqlens_q;
   a.cu_k = cu_seqlens_k;
   a.table = block_table;
-  a.plan = nullptr;
+  a.seg_ranges = nullptr;
   a.ws_ml = nullptr;
   a.ws_o = nullptr;
   a.bal = nullptr;

@@ -45,7 +45,7 @@ struct AttnArgs {
   const uint32_t* cu_q;
   const uint32_t* cu_k;
   const uint32_t* table;
-  uint32_t* plan;      // decode: step prefix sums (batch + 1), then group bounds (9)
+  uint32_t* seg_ranges;  // decode: first and last range of each (sequence, kv head) segment
   float* ws_ml;        // decode: partial (m, l) per slot and head
   float* ws_o;         // decode: partial outputs per slot and head
   uint32_t* bal;       // decode: XCD shares and per-wave timings, kept across launches

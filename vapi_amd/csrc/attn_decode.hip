@@ -22,7 +22,10 @@
 // whole segment writes the normalised output; the first and last piece of a
 // slice may be partial and write (m, l, o) to slot range + segment (ranges
 // and segments are both numbered in step order, so slots are unique), and
-// paged_decode_merge, one wave per split segment, combines them. The merge
+// paged_decode_merge, one wave per split segment, combines them. Each
+// segment's first and last range are recorded by the waves holding its first
+// and last step, and a wave whose slice is empty marks its slot empty, so
+// the merge needs no step arithmetic. The merge
 // kernel's extra workgroup turns the stream's per-wave timings into the
 // next launch's shares. (Merging inside the stream, by the wave that
 // completes a segment, needs write-through stores, L2-bypassing loads and
@@ -102,26 +105,6 @@ __device__ __forceinline__ void group_bounds(const float (&w)[kGroups], uint32_t
     F[x] = max(F[x - 1], f);
   }
   F[kGroups] = S;
-}
-
-// Whether range r (wave slice) holds no steps: empty slices exist whenever a
-// group has more waves than steps, and their partial slots hold stale data.
-__device__ __forceinline__ bool range_empty(const uint32_t (&F)[kGroups + 1], uint32_t nwg,
-                                            uint32_t r) {
-  uint32_t x = 0, off = 0;
-  while (x + 1 < kGroups && off + group_waves(nwg, x) <= r) off += group_waves(nwg, x++);
-  const uint64_t j = r - off, len = F[x + 1] - F[x], nw = group_waves(nwg, x);
-  return j * len / nw == (j + 1) * len / nw;
-}
-
-// Range (wave slice) holding step t, given the group bounds.
-__device__ __forceinline__ uint32_t range_of(const uint32_t (&F)[kGroups + 1], uint32_t nwg,
-                                             uint32_t t) {
-  uint32_t x = 0;
-  while (x + 1 < kGroups && F[x + 1] <= t) ++x;
-  const uint32_t len = F[x + 1] - F[x], nw = group_waves(nwg, x);
-  const uint32_t j = (uint32_t)((((uint64_t)(t - F[x]) + 1) * nw - 1) / len);
-  return group_offset(nwg, x) + j;
 }
 
 // Where global step t lives.
@@ -262,11 +245,6 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
   load_shares(a, nwg, w);
   uint32_t F[kGroups + 1];
   group_bounds(w, S, F);
-  if (blockIdx.x == 0) {  // the merge kernel reads the plan back
-    for (uint32_t s = tid; s <= B; s += 64 * kDecodeWavesPerWG) a.plan[s] = P[s];
-    if (tid == 0)
-      for (uint32_t y = 0; y <= kGroups; ++y) a.plan[B + 1 + y] = F[y];
-  }
   const uint32_t x = blockIdx.x % kGroups;
   const uint32_t j = (blockIdx.x / kGroups) * kDecodeWavesPerWG + wave;
   const uint32_t len = F[x + 1] - F[x], nw = group_waves(nwg, x);
@@ -277,6 +255,13 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
   uint32_t* stat = a.bal + kBalStats + 2 * gw;
   if (t_begin >= t_end) {
     if (lane == 0) stat[0] = 0u, stat[1] = 0u;
+    // An empty slice between the first and last range of a segment: its
+    // partial slot is marked empty (l = 0) for the merge.
+    if (t_begin < S) {
+      const DecodePos p = locate(a, cu_q, cu_k, P, t_begin);
+      const uint64_t slot = r + p.seq * a.kvh + p.kh;
+      if (lane < a.group) *(float2*)(a.ws_ml + (slot * a.group + lane) * 2) = make_float2(kNegBig, 0.f);
+    }
     return;
   }
   const uint64_t tr0 = __builtin_amdgcn_s_memrealtime();
@@ -331,6 +316,10 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
     attend_pv<T, D>(vc, pf, o);
     if (!same_piece) {
       const uint32_t seg = pos.seq * a.kvh + pos.kh;
+      if (lane == 0) {
+        if (piece_first) a.seg_ranges[2 * seg] = r;
+        if (seg_ends) a.seg_ranges[2 * seg + 1] = r;
+      }
       flush_piece<T, D>(a, pos, piece_first && seg_ends, r + seg, o, m_run, l_run, col, g);
       if (!more) return false;
       m_run = kNegBig;
@@ -372,10 +361,20 @@ __device__ __forceinline__ void update_shares(const AttnArgs& a, uint32_t nwg, u
   const uint32_t W = nwg * kDecodeWavesPerWG;
   // Wave gw belongs to group (gw / 4) % 8, so the waves lane l reads (l,
   // l + 64, ...) all belong to group (l / 4) % 8.
+  // All of a lane's loads are issued before the first is used (one memory
+  // round trip instead of W / 64 dependent ones).
+  constexpr uint32_t kBatch = 16;
   float st = 0.f, tk = 0.f;
-  for (uint32_t gw = lane; gw < W; gw += 64) {
-    const uint2 v = *(const uint2*)(a.bal + kBalStats + 2 * gw);
-    if (v.x) st += (float)v.x, tk += (float)v.y;
+  for (uint32_t base = 0; base < W; base += 64 * kBatch) {
+    uint2 v[kBatch];
+#pragma unroll
+    for (uint32_t i = 0; i < kBatch; ++i) {
+      const uint32_t gw = base + 64 * i + lane;
+      v[i] = gw < W ? *(const uint2*)(a.bal + kBalStats + 2 * gw) : make_uint2(0u, 0u);
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kBatch; ++i)
+      if (v[i].x) st += (float)v[i].x, tk += (float)v[i].y;
   }
   // Sum over the lanes of each group: lanes with equal (l / 4) % 8 are
   // l ^ 32 and l ^ 1, l ^ 2 (same l / 4).
@@ -403,7 +402,7 @@ __device__ __forceinline__ void update_shares(const AttnArgs& a, uint32_t nwg, u
 // One wave per (sequence, kv head) segment combines the segment's partials
 // if it was split; the extra last wave updates the shares. Lane l owns the
 // E = G*D/64 contiguous outputs from l*E (at most two heads), merged 8 at a
-// time over batches of 8 ranges.
+// time over batches of 8 ranges. A partial with l = 0 is an empty slice's.
 template <typename T, int D>
 __global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_merge(AttnArgs a, uint32_t nwg) {
   const uint32_t lane = threadIdx.x & 63;
@@ -416,20 +415,19 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_merge(AttnArgs 
   }
   if (segi > nseg) return;
   const uint32_t seq = segi / a.kvh, kh = segi - seq * a.kvh;
-  const uint32_t p0 = a.plan[seq], p1 = a.plan[seq + 1];
-  if (p0 == p1) return;  // not a decode row
-  uint32_t F[kGroups + 1];
-#pragma unroll
-  for (uint32_t y = 0; y <= kGroups; ++y) F[y] = a.plan[a.batch + 1 + y];
-  const uint32_t nst = (p1 - p0) / a.kvh;
-  const uint32_t t0 = p0 + kh * nst, t1 = t0 + nst - 1;
-  const uint32_t r0 = range_of(F, nwg, t0), r1 = range_of(F, nwg, t1);
-  if (r0 == r1) return;  // one range held the whole segment and wrote the output
+  // One round trip: the row's extents and the segment's ranges (stale for
+  // rows that are not decode rows, which return here).
+  const uint32_t q0 = a.cu_q[seq], q1 = a.cu_q[seq + 1];
+  const uint32_t k0 = a.cu_k[seq], k1 = a.cu_k[seq + 1];
+  const uint32_t r0 = a.seg_ranges[2 * segi], r1 = a.seg_ranges[2 * segi + 1];
+  if (q1 - q0 != 1 || (int32_t)(k1 - k0) <= 0) return;
+  // r0 == r1: one range held the whole segment and wrote the output.
+  if (r0 >= r1 || r1 >= nwg * kDecodeWavesPerWG) return;
   const uint32_t G = a.group, seg = segi;
   const uint32_t E = G * D / 64;
   const uint32_t e_lane = lane * E;
   const uint32_t h0 = e_lane / D, h1 = (e_lane + E - 1) / D;
-  T* orow = (T*)a.out + ((uint64_t)a.cu_q[seq] * a.num_heads + kh * G) * D;
+  T* orow = (T*)a.out + ((uint64_t)q0 * a.num_heads + kh * G) * D;
   // Up to 8 ranges per round trip; E is a multiple of 4 for G*D >= 256
   // (D is 64 or 128), so outputs move as float4.
   constexpr int R = 8;
@@ -442,20 +440,22 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_merge(AttnArgs 
       float om[R][8], mm[R][2], ll[R][2];
 #pragma unroll
       for (int u = 0; u < R; ++u) {
-        const bool valid = w + u <= r1 && !range_empty(F, nwg, w + u);
+        const bool in = w + u <= r1;
         const uint64_t sl = (uint64_t)(w + u + seg) * G;
         const float* po = a.ws_o + sl * D + e_lane + j0;
-        if (valid && n == 8) {
+        if (in && n == 8) {
           const float4 v0 = *(const float4*)po, v1 = *(const float4*)(po + 4);
           om[u][0] = v0.x, om[u][1] = v0.y, om[u][2] = v0.z, om[u][3] = v0.w;
           om[u][4] = v1.x, om[u][5] = v1.y, om[u][6] = v1.z, om[u][7] = v1.w;
         } else {
 #pragma unroll
-          for (int j = 0; j < 8; ++j) om[u][j] = valid && j < (int)n ? po[j] : 0.f;
+          for (int j = 0; j < 8; ++j) om[u][j] = in && j < (int)n ? po[j] : 0.f;
         }
-        const float2 x0 = valid ? *(const float2*)(a.ws_ml + (sl + h0) * 2) : make_float2(kNegBig, 0.f);
-        const float2 x1 = valid ? *(const float2*)(a.ws_ml + (sl + h1) * 2) : make_float2(kNegBig, 0.f);
-        mm[u][0] = x0.x, ll[u][0] = x0.y, mm[u][1] = x1.x, ll[u][1] = x1.y;
+        const float2 x0 = in ? *(const float2*)(a.ws_ml + (sl + h0) * 2) : make_float2(kNegBig, 0.f);
+        const float2 x1 = in ? *(const float2*)(a.ws_ml + (sl + h1) * 2) : make_float2(kNegBig, 0.f);
+        // Empty partials (l = 0) weigh nothing, whatever their m and o hold.
+        mm[u][0] = x0.y > 0.f ? x0.x : kNegBig, ll[u][0] = x0.y;
+        mm[u][1] = x1.y > 0.f ? x1.x : kNegBig, ll[u][1] = x1.y;
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -467,9 +467,10 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_merge(AttnArgs 
         float Lj = L[j] * f, Oj = O[j] * f;
 #pragma unroll
         for (int u = 0; u < R; ++u) {
+          const bool live = ll[u][hw] > 0.f;
           const float e = fast_exp2(mm[u][hw] - Mn);
-          Lj += ll[u][hw] * e;
-          Oj += om[u][j] * e;
+          Lj += live ? ll[u][hw] * e : 0.f;
+          Oj += live ? om[u][j] * e : 0.f;
         }
         M[j] = Mn, L[j] = Lj, O[j] = Oj;
       }
@@ -497,19 +498,20 @@ static size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Workspace: the balance block (shares and per-wave timings; the shares
 // carry over between launches, so the block leads the workspace whatever
-// the batch), the plan, and the partials: one slot per range plus one per
-// segment. Only the shares persist; everything else is rewritten by each
-// launch before it is read. A zeroed workspace starts from uniform shares.
+// the batch), the first and last range of every segment, and the partials:
+// one slot per range plus one per segment. Only the shares persist;
+// everything else that a launch reads was written by that launch. A zeroed
+// workspace starts from uniform shares.
 struct DecodeWs {
-  size_t bal, plan, ml, o, trace, total;
+  size_t bal, ranges, ml, o, trace, total;
 };
 static DecodeWs decode_ws(uint32_t b, uint32_t kvh, uint32_t group, uint32_t head_dim,
                           uint32_t num_waves) {
   const size_t slots = (size_t)num_waves + (size_t)b * kvh;
   DecodeWs w;
   w.bal = 0;
-  w.plan = up256((kBalStats + 2 * (size_t)num_waves) * sizeof(uint32_t));
-  w.ml = w.plan + up256((b + 2 + kGroups) * sizeof(uint32_t));
+  w.ranges = up256((kBalStats + 2 * (size_t)num_waves) * sizeof(uint32_t));
+  w.ml = w.ranges + up256((size_t)b * kvh * 2 * sizeof(uint32_t));
   w.o = w.ml + up256(slots * group * 2 * sizeof(float));
   w.trace = w.o + up256(slots * group * head_dim * sizeof(float));
   w.total = w.trace;
@@ -541,7 +543,7 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t max_
     const DecodeWs w = decode_ws(nb, a.kvh, a.group, head_dim, W);
     char* ws = (char*)workspace;
     c.bal = (uint32_t*)(ws + w.bal);
-    c.plan = (uint32_t*)(ws + w.plan);
+    c.seg_ranges = (uint32_t*)(ws + w.ranges);
     c.ws_ml = (float*)(ws + w.ml);
     c.ws_o = (float*)(ws + w.o);
 #ifdef VK_DECODE_TRACE
