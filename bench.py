@@ -30,7 +30,8 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 from vapi_amd import workload  # noqa: E402
-from vapi_amd.attention import ForwardBatch, PreparedAttention, paged_attention_prepared  # noqa: E402
+from vapi_amd.attention import (ForwardBatch, PreparedAttention, paged_attention_append_prepared,  # noqa: E402
+                                paged_attention_prepared)
 from vapi_amd.backend import KvBlockBackend  # noqa: E402
 from vapi_amd.cache import PagedKvCache, write_rows_indexed, scatter_index  # noqa: E402
 
@@ -119,6 +120,34 @@ def bench_decode(steps, warmup):
         f"{ms * 1e3:.1f} us/step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of 8 TB/s)")
     d.update(ms=ms, wall=wall, gbs=gbs)
     return d
+
+
+def bench_fused_step(d, steps, warmup):
+    """Config 2's decode step with its 64 new tokens appended: the two calls
+    (vapi_kv_append, vapi_paged_attention) against the fused
+    vapi_paged_attention_append, back to back on one stream."""
+    w = d["w"]
+    g = torch.Generator(device=DEV).manual_seed(workload.seed_for(2) + 2)
+    k_new = torch.randn(w.batch, w.num_kv_heads, w.head_dim, generator=g,
+                        device=DEV).to(torch.bfloat16)
+    v_new = torch.randn_like(k_new)
+    slots = np.array([int(t[(l - 1) // w.block_size]) * w.block_size + (l - 1) % w.block_size
+                      for t, l in zip(w.tables, w.lens)], dtype=np.uint32)
+    dslots = torch.from_numpy(slots.view(np.int32)).to(DEV)
+    cache, q, prep, scale, out = d["cache"], d["q"], d["prep"], d["scale"], torch.empty_like(d["q"])
+
+    def two():
+        write_rows_indexed(cache, 0, k_new, v_new, dslots)
+        paged_attention_prepared(q, cache, 0, prep, scale, out=out)
+
+    def fused():
+        paged_attention_append_prepared(q, k_new, v_new, dslots, cache, 0, prep, scale, out=out)
+
+    ms_two, _ = timed(two, steps, warmup)
+    ms_fused, _ = timed(fused, steps, warmup)
+    log(f"decode cfg2 + append of {w.batch} tokens: two calls {ms_two * 1e3:.1f} us, "
+        f"fused {ms_fused * 1e3:.1f} us")
+    return {"two_calls_us": round(ms_two * 1e3, 2), "fused_us": round(ms_fused * 1e3, 2)}
 
 
 # ---- config 1: append --------------------------------------------------------------
@@ -369,6 +398,7 @@ def main():
     if args.only == "decode":
         return
     extras = {}
+    extras["fused_step_cfg2"] = bench_fused_step(dec, args.steps, args.warmup)
     if args.only in (None,):
         extras["append_cfg1"] = bench_append(args.steps, args.warmup)
         extras["prefill_cfg3"] = bench_prefill(max(args.steps // 5, 3), 2)

@@ -169,6 +169,38 @@ int vapi_paged_attention(const vapi_kv_pool* pool, uint32_t layer,
                          vapi_stream_t stream);
 
 /*
+ * One decode step's K/V append and paged attention in one call: the result
+ * is that of vapi_kv_append(k_src, v_src, slot_mapping, n_tokens) followed
+ * by vapi_paged_attention(...) with the same arguments. It fuses the
+ * per-layer pair the reference issues in every model forward (the cache
+ * write, then the attention: models/qwen.rs:371-391, models/llama.rs:157-165).
+ *
+ * When every row is a decode row (max_seqlen_q == 1) on the MFMA path
+ * (bf16/f16, head_dim 64 or 128), it takes one launch fewer: the attention
+ * reads the new key of row s (position len_k - 1) straight from token
+ * cu_seqlens_q[s] of k_src/v_src, provided slot_mapping sends that token to
+ * the slot the row's block table gives position len_k - 1 (checked per row
+ * on the device; a row that fails the check reads the pool, as the two-call
+ * sequence would), and the pool writes of all n_tokens tokens complete
+ * within the call. The fused path also requires that no row reads a slot
+ * this call writes other than its own new key at len_k - 1, which holds for
+ * the scheduler's slot mapping (scheduler.rs:525-565). Every other shape
+ * runs the two calls. Same workspace contract as vapi_paged_attention.
+ */
+int vapi_paged_attention_append(const vapi_kv_pool* pool, uint32_t layer,
+                                const void* k_src, const void* v_src,
+                                const uint32_t* slot_mapping, uint32_t n_tokens,
+                                const void* q, void* out,
+                                const uint32_t* cu_seqlens_q,
+                                const uint32_t* cu_seqlens_k,
+                                const uint32_t* block_table, uint32_t batch,
+                                uint32_t max_blocks, uint32_t max_seqlen_q,
+                                uint32_t max_seqlen_k, uint32_t num_heads,
+                                float scale, int32_t window_left,
+                                int32_t window_right, void* workspace,
+                                size_t workspace_bytes, vapi_stream_t stream);
+
+/*
  * Copy-on-write block copy over every layer, K and V, in one launch.
  * Replaces CandleBackend::copy_blocks (backend.rs:781-797), which the
  * engine calls with Scheduler::fork's pairs (scheduler.rs:217-281).

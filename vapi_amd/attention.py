@@ -116,6 +116,18 @@ def workspace_bytes(cache: PagedKvCache, batch: int, num_heads: int, max_q: int,
                                                       max_q, max_k)
 
 
+def _workspace(cache, prepared: PreparedAttention, b: int, num_heads: int, max_q: int,
+               max_k: int, device):
+    need = workspace_bytes(cache, b, num_heads, max_q, max_k)
+    ws = prepared.workspace
+    if need and (ws is None or ws.numel() < need):
+        # Zero-filled once: a zeroed workspace starts the decode from equal
+        # per-XCD shares; later calls carry the shares over.
+        ws = torch.zeros(need, dtype=torch.uint8, device=device)
+        prepared.workspace = ws
+    return need, ws
+
+
 def paged_attention_prepared(q: torch.Tensor, cache: PagedKvCache, layer: int,
                              prepared: PreparedAttention, softmax_scale: float,
                              window_size_left: int | None = None,
@@ -134,13 +146,7 @@ def paged_attention_prepared(q: torch.Tensor, cache: PagedKvCache, layer: int,
     num_heads = q.shape[1]
     max_q = max(int(prepared.max_seqlen_q), 1)
     max_k = max(int(prepared.max_seqlen_k), 1)
-    need = workspace_bytes(cache, b, num_heads, max_q, max_k)
-    ws = prepared.workspace
-    if need and (ws is None or ws.numel() < need):
-        # Zero-filled once: the split-K arrival counters must start at 0 (the
-        # kernels leave them at 0 when they finish).
-        ws = torch.zeros(need, dtype=torch.uint8, device=q.device)
-        prepared.workspace = ws
+    need, ws = _workspace(cache, prepared, b, num_heads, max_q, max_k, q.device)
     check(lib().vapi_paged_attention(
         cache.pool, layer, q.data_ptr(), out.data_ptr(), prepared.seqlens_q.data_ptr(),
         prepared.seqlens_k.data_ptr(), prepared.block_table.data_ptr(), b,
@@ -166,3 +172,48 @@ def paged_attention(q, cache, layer, batch: ForwardBatch, softmax_scale,
     wl = None if sliding_window is None else max(int(sliding_window) - 1, 0)
     return paged_attention_windowed(q, cache, layer, batch, softmax_scale, wl, 0,
                                     stream=stream)
+
+
+def paged_attention_append_prepared(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                                    slot_mapping: torch.Tensor, cache: PagedKvCache,
+                                    layer: int, prepared: PreparedAttention,
+                                    softmax_scale: float,
+                                    window_size_left: int | None = None,
+                                    window_size_right: int | None = 0,
+                                    out: torch.Tensor | None = None,
+                                    stream=None) -> torch.Tensor:
+    """One layer's cache write and attention in one call (the pair of
+    models/qwen.rs:371-391 and models/llama.rs:157-165): the same result as
+    write_kv_to_cache(k, v, slot_mapping) then paged_attention_prepared(q),
+    in one launch pair fewer for decode batches.
+
+    k, v: [n, num_kv_heads, head_dim] in the cache dtype; slot_mapping: a
+    device u32 (int32 view) tensor of n slots.
+    """
+    if q.dim() != 3 or q.shape[2] != cache.head_dim:
+        raise ValueError(f"q must be (tokens, heads, {cache.head_dim}), got {tuple(q.shape)}")
+    if q.dtype != cache.dtype or k.dtype != cache.dtype or v.dtype != cache.dtype:
+        raise ValueError(f"q/k/v must be {cache.dtype}")
+    if tuple(k.shape) != tuple(v.shape) or k.dim() != 3 or \
+            tuple(k.shape[1:]) != (cache.num_kv_heads, cache.head_dim):
+        raise ValueError(f"k/v must be (n, {cache.num_kv_heads}, {cache.head_dim}), "
+                         f"got {tuple(k.shape)} and {tuple(v.shape)}")
+    if slot_mapping.numel() != k.shape[0] or slot_mapping.element_size() != 4:
+        raise ValueError("slot_mapping must hold one 32-bit slot per row")
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    b = prepared.seqlens_q.shape[0] - 1
+    num_heads = q.shape[1]
+    max_q = max(int(prepared.max_seqlen_q), 1)
+    max_k = max(int(prepared.max_seqlen_k), 1)
+    need, ws = _workspace(cache, prepared, b, num_heads, max_q, max_k, q.device)
+    check(lib().vapi_paged_attention_append(
+        cache.pool, layer, k.data_ptr(), v.data_ptr(), slot_mapping.data_ptr(), k.shape[0],
+        q.data_ptr(), out.data_ptr(), prepared.seqlens_q.data_ptr(),
+        prepared.seqlens_k.data_ptr(), prepared.block_table.data_ptr(), b,
+        prepared.block_table.shape[1], max_q, max_k, num_heads, float(softmax_scale),
+        -1 if window_size_left is None else int(window_size_left),
+        -1 if window_size_right is None else int(window_size_right),
+        ws.data_ptr() if need else None, need, stream_handle(stream)))
+    return out

@@ -19,9 +19,26 @@ static bool mfma_ok(const vapi_kv_pool* p, uint32_t num_heads) {
   return G >= 1 && G <= 16;
 }
 
+// The fused append's new rows (decode batches on the MFMA path only).
+struct NewRows {
+  const void* k;
+  const void* v;
+  const uint32_t* slots;
+  uint32_t n;
+};
+
 }  // namespace vk
 
 using namespace vk;
+
+static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const void* q,
+                                void* out, const uint32_t* cu_seqlens_q,
+                                const uint32_t* cu_seqlens_k, const uint32_t* block_table,
+                                uint32_t batch, uint32_t max_blocks, uint32_t max_seqlen_q,
+                                uint32_t max_seqlen_k, uint32_t num_heads, float scale,
+                                int32_t window_left, int32_t window_right, void* workspace,
+                                size_t workspace_bytes, vapi_stream_t stream,
+                                const NewRows* fuse);
 
 extern "C" {
 
@@ -47,6 +64,50 @@ int vapi_paged_attention(const vapi_kv_pool* pool, uint32_t layer,
                          int32_t window_left, int32_t window_right,
                          void* workspace, size_t workspace_bytes,
                          vapi_stream_t stream) {
+  return paged_attention_impl(pool, layer, q, out, cu_seqlens_q, cu_seqlens_k, block_table,
+                              batch, max_blocks, max_seqlen_q, max_seqlen_k, num_heads, scale,
+                              window_left, window_right, workspace, workspace_bytes, stream,
+                              nullptr);
+}
+
+int vapi_paged_attention_append(const vapi_kv_pool* pool, uint32_t layer, const void* k_src,
+                                const void* v_src, const uint32_t* slot_mapping,
+                                uint32_t n_tokens, const void* q, void* out,
+                                const uint32_t* cu_seqlens_q, const uint32_t* cu_seqlens_k,
+                                const uint32_t* block_table, uint32_t batch,
+                                uint32_t max_blocks, uint32_t max_seqlen_q,
+                                uint32_t max_seqlen_k, uint32_t num_heads, float scale,
+                                int32_t window_left, int32_t window_right, void* workspace,
+                                size_t workspace_bytes, vapi_stream_t stream) {
+  if (int rc = check_pool(pool, "vapi_paged_attention_append")) return rc;
+  const bool fused = n_tokens > 0 && batch > 0 && max_seqlen_q == 1 && num_heads > 0 &&
+                     num_heads % pool->num_kv_heads == 0 && mfma_ok(pool, num_heads);
+  if (!fused) {
+    if (int rc = vapi_kv_append(pool, layer, k_src, v_src, slot_mapping, n_tokens, stream))
+      return rc;
+    return vapi_paged_attention(pool, layer, q, out, cu_seqlens_q, cu_seqlens_k, block_table,
+                                batch, max_blocks, max_seqlen_q, max_seqlen_k, num_heads, scale,
+                                window_left, window_right, workspace, workspace_bytes, stream);
+  }
+  if (!k_src || !v_src || !slot_mapping)
+    VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention_append: null source or slot_mapping");
+  const NewRows rows{k_src, v_src, slot_mapping, n_tokens};
+  return paged_attention_impl(pool, layer, q, out, cu_seqlens_q, cu_seqlens_k, block_table,
+                              batch, max_blocks, max_seqlen_q, max_seqlen_k, num_heads, scale,
+                              window_left, window_right, workspace, workspace_bytes, stream,
+                              &rows);
+}
+
+}  // extern "C"
+
+static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const void* q,
+                                void* out, const uint32_t* cu_seqlens_q,
+                                const uint32_t* cu_seqlens_k, const uint32_t* block_table,
+                                uint32_t batch, uint32_t max_blocks, uint32_t max_seqlen_q,
+                                uint32_t max_seqlen_k, uint32_t num_heads, float scale,
+                                int32_t window_left, int32_t window_right, void* workspace,
+                                size_t workspace_bytes, vapi_stream_t stream,
+                                const NewRows* fuse) {
   if (int rc = check_pool(pool, "vapi_paged_attention")) return rc;
   if (layer >= pool->num_layers)
     VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: layer %u of %u", layer,
@@ -84,6 +145,11 @@ int vapi_paged_attention(const vapi_kv_pool* pool, uint32_t layer,
   a.ws_o = nullptr;
   a.bal = nullptr;
   a.trace = nullptr;
+  a.k_new = fuse ? (const char*)fuse->k : nullptr;
+  a.v_new = fuse ? (const char*)fuse->v : nullptr;
+  a.slots = fuse ? fuse->slots : nullptr;
+  a.n_new = fuse ? fuse->n : 0;
+  a.num_slots = g.num_blocks * g.block_size;
   a.blk_e = g.blk;
   a.head_e = g.head;
   a.tok_e = (uint32_t)g.tok;
@@ -121,5 +187,3 @@ int vapi_paged_attention(const vapi_kv_pool* pool, uint32_t layer,
   VK_LAUNCHED("paged_attention");
   return 0;
 }
-
-}  // extern "C"

@@ -50,6 +50,12 @@ struct AttnArgs {
   float* ws_o;         // decode: partial outputs per slot and head
   uint32_t* bal;       // decode: XCD shares and per-wave timings, kept across launches
   uint64_t* trace;  // decode timing probes (VK_DECODE_TRACE builds only)
+  // Fused append (decode only; null otherwise): the step's new K/V rows
+  // [n_new, kvh, D] and their slots.
+  const char* k_new;
+  const char* v_new;
+  const uint32_t* slots;
+  uint32_t n_new, num_slots;
   uint64_t blk_e, head_e;  // element strides in the pool
   uint32_t tok_e;
   uint32_t max_blocks, batch, num_heads, kvh, group, block_size, bs_shift;
@@ -204,25 +210,30 @@ __device__ __forceinline__ const char* tile_base(const uint32_t* __restrict__ ta
   return (const char*)(base + (uint64_t)blk * a.blk_e + (uint64_t)off0 * a.tok_e);
 }
 
+// K and V tiles of the 32-key step at s0 (keys past `last` re-read it). With
+// `knew` / `vnew` (the row's new key, D contiguous elements) key `last` is
+// read from there instead of the pool: a per-lane address select, no branch.
 template <typename T, int D>
 __device__ __forceinline__ void load_k(KTile<D>& st, const uint32_t* __restrict__ tab,
                                        const T* kb, const AttnArgs& a, int32_t s0, int32_t last,
-                                       uint32_t col, uint32_t g) {
+                                       uint32_t col, uint32_t g, const char* knew = nullptr) {
   constexpr int KC = D / 32;
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     const int32_t ts = min(s0 + 16 * tt, last & ~15);
     const char* kt = tile_base(tab, kb, a, ts);
     const uint32_t kr = ((uint32_t)min((int32_t)col, last - ts) * a.tok_e + 8 * g) * sizeof(T);
+    const char* src = kt + kr;
+    if (knew != nullptr && (int32_t)col >= last - ts) src = knew + 8 * g * sizeof(T);
 #pragma unroll
-    for (int c = 0; c < KC; ++c) st.k[tt][c] = *(const uint4*)(kt + (kr + 64u * c));
+    for (int c = 0; c < KC; ++c) st.k[tt][c] = *(const uint4*)(src + 64u * c);
   }
 }
 
 template <typename T, int D>
 __device__ __forceinline__ void load_v(VTile<D>& st, const uint32_t* __restrict__ tab,
                                        const T* vb, const AttnArgs& a, int32_t s0, int32_t last,
-                                       uint32_t col, uint32_t g) {
+                                       uint32_t col, uint32_t g, const char* vnew = nullptr) {
   constexpr int DPL = D / 16;
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
@@ -233,7 +244,9 @@ __device__ __forceinline__ void load_v(VTile<D>& st, const uint32_t* __restrict_
     for (int i = 0; i < 4; ++i) {
       const uint32_t vr =
           ((uint32_t)min((int32_t)(4 * g + i), lim) * a.tok_e + DPL * col) * sizeof(T);
-      st.v[4 * tt + i] = load_vrow<DPL>(vt + vr);
+      const char* src = vt + vr;
+      if (vnew != nullptr && (int32_t)(4 * g + i) >= lim) src = vnew + DPL * col * sizeof(T);
+      st.v[4 * tt + i] = load_vrow<DPL>(src);
     }
   }
 }

@@ -112,11 +112,12 @@ struct DecodePos {
   uint32_t seq, kh, q0;
   int32_t key0, len_k, lo;
   uint32_t seg_first;  // key0 is the segment's first step (a word, not a bool: no stack copy)
+  uint32_t fuse;       // fused append: key len_k - 1 is read from the new rows
 };
 
 __device__ __forceinline__ DecodePos locate(const AttnArgs& a, const uint32_t* __restrict__ cu_q,
                                             const uint32_t* __restrict__ cu_k, const uint32_t* P,
-                                            uint32_t t) {
+                                            const uint32_t* FZ, uint32_t t) {
   uint32_t lo_i = 0, hi_i = a.batch;  // P[lo_i] <= t < P[hi_i]
   while (hi_i - lo_i > 1) {
     const uint32_t mid = (lo_i + hi_i) >> 1;
@@ -135,6 +136,7 @@ __device__ __forceinline__ DecodePos locate(const AttnArgs& a, const uint32_t* _
   p.lo = a.wl >= 0 ? max(0, p.len_k - 1 - a.wl) : 0;
   p.key0 = (p.lo & ~31) + 32 * (int32_t)ks;
   p.seg_first = ks == 0;
+  p.fuse = FZ ? FZ[lo_i] : 0u;
   return p;
 }
 
@@ -160,7 +162,9 @@ __device__ __forceinline__ void load_step_k(KTile<D>& st, const AttnArgs& a,
                                             const DecodePos& p, uint32_t col, uint32_t g) {
   const uint32_t* __restrict__ tab = table + (uint64_t)p.seq * a.max_blocks;
   const T* kb = (const T*)a.k + p.kh * a.head_e;
-  load_k<T, D>(st, tab, kb, a, p.key0, p.len_k - 1, col, g);
+  const char* knew =
+      p.fuse ? a.k_new + ((uint64_t)p.q0 * a.kvh + p.kh) * D * sizeof(T) : nullptr;
+  load_k<T, D>(st, tab, kb, a, p.key0, p.len_k - 1, col, g, knew);
 }
 
 template <typename T, int D>
@@ -169,7 +173,9 @@ __device__ __forceinline__ void load_step_v(VTile<D>& st, const AttnArgs& a,
                                             const DecodePos& p, uint32_t col, uint32_t g) {
   const uint32_t* __restrict__ tab = table + (uint64_t)p.seq * a.max_blocks;
   const T* vb = (const T*)a.v + p.kh * a.head_e;
-  load_v<T, D>(st, tab, vb, a, p.key0, p.len_k - 1, col, g);
+  const char* vnew =
+      p.fuse ? a.v_new + ((uint64_t)p.q0 * a.kvh + p.kh) * D * sizeof(T) : nullptr;
+  load_v<T, D>(st, tab, vb, a, p.key0, p.len_k - 1, col, g, vnew);
 }
 
 
@@ -202,12 +208,15 @@ __device__ __forceinline__ void flush_piece(const AttnArgs& a, const DecodePos& 
   }
 }
 
-template <typename T, int D>
+template <typename T, int D, bool kFuse>
 __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged_decode_stream(
     AttnArgs a, const uint32_t* __restrict__ cu_q, const uint32_t* __restrict__ cu_k,
     const uint32_t* __restrict__ table) {
   constexpr int DPL = D / 16;
-  extern __shared__ uint32_t P[];  // batch + 1 entries (dynamic LDS)
+  // Dynamic LDS: step prefix sums P (batch + 1), then with kFuse the
+  // per-sequence fused-append flags FZ (batch).
+  extern __shared__ uint32_t P[];
+  uint32_t* const FZ = kFuse ? P + a.batch + 1 : nullptr;
   __shared__ uint32_t wave_tot[kDecodeWavesPerWG];
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63;
@@ -234,7 +243,21 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
     for (uint32_t w = 0; w < wave; ++w) run += wave_tot[w];
     for (uint32_t s = b0; s < b1; ++s) {
       P[s] = run;
-      run += decode_steps(a, cu_q, cu_k, s) * a.kvh;
+      const uint32_t ns = decode_steps(a, cu_q, cu_k, s);
+      run += ns * a.kvh;
+      if (kFuse) {
+        // The row's new key (position len_k - 1) comes from token cu_q[s]
+        // of the new rows if that token's slot is the one the block table
+        // gives the position; otherwise the pool is read.
+        uint32_t f = 0;
+        if (ns) {
+          const uint32_t q0 = cu_q[s], last = cu_k[s + 1] - cu_k[s] - 1;
+          const uint32_t slot = q0 < a.n_new ? a.slots[q0] : 0xFFFFFFFFu;
+          const uint32_t blk = table[(uint64_t)s * a.max_blocks + (last >> a.bs_shift)];
+          f = slot < a.num_slots && slot == blk * a.block_size + (last & (a.block_size - 1));
+        }
+        FZ[s] = f;
+      }
     }
     if (tid == NT - 1) P[B] = run;
     __syncthreads();
@@ -258,7 +281,7 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
     // An empty slice between the first and last range of a segment: its
     // partial slot is marked empty (l = 0) for the merge.
     if (t_begin < S) {
-      const DecodePos p = locate(a, cu_q, cu_k, P, t_begin);
+      const DecodePos p = locate(a, cu_q, cu_k, P, FZ, t_begin);
       const uint64_t slot = r + p.seq * a.kvh + p.kh;
       if (lane < a.group) *(float2*)(a.ws_ml + (slot * a.group + lane) * 2) = make_float2(kNegBig, 0.f);
     }
@@ -268,7 +291,7 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
 
   uint32_t t = t_begin;
   const uint32_t col = lane & 15, g = lane >> 4;
-  DecodePos pos = locate(a, cu_q, cu_k, P, t);
+  DecodePos pos = locate(a, cu_q, cu_k, P, FZ, t);
   // The Q^T operand of the current segment lives in LDS (read back every
   // step) to keep the K/V buffers in registers.
   __shared__ uint4 q_lds[kDecodeWavesPerWG][D / 32 * 64];
@@ -301,7 +324,7 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
       nxt.key0 += 32;
       nxt.seg_first = false;
     } else if (more) {
-      nxt = locate(a, cu_q, cu_k, P, t + 1);
+      nxt = locate(a, cu_q, cu_k, P, FZ, t + 1);
     }
     load_step_k<T, D>(kn, a, table, nxt, col, g);
     load_step_v<T, D>(vn, a, table, nxt, col, g);
@@ -403,8 +426,40 @@ __device__ __forceinline__ void update_shares(const AttnArgs& a, uint32_t nwg, u
 // if it was split; the extra last wave updates the shares. Lane l owns the
 // E = G*D/64 contiguous outputs from l*E (at most two heads), merged 8 at a
 // time over batches of 8 ranges. A partial with l = 0 is an empty slice's.
+// Fused append: workgroups past the merge's write the new K/V rows to their
+// slots (the stream read them from the new rows, so no read of this launch
+// pair depends on these writes). Rows are D contiguous elements; 16-byte
+// chunks, one per lane.
 template <typename T, int D>
-__global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_merge(AttnArgs a, uint32_t nwg) {
+__device__ __forceinline__ void copy_new_rows(const AttnArgs& a, uint32_t wg, uint32_t n_wg) {
+  static_assert(sizeof(T) == 2, "16-bit pools: 8 elements per 16-byte chunk");
+  constexpr uint32_t kChunks = D / 8;  // per row
+  constexpr uint32_t kThreads = 64 * kMergeWaves;
+  const uint32_t rows = a.n_new * a.kvh;             // per tensor
+  const uint64_t total = 2ull * rows * kChunks;
+  for (uint64_t i = (uint64_t)wg * kThreads + threadIdx.x; i < total; i += (uint64_t)n_wg * kThreads) {
+    const uint32_t c = (uint32_t)(i % kChunks);
+    const uint64_t r2 = i / kChunks;
+    const bool is_v = r2 >= rows;
+    const uint32_t r = (uint32_t)(is_v ? r2 - rows : r2);
+    const uint32_t t = r / a.kvh, h = r - t * a.kvh;
+    const uint32_t slot = a.slots[t];
+    const uint4 x = *(const uint4*)((const T*)(is_v ? a.v_new : a.k_new) + (uint64_t)r * D + 8 * c);
+    if (slot < a.num_slots) {
+      const uint32_t blk = slot >> a.bs_shift, off = slot & (a.block_size - 1);
+      T* dst = (T*)(is_v ? a.v : a.k) + blk * a.blk_e + h * a.head_e + (uint64_t)off * a.tok_e;
+      *(uint4*)(dst + 8 * c) = x;
+    }
+  }
+}
+
+template <typename T, int D, bool kFuse>
+__global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_merge(AttnArgs a, uint32_t nwg,
+                                                                      uint32_t merge_wgs) {
+  if (kFuse && blockIdx.x >= merge_wgs) {
+    copy_new_rows<T, D>(a, blockIdx.x - merge_wgs, gridDim.x - merge_wgs);
+    return;
+  }
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t nseg = a.batch * a.kvh;
   const uint32_t segi =
@@ -549,21 +604,38 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t max_
 #ifdef VK_DECODE_TRACE
     c.trace = (uint64_t*)(ws + w.trace);
 #endif
-#define VK_DEC(T, DD)                                                                           \
+    // Fused append: the first chunk's merge launch also writes the new rows
+    // (every chunk's stream reads a row's new key from the new rows).
+    const bool fuse = a.k_new != nullptr;
+    const uint32_t merge_wgs = (nb * a.kvh + kMergeWaves) / kMergeWaves;
+    uint32_t copy_wgs = 0;
+    if (fuse && b0 == 0) {
+      const uint64_t chunks = 2ull * a.n_new * a.kvh * (head_dim / 8);
+      copy_wgs = (uint32_t)std::min<uint64_t>((chunks + 64 * kMergeWaves - 1) / (64 * kMergeWaves), 1024);
+    }
+    const size_t lds = (nb + 1 + (fuse ? nb : 0)) * sizeof(uint32_t);
+#define VK_DEC(T, DD, F)                                                                        \
   do {                                                                                          \
-    hipLaunchKernelGGL((paged_decode_stream<T, DD>), dim3(nwg), dim3(64 * kDecodeWavesPerWG), \
-                       (nb + 1) * sizeof(uint32_t), s, c, c.cu_q, c.cu_k, c.table);            \
-    hipLaunchKernelGGL((paged_decode_merge<T, DD>), dim3((nb * a.kvh + kMergeWaves) / kMergeWaves), \
-                       dim3(64 * kMergeWaves), 0, s, c,                                         \
-                       nwg);                                                                    \
+    hipLaunchKernelGGL((paged_decode_stream<T, DD, F>), dim3(nwg), dim3(64 * kDecodeWavesPerWG), \
+                       lds, s, c, c.cu_q, c.cu_k, c.table);                                    \
+    hipLaunchKernelGGL((paged_decode_merge<T, DD, F>), dim3(merge_wgs + copy_wgs),             \
+                       dim3(64 * kMergeWaves), 0, s, c, nwg, merge_wgs);                        \
+  } while (0)
+#define VK_DEC2(T, DD) \
+  do {                 \
+    if (fuse)          \
+      VK_DEC(T, DD, true); \
+    else               \
+      VK_DEC(T, DD, false); \
   } while (0)
     if (bf16) {
-      if (head_dim == 128) VK_DEC(bf16_t, 128);
-      else VK_DEC(bf16_t, 64);
+      if (head_dim == 128) VK_DEC2(bf16_t, 128);
+      else VK_DEC2(bf16_t, 64);
     } else {
-      if (head_dim == 128) VK_DEC(f16_t, 128);
-      else VK_DEC(f16_t, 64);
+      if (head_dim == 128) VK_DEC2(f16_t, 128);
+      else VK_DEC2(f16_t, 64);
     }
+#undef VK_DEC2
 #undef VK_DEC
   }
 }
