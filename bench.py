@@ -33,7 +33,8 @@ from vapi_amd import workload  # noqa: E402
 from vapi_amd.attention import (ForwardBatch, PreparedAttention, paged_attention_append_prepared,  # noqa: E402
                                 paged_attention_prepared)
 from vapi_amd.backend import KvBlockBackend  # noqa: E402
-from vapi_amd.cache import PagedKvCache, write_rows_indexed, scatter_index  # noqa: E402
+from vapi_amd.cache import (PagedKvCache, scatter_index, write_kv_to_cache_layers,  # noqa: E402
+                             write_rows_indexed)
 
 HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2500.0
@@ -175,9 +176,21 @@ def bench_append(steps, warmup):
     log(f"append cfg1: {alg / 1e6:.1f} MB, {ms * 1e3:.2f} us/append in a graph "
         f"({gbs:.0f} GB/s), {ms_host * 1e3:.1f} us/append host-launched")
     del cache
+    # The same step's rows for 4 layers in one launch (vapi_kv_append_layers).
+    L = 4
+    cache = PagedKvCache(L, w.num_blocks, w.block_size, w.num_kv_heads, w.head_dim,
+                         torch.bfloat16, "HND")
+    kl = torch.randn(L, w.n_tokens, 8, 128, generator=g, device=DEV).to(torch.bfloat16)
+    vl = torch.randn_like(kl)
+    ms_l, _ = timed(lambda: write_kv_to_cache_layers(cache, 0, kl, vl, idx), steps, warmup)
+    gbs_l = L * alg / (ms_l * 1e-3) / 1e9
+    log(f"append cfg1 x {L} layers in one launch: {ms_l * 1e3:.2f} us "
+        f"({ms_l * 1e3 / L:.2f} us/layer, {gbs_l:.0f} GB/s)")
+    del cache, kl, vl
     return dict(us=ms * 1e3, gbs=gbs, frac=gbs / HBM_PEAK_GBS, bytes=alg,
                 us_host_launched=ms_host * 1e3,
-                gbs_host_launched=alg / (ms_host * 1e-3) / 1e9)
+                gbs_host_launched=alg / (ms_host * 1e-3) / 1e9,
+                layers4_one_launch_us=ms_l * 1e3, layers4_gbs=gbs_l)
 
 
 # ---- config 3: chunked prefill ----------------------------------------------------

@@ -113,6 +113,20 @@ int vapi_kv_append(const vapi_kv_pool* pool, uint32_t layer, const void* k_src,
                    uint32_t n_tokens, vapi_stream_t stream);
 
 /*
+ * The same append over layers layer0 .. layer0 + n_layers - 1 in one launch
+ * (one slot_mapping for all of them): layer l's rows are at k_src/v_src +
+ * (l - layer0) * src_layer_stride bytes, each [n_tokens, num_kv_heads,
+ * head_dim]. Equals n_layers vapi_kv_append calls. No counterpart call in
+ * the reference, which writes each layer inside its forward
+ * (models/qwen.rs:371-387); it is the multi-layer write of a step whose K/V
+ * are all at hand, e.g. a restored prefix.
+ */
+int vapi_kv_append_layers(const vapi_kv_pool* pool, uint32_t layer0, uint32_t n_layers,
+                          const void* k_src, const void* v_src, uint64_t src_layer_stride,
+                          const uint32_t* slot_mapping, uint32_t n_tokens,
+                          vapi_stream_t stream);
+
+/*
  * Block-table gather into logical order. Replaces gather_kv (cache.rs:283-290).
  * block_table: device u32[n_table]; out: device [len_k, num_kv_heads,
  * head_dim] for K and for V (either may be NULL). len_k <= n_table*block_size.

@@ -59,6 +59,20 @@ def test_bad_arguments_are_errors_not_crashes():
     assert L.vapi_paged_attention(pool(), 0, *args) == _lib.ESPACE
     assert L.vapi_kv_copy_blocks(pool(num_layers=2, layer_stride_bytes=16), 1, 1, None) == _lib.EINVAL
     assert L.vapi_kv_swap_out(pool(), 1, 1, 1, 1, 10, None) == _lib.ESPACE
+    # Multi-layer append: the layer range, the source layer stride.
+    assert L.vapi_kv_append_layers(pool(), 0, 2, 1, 1, 1 << 20, 1, 1, None) == _lib.EINVAL
+    assert L.vapi_kv_append_layers(pool(), 0, 0, 1, 1, 0, 1, 1, None) == _lib.EINVAL
+    two = pool(num_layers=2, layer_stride_bytes=1 << 20)
+    assert L.vapi_kv_append_layers(two, 0, 2, 1, 1, 255, 1, 1, None) == _lib.EINVAL
+    assert b"stride" in L.vapi_kv_last_error()
+    assert L.vapi_kv_append_layers(two, 1, 1, 1, 1, 0, 1, 0, None) == _lib.OK
+    # Fused append + attention: the append's and the attention's errors.
+    args = [1, 1, 1, 1, 1, 1, 2, 4, 1, 100, 8, 0.1, -1, 0, None, 0, None]
+    assert L.vapi_paged_attention_append(pool(dtype=9), 0, 1, 1, 1, *args) == _lib.EINVAL
+    assert L.vapi_paged_attention_append(pool(), 0, None, 1, 1, *args) == _lib.EINVAL
+    assert b"null source" in L.vapi_kv_last_error()
+    args = [1, 1, 1, 1, 1, 1, 2, 320, 1, 5000, 8, 0.1, -1, 0, None, 0, None]
+    assert L.vapi_paged_attention_append(pool(), 0, 1, 1, 1, *args) == _lib.ESPACE
 
 
 def test_block_bytes_is_layers_times_kv_times_block():

@@ -108,6 +108,36 @@ def test_append_matches_the_oracle_bit_exactly(layout, dtype, kvh, d):
 
 
 @pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("dtype,kvh,d", [(torch.bfloat16, 8, 128), (torch.float32, 3, 5)])
+def test_a_multi_layer_append_is_one_append_per_layer(layout, dtype, kvh, d):
+    """vapi_kv_append_layers over layers 1..3 of a 4-layer pool, the rows of
+    each layer a slice of a wider tensor (layer stride != rows): every layer
+    equals the oracle's scatter of its rows; layer 0 is untouched."""
+    from vapi_amd.cache import write_kv_to_cache_layers
+    rng = np.random.default_rng(12)
+    bs, nb, n, L = 16, 64, 200, 4
+    c = PagedKvCache(L, nb, bs, kvh, d, dtype, layout)
+    c._slab.copy_(torch.randn(c._slab.shape, device=DEV).to(dtype))
+    slots = rng.permutation(nb * bs)[:n].astype(np.uint32)
+    slots[rng.choice(n, 9, replace=False)] = _lib.SLOT_SKIP
+    slots[0] = nb * bs + 3  # past the end: dropped on the device
+    wide_k = torch.randn(L - 1, n + 7, kvh, d, device=DEV).to(dtype)
+    wide_v = torch.randn(L - 1, n + 7, kvh, d, device=DEV).to(dtype)
+    k, v = wide_k[:, 3:3 + n], wide_v[:, 3:3 + n]
+    want = {(l, w): as_np(ref_pool(c, l, w)) for l in range(L) for w in "kv"}
+    dropped = slots.copy()
+    dropped[0] = _lib.SLOT_SKIP  # the oracle rejects what the device drops
+    for l in range(1, L):
+        oracle.write_rows(want[(l, "k")], as_np(k[l - 1]), dropped)
+        oracle.write_rows(want[(l, "v")], as_np(v[l - 1]), dropped)
+    idx = torch.from_numpy(slots.view(np.int32)).to(DEV)
+    write_kv_to_cache_layers(c, 1, k, v, idx)
+    torch.cuda.synchronize()
+    for (l, w), arr in want.items():
+        np.testing.assert_array_equal(as_np(ref_pool(c, l, w)), arr, err_msg=f"layer {l} {w}")
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
 def test_config1_append_full_size_is_bit_exact(layout):
     """BASELINE config 1 at full size: 4,096 tokens (5% padded) into a
     65,536-block bf16 pool pre-filled with noise; the whole pool (4 GiB) must

@@ -22,7 +22,7 @@ EXPORTS = (
     "vapi_kv_last_error", "vapi_kv_version", "vapi_kv_block_bytes",
     "vapi_kv_layer_bytes", "vapi_kv_append", "vapi_kv_gather",
     "vapi_paged_attention_workspace_size", "vapi_paged_attention",
-    "vapi_paged_attention_append",
+    "vapi_paged_attention_append", "vapi_kv_append_layers",
     "vapi_kv_copy_blocks", "vapi_kv_export_blocks", "vapi_kv_import_blocks",
     "vapi_kv_swap_out", "vapi_kv_swap_in", "vapi_forward_batch_validate",
     "vapi_pack_block_tables", "vapi_cache_new", "vapi_cache_free",
@@ -89,6 +89,8 @@ def lib():
     L.vapi_paged_attention_append.argtypes = [
         _poolp, _u32, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
         _u32, ctypes.c_float, _i32, _i32, _vp, _sz, _vp]
+    L.vapi_kv_append_layers.argtypes = [_poolp, _u32, _u32, _vp, _vp, ctypes.c_uint64, _vp,
+                                         _u32, _vp]
     L.vapi_kv_copy_blocks.argtypes = [_poolp, _vp, _u32, _vp]
     L.vapi_kv_export_blocks.argtypes = [_poolp, _vp, _u32, _vp, _vp]
     L.vapi_kv_import_blocks.argtypes = [_poolp, _vp, _u32, _vp, _vp]

@@ -148,6 +148,30 @@ def write_rows_indexed(cache: PagedKvCache, layer: int, k: torch.Tensor, v: torc
                                idx.data_ptr(), k.shape[0], stream_handle(stream)))
 
 
+def write_kv_to_cache_layers(cache: PagedKvCache, layer0: int, k: torch.Tensor,
+                             v: torch.Tensor, idx: torch.Tensor, stream=None) -> None:
+    """One step's K/V for layers layer0 .. layer0 + L - 1 in one launch: k, v
+    are [L, n, num_kv_heads, head_dim] (any common stride between layers,
+    rows contiguous within one) and idx a device u32 (int32 view) slot per
+    row. Equals L single-layer appends."""
+    if k.dim() != 4 or tuple(k.shape) != tuple(v.shape):
+        raise ValueError(f"k/v must be (layers, n, heads, width), got {tuple(k.shape)} "
+                         f"and {tuple(v.shape)}")
+    if tuple(k.shape[2:]) != (cache.num_kv_heads, cache.head_dim):
+        raise ValueError(f"rows {tuple(k.shape)} do not match the cache's "
+                         f"({cache.num_kv_heads}, {cache.head_dim})")
+    if k.dtype != cache.dtype or v.dtype != cache.dtype:
+        raise ValueError(f"cache is {cache.dtype} but the rows are {k.dtype}")
+    if idx.dim() != 1 or idx.shape[0] != k.shape[1] or idx.dtype not in (torch.int32,
+                                                                         torch.uint32):
+        raise ValueError("idx must hold one 32-bit slot per row")
+    if not (k[0].is_contiguous() and v[0].is_contiguous()) or k.stride(0) != v.stride(0):
+        raise ValueError("each layer's rows must be contiguous, with one layer stride for K and V")
+    check(lib().vapi_kv_append_layers(cache.pool, layer0, k.shape[0], k.data_ptr(), v.data_ptr(),
+                                      k.stride(0) * k.element_size(), idx.data_ptr(),
+                                      k.shape[1], stream_handle(stream)))
+
+
 def gather_kv(cache: PagedKvCache, layer: int, block_table, len_k: int,
               which: str = "k", stream=None) -> torch.Tensor:
     """One sequence's K (or V) rows in logical order, [len_k, kvh, d]

@@ -64,11 +64,18 @@ struct AppendArgs {
   FastDiv upr, kvh, bs;
   uint32_t row_bytes;  // head_dim * elt
   uint64_t blk_b, head_b, tok_b;  // byte strides
+  uint64_t src_layer_b, dst_layer_b;  // layer strides (grid y = layer)
 };
 
 template <int C, int ITEMS>
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   using V = typename Chunk<C>::T;
+  // Layer blockIdx.y of a multi-layer append (0 for one layer).
+  const uint64_t ly = blockIdx.y;
+  a.k_src += ly * a.src_layer_b;
+  a.v_src += ly * a.src_layer_b;
+  a.k_dst += ly * a.dst_layer_b;
+  a.v_dst += ly * a.dst_layer_b;
   const uint32_t base = blockIdx.x * (256u * ITEMS) + threadIdx.x;
   V val[ITEMS];
   char* dst[ITEMS];
@@ -105,10 +112,10 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
 // thread ran 12.3 us per call against 20.7 / 21 / 12.7 / 16.5 us for
 // 2 / 4 / 8 / 16.
 template <int C>
-static void launch_append(const AppendArgs& a, hipStream_t s) {
+static void launch_append(const AppendArgs& a, uint32_t layers, hipStream_t s) {
   constexpr int ITEMS = 1;
   uint32_t grid = (a.total + 256 * ITEMS - 1) / (256 * ITEMS);
-  hipLaunchKernelGGL((kv_append_kernel<C, ITEMS>), dim3(grid), dim3(256), 0, s,
+  hipLaunchKernelGGL((kv_append_kernel<C, ITEMS>), dim3(grid, layers), dim3(256), 0, s,
                      a);
 }
 
@@ -295,25 +302,36 @@ size_t vapi_kv_layer_bytes(const vapi_kv_pool* p) {
          p->head_dim * dtype_size(p->dtype);
 }
 
-int vapi_kv_append(const vapi_kv_pool* pool, uint32_t layer, const void* k_src,
-                   const void* v_src, const uint32_t* slot_mapping,
-                   uint32_t n_tokens, vapi_stream_t stream) {
-  if (int rc = check_pool(pool, "vapi_kv_append")) return rc;
-  if (layer >= pool->num_layers)
-    VK_FAIL(VAPI_KV_EINVAL, "vapi_kv_append: layer %u of %u", layer,
+// One launch over layers [layer0, layer0 + n_layers): layer l's rows at
+// k_src/v_src + (l - layer0) * src_layer_stride bytes.
+static int append_impl(const char* who, const vapi_kv_pool* pool, uint32_t layer0,
+                       uint32_t n_layers, const void* k_src, const void* v_src,
+                       uint64_t src_layer_stride, const uint32_t* slot_mapping,
+                       uint32_t n_tokens, vapi_stream_t stream) {
+  if (int rc = check_pool(pool, who)) return rc;
+  if (n_layers == 0 || layer0 >= pool->num_layers || n_layers > pool->num_layers - layer0)
+    VK_FAIL(VAPI_KV_EINVAL, "%s: layers %u..%u of %u", who, layer0, layer0 + n_layers,
             pool->num_layers);
   if (n_tokens == 0) return 0;
   if (!k_src || !v_src || !slot_mapping)
-    VK_FAIL(VAPI_KV_EINVAL, "vapi_kv_append: null source or slot_mapping");
+    VK_FAIL(VAPI_KV_EINVAL, "%s: null source or slot_mapping", who);
+  if (n_layers > 65535) VK_FAIL(VAPI_KV_EUNSUP, "%s: %u layers in one call", who, n_layers);
   const Geom g = make_geom(pool);
   const uint32_t elt = dtype_size(pool->dtype);
   const uint32_t row_bytes = g.d * elt;
-  const int c = chunk_bytes_for(row_bytes);
+  if (n_layers > 1 && src_layer_stride < (uint64_t)n_tokens * g.kvh * row_bytes)
+    VK_FAIL(VAPI_KV_EINVAL, "%s: source layer stride %llu < %u rows of %u heads", who,
+            (unsigned long long)src_layer_stride, n_tokens, g.kvh);
+  // Chunk size: the largest power of two up to 16 B that divides the row,
+  // the source addresses and (several layers) both layer strides.
+  int c = chunk_bytes_for(row_bytes);
+  const uint64_t align = (uint64_t)(uintptr_t)k_src | (uint64_t)(uintptr_t)v_src |
+                         (n_layers > 1 ? src_layer_stride | pool->layer_stride_bytes : 0);
+  while (c > 1 && align % c) c >>= 1;
   const uint64_t total = (uint64_t)n_tokens * 2 * g.kvh * (row_bytes / c);
   if (total >= (1ull << 31))
-    VK_FAIL(VAPI_KV_EUNSUP, "vapi_kv_append: %u tokens is too many for one call",
-            n_tokens);
-  LayerPtrs lp = layer_ptrs(pool, layer);
+    VK_FAIL(VAPI_KV_EUNSUP, "%s: %u tokens is too many for one call", who, n_tokens);
+  LayerPtrs lp = layer_ptrs(pool, layer0);
   AppendArgs a;
   a.k_src = (const char*)k_src;
   a.v_src = (const char*)v_src;
@@ -329,11 +347,28 @@ int vapi_kv_append(const vapi_kv_pool* pool, uint32_t layer, const void* k_src,
   a.blk_b = g.blk * elt;
   a.head_b = g.head * elt;
   a.tok_b = g.tok * elt;
-#define L_APPEND(C) launch_append<C>(a, hs(stream))
+  a.src_layer_b = n_layers > 1 ? src_layer_stride : 0;
+  a.dst_layer_b = n_layers > 1 ? pool->layer_stride_bytes : 0;
+#define L_APPEND(C) launch_append<C>(a, n_layers, hs(stream))
   VK_DISPATCH_CHUNK(c, L_APPEND)
 #undef L_APPEND
   VK_LAUNCHED("kv_append");
   return 0;
+}
+
+int vapi_kv_append(const vapi_kv_pool* pool, uint32_t layer, const void* k_src,
+                   const void* v_src, const uint32_t* slot_mapping,
+                   uint32_t n_tokens, vapi_stream_t stream) {
+  return append_impl("vapi_kv_append", pool, layer, 1, k_src, v_src, 0, slot_mapping,
+                     n_tokens, stream);
+}
+
+int vapi_kv_append_layers(const vapi_kv_pool* pool, uint32_t layer0, uint32_t n_layers,
+                          const void* k_src, const void* v_src, uint64_t src_layer_stride,
+                          const uint32_t* slot_mapping, uint32_t n_tokens,
+                          vapi_stream_t stream) {
+  return append_impl("vapi_kv_append_layers", pool, layer0, n_layers, k_src, v_src,
+                     src_layer_stride, slot_mapping, n_tokens, stream);
 }
 
 int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
