@@ -290,6 +290,32 @@ def bench_blocks(steps, warmup, decode):
     h2d = on_side(lambda: _copy_on(side, probe, ph))
     link = dict(d2h_gbs=(1 << 30) / (d2h * 1e-3) / 1e9, h2d_gbs=(1 << 30) / (h2d * 1e-3) / 1e9)
     gb = n * bb / 1e9
+    # Spill tier: 512 evicted blocks into a host-memory store through a
+    # 64-block pinned buffer, then promoted into other blocks (batched
+    # spill_evicted / promote_from_spill), wall clock.
+    from vapi_amd.spill import SpillStore, pinned_buffer, promote, spill_evicted
+    ns = 512
+    hs = [int(i).to_bytes(32, "little") for i in range(ns)]
+    store = SpillStore(None, ns * bb, 0)
+    pin = pinned_buffer(cache, 64)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    exported = spill_evicted(store, cache, zip(hs, w.swap_ids[:ns].tolist()), pin)
+    t1 = time.perf_counter()
+    restored = promote(store, cache, hs, w.swap_in_ids[:ns].tolist(), pin)
+    t2 = time.perf_counter()
+    spill_ok = exported == ns and restored == ns and all(
+        be.export_block(int(w.swap_ids[i])) == be.export_block(int(w.swap_in_ids[i]))
+        for i in (0, ns // 2, ns - 1))
+    spill = dict(blocks=ns, export_us_per_block=(t1 - t0) * 1e6 / ns,
+                 import_us_per_block=(t2 - t1) * 1e6 / ns,
+                 export_gbs=ns * bb / (t1 - t0) / 1e9, import_gbs=ns * bb / (t2 - t1) / 1e9,
+                 round_trip_bit_exact=bool(spill_ok))
+    log(f"spill tier: {ns} blocks out {spill['export_us_per_block']:.0f} us/block "
+        f"({spill['export_gbs']:.1f} GB/s), back {spill['import_us_per_block']:.0f} us/block "
+        f"({spill['import_gbs']:.1f} GB/s)")
+    store.close()
+    del pin
     res = dict(copy_ms=ms, copy_gbs=copy_gbs, copy_frac=copy_gbs / HBM_PEAK_GBS,
                copy_bit_exact=bool(copy_ok),
                swap_out_gbs=gb / (out_ms * 1e-3), swap_in_gbs=gb / (in_ms * 1e-3),
@@ -297,7 +323,7 @@ def bench_blocks(steps, warmup, decode):
                swap_out_overlapped_gbs=gb / (overlap_out_ms * 1e-3),
                decode_us_alone=dec_alone * 1e3,
                decode_us_during_swap=float(np.median(dec_ms)) * 1e3 if dec_ms else None,
-               pinned_probe=link, swap_bytes_per_direction=n * bb)
+               pinned_probe=link, swap_bytes_per_direction=n * bb, spill_tier=spill)
     log(f"swap cfg4b: out {res['swap_out_gbs']:.1f} GB/s, in {res['swap_in_gbs']:.1f} GB/s, "
         f"pinned probe d2h {link['d2h_gbs']:.1f} h2d {link['h2d_gbs']:.1f}; decode "
         f"{res['decode_us_alone']:.0f} us alone, {res['decode_us_during_swap']} us during swap")

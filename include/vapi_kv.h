@@ -254,6 +254,66 @@ int vapi_kv_swap_in(const vapi_kv_pool* pool, const uint32_t* ids, uint32_t n,
                     vapi_stream_t stream);
 
 /*
+ * Spill store: exported blocks kept in host memory, with an optional disk
+ * tier behind it, both least-recently-used. Replaces SpillStore
+ * (crates/vapi-cache/src/spill.rs:43-212) with the same behaviour: put()
+ * ignores a hash already held and drops a blob that fits neither tier;
+ * host memory over its cap pushes its oldest entries to disk (or drops
+ * them without a disk tier); a disk hit is not promoted back into memory;
+ * a disk entry that cannot be read is forgotten and counted as an error.
+ * Keys are 32-byte block hashes; disk entries are "<64 hex>.kv" files of
+ * the export byte order, indexed again when a store opens the directory.
+ * The store is host-only and not thread-safe (one engine thread).
+ */
+typedef struct vapi_spill_store vapi_spill_store;
+typedef struct vapi_spill_stats {
+  uint64_t ram_blocks, ram_bytes, disk_blocks, disk_bytes;
+  uint64_t hits;   /* blocks handed back */
+  uint64_t misses; /* blocks asked for and not held */
+  uint64_t writes;
+  uint64_t drops;  /* blocks dropped because both tiers were full */
+  uint64_t errors;
+} vapi_spill_stats;
+
+/* dir = NULL (or disk_max = 0): host memory only. Allocates the store. */
+int vapi_spill_open(const char* dir, uint64_t ram_max, uint64_t disk_max,
+                    vapi_spill_store** out);
+void vapi_spill_close(vapi_spill_store* store);
+int vapi_spill_contains(const vapi_spill_store* store, const uint8_t* hash32);
+int vapi_spill_put(vapi_spill_store* store, const uint8_t* hash32, const void* bytes,
+                   size_t len);
+/* Copies the blob into out: its length, -1 if not held (a miss), or
+ * VAPI_KV_ESPACE if cap is too small (nothing counted). */
+int64_t vapi_spill_get(vapi_spill_store* store, const uint8_t* hash32, void* out, size_t cap);
+void vapi_spill_get_stats(const vapi_spill_store* store, vapi_spill_stats* out);
+
+/*
+ * spill_evicted (crates/vapi-worker/src/engine.rs:369-393) for a batch:
+ * ids/hashes (host arrays, n and n*32 bytes) are the blocks the pool just
+ * evicted; those the store does not hold are exported in batches with
+ * vapi_kv_export_blocks into `pinned` (hipHostMalloc memory of at least
+ * 4096 + vapi_kv_block_bytes bytes; its first 4 KiB stage the ids) and put
+ * into the store. Synchronous on `stream`: the blocks may be overwritten
+ * once it returns. Returns the number exported, or a negative error.
+ */
+int64_t vapi_spill_evicted(vapi_spill_store* store, const vapi_kv_pool* pool,
+                           const uint32_t* ids, const uint8_t* hashes, uint32_t n,
+                           void* pinned, size_t pinned_bytes, vapi_stream_t stream);
+
+/*
+ * The device half of promote_from_spill (engine.rs:400-456): hashes[0..n)
+ * are a prompt's block chain and ids[0..n) (host) the blocks allocated for
+ * them. Blobs are taken in order up to the first hash the store does not
+ * hold (counted as a miss, as the reference's get() does) and imported
+ * with vapi_kv_import_blocks through `pinned` (sized as for
+ * vapi_spill_evicted). A blob that is not vapi_kv_block_bytes long is an
+ * error (backend.rs:739-745). Returns the number restored (a prefix).
+ */
+int64_t vapi_spill_promote(vapi_spill_store* store, const vapi_kv_pool* pool,
+                           const uint8_t* hashes, const uint32_t* ids, uint32_t n,
+                           void* pinned, size_t pinned_bytes, vapi_stream_t stream);
+
+/*
  * Host-side check of a step descriptor: ForwardBatch::validate
  * (crates/vapi-engine/src/backend.rs:96-204). All arrays are host memory.
  * block_tables is ragged: row i is table_data[table_offsets[i] ..

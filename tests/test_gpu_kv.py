@@ -318,3 +318,42 @@ def test_a_fork_executed_through_copy_blocks_gives_every_child_the_parent_kv(lay
     assert all(np.array_equal(a, b) for a, b in zip(before, after))
     mine = gather_kv(cache, 0, children[0], computed, "k")
     assert torch.equal(mine[40], row[0]) and not torch.equal(mine[40], gather_kv(cache, 0, parent, computed, "k")[40])
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_spilled_blocks_come_back_bit_exact_through_host_memory_and_disk(layout, tmp_path):
+    """spill_evicted then promote_from_spill (engine.rs:369-456), batched:
+    20 evicted blocks go through a pinned buffer of 3 blocks into a store
+    whose host memory holds 8 (the rest on disk); every stored blob is the
+    reference's export byte order, and the blobs promoted into other blocks
+    equal the originals. A chain is restored up to its first missing hash."""
+    import hashlib
+    from vapi_amd.spill import SpillStore, pinned_buffer, promote, spill_evicted
+    L, nb, n = 3, 64, 20
+    c = PagedKvCache(L, nb, 16, 4, 128, torch.bfloat16, layout)
+    workload.fill_normal(c._slab, 8)
+    be = KvBlockBackend(c)
+    bb = be.block_bytes()
+    rng = np.random.default_rng(9)
+    perm = rng.permutation(nb)
+    out_ids, in_ids = perm[:n].tolist(), perm[n:2 * n].tolist()
+    hs = [hashlib.sha256(b"chain %d" % i).digest() for i in range(n)]
+    ks = [as_np(ref_pool(c, l, "k")) for l in range(L)]
+    vs = [as_np(ref_pool(c, l, "v")) for l in range(L)]
+    store = SpillStore(tmp_path, 8 * bb, 1 << 30)
+    pinned = pinned_buffer(c, 3)
+    assert spill_evicted(store, c, zip(hs, out_ids), pinned) == n
+    st = store.stats()
+    assert (st["ram_blocks"], st["disk_blocks"], st["writes"]) == (8, n - 8, n)
+    assert spill_evicted(store, c, zip(hs, out_ids), pinned) == 0  # all held already
+    for h, b in zip(hs, out_ids):
+        assert store.get(h, bb) == oracle.export_block(ks, vs, b)
+    assert promote(store, c, hs, in_ids, pinned) == n
+    for a, b in zip(out_ids, in_ids):
+        assert be.export_block(b) == be.export_block(a)
+    missing = hashlib.sha256(b"never spilled").digest()
+    chain = hs[:5] + [missing] + hs[5:7]
+    before = store.stats()
+    assert promote(store, c, chain, perm[40:48].tolist(), pinned) == 5
+    after = store.stats()
+    assert (after["hits"] - before["hits"], after["misses"] - before["misses"]) == (5, 1)

@@ -29,6 +29,8 @@ EXPORTS = (
     "vapi_cache_pool", "vapi_cache_num_slots", "vapi_cache_write_kv",
     "vapi_cache_block_bytes", "vapi_cache_export_block",
     "vapi_cache_import_block", "vapi_cache_copy_blocks",
+    "vapi_spill_open", "vapi_spill_close", "vapi_spill_contains", "vapi_spill_put",
+    "vapi_spill_get", "vapi_spill_get_stats", "vapi_spill_evicted", "vapi_spill_promote",
 )
 
 
@@ -61,6 +63,13 @@ _i32 = ctypes.c_int32
 _sz = ctypes.c_size_t
 _u32p = ctypes.POINTER(ctypes.c_uint32)
 _poolp = ctypes.POINTER(Pool)
+
+
+class SpillStats(ctypes.Structure):
+    """vapi_spill_stats (SpillStats, spill.rs:27-40)."""
+    _fields_ = [(n, ctypes.c_uint64) for n in (
+        "ram_blocks", "ram_bytes", "disk_blocks", "disk_bytes", "hits", "misses", "writes",
+        "drops", "errors")]
 
 
 def lib():
@@ -112,6 +121,20 @@ def lib():
     L.vapi_cache_export_block.argtypes = [_vp, _u32, _vp, _sz]
     L.vapi_cache_import_block.argtypes = [_vp, _u32, _vp, _sz]
     L.vapi_cache_copy_blocks.argtypes = [_vp, _u32p, _u32]
+    L.vapi_spill_open.argtypes = [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_uint64,
+                                  ctypes.POINTER(_vp)]
+    L.vapi_spill_close.argtypes = [_vp]
+    L.vapi_spill_close.restype = None
+    L.vapi_spill_contains.argtypes = [_vp, _vp]
+    L.vapi_spill_put.argtypes = [_vp, _vp, _vp, _sz]
+    L.vapi_spill_get.argtypes = [_vp, _vp, _vp, _sz]
+    L.vapi_spill_get.restype = ctypes.c_int64
+    L.vapi_spill_get_stats.argtypes = [_vp, ctypes.POINTER(SpillStats)]
+    L.vapi_spill_get_stats.restype = None
+    L.vapi_spill_evicted.argtypes = [_vp, _poolp, _u32p, _vp, _u32, _vp, _sz, _vp]
+    L.vapi_spill_evicted.restype = ctypes.c_int64
+    L.vapi_spill_promote.argtypes = [_vp, _poolp, _vp, _u32p, _u32, _vp, _sz, _vp]
+    L.vapi_spill_promote.restype = ctypes.c_int64
     _lib = L
     return L
 

@@ -35,7 +35,7 @@ COMMON_FLAGS = [
 ]
 
 SOURCES = ["kv_ops.hip", "attention.hip", "attn_decode.hip", "attn_prefill.hip",
-           "attn_generic.hip", "host.cpp"]
+           "attn_generic.hip", "host.cpp", "spill.cpp"]
 
 # The MFMA attention kernels never produce NaN from finite K/V/Q (masked
 # scores are -inf, running maxima start finite), so fmaxf on MFMA results

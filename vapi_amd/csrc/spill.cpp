@@ -1,0 +1,427 @@
+// Spill tier: a host-memory store of exported KV blocks with an optional disk
+// tier behind it, both least-recently-used (vapi's SpillStore,
+// crates/vapi-cache/src/spill.rs:43-212), and the two engine steps that move
+// blocks between it and the pool in batches (spill_evicted and the device
+// half of promote_from_spill, crates/vapi-worker/src/engine.rs:369-456).
+//
+// Entries are keyed by the 32-byte block hash; a disk entry is the file
+// "<64 lowercase hex>.kv" holding the block's blob in the export byte order
+// (K of every layer, then V of every layer, each [block_size, kv_heads,
+// head_dim]), so spill files are interchangeable with the reference's.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <filesystem>
+#include <fstream>
+#include <list>
+#include <string>
+#include <thread>
+#include <unordered_map>
+#include <vector>
+
+#include "common.hpp"
+
+using namespace vk;
+namespace fs = std::filesystem;
+
+namespace {
+
+struct Hash {
+  uint8_t b[32];
+  bool operator==(const Hash& o) const { return std::memcmp(b, o.b, 32) == 0; }
+};
+struct HashHash {
+  size_t operator()(const Hash& h) const {
+    size_t x;
+    std::memcpy(&x, h.b, sizeof(x));  // already a cryptographic hash
+    return x;
+  }
+};
+
+Hash to_hash(const uint8_t* p) {
+  Hash h;
+  std::memcpy(h.b, p, 32);
+  return h;
+}
+
+std::string to_hex(const Hash& h) {
+  static const char* d = "0123456789abcdef";
+  std::string s(64, '0');
+  for (int i = 0; i < 32; ++i) {
+    s[2 * i] = d[h.b[i] >> 4];
+    s[2 * i + 1] = d[h.b[i] & 15];
+  }
+  return s;
+}
+
+// Inverse of to_hex (either case, as from_str_radix accepts); false for any
+// other name, so stray files in the directory are ignored.
+bool from_hex(const std::string& s, Hash& h) {
+  if (s.size() != 64) return false;
+  auto nib = [](char c) -> int {
+    if (c >= '0' && c <= '9') return c - '0';
+    if (c >= 'a' && c <= 'f') return c - 'a' + 10;
+    if (c >= 'A' && c <= 'F') return c - 'A' + 10;
+    return -1;
+  };
+  for (int i = 0; i < 32; ++i) {
+    const int hi = nib(s[2 * i]), lo = nib(s[2 * i + 1]);
+    if (hi < 0 || lo < 0) return false;
+    h.b[i] = (uint8_t)(hi << 4 | lo);
+  }
+  return true;
+}
+
+// An LRU index: least recently used at the front.
+template <typename V>
+struct Lru {
+  std::list<Hash> order;
+  std::unordered_map<Hash, std::pair<V, std::list<Hash>::iterator>, HashHash> map;
+  bool contains(const Hash& h) const { return map.count(h) != 0; }
+  void push(const Hash& h, V v) {
+    order.push_back(h);
+    map.emplace(h, std::make_pair(std::move(v), std::prev(order.end())));
+  }
+  void touch(const Hash& h) {
+    auto it = map.find(h);
+    order.splice(order.end(), order, it->second.second);
+  }
+  V* find(const Hash& h) {
+    auto it = map.find(h);
+    return it == map.end() ? nullptr : &it->second.first;
+  }
+  bool pop_front(Hash& h, V& v) {
+    if (order.empty()) return false;
+    h = order.front();
+    order.pop_front();
+    auto it = map.find(h);
+    v = std::move(it->second.first);
+    map.erase(it);
+    return true;
+  }
+  bool erase(const Hash& h, V& v) {
+    auto it = map.find(h);
+    if (it == map.end()) return false;
+    v = std::move(it->second.first);
+    order.erase(it->second.second);
+    map.erase(it);
+    return true;
+  }
+};
+
+// f(i) for i in [0, n) on up to 8 threads: the blob copies of a batch
+// (page faults of fresh host memory and the copy itself) cost ~150 us per
+// 0.9 MB block on one thread, several times the PCIe transfer.
+template <typename F>
+void parallel_for(uint32_t n, F f) {
+  const uint32_t t = std::min<uint32_t>(n, std::max(1u, std::min(8u, std::thread::hardware_concurrency())));
+  if (t <= 1) {
+    for (uint32_t i = 0; i < n; ++i) f(i);
+    return;
+  }
+  std::vector<std::thread> pool;
+  for (uint32_t k = 0; k < t; ++k)
+    pool.emplace_back([&, k] {
+      for (uint32_t i = k; i < n; i += t) f(i);
+    });
+  for (auto& th : pool) th.join();
+}
+
+}  // namespace
+
+struct vapi_spill_store {
+  Lru<std::vector<uint8_t>> ram;
+  uint64_t ram_max = 0, ram_bytes = 0;
+  bool has_dir = false;
+  fs::path dir;
+  Lru<uint64_t> disk;  // value: file length
+  uint64_t disk_max = 0, disk_bytes = 0;
+  vapi_spill_stats st{};
+
+  fs::path path(const Hash& h) const { return dir / (to_hex(h) + ".kv"); }
+
+  void evict_disk() {
+    Hash h;
+    uint64_t len;
+    while (disk_bytes > disk_max && disk.pop_front(h, len)) {
+      std::error_code ec;
+      fs::remove(path(h), ec);
+      disk_bytes -= len;
+    }
+  }
+
+  // Push host-memory entries out to disk until the cap is met.
+  void evict_ram() {
+    Hash h;
+    std::vector<uint8_t> bytes;
+    while (ram_bytes > ram_max && ram.pop_front(h, bytes)) {
+      ram_bytes -= bytes.size();
+      if (!has_dir || bytes.size() > disk_max) {
+        ++st.drops;
+        continue;
+      }
+      std::ofstream f(path(h), std::ios::binary | std::ios::trunc);
+      f.write((const char*)bytes.data(), (std::streamsize)bytes.size());
+      f.close();
+      if (!f) {
+        ++st.errors;
+        continue;
+      }
+      disk_bytes += bytes.size();
+      disk.push(h, bytes.size());
+      evict_disk();
+    }
+  }
+
+  bool holds(const Hash& h) const { return ram.contains(h) || disk.contains(h); }
+
+  // SpillStore::put (spill.rs:128-146), taking the blob's buffer.
+  void put(const Hash& h, std::vector<uint8_t>&& bytes) {
+    if (holds(h)) return;
+    const uint64_t len = bytes.size();
+    if (len > ram_max && len > disk_max) {
+      ++st.drops;
+      return;
+    }
+    ++st.writes;
+    ram_bytes += len;
+    ram.push(h, std::move(bytes));
+    evict_ram();
+  }
+  void put(const Hash& h, const uint8_t* p, size_t len) {
+    if (holds(h)) return;
+    put(h, std::vector<uint8_t>(p, p + len));
+  }
+
+  // The entry's bytes into `out` (capacity `cap`): its length, -1 if not
+  // held, VAPI_KV_ESPACE (nothing counted) if it does not fit.
+  int64_t get(const Hash& h, void* out, size_t cap) {
+    if (auto* v = ram.find(h)) {
+      if (v->size() > cap) return VAPI_KV_ESPACE;
+      std::memcpy(out, v->data(), v->size());
+      ram.touch(h);
+      ++st.hits;
+      return (int64_t)v->size();
+    }
+    if (auto* len = disk.find(h)) {
+      if (*len > cap) return VAPI_KV_ESPACE;
+      std::ifstream f(path(h), std::ios::binary);
+      const uint64_t n = *len;
+      if (f && f.read((char*)out, (std::streamsize)n) && f.gcount() == (std::streamsize)n) {
+        disk.touch(h);
+        ++st.hits;
+        return (int64_t)n;
+      }
+      uint64_t gone;  // deleted under us, or unreadable: forget it
+      disk.erase(h, gone);
+      disk_bytes -= gone;
+      ++st.errors;
+    }
+    ++st.misses;
+    return -1;
+  }
+};
+
+extern "C" {
+
+int vapi_spill_open(const char* dir, uint64_t ram_max, uint64_t disk_max,
+                    vapi_spill_store** out) {
+  clear_error();
+  if (!out) VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_open: null out");
+  *out = nullptr;
+  auto* s = new vapi_spill_store();
+  s->ram_max = ram_max;
+  s->disk_max = disk_max;
+  if (dir && *dir && disk_max > 0) {
+    std::error_code ec;
+    fs::create_directories(dir, ec);
+    if (ec) {
+      delete s;
+      VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_open: cannot create %s: %s", dir,
+              ec.message().c_str());
+    }
+    s->dir = dir;
+    s->has_dir = true;
+    // Index what a previous run left: a hash pins the model and its
+    // weights, so those blocks are still valid.
+    for (const auto& e : fs::directory_iterator(s->dir, ec)) {
+      Hash h;
+      if (!e.is_regular_file() || e.path().extension() != ".kv" ||
+          !from_hex(e.path().stem().string(), h))
+        continue;
+      const uint64_t len = e.file_size();
+      s->disk.push(h, len);
+      s->disk_bytes += len;
+    }
+    s->evict_disk();
+  }
+  *out = s;
+  return 0;
+}
+
+void vapi_spill_close(vapi_spill_store* s) { delete s; }
+
+int vapi_spill_contains(const vapi_spill_store* s, const uint8_t* hash) {
+  if (!s || !hash) return 0;
+  const Hash h = to_hash(hash);
+  return s->ram.contains(h) || s->disk.contains(h);
+}
+
+int vapi_spill_put(vapi_spill_store* s, const uint8_t* hash, const void* bytes, size_t len) {
+  clear_error();
+  if (!s || !hash || (len && !bytes)) VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_put: null argument");
+  s->put(to_hash(hash), (const uint8_t*)bytes, len);
+  return 0;
+}
+
+int64_t vapi_spill_get(vapi_spill_store* s, const uint8_t* hash, void* out, size_t cap) {
+  clear_error();
+  if (!s || !hash || (cap && !out)) VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_get: null argument");
+  const int64_t n = s->get(to_hash(hash), out, cap);
+  if (n == VAPI_KV_ESPACE) VK_FAIL(VAPI_KV_ESPACE, "vapi_spill_get: %zu bytes is too small", cap);
+  return n;
+}
+
+void vapi_spill_get_stats(const vapi_spill_store* s, vapi_spill_stats* out) {
+  if (!s || !out) return;
+  *out = s->st;
+  out->ram_blocks = s->ram.map.size();
+  out->ram_bytes = s->ram_bytes;
+  out->disk_blocks = s->disk.map.size();
+  out->disk_bytes = s->disk_bytes;
+}
+
+// spill_evicted (engine.rs:369-393) for n evicted blocks at once: the blocks
+// the store does not hold yet are exported with vapi_kv_export_blocks into
+// `pinned` (hipHostMalloc memory the kernel writes directly; the block ids
+// are staged at its start) in as many rounds as it needs, and each blob is
+// put into the store. Returns the number exported; the blocks may be
+// overwritten once it returns.
+int64_t vapi_spill_evicted(vapi_spill_store* s, const vapi_kv_pool* pool, const uint32_t* ids,
+                           const uint8_t* hashes, uint32_t n, void* pinned, size_t pinned_bytes,
+                           vapi_stream_t stream) {
+  clear_error();
+  if (int rc = check_pool(pool, "vapi_spill_evicted")) return rc;
+  if (!s || (n && (!ids || !hashes || !pinned)))
+    VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_evicted: null argument");
+  const size_t bb = vapi_kv_block_bytes(pool);
+  const size_t head = 4096;  // id staging, 1,024 ids per round at most
+  if (pinned_bytes < head + bb)
+    VK_FAIL(VAPI_KV_ESPACE, "vapi_spill_evicted: %zu pinned bytes < %zu (one block)",
+            pinned_bytes, head + bb);
+  const uint32_t per = (uint32_t)std::min<size_t>((pinned_bytes - head) / bb, head / 4);
+  uint32_t* id_stage = (uint32_t*)pinned;
+  uint8_t* blobs = (uint8_t*)pinned + head;
+  std::vector<uint32_t> todo;
+  for (uint32_t i = 0; i < n; ++i)
+    if (!vapi_spill_contains(s, hashes + 32ull * i)) todo.push_back(i);
+  const hipStream_t st = hs(stream);
+  for (size_t at = 0; at < todo.size(); at += per) {
+    const uint32_t m = (uint32_t)std::min<size_t>(per, todo.size() - at);
+    for (uint32_t j = 0; j < m; ++j) id_stage[j] = ids[todo[at + j]];
+    if (int rc = vapi_kv_export_blocks(pool, id_stage, m, blobs, stream)) return rc;
+    VK_HIP(hipStreamSynchronize(st));
+    std::vector<std::vector<uint8_t>> copies(m);
+    parallel_for(m, [&](uint32_t j) {
+      copies[j].assign(blobs + (size_t)j * bb, blobs + (size_t)(j + 1) * bb);
+    });
+    for (uint32_t j = 0; j < m; ++j)
+      s->put(to_hash(hashes + 32ull * todo[at + j]), std::move(copies[j]));
+  }
+  return (int64_t)todo.size();
+}
+
+// The device half of promote_from_spill (engine.rs:400-456): hashes[0..n)
+// are a prompt's block chain and ids[0..n) the blocks allocated for them.
+// Blobs are taken from the store in order up to the first it does not hold
+// (only a contiguous prefix is worth restoring) and imported with
+// vapi_kv_import_blocks through `pinned`. A blob whose length is not
+// vapi_kv_block_bytes is an error (backend.rs:739-745). Returns the number
+// restored.
+int64_t vapi_spill_promote(vapi_spill_store* s, const vapi_kv_pool* pool, const uint8_t* hashes,
+                           const uint32_t* ids, uint32_t n, void* pinned, size_t pinned_bytes,
+                           vapi_stream_t stream) {
+  clear_error();
+  if (int rc = check_pool(pool, "vapi_spill_promote")) return rc;
+  if (!s || (n && (!ids || !hashes || !pinned)))
+    VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_promote: null argument");
+  const size_t bb = vapi_kv_block_bytes(pool);
+  const size_t head = 4096;
+  if (pinned_bytes < head + bb)
+    VK_FAIL(VAPI_KV_ESPACE, "vapi_spill_promote: %zu pinned bytes < %zu (one block)",
+            pinned_bytes, head + bb);
+  const uint32_t per = (uint32_t)std::min<size_t>((pinned_bytes - head) / bb, head / 4);
+  uint32_t* id_stage = (uint32_t*)pinned;
+  uint8_t* blobs = (uint8_t*)pinned + head;
+  const hipStream_t st = hs(stream);
+  uint32_t done = 0;
+  bool more = true;
+  while (more && done < n) {
+    // Resolve this round's chain entries in order, copy (or read from disk)
+    // their blobs into the pinned slots on several threads, then account
+    // in order as a get() per entry would: LRU touch and hit, or for an
+    // unreadable disk entry forget it, count the error and the miss and end
+    // the chain there. A hash the store does not hold ends it too (a miss).
+    struct Src {
+      Hash h;
+      const std::vector<uint8_t>* ram;  // else on disk
+      bool ok;
+    };
+    std::vector<Src> src;
+    bool absent = false;
+    while (src.size() < per && done + src.size() < n) {
+      const Hash h = to_hash(hashes + 32ull * (done + src.size()));
+      const std::vector<uint8_t>* r = s->ram.find(h);
+      const uint64_t* d = r ? nullptr : s->disk.find(h);
+      if (!r && !d) {
+        absent = true;
+        break;
+      }
+      const uint64_t len = r ? r->size() : *d;
+      if (len != bb)
+        VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_promote: blob of %llu bytes, blocks are %zu",
+                (unsigned long long)len, bb);
+      src.push_back(Src{h, r, false});
+    }
+    parallel_for((uint32_t)src.size(), [&](uint32_t k) {
+      uint8_t* dst = blobs + (size_t)k * bb;
+      if (src[k].ram) {
+        std::memcpy(dst, src[k].ram->data(), bb);
+        src[k].ok = true;
+      } else {
+        std::ifstream f(s->path(src[k].h), std::ios::binary);
+        src[k].ok = f && f.read((char*)dst, (std::streamsize)bb) &&
+                    f.gcount() == (std::streamsize)bb;
+      }
+    });
+    uint32_t m = 0;
+    for (; m < src.size(); ++m) {
+      const Hash& h = src[m].h;
+      if (!src[m].ok) {  // deleted under us, or unreadable: forget it
+        uint64_t gone;
+        s->disk.erase(h, gone);
+        s->disk_bytes -= gone;
+        ++s->st.errors;
+        ++s->st.misses;
+        more = false;
+        break;
+      }
+      if (src[m].ram) s->ram.touch(h);
+      else s->disk.touch(h);
+      ++s->st.hits;
+      id_stage[m] = ids[done + m];
+    }
+    if (more && absent) {
+      ++s->st.misses;
+      more = false;
+    }
+    if (!m) break;
+    if (int rc = vapi_kv_import_blocks(pool, id_stage, m, blobs, stream)) return rc;
+    VK_HIP(hipStreamSynchronize(st));
+    done += m;
+  }
+  return done;
+}
+
+}  // extern "C"
