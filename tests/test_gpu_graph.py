@@ -12,14 +12,17 @@ import torch
 
 import oracle
 from vapi_amd import workload
-from vapi_amd.attention import ForwardBatch, PreparedAttention, paged_attention_prepared
+from vapi_amd.attention import (ForwardBatch, PreparedAttention, paged_attention_append_prepared,
+                                paged_attention_prepared)
 from vapi_amd.cache import PagedKvCache, scatter_index, write_rows_indexed, write_kv_to_cache
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def test_a_captured_decode_step_replays_like_the_eager_step():
+@pytest.mark.parametrize("fused", [False, True], ids=["append-then-attention", "fused"])
+def test_a_captured_decode_step_replays_like_the_eager_step(fused):
+    """Per layer either the two calls or vapi_paged_attention_append."""
     rng = np.random.default_rng(33)
     L, nb, bs, hq, kvh, d = 2, 2048, 16, 32, 8, 128
     cache = PagedKvCache(L, nb, bs, kvh, d, torch.bfloat16)
@@ -49,8 +52,12 @@ def test_a_captured_decode_step_replays_like_the_eager_step():
 
     def step():
         for layer in range(L):
-            write_rows_indexed(cache, layer, k_new[layer], v_new[layer], idx)
-            paged_attention_prepared(q[layer], cache, layer, prep, scale, out=out[layer])
+            if fused:
+                paged_attention_append_prepared(q[layer], k_new[layer], v_new[layer], idx, cache,
+                                                layer, prep, scale, out=out[layer])
+            else:
+                write_rows_indexed(cache, layer, k_new[layer], v_new[layer], idx)
+                paged_attention_prepared(q[layer], cache, layer, prep, scale, out=out[layer])
 
     step()  # eager; also allocates the workspace outside the capture
     torch.cuda.synchronize()
