@@ -155,8 +155,8 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
  * window_right: keys k > p + window_right are hidden; 0 = causal, -1 =
  *   unlimited (bidirectional).
  * workspace: device scratch of at least vapi_paged_attention_workspace_size()
- *   bytes (the decode's per-XCD work shares, its plan and split-context
- *   partials); may be NULL when that size is 0. Zero-fill it once before its
+ *   bytes (the decode's per-XCD work shares, per-segment ranges and
+ *   split-context partials); may be NULL when that size is 0. Zero-fill it once before its
  *   first use. Keep one workspace per stream across calls and layers: each
  *   call measures how fast each XCD streamed and moves the shares the next
  *   call on that workspace uses (a fresh workspace starts from equal
@@ -164,7 +164,9 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
  *   split merge. Calls sharing one workspace must not overlap (same stream,
  *   or ordered streams).
  * max_seqlen_q/k must bound every sequence's len_q/len_k (as in
- *   flash-attention); they size the grid and the workspace.
+ *   flash-attention); max_seqlen_q sizes the prefill grid. The workspace
+ *   size depends on the batch, the heads and the GPU's CU count, not on the
+ *   lengths.
  */
 size_t vapi_paged_attention_workspace_size(const vapi_kv_pool* pool,
                                            uint32_t batch, uint32_t num_heads,

@@ -11,7 +11,6 @@ import pytest
 import torch
 
 import oracle
-from vapi_amd import workload
 from vapi_amd.attention import (ForwardBatch, PreparedAttention, paged_attention_append_prepared,
                                 paged_attention_prepared)
 from vapi_amd.cache import PagedKvCache, scatter_index, write_rows_indexed, write_kv_to_cache

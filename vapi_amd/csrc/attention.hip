@@ -47,11 +47,12 @@ size_t vapi_paged_attention_workspace_size(const vapi_kv_pool* pool,
                                            uint32_t max_seqlen_q,
                                            uint32_t max_seqlen_k) {
   (void)max_seqlen_q;
+  (void)max_seqlen_k;
   if (!pool || pool->num_kv_heads == 0 || num_heads % pool->num_kv_heads ||
       !mfma_ok(pool, num_heads) || batch == 0)
     return 0;
   return decode_workspace_bytes(batch, pool->num_kv_heads, num_heads / pool->num_kv_heads,
-                                pool->head_dim, max_seqlen_k, decode_num_waves());
+                                pool->head_dim, decode_num_waves());
 }
 
 int vapi_paged_attention(const vapi_kv_pool* pool, uint32_t layer,
@@ -173,7 +174,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   if (mfma_ok(pool, num_heads)) {
     const bool bf16 = pool->dtype == VAPI_KV_BF16;
     a.num_waves = decode_num_waves();
-    launch_decode(a, workspace, g.d, max_seqlen_k, bf16, s);
+    launch_decode(a, workspace, g.d, bf16, s);
     if (max_seqlen_q > 1) {
       if (batch > 65535)
         VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: %u prefill sequences > 65535", batch);

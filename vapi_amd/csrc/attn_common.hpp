@@ -405,9 +405,8 @@ __device__ __forceinline__ void attend_step(const KVStep<D>& st, const uint4 (&q
 
 // Decode rows (len_q == 1) of the batch; bf16/f16, head_dim 64 or 128.
 size_t decode_workspace_bytes(uint32_t batch, uint32_t kvh, uint32_t group,
-                              uint32_t head_dim, uint32_t max_k, uint32_t num_waves);
-void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t max_k,
-                   bool bf16, hipStream_t s);
+                              uint32_t head_dim, uint32_t num_waves);
+void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, bool bf16, hipStream_t s);
 // Prefill rows (len_q > 1); same dtypes and head dims.
 void launch_prefill(const AttnArgs& a, uint32_t max_q, uint32_t head_dim, bool bf16,
                     hipStream_t s);

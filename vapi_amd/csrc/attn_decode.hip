@@ -577,14 +577,12 @@ static DecodeWs decode_ws(uint32_t b, uint32_t kvh, uint32_t group, uint32_t hea
 }
 
 size_t decode_workspace_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t head_dim,
-                              uint32_t max_k, uint32_t num_waves) {
-  (void)max_k;
+                              uint32_t num_waves) {
   return decode_ws(std::min(batch, kMaxPlanSeqs), kvh, group, head_dim, num_waves).total;
 }
 
-void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t max_k, bool bf16,
+void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, bool bf16,
                    hipStream_t s) {
-  (void)max_k;
   const uint32_t W = a.num_waves;
   const uint32_t nwg = W / kDecodeWavesPerWG;
   const uint32_t total = a.batch;
