@@ -175,6 +175,10 @@ CASES = [
     (torch.float32, 6, 2, 80, 8, [3, 1], [10, 50], 4, "NHD"),
     # Sequences with no new query rows (attention.rs:104-106 skips them).
     (torch.bfloat16, 32, 8, 128, 16, [0, 1, 3, 0, 1], [5, 100, 40, 7, 1], None, "HND"),
+    # Larger blocks on the MFMA paths (a 16-key tile is part of one block).
+    (torch.bfloat16, 32, 8, 128, 64, [1, 20, 1], [1000, 200, 65], None, "HND"),
+    (torch.float16, 16, 4, 64, 128, [1, 33, 1], [700, 300, 129], 50, "NHD"),
+    (torch.bfloat16, 8, 8, 128, 256, [1, 1, 17], [2000, 257, 600], None, "HND"),
 ]
 
 
@@ -349,6 +353,19 @@ def test_more_decode_rows_than_one_launch_plans_for():
     nb = sum(-(-lk // 16) for lk in lens_k)
     c, q, batch = random_case(rng, torch.bfloat16, 8, 2, 128, 16, [1] * 5000, lens_k, "HND")
     assert c.num_blocks >= nb
+    want = oracle_out(q, c, 0, batch, 128 ** -0.5)
+    got = paged_attention(q, c, 0, batch, 128 ** -0.5)
+    assert max_abs(got, want) <= 2e-2 * float(want.abs().max())
+
+
+@pytest.mark.parametrize("lens_q,lens_k", [([1], [131072]), ([1, 1], [65536, 3]),
+                                           ([16], [32768])])
+def test_one_very_long_context_matches_the_oracle(lens_q, lens_k):
+    """A single context of 64k-128k keys: each (sequence, kv head) segment of
+    the decode is split over a hundred or more wave slices, so the merge
+    walks long chains of partials; and a prefill chunk over a long context."""
+    rng = np.random.default_rng(sum(lens_k))
+    c, q, batch = random_case(rng, torch.bfloat16, 32, 8, 128, 16, lens_q, lens_k, "HND")
     want = oracle_out(q, c, 0, batch, 128 ** -0.5)
     got = paged_attention(q, c, 0, batch, 128 ** -0.5)
     assert max_abs(got, want) <= 2e-2 * float(want.abs().max())
