@@ -93,7 +93,8 @@ def cu_seqlens(values, device) -> torch.Tensor:
 @dataclass
 class PreparedAttention:
     """Per-step device inputs, built once per step rather than per layer
-    (attention.rs:237-256). Also holds the split-K workspace."""
+    (attention.rs:237-256). Also holds the decode workspace (per-XCD shares
+    and split-context partials), reused by every layer of the step."""
     block_table: torch.Tensor
     seqlens_q: torch.Tensor
     seqlens_k: torch.Tensor
