@@ -123,6 +123,31 @@ def bench_decode(steps, warmup):
     return d
 
 
+def bench_gather(d, steps, warmup):
+    """gather_kv (a7) on config 2's pool: the longest context's K and V into
+    logical order, one launch."""
+    w = d["w"]
+    i = int(np.argmax(w.lens))
+    lk = int(w.lens[i])
+    table = torch.from_numpy(w.tables[i].astype(np.int32)).to(DEV)
+    k_out = torch.empty(lk, w.num_kv_heads, w.head_dim, dtype=torch.bfloat16, device=DEV)
+    v_out = torch.empty_like(k_out)
+    from vapi_amd._lib import check, lib
+    from vapi_amd.cache import stream_handle
+    cache = d["cache"]
+
+    def gather():
+        check(lib().vapi_kv_gather(cache.pool, 0, table.data_ptr(), table.shape[0], lk,
+                                   k_out.data_ptr(), v_out.data_ptr(), stream_handle()))
+
+    ms, _ = timed(gather, steps, warmup)
+    alg = 2 * 2 * k_out.numel() * k_out.element_size() + table.numel() * 4
+    gbs = alg / (ms * 1e-3) / 1e9
+    ok = torch.equal(k_out[: w.block_size], cache.reference_view(0, "k")[int(w.tables[i][0])])
+    log(f"gather cfg2: {lk} keys x K and V, {alg / 1e6:.1f} MB, {ms * 1e3:.1f} us, {gbs:.0f} GB/s")
+    return {"keys": lk, "us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "first_block_exact": bool(ok)}
+
+
 def bench_fused_step(d, steps, warmup):
     """Config 2's decode step with its 64 new tokens appended: the two calls
     (vapi_kv_append, vapi_paged_attention) against the fused
@@ -437,6 +462,7 @@ def main():
     if args.only == "decode":
         return
     extras = {}
+    extras["gather_cfg2"] = bench_gather(dec, args.steps, args.warmup)
     extras["fused_step_cfg2"] = bench_fused_step(dec, args.steps, args.warmup)
     if args.only in (None,):
         extras["append_cfg1"] = bench_append(args.steps, args.warmup)

@@ -51,6 +51,26 @@ int check_pool(const vapi_kv_pool* p, const char* who) {
   return 0;
 }
 
+// A streaming (non-temporal) store: the line goes to memory without staying
+// dirty in L2. For a kernel whose writes are a few times the L2's size the
+// write-back of dirty lines at kernel end is a large share of its time:
+// measured, a config-1 append (16 MB written) 5.44 -> 4.41 us and an
+// 8,192-key gather (67 MB) 22.4 -> 9.8 us; a 4-layer append (67 MB of
+// scattered rows) 5.26 -> 5.40 us per layer and the 3.76 GB block copy
+// 4.9 -> 4.6 TB/s, so those keep ordinary stores.
+template <typename V>
+__device__ __forceinline__ void store_stream(V* p, V v) {
+  if constexpr (sizeof(V) == 16) {
+    typedef uint32_t v4 __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(v4{v.x, v.y, v.z, v.w}, (v4*)p);
+  } else if constexpr (sizeof(V) == 8) {
+    typedef uint32_t v2 __attribute__((ext_vector_type(2)));
+    __builtin_nontemporal_store(v2{v.x, v.y}, (v2*)p);
+  } else {
+    __builtin_nontemporal_store(v, p);
+  }
+}
+
 // ---- append ---------------------------------------------------------------
 
 struct AppendArgs {
@@ -67,7 +87,7 @@ struct AppendArgs {
   uint64_t src_layer_b, dst_layer_b;  // layer strides (grid y = layer)
 };
 
-template <int C, int ITEMS>
+template <int C, int ITEMS, bool kStream>
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   using V = typename Chunk<C>::T;
   // Layer blockIdx.y of a multi-layer append (0 for one layer).
@@ -105,7 +125,10 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   }
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j)
-    if (dst[j]) *(V*)dst[j] = val[j];
+    if (dst[j]) {
+      if (kStream) store_stream((V*)dst[j], val[j]);
+      else *(V*)dst[j] = val[j];
+    }
 }
 
 // One chunk per thread: measured on config 1 (4,096 tokens), 1 chunk per
@@ -115,8 +138,11 @@ template <int C>
 static void launch_append(const AppendArgs& a, uint32_t layers, hipStream_t s) {
   constexpr int ITEMS = 1;
   uint32_t grid = (a.total + 256 * ITEMS - 1) / (256 * ITEMS);
-  hipLaunchKernelGGL((kv_append_kernel<C, ITEMS>), dim3(grid, layers), dim3(256), 0, s,
-                     a);
+  if (layers == 1)
+    hipLaunchKernelGGL((kv_append_kernel<C, ITEMS, true>), dim3(grid), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((kv_append_kernel<C, ITEMS, false>), dim3(grid, layers), dim3(256), 0, s,
+                       a);
 }
 
 // ---- gather -----------------------------------------------------------------
@@ -134,6 +160,10 @@ struct GatherArgs {
   uint64_t blk_b, head_b, tok_b;
 };
 
+// Item i -> (kv, token t, head h, chunk u), walked in the output's order.
+// Streaming stores: 8,192 keys of K and V (67 MB) in 9.8 us against 22.4 us
+// with ordinary stores (walking an HND pool tile by tile instead measured the
+// same either way).
 template <int C, int ITEMS>
 __global__ __launch_bounds__(256) void kv_gather_kernel(GatherArgs a) {
   using V = typename Chunk<C>::T;
@@ -166,7 +196,7 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(GatherArgs a) {
   }
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j)
-    if (dst[j]) *(V*)dst[j] = val[j];
+    if (dst[j]) store_stream((V*)dst[j], val[j]);
 }
 
 // ---- block copy ---------------------------------------------------------------
