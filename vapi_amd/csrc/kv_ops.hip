@@ -51,26 +51,6 @@ int check_pool(const vapi_kv_pool* p, const char* who) {
   return 0;
 }
 
-// A streaming (non-temporal) store: the line goes to memory without staying
-// dirty in L2. For a kernel whose writes are a few times the L2's size the
-// write-back of dirty lines at kernel end is a large share of its time:
-// measured, a config-1 append (16 MB written) 5.44 -> 4.41 us and an
-// 8,192-key gather (67 MB) 22.4 -> 9.8 us; a 4-layer append (67 MB of
-// scattered rows) 5.26 -> 5.40 us per layer and the 3.76 GB block copy
-// 4.9 -> 4.6 TB/s, so those keep ordinary stores.
-template <typename V>
-__device__ __forceinline__ void store_stream(V* p, V v) {
-  if constexpr (sizeof(V) == 16) {
-    typedef uint32_t v4 __attribute__((ext_vector_type(4)));
-    __builtin_nontemporal_store(v4{v.x, v.y, v.z, v.w}, (v4*)p);
-  } else if constexpr (sizeof(V) == 8) {
-    typedef uint32_t v2 __attribute__((ext_vector_type(2)));
-    __builtin_nontemporal_store(v2{v.x, v.y}, (v2*)p);
-  } else {
-    __builtin_nontemporal_store(v, p);
-  }
-}
-
 // ---- append ---------------------------------------------------------------
 
 struct AppendArgs {
