@@ -414,6 +414,69 @@ def cpu_baseline(decode, budget_s=12.0):
                        f"bf16-valued K/V", ms_per_step=sec * 1e3)
 
 
+def cpu_baselines_more(decode, budget_s=4.0):
+    """BASELINE.md's other CPU legs, each on a bounded sample with the C
+    oracle: config-2 decode on one thread, the config-1 append scatter
+    (write_rows) and the config-4a block copy (copy_blocks), single-threaded
+    as the reference's own loops are."""
+    import oracle  # checker/baseline only
+    out = {}
+    # Decode on one core: the same batch as the headline leg.
+    w = decode["w"]
+    cache = decode["cache"]
+    used = np.concatenate(w.tables).astype(np.int64)
+    remap = {int(b): i for i, b in enumerate(used)}
+    idx = torch.from_numpy(used).to(DEV)
+    kc = cache.reference_view(0, "k")[idx].float().cpu().numpy()
+    vc = cache.reference_view(0, "v")[idx].float().cpu().numpy()
+    tables = [[remap[int(b)] for b in t] for t in w.tables]
+    q = decode["q"].float().cpu().numpy()
+    reps, t0 = 0, time.perf_counter()
+    while reps < 1 or time.perf_counter() - t0 < budget_s:
+        oracle.paged_attention(q, kc, vc, w.cu_q(), w.cu_k(), tables, decode["scale"], threads=1)
+        reps += 1
+    sec = (time.perf_counter() - t0) / reps
+    out["decode_cfg2_1core"] = dict(gbs=decode["alg_bytes"] / sec / 1e9, ms=sec * 1e3, reps=reps)
+    del kc, vc
+    # Append scatter (config 1) into a host pool of the config's size (K only;
+    # V is the same work again, counted in the bytes).
+    a = workload.config1_append()
+    row = a.num_kv_heads * a.head_dim * 2
+    pool = np.zeros((a.num_blocks * a.block_size, row), dtype=np.uint8)
+    src = np.random.default_rng(1).integers(0, 255, size=(a.n_tokens, row), dtype=np.uint8)
+    oracle.write_rows(pool, src, a.slots)  # untimed: first touch of the pool's pages
+    reps, t0 = 0, time.perf_counter()
+    while reps < 3 or time.perf_counter() - t0 < budget_s / 4:
+        oracle.write_rows(pool, src, a.slots)
+        reps += 1
+    sec = 2 * (time.perf_counter() - t0) / reps
+    alg = a.n_valid * 2 * row * 2 + a.n_tokens * 4
+    out["append_cfg1_1core"] = dict(gbs=alg / sec / 1e9, us=sec * 1e6, reps=reps)
+    del pool
+    # Block copy (config 4a) over per-layer pools holding just the pairs'
+    # blocks, renumbered densely.
+    c = workload.config4_block_ops()
+    blocks = np.unique(c.pairs.reshape(-1))
+    ren = {int(b): i for i, b in enumerate(blocks)}
+    pairs = np.array([[ren[int(x)], ren[int(y)]] for x, y in c.pairs], dtype=np.uint32)
+    blk = c.block_size * c.num_kv_heads * c.head_dim * 2
+    ks = [np.zeros((len(blocks), blk), dtype=np.uint8) for _ in range(c.num_layers)]
+    vs = [np.zeros((len(blocks), blk), dtype=np.uint8) for _ in range(c.num_layers)]
+    oracle.copy_blocks(ks, vs, pairs)  # untimed: first touch of the pools' pages
+    reps, t0 = 0, time.perf_counter()
+    while reps < 1 or time.perf_counter() - t0 < budget_s / 2:
+        oracle.copy_blocks(ks, vs, pairs)
+        reps += 1
+    sec = (time.perf_counter() - t0) / reps
+    alg = len(pairs) * 2 * c.num_layers * blk * 2
+    out["copy_cfg4a_1core"] = dict(gbs=alg / sec / 1e9, ms=sec * 1e3, reps=reps)
+    del ks, vs
+    log("cpu baselines: decode 1 core {:.2f} GB/s, append {:.2f} GB/s, copy {:.2f} GB/s".format(
+        out["decode_cfg2_1core"]["gbs"], out["append_cfg1_1core"]["gbs"],
+        out["copy_cfg4a_1core"]["gbs"]))
+    return out
+
+
 def load_traffic():
     p = ROOT / "profiles" / "paged_decode_config2_traffic.json"
     if p.exists():
@@ -473,6 +536,8 @@ def main():
     extras["hbm_copy_probe_gbs"] = hbm_probe()
     traffic = load_traffic()
     cpu = None if args.no_cpu else cpu_baseline(dec)
+    if not args.no_cpu:
+        extras["cpu_baselines"] = cpu_baselines_more(dec)
     alg = dec["alg_bytes"]
     line = {
         "metric": "decode paged-attn HBM GB/s & % of peak (B=64, 8B GQA); KV append GB/s",
