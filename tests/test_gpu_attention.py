@@ -179,6 +179,11 @@ CASES = [
     (torch.bfloat16, 32, 8, 128, 64, [1, 20, 1], [1000, 200, 65], None, "HND"),
     (torch.float16, 16, 4, 64, 128, [1, 33, 1], [700, 300, 129], 50, "NHD"),
     (torch.bfloat16, 8, 8, 128, 256, [1, 1, 17], [2000, 257, 600], None, "HND"),
+    # 16-bit pools the MFMA paths do not take, on the generic kernel: more
+    # than 16 query heads per kv head, head_dim 256, block_size 8.
+    (torch.bfloat16, 32, 1, 128, 16, [1, 9, 1], [300, 40, 77], None, "HND"),
+    (torch.float16, 8, 4, 256, 16, [1, 6], [500, 70], 30, "NHD"),
+    (torch.bfloat16, 16, 8, 128, 8, [1, 12], [210, 50], None, "HND"),
 ]
 
 
