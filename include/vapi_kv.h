@@ -303,6 +303,30 @@ int64_t vapi_spill_evicted(vapi_spill_store* store, const vapi_kv_pool* pool,
                            void* pinned, size_t pinned_bytes, vapi_stream_t stream);
 
 /*
+ * vapi_spill_evicted overlapped with the forward (no counterpart in the
+ * reference, whose spill_evicted, engine.rs:369-393, blocks the step). The
+ * blocks the store does not hold are packed into device `staging` on
+ * `stream` (an HBM copy: the forward may overwrite the blocks once it has
+ * run on `stream`), then copied to `pinned` on `side`. The blobs enter the
+ * store at vapi_spill_drain or at the next put / get / evicted / promote
+ * call, which drain first; until then contains() does not report them.
+ * One export is in flight per store. staging must hold every block to
+ * export and pinned 4 KiB more; at most 1,024 blocks (else VAPI_KV_ESPACE).
+ * Neither buffer may be touched until the drain. Returns the number exported.
+ */
+int64_t vapi_spill_evicted_async(vapi_spill_store* store, const vapi_kv_pool* pool,
+                                 const uint32_t* ids, const uint8_t* hashes, uint32_t n,
+                                 void* staging, size_t staging_bytes, void* pinned,
+                                 size_t pinned_bytes, vapi_stream_t stream, vapi_stream_t side);
+
+/*
+ * Puts the in-flight asynchronous export's blobs into the store: at once if
+ * `wait` (blocking on its copy), else only if the copy has completed.
+ * Returns the number of blobs stored (0 if none), or a negative error.
+ */
+int64_t vapi_spill_drain(vapi_spill_store* store, int wait);
+
+/*
  * The device half of promote_from_spill (engine.rs:400-456): hashes[0..n)
  * are a prompt's block chain and ids[0..n) (host) the blocks allocated for
  * them. Blobs are taken in order up to the first hash the store does not

@@ -357,3 +357,42 @@ def test_spilled_blocks_come_back_bit_exact_through_host_memory_and_disk(layout,
     assert promote(store, c, chain, perm[40:48].tolist(), pinned) == 5
     after = store.stats()
     assert (after["hits"] - before["hits"], after["misses"] - before["misses"]) == (5, 1)
+
+
+@pytest.mark.gpu
+def test_async_spill_keeps_the_bytes_the_blocks_held_when_it_was_called(tmp_path):
+    """vapi_spill_evicted_async: the blocks are overwritten on the same
+    stream right after the call (as the next forward would), the copy to
+    host runs on a side stream, and after the drain the store holds each
+    block's bytes from before the overwrite, in the export byte order.
+    Blocks the store already holds are skipped; put/get drain first."""
+    import hashlib
+    from vapi_amd.spill import SpillStore, drain, pinned_buffer, spill_evicted_async
+    L, nb, n = 2, 48, 12
+    c = PagedKvCache(L, nb, 16, 4, 128, torch.bfloat16, "HND")
+    workload.fill_normal(c._slab, 3)
+    be = KvBlockBackend(c)
+    bb = be.block_bytes()
+    ids = list(range(5, 5 + n))
+    want = [oracle.export_block([as_np(ref_pool(c, l, "k")) for l in range(L)],
+                                [as_np(ref_pool(c, l, "v")) for l in range(L)], b) for b in ids]
+    hs = [hashlib.sha256(b"async %d" % i).digest() for i in range(n)]
+    store = SpillStore(None, 1 << 30, 0)
+    store.put(hs[0], want[0])
+    staging = torch.empty(n * bb, dtype=torch.uint8, device="cuda")
+    pinned = pinned_buffer(c, n)
+    side = torch.cuda.Stream()
+    assert spill_evicted_async(store, c, zip(hs, ids), staging, pinned, side=side) == n - 1
+    c._slab.zero_()  # the next forward reuses the blocks, on the same stream
+    assert drain(store) == n - 1
+    assert drain(store) == 0
+    torch.cuda.synchronize()
+    for h, w in zip(hs, want):
+        assert store.get(h, bb) == w
+    # A second export drains by itself at the next store call.
+    h2 = hashlib.sha256(b"async second").digest()
+    assert spill_evicted_async(store, c, [(h2, 7)], staging, pinned, side=side) == 1
+    assert store.get(h2, bb) == bytes(bb)
+    with pytest.raises(Exception, match="staging"):
+        spill_evicted_async(store, c, [(hashlib.sha256(b"x%d" % i).digest(), i) for i in range(3)],
+                            staging[:bb], pinned, side=side)

@@ -137,3 +137,17 @@ def test_a_too_small_buffer_is_an_error_and_counts_nothing():
     st = s.stats()
     assert (st["hits"], st["misses"]) == (0, 0)
     assert s.get(h[0]) == b"y" * 50
+
+
+def test_drain_without_an_export_in_flight_does_nothing_and_null_args_are_errors():
+    """vapi_spill_drain / vapi_spill_evicted_async host checks (no GPU call:
+    nothing is in flight, and a null store or pool fails before any)."""
+    L = _lib.lib()
+    s = SpillStore(None, 100, 0)
+    assert L.vapi_spill_drain(s.handle, 1) == 0
+    assert L.vapi_spill_drain(s.handle, 0) == 0
+    assert L.vapi_spill_drain(None, 1) == _lib.EINVAL
+    assert L.vapi_spill_evicted_async(None, None, None, None, 0, None, 0, None, 0, None,
+                                      None) == _lib.EINVAL
+    s.put(hashes(1)[0], b"z" * 5)
+    assert s.get(hashes(1)[0]) == b"z" * 5

@@ -31,6 +31,7 @@ EXPORTS = (
     "vapi_cache_import_block", "vapi_cache_copy_blocks",
     "vapi_spill_open", "vapi_spill_close", "vapi_spill_contains", "vapi_spill_put",
     "vapi_spill_get", "vapi_spill_get_stats", "vapi_spill_evicted", "vapi_spill_promote",
+    "vapi_spill_evicted_async", "vapi_spill_drain",
 )
 
 
@@ -135,6 +136,11 @@ def lib():
     L.vapi_spill_evicted.restype = ctypes.c_int64
     L.vapi_spill_promote.argtypes = [_vp, _poolp, _vp, _u32p, _u32, _vp, _sz, _vp]
     L.vapi_spill_promote.restype = ctypes.c_int64
+    L.vapi_spill_evicted_async.argtypes = [_vp, _poolp, _u32p, _vp, _u32, _vp, _sz, _vp, _sz,
+                                           _vp, _vp]
+    L.vapi_spill_evicted_async.restype = ctypes.c_int64
+    L.vapi_spill_drain.argtypes = [_vp, ctypes.c_int]
+    L.vapi_spill_drain.restype = ctypes.c_int64
     _lib = L
     return L
 

@@ -139,6 +139,21 @@ struct vapi_spill_store {
   uint64_t disk_max = 0, disk_bytes = 0;
   vapi_spill_stats st{};
 
+  // The one in-flight asynchronous export: blobs of `pend_hashes`, back to
+  // back at `pend_blobs` (pinned) once `ev_copied` has completed. Events
+  // are created on first use (a store without a GPU never needs them).
+  bool pending = false;
+  std::vector<Hash> pend_hashes;
+  const uint8_t* pend_blobs = nullptr;
+  size_t pend_bb = 0;
+  hipEvent_t ev_packed = nullptr, ev_copied = nullptr;
+
+  ~vapi_spill_store() {
+    if (pending) (void)hipEventSynchronize(ev_copied);
+    if (ev_packed) (void)hipEventDestroy(ev_packed);
+    if (ev_copied) (void)hipEventDestroy(ev_copied);
+  }
+
   fs::path path(const Hash& h) const { return dir / (to_hex(h) + ".kv"); }
 
   void evict_disk() {
@@ -221,6 +236,29 @@ struct vapi_spill_store {
     ++st.misses;
     return -1;
   }
+
+  // Puts the in-flight export's blobs into the store once its device-to-host
+  // copy has completed (at once if `wait`). Returns the blobs stored, 0 if
+  // none was in flight or it has not completed, or a negative error.
+  int64_t drain(bool wait) {
+    if (!pending) return 0;
+    if (!wait) {
+      const hipError_t q = hipEventQuery(ev_copied);
+      if (q == hipErrorNotReady) return 0;
+      if (q != hipSuccess) VK_FAIL(VAPI_KV_EHIP, "vapi_spill_drain: %s", hipGetErrorString(q));
+    } else {
+      VK_HIP(hipEventSynchronize(ev_copied));
+    }
+    const uint32_t m = (uint32_t)pend_hashes.size();
+    std::vector<std::vector<uint8_t>> copies(m);
+    parallel_for(m, [&](uint32_t j) {
+      copies[j].assign(pend_blobs + (size_t)j * pend_bb, pend_blobs + (size_t)(j + 1) * pend_bb);
+    });
+    for (uint32_t j = 0; j < m; ++j) put(pend_hashes[j], std::move(copies[j]));
+    pending = false;
+    pend_hashes.clear();
+    return m;
+  }
 };
 
 extern "C" {
@@ -271,6 +309,7 @@ int vapi_spill_contains(const vapi_spill_store* s, const uint8_t* hash) {
 int vapi_spill_put(vapi_spill_store* s, const uint8_t* hash, const void* bytes, size_t len) {
   clear_error();
   if (!s || !hash || (len && !bytes)) VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_put: null argument");
+  if (int64_t rc = s->drain(true); rc < 0) return (int)rc;
   s->put(to_hash(hash), (const uint8_t*)bytes, len);
   return 0;
 }
@@ -278,6 +317,7 @@ int vapi_spill_put(vapi_spill_store* s, const uint8_t* hash, const void* bytes, 
 int64_t vapi_spill_get(vapi_spill_store* s, const uint8_t* hash, void* out, size_t cap) {
   clear_error();
   if (!s || !hash || (cap && !out)) VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_get: null argument");
+  if (int64_t rc = s->drain(true); rc < 0) return rc;
   const int64_t n = s->get(to_hash(hash), out, cap);
   if (n == VAPI_KV_ESPACE) VK_FAIL(VAPI_KV_ESPACE, "vapi_spill_get: %zu bytes is too small", cap);
   return n;
@@ -305,6 +345,7 @@ int64_t vapi_spill_evicted(vapi_spill_store* s, const vapi_kv_pool* pool, const 
   if (int rc = check_pool(pool, "vapi_spill_evicted")) return rc;
   if (!s || (n && (!ids || !hashes || !pinned)))
     VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_evicted: null argument");
+  if (int64_t rc = s->drain(true); rc < 0) return rc;
   const size_t bb = vapi_kv_block_bytes(pool);
   const size_t head = 4096;  // id staging, 1,024 ids per round at most
   if (pinned_bytes < head + bb)
@@ -332,6 +373,61 @@ int64_t vapi_spill_evicted(vapi_spill_store* s, const vapi_kv_pool* pool, const 
   return (int64_t)todo.size();
 }
 
+// spill_evicted overlapped with the forward: the blocks the store does not
+// hold are packed by vapi_kv_export_blocks into device staging on `stream`
+// (an HBM-to-HBM copy; the forward may overwrite the blocks once it has run),
+// then copied to `pinned` on `side`; vapi_spill_drain (or the next spill
+// call) puts them into the store. One export in flight per store: a call
+// first drains the previous one. staging and pinned (after its 4 KiB id
+// stage) must hold every block to export, at most 1,024. Returns the number
+// exported.
+int64_t vapi_spill_evicted_async(vapi_spill_store* s, const vapi_kv_pool* pool,
+                                 const uint32_t* ids, const uint8_t* hashes, uint32_t n,
+                                 void* staging, size_t staging_bytes, void* pinned,
+                                 size_t pinned_bytes, vapi_stream_t stream, vapi_stream_t side) {
+  clear_error();
+  if (int rc = check_pool(pool, "vapi_spill_evicted_async")) return rc;
+  if (!s || (n && (!ids || !hashes || !pinned || !staging)))
+    VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_evicted_async: null argument");
+  if (int64_t rc = s->drain(true); rc < 0) return rc;
+  const size_t bb = vapi_kv_block_bytes(pool);
+  const size_t head = 4096;
+  std::vector<uint32_t> todo;
+  for (uint32_t i = 0; i < n; ++i)
+    if (!s->holds(to_hash(hashes + 32ull * i))) todo.push_back(i);
+  const uint32_t m = (uint32_t)todo.size();
+  if (!m) return 0;
+  if (m > head / 4 || staging_bytes < (size_t)m * bb || pinned_bytes < head + (size_t)m * bb)
+    VK_FAIL(VAPI_KV_ESPACE,
+            "vapi_spill_evicted_async: %u blocks of %zu bytes need %zu staging and %zu pinned "
+            "bytes (at most 1024 blocks)",
+            m, bb, (size_t)m * bb, head + (size_t)m * bb);
+  if (!s->ev_packed) {
+    VK_HIP(hipEventCreateWithFlags(&s->ev_packed, hipEventDisableTiming));
+    VK_HIP(hipEventCreateWithFlags(&s->ev_copied, hipEventDisableTiming));
+  }
+  uint32_t* id_stage = (uint32_t*)pinned;
+  uint8_t* blobs = (uint8_t*)pinned + head;
+  for (uint32_t j = 0; j < m; ++j) id_stage[j] = ids[todo[j]];
+  if (int rc = vapi_kv_export_blocks(pool, id_stage, m, staging, stream)) return rc;
+  VK_HIP(hipEventRecord(s->ev_packed, hs(stream)));
+  VK_HIP(hipStreamWaitEvent(hs(side), s->ev_packed, 0));
+  VK_HIP(hipMemcpyAsync(blobs, staging, (size_t)m * bb, hipMemcpyDeviceToHost, hs(side)));
+  VK_HIP(hipEventRecord(s->ev_copied, hs(side)));
+  s->pend_hashes.clear();
+  for (uint32_t j = 0; j < m; ++j) s->pend_hashes.push_back(to_hash(hashes + 32ull * todo[j]));
+  s->pend_blobs = blobs;
+  s->pend_bb = bb;
+  s->pending = true;
+  return m;
+}
+
+int64_t vapi_spill_drain(vapi_spill_store* s, int wait) {
+  clear_error();
+  if (!s) VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_drain: null store");
+  return s->drain(wait != 0);
+}
+
 // The device half of promote_from_spill (engine.rs:400-456): hashes[0..n)
 // are a prompt's block chain and ids[0..n) the blocks allocated for them.
 // Blobs are taken from the store in order up to the first it does not hold
@@ -346,6 +442,7 @@ int64_t vapi_spill_promote(vapi_spill_store* s, const vapi_kv_pool* pool, const 
   if (int rc = check_pool(pool, "vapi_spill_promote")) return rc;
   if (!s || (n && (!ids || !hashes || !pinned)))
     VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_promote: null argument");
+  if (int64_t rc = s->drain(true); rc < 0) return rc;
   const size_t bb = vapi_kv_block_bytes(pool);
   const size_t head = 4096;
   if (pinned_bytes < head + bb)

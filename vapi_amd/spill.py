@@ -95,6 +95,32 @@ def spill_evicted(store: SpillStore, cache: PagedKvCache, evicted, pinned: torch
         pinned.data_ptr(), pinned.numel(), stream_handle(stream)))
 
 
+def spill_evicted_async(store: SpillStore, cache: PagedKvCache, evicted, staging: torch.Tensor,
+                        pinned: torch.Tensor, stream=None, side=None) -> int:
+    """spill_evicted overlapped with the forward: the blocks are packed into
+    device `staging` on `stream` and copied to `pinned` on `side`; they
+    enter the store at drain() or the next store call. Returns how many.
+    `staging` and `pinned` must stay untouched until then."""
+    evicted = list(evicted)
+    if any(len(h) != 32 for h, _ in evicted):
+        raise ValueError("block hashes are 32 bytes")
+    if not staging.is_cuda:
+        raise ValueError("staging is device memory")
+    ids = np.array([i for _, i in evicted], dtype=np.uint32)
+    hashes = b"".join(h for h, _ in evicted)
+    hb = (ctypes.c_uint8 * max(len(hashes), 1)).from_buffer_copy(hashes or b"\0")
+    return check(lib().vapi_spill_evicted_async(
+        store.handle, cache.pool, ids.ctypes.data_as(_lib._u32p), hb, len(ids),
+        staging.data_ptr(), staging.numel() * staging.element_size(), pinned.data_ptr(),
+        pinned.numel(), stream_handle(stream), stream_handle(side)))
+
+
+def drain(store: SpillStore, wait: bool = True) -> int:
+    """Put the in-flight asynchronous export into the store; returns how
+    many blobs (0 if none, or if not `wait` and its copy is still running)."""
+    return check(lib().vapi_spill_drain(store.handle, int(wait)))
+
+
 def promote(store: SpillStore, cache: PagedKvCache, hashes, ids, pinned: torch.Tensor,
             stream=None) -> int:
     """Import the held prefix of a block chain into `ids` (the device half
