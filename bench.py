@@ -119,7 +119,12 @@ def bench_decode(steps, warmup):
     gbs = d["alg_bytes"] / (ms * 1e-3) / 1e9
     log(f"decode cfg2: sum_len {d['sum_len']}, {d['alg_bytes'] / 1e6:.1f} MB/step, "
         f"{ms * 1e3:.1f} us/step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of 8 TB/s)")
-    d.update(ms=ms, wall=wall, gbs=gbs)
+    # The same call replayed from a HIP graph, as a serving loop that
+    # captures its decode step runs it (GraphRunner, backend.rs:893-1216).
+    gms = timed_graph(d["step"], steps, warmup)
+    log(f"decode cfg2 in a graph: {gms * 1e3:.1f} us/step, "
+        f"{d['alg_bytes'] / (gms * 1e-3) / 1e9:.0f} GB/s")
+    d.update(ms=ms, wall=wall, gbs=gbs, graph_ms=gms)
     return d
 
 
@@ -388,10 +393,14 @@ def bench_copy(steps, warmup):
     cache = PagedKvCache(w.num_layers, w.num_blocks, w.block_size, w.num_kv_heads,
                          w.head_dim, torch.bfloat16, "HND")
     workload.fill_normal(cache._slab, workload.seed_for(4))
-    pairs = w.pairs.tolist()
     be = KvBlockBackend(cache)
-    ms, _ = timed(lambda: be.copy_blocks(pairs), steps, warmup)
-    alg = len(pairs) * be.block_bytes() * 2
+    pairs_dev = torch.from_numpy(w.pairs.astype(np.int32).reshape(-1)).to(DEV)
+    from vapi_amd._lib import check, lib
+    from vapi_amd.cache import stream_handle
+    n = w.pairs.shape[0]
+    ms, _ = timed(lambda: check(lib().vapi_kv_copy_blocks(cache.pool, pairs_dev.data_ptr(), n,
+                                                          stream_handle())), steps, warmup)
+    alg = n * be.block_bytes() * 2
     log(f"copy cfg4a: {alg / 1e9:.2f} GB moved, {ms:.3f} ms, {alg / (ms * 1e-3) / 1e9:.0f} GB/s")
 
 
