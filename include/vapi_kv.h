@@ -308,11 +308,15 @@ int64_t vapi_spill_evicted(vapi_spill_store* store, const vapi_kv_pool* pool,
  * blocks the store does not hold are packed into device `staging` on
  * `stream` (an HBM copy: the forward may overwrite the blocks once it has
  * run on `stream`), then copied to `pinned` on `side`. The blobs enter the
- * store at vapi_spill_drain or at the next put / get / evicted / promote
- * call, which drain first; until then contains() does not report them.
- * One export is in flight per store. staging must hold every block to
- * export and pinned 4 KiB more; at most 1,024 blocks (else VAPI_KV_ESPACE).
- * Neither buffer may be touched until the drain. Returns the number exported.
+ * store at a drain: vapi_spill_drain, and every store call drains the
+ * exports whose copies have completed (get waits for a blob in flight;
+ * vapi_spill_evicted and vapi_spill_promote wait for all); contains() does
+ * not report blobs in flight. Blocks already held or in flight are skipped.
+ * Up to 16 exports are in flight per store, each owning its staging and
+ * pinned buffers until it is drained: rotate a ring of buffers; a call
+ * whose buffers overlap an in-flight export's waits for it first. staging
+ * must hold every block to export and pinned 4 KiB more; at most 1,024
+ * blocks (else VAPI_KV_ESPACE). Returns the number exported.
  */
 int64_t vapi_spill_evicted_async(vapi_spill_store* store, const vapi_kv_pool* pool,
                                  const uint32_t* ids, const uint8_t* hashes, uint32_t n,
@@ -320,9 +324,10 @@ int64_t vapi_spill_evicted_async(vapi_spill_store* store, const vapi_kv_pool* po
                                  size_t pinned_bytes, vapi_stream_t stream, vapi_stream_t side);
 
 /*
- * Puts the in-flight asynchronous export's blobs into the store: at once if
- * `wait` (blocking on its copy), else only if the copy has completed.
- * Returns the number of blobs stored (0 if none), or a negative error.
+ * Puts the blobs of in-flight asynchronous exports into the store, oldest
+ * first: all of them if `wait` (blocking on their copies), else those whose
+ * copies have completed. Returns the number of blobs stored, or a negative
+ * error.
  */
 int64_t vapi_spill_drain(vapi_spill_store* store, int wait);
 

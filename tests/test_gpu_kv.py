@@ -396,3 +396,42 @@ def test_async_spill_keeps_the_bytes_the_blocks_held_when_it_was_called(tmp_path
     with pytest.raises(Exception, match="staging"):
         spill_evicted_async(store, c, [(hashlib.sha256(b"x%d" % i).digest(), i) for i in range(3)],
                             staging[:bb], pinned, side=side)
+
+
+@pytest.mark.gpu
+def test_async_spills_in_flight_on_a_ring_of_buffers_all_arrive_intact():
+    """Five asynchronous exports over a ring of three staging/pinned pairs,
+    each followed by an overwrite of its blocks on the model's stream: the
+    fourth and fifth reuse buffers still in flight (the call waits for those
+    first). Hashes already in flight are skipped. After the drain every blob
+    is its block's bytes from before the overwrite."""
+    import hashlib
+    from vapi_amd.spill import SpillStore, drain, pinned_buffer, spill_evicted_async
+    L, nb, per = 2, 64, 4
+    c = PagedKvCache(L, nb, 16, 4, 128, torch.bfloat16, "HND")
+    workload.fill_normal(c._slab, 5)
+    be = KvBlockBackend(c)
+    bb = be.block_bytes()
+    ring = [(torch.empty(per * bb, dtype=torch.uint8, device="cuda"), pinned_buffer(c, per))
+            for _ in range(3)]
+    side = torch.cuda.Stream()
+    store = SpillStore(None, 1 << 30, 0)
+    want = {}
+    for call in range(5):
+        ids = list(range(per * call, per * call + per))
+        hs = [hashlib.sha256(b"ring %d" % b).digest() for b in ids]
+        for h, b in zip(hs, ids):
+            want[h] = be.export_block(b)
+        staging, pinned = ring[call % 3]
+        assert spill_evicted_async(store, c, zip(hs, ids), staging, pinned, side=side) == per
+        if call == 0:  # the same hashes again while in flight: nothing to do
+            assert spill_evicted_async(store, c, zip(hs, ids), ring[1][0], ring[1][1],
+                                       side=side) == 0
+        for b in ids:  # the next forward reuses the blocks
+            for t in c.k + c.v:
+                t[b].fill_(float(call + 1))
+    drain(store)
+    torch.cuda.synchronize()
+    assert store.stats()["ram_blocks"] == 5 * per
+    for h, w in want.items():
+        assert store.get(h, bb) == w

@@ -12,6 +12,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <deque>
 #include <filesystem>
 #include <fstream>
 #include <list>
@@ -130,6 +131,8 @@ void parallel_for(uint32_t n, F f) {
 
 }  // namespace
 
+constexpr size_t kMaxInflight = 16;  // asynchronous exports in flight per store
+
 struct vapi_spill_store {
   Lru<std::vector<uint8_t>> ram;
   uint64_t ram_max = 0, ram_bytes = 0;
@@ -139,19 +142,26 @@ struct vapi_spill_store {
   uint64_t disk_max = 0, disk_bytes = 0;
   vapi_spill_stats st{};
 
-  // The one in-flight asynchronous export: blobs of `pend_hashes`, back to
-  // back at `pend_blobs` (pinned) once `ev_copied` has completed. Events
-  // are created on first use (a store without a GPU never needs them).
-  bool pending = false;
-  std::vector<Hash> pend_hashes;
-  const uint8_t* pend_blobs = nullptr;
-  size_t pend_bb = 0;
-  hipEvent_t ev_packed = nullptr, ev_copied = nullptr;
+  // Asynchronous exports in flight, oldest first: the blobs of `hashes`,
+  // back to back at `blobs` (pinned) once `copied` has completed. Each owns
+  // the caller's staging and pinned ranges until it is drained. Events are
+  // created on first use (a store without a GPU never needs them) and
+  // recycled.
+  struct Inflight {
+    std::vector<Hash> hashes;
+    const uint8_t* blobs;
+    size_t bb;
+    uintptr_t pin_lo, pin_hi, stg_lo, stg_hi;
+    hipEvent_t packed, copied;
+  };
+  std::deque<Inflight> inflight;
+  std::unordered_map<Hash, uint32_t, HashHash> in_flight_hashes;  // hash -> count
+  std::vector<hipEvent_t> spare_events;
 
   ~vapi_spill_store() {
-    if (pending) (void)hipEventSynchronize(ev_copied);
-    if (ev_packed) (void)hipEventDestroy(ev_packed);
-    if (ev_copied) (void)hipEventDestroy(ev_copied);
+    for (auto& e : inflight) (void)hipEventSynchronize(e.copied);
+    for (auto& e : inflight) spare_events.push_back(e.packed), spare_events.push_back(e.copied);
+    for (hipEvent_t e : spare_events) (void)hipEventDestroy(e);
   }
 
   fs::path path(const Hash& h) const { return dir / (to_hex(h) + ".kv"); }
@@ -237,27 +247,64 @@ struct vapi_spill_store {
     return -1;
   }
 
-  // Puts the in-flight export's blobs into the store once its device-to-host
-  // copy has completed (at once if `wait`). Returns the blobs stored, 0 if
-  // none was in flight or it has not completed, or a negative error.
-  int64_t drain(bool wait) {
-    if (!pending) return 0;
-    if (!wait) {
-      const hipError_t q = hipEventQuery(ev_copied);
-      if (q == hipErrorNotReady) return 0;
-      if (q != hipSuccess) VK_FAIL(VAPI_KV_EHIP, "vapi_spill_drain: %s", hipGetErrorString(q));
-    } else {
-      VK_HIP(hipEventSynchronize(ev_copied));
+  // Puts the blobs of in-flight exports into the store, oldest first: the
+  // first `force` of them after waiting for their copies, then the rest
+  // while their copies have completed (all of them if `wait`). Returns the
+  // blobs stored or a negative error.
+  int64_t drain(bool wait, size_t force = 0) {
+    int64_t stored = 0;
+    while (!inflight.empty()) {
+      Inflight& e = inflight.front();
+      if (wait || force) {
+        VK_HIP(hipEventSynchronize(e.copied));
+      } else {
+        const hipError_t q = hipEventQuery(e.copied);
+        if (q == hipErrorNotReady) break;
+        if (q != hipSuccess) VK_FAIL(VAPI_KV_EHIP, "vapi_spill_drain: %s", hipGetErrorString(q));
+      }
+      if (force) --force;
+      const uint32_t m = (uint32_t)e.hashes.size();
+      std::vector<std::vector<uint8_t>> copies(m);
+      parallel_for(m, [&](uint32_t j) {
+        copies[j].assign(e.blobs + (size_t)j * e.bb, e.blobs + (size_t)(j + 1) * e.bb);
+      });
+      for (uint32_t j = 0; j < m; ++j) {
+        put(e.hashes[j], std::move(copies[j]));
+        auto it = in_flight_hashes.find(e.hashes[j]);
+        if (it != in_flight_hashes.end() && --it->second == 0) in_flight_hashes.erase(it);
+      }
+      spare_events.push_back(e.packed);
+      spare_events.push_back(e.copied);
+      inflight.pop_front();
+      stored += m;
     }
-    const uint32_t m = (uint32_t)pend_hashes.size();
-    std::vector<std::vector<uint8_t>> copies(m);
-    parallel_for(m, [&](uint32_t j) {
-      copies[j].assign(pend_blobs + (size_t)j * pend_bb, pend_blobs + (size_t)(j + 1) * pend_bb);
-    });
-    for (uint32_t j = 0; j < m; ++j) put(pend_hashes[j], std::move(copies[j]));
-    pending = false;
-    pend_hashes.clear();
-    return m;
+    return stored;
+  }
+
+  // Drains (waiting) every in-flight export up to the newest one whose
+  // buffers overlap [pin_lo, pin_hi) or [stg_lo, stg_hi).
+  int64_t release(uintptr_t pin_lo, uintptr_t pin_hi, uintptr_t stg_lo, uintptr_t stg_hi) {
+    size_t upto = 0;
+    for (size_t i = 0; i < inflight.size(); ++i) {
+      const Inflight& e = inflight[i];
+      const bool hit = (e.pin_lo < pin_hi && pin_lo < e.pin_hi) ||
+                       (e.stg_lo < stg_hi && stg_lo < e.stg_hi) ||
+                       (e.pin_lo < stg_hi && stg_lo < e.pin_hi) ||
+                       (e.stg_lo < pin_hi && pin_lo < e.stg_hi);
+      if (hit) upto = i + 1;
+    }
+    return upto ? drain(false, upto) : 0;
+  }
+
+  hipEvent_t event() {
+    if (!spare_events.empty()) {
+      hipEvent_t e = spare_events.back();
+      spare_events.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) return nullptr;
+    return e;
   }
 };
 
@@ -309,7 +356,7 @@ int vapi_spill_contains(const vapi_spill_store* s, const uint8_t* hash) {
 int vapi_spill_put(vapi_spill_store* s, const uint8_t* hash, const void* bytes, size_t len) {
   clear_error();
   if (!s || !hash || (len && !bytes)) VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_put: null argument");
-  if (int64_t rc = s->drain(true); rc < 0) return (int)rc;
+  if (int64_t rc = s->drain(false); rc < 0) return (int)rc;
   s->put(to_hash(hash), (const uint8_t*)bytes, len);
   return 0;
 }
@@ -317,7 +364,8 @@ int vapi_spill_put(vapi_spill_store* s, const uint8_t* hash, const void* bytes, 
 int64_t vapi_spill_get(vapi_spill_store* s, const uint8_t* hash, void* out, size_t cap) {
   clear_error();
   if (!s || !hash || (cap && !out)) VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_get: null argument");
-  if (int64_t rc = s->drain(true); rc < 0) return rc;
+  // A blob still in flight is waited for; completed exports enter anyway.
+  if (int64_t rc = s->drain(s->in_flight_hashes.count(to_hash(hash)) > 0); rc < 0) return rc;
   const int64_t n = s->get(to_hash(hash), out, cap);
   if (n == VAPI_KV_ESPACE) VK_FAIL(VAPI_KV_ESPACE, "vapi_spill_get: %zu bytes is too small", cap);
   return n;
@@ -373,14 +421,15 @@ int64_t vapi_spill_evicted(vapi_spill_store* s, const vapi_kv_pool* pool, const 
   return (int64_t)todo.size();
 }
 
-// spill_evicted overlapped with the forward: the blocks the store does not
-// hold are packed by vapi_kv_export_blocks into device staging on `stream`
-// (an HBM-to-HBM copy; the forward may overwrite the blocks once it has run),
-// then copied to `pinned` on `side`; vapi_spill_drain (or the next spill
-// call) puts them into the store. One export in flight per store: a call
-// first drains the previous one. staging and pinned (after its 4 KiB id
-// stage) must hold every block to export, at most 1,024. Returns the number
-// exported.
+// spill_evicted overlapped with the forward: the blocks the store neither
+// holds nor has in flight are packed by vapi_kv_export_blocks into device
+// staging on `stream` (an HBM-to-HBM copy; the forward may overwrite the
+// blocks once it has run), then copied to `pinned` on `side`; a drain puts
+// them into the store. Up to kMaxInflight exports are in flight, each on
+// its own staging and pinned buffers (a ring the caller rotates); a call
+// whose buffers overlap an in-flight export's first drains up to that one.
+// staging and pinned (after its 4 KiB id stage) must hold every block to
+// export, at most 1,024. Returns the number exported.
 int64_t vapi_spill_evicted_async(vapi_spill_store* s, const vapi_kv_pool* pool,
                                  const uint32_t* ids, const uint8_t* hashes, uint32_t n,
                                  void* staging, size_t staging_bytes, void* pinned,
@@ -389,12 +438,21 @@ int64_t vapi_spill_evicted_async(vapi_spill_store* s, const vapi_kv_pool* pool,
   if (int rc = check_pool(pool, "vapi_spill_evicted_async")) return rc;
   if (!s || (n && (!ids || !hashes || !pinned || !staging)))
     VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_evicted_async: null argument");
-  if (int64_t rc = s->drain(true); rc < 0) return rc;
   const size_t bb = vapi_kv_block_bytes(pool);
   const size_t head = 4096;
+  // Exports whose copies have completed enter the store now; the ones using
+  // this call's buffers are waited for.
+  if (int64_t rc = s->drain(false); rc < 0) return rc;
+  const uintptr_t pin0 = (uintptr_t)pinned, stg0 = (uintptr_t)staging;
+  if (int64_t rc = s->release(pin0, pin0 + pinned_bytes, stg0, stg0 + staging_bytes); rc < 0)
+    return rc;
+  if (s->inflight.size() >= kMaxInflight)
+    if (int64_t rc = s->drain(false, s->inflight.size() - kMaxInflight + 1); rc < 0) return rc;
   std::vector<uint32_t> todo;
-  for (uint32_t i = 0; i < n; ++i)
-    if (!s->holds(to_hash(hashes + 32ull * i))) todo.push_back(i);
+  for (uint32_t i = 0; i < n; ++i) {
+    const Hash h = to_hash(hashes + 32ull * i);
+    if (!s->holds(h) && !s->in_flight_hashes.count(h)) todo.push_back(i);
+  }
   const uint32_t m = (uint32_t)todo.size();
   if (!m) return 0;
   if (m > head / 4 || staging_bytes < (size_t)m * bb || pinned_bytes < head + (size_t)m * bb)
@@ -402,23 +460,42 @@ int64_t vapi_spill_evicted_async(vapi_spill_store* s, const vapi_kv_pool* pool,
             "vapi_spill_evicted_async: %u blocks of %zu bytes need %zu staging and %zu pinned "
             "bytes (at most 1024 blocks)",
             m, bb, (size_t)m * bb, head + (size_t)m * bb);
-  if (!s->ev_packed) {
-    VK_HIP(hipEventCreateWithFlags(&s->ev_packed, hipEventDisableTiming));
-    VK_HIP(hipEventCreateWithFlags(&s->ev_copied, hipEventDisableTiming));
+  vapi_spill_store::Inflight e;
+  e.packed = s->event();
+  e.copied = s->event();
+  if (!e.packed || !e.copied) {
+    if (e.packed) s->spare_events.push_back(e.packed);
+    if (e.copied) s->spare_events.push_back(e.copied);
+    VK_FAIL(VAPI_KV_EHIP, "vapi_spill_evicted_async: hipEventCreate failed");
   }
   uint32_t* id_stage = (uint32_t*)pinned;
   uint8_t* blobs = (uint8_t*)pinned + head;
   for (uint32_t j = 0; j < m; ++j) id_stage[j] = ids[todo[j]];
-  if (int rc = vapi_kv_export_blocks(pool, id_stage, m, staging, stream)) return rc;
-  VK_HIP(hipEventRecord(s->ev_packed, hs(stream)));
-  VK_HIP(hipStreamWaitEvent(hs(side), s->ev_packed, 0));
-  VK_HIP(hipMemcpyAsync(blobs, staging, (size_t)m * bb, hipMemcpyDeviceToHost, hs(side)));
-  VK_HIP(hipEventRecord(s->ev_copied, hs(side)));
-  s->pend_hashes.clear();
-  for (uint32_t j = 0; j < m; ++j) s->pend_hashes.push_back(to_hash(hashes + 32ull * todo[j]));
-  s->pend_blobs = blobs;
-  s->pend_bb = bb;
-  s->pending = true;
+  auto fail = [&](int rc) {
+    s->spare_events.push_back(e.packed);
+    s->spare_events.push_back(e.copied);
+    return rc;
+  };
+  if (int rc = vapi_kv_export_blocks(pool, id_stage, m, staging, stream)) return fail(rc);
+  hipError_t err = hipEventRecord(e.packed, hs(stream));
+  if (err == hipSuccess) err = hipStreamWaitEvent(hs(side), e.packed, 0);
+  if (err == hipSuccess)
+    err = hipMemcpyAsync(blobs, staging, (size_t)m * bb, hipMemcpyDeviceToHost, hs(side));
+  if (err == hipSuccess) err = hipEventRecord(e.copied, hs(side));
+  if (err != hipSuccess) {
+    set_error("vapi_spill_evicted_async: %s", hipGetErrorString(err));
+    return fail(VAPI_KV_EHIP);
+  }
+  e.blobs = blobs;
+  e.bb = bb;
+  e.pin_lo = pin0, e.pin_hi = pin0 + head + (size_t)m * bb;
+  e.stg_lo = stg0, e.stg_hi = stg0 + (size_t)m * bb;
+  e.hashes.reserve(m);
+  for (uint32_t j = 0; j < m; ++j) {
+    e.hashes.push_back(to_hash(hashes + 32ull * todo[j]));
+    ++s->in_flight_hashes[e.hashes.back()];
+  }
+  s->inflight.push_back(std::move(e));
   return m;
 }
 

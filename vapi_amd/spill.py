@@ -99,8 +99,10 @@ def spill_evicted_async(store: SpillStore, cache: PagedKvCache, evicted, staging
                         pinned: torch.Tensor, stream=None, side=None) -> int:
     """spill_evicted overlapped with the forward: the blocks are packed into
     device `staging` on `stream` and copied to `pinned` on `side`; they
-    enter the store at drain() or the next store call. Returns how many.
-    `staging` and `pinned` must stay untouched until then."""
+    enter the store at a drain (drain(), or any later store call once their
+    copy has completed). Returns how many. Up to 16 exports are in flight,
+    each owning its buffers until drained: rotate a ring of them (a call
+    reusing an in-flight export's buffers waits for it)."""
     evicted = list(evicted)
     if any(len(h) != 32 for h, _ in evicted):
         raise ValueError("block hashes are 32 bytes")
