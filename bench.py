@@ -241,8 +241,23 @@ def bench_prefill(steps, warmup):
     tf = w.flops() / (ms * 1e-3) / 1e12
     log(f"prefill cfg3: {w.flops() / 1e12:.3f} TFLOP, {ms:.2f} ms, {tf:.1f} TFLOP/s "
         f"({tf / BF16_MFMA_PEAK_TFLOPS:.1%} of 2.5 PF)")
-    del cache
-    return dict(ms=ms, tflops=tf, frac=tf / BF16_MFMA_PEAK_TFLOPS, flops=w.flops())
+    del cache, q, out
+    gemm = mfma_probe()
+    log(f"bf16 GEMM probe (hipBLASLt, 8192^3): {gemm:.0f} TFLOP/s; prefill at "
+        f"{tf / gemm:.1%} of it")
+    return dict(ms=ms, tflops=tf, frac=tf / BF16_MFMA_PEAK_TFLOPS, flops=w.flops(),
+                gemm_probe_tflops=gemm, frac_of_gemm_probe=tf / gemm)
+
+
+def mfma_probe():
+    """Dense bf16 GEMM (torch.matmul -> hipBLASLt), 8192 x 8192 x 8192: what
+    a library GEMM reaches of the MFMA peak on this box."""
+    n = 8192
+    a = torch.randn(n, n, device=DEV).to(torch.bfloat16)
+    b = torch.randn(n, n, device=DEV).to(torch.bfloat16)
+    c = torch.empty(n, n, device=DEV, dtype=torch.bfloat16)
+    ms, _ = timed(lambda: torch.matmul(a, b, out=c), 20, 5)
+    return 2.0 * n ** 3 / (ms * 1e-3) / 1e12
 
 
 # ---- config 4: copy-on-write and swap ---------------------------------------------
