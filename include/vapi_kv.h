@@ -68,6 +68,18 @@ typedef enum {
  * l*layer_stride_bytes; each is num_blocks blocks in `layout`. A slot is
  * block*block_size + offset, the addressing of ForwardBatch::slot_mapping
  * (crates/vapi-engine/src/backend.rs:62-64).
+ *
+ * v == NULL makes a K-only pool: LayerLayout::Rows layers (cache.rs:24-33,
+ * 89-96), one (1, width) row per token, num_kv_heads 1 and head_dim width.
+ * Appends and gathers then move K only; attention rejects the pool.
+ *
+ * next chains further pools of the same cache (same num_blocks and
+ * block_size; any geometry, dtype, layout, with or without V), in layer
+ * order: a cache whose layers differ (PagedKvCache::with_layouts,
+ * cache.rs:71-105) is one pool per run of alike layers. Block-level calls
+ * (block_bytes, copy_blocks, export/import, swap, the spill tier) walk the
+ * chain; per-layer calls (append, gather, attention) use the pool they are
+ * given and ignore next. NULL ends the chain.
  */
 typedef struct vapi_kv_pool {
   void* k;
@@ -80,6 +92,7 @@ typedef struct vapi_kv_pool {
   uint32_t head_dim;
   uint32_t dtype;  /* vapi_kv_dtype */
   uint32_t layout; /* vapi_kv_layout */
+  const struct vapi_kv_pool* next; /* the next pool of the same cache, or NULL */
 } vapi_kv_pool;
 
 /* Thread-local message for the last failing call on this thread ("" if none). */
@@ -89,7 +102,8 @@ const char* vapi_kv_last_error(void);
 const char* vapi_kv_version(void);
 
 /* Bytes of one block across every layer, K then V (backend.rs:695-708):
- * num_layers * 2 * block_size * num_kv_heads * head_dim * sizeof(dtype). */
+ * num_layers * 2 * block_size * num_kv_heads * head_dim * sizeof(dtype)
+ * (1 instead of 2 for a K-only pool), summed over the pool chain. */
 size_t vapi_kv_block_bytes(const vapi_kv_pool* pool);
 
 /* Bytes of one layer's K (or V) buffer: num_blocks * block elements. */
@@ -217,7 +231,8 @@ int vapi_paged_attention_append(const vapi_kv_pool* pool, uint32_t layer,
                                 size_t workspace_bytes, vapi_stream_t stream);
 
 /*
- * Copy-on-write block copy over every layer, K and V, in one launch.
+ * Copy-on-write block copy over every layer, K and V, in one launch (one
+ * per chained pool; a K-only pool copies K).
  * Replaces CandleBackend::copy_blocks (backend.rs:781-797), which the
  * engine calls with Scheduler::fork's pairs (scheduler.rs:217-281).
  * pairs: device u32[n_pairs][2] = (src, dst). A dst must not also be a src
@@ -230,7 +245,9 @@ int vapi_kv_copy_blocks(const vapi_kv_pool* pool, const uint32_t* pairs,
  * Spill export / import. Block i's blob (vapi_kv_block_bytes bytes) is the
  * reference's byte order (backend.rs:718-734, 738-773): K of layers
  * 0..L-1, then V of layers 0..L-1, each [block_size, num_kv_heads, head_dim]
- * in native little-endian element bytes, whatever the pool layout.
+ * in native little-endian element bytes, whatever the pool layout. Over a
+ * pool chain the layers are those of every pool in order, and K-only
+ * pools contribute no V segments (rank-1 V buffers are skipped there).
  * ids: device u32[n]. dst/src: n blobs back to back; device memory or
  * host-mapped pinned memory (hipHostMalloc), either is read/written directly
  * by the kernel.

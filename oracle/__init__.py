@@ -23,6 +23,7 @@ SKIP = 0xFFFFFFFF
 
 _u8p = ctypes.POINTER(ctypes.c_uint8)
 _u32p = ctypes.POINTER(ctypes.c_uint32)
+_u64p = ctypes.POINTER(ctypes.c_uint64)
 _f32p = ctypes.POINTER(ctypes.c_float)
 _f64p = ctypes.POINTER(ctypes.c_double)
 
@@ -53,16 +54,17 @@ def lib():
             ctypes.c_uint32, ctypes.c_uint32, ctypes.c_double, ctypes.c_int32,
             ctypes.c_int32, _f64p]
         L.oracle_dense_attention_f64.restype = None
-        L.oracle_block_bytes.argtypes = [ctypes.c_uint32] * 5
+        _u64p = ctypes.POINTER(ctypes.c_uint64)
+        L.oracle_block_bytes.argtypes = [_u64p, ctypes.c_uint32]
         L.oracle_block_bytes.restype = ctypes.c_uint64
         pp = ctypes.POINTER(_u8p)
-        L.oracle_export_block.argtypes = [pp, pp, ctypes.c_uint32, ctypes.c_uint64,
-                                          ctypes.c_uint32, _u8p]
-        L.oracle_import_block.argtypes = [pp, pp, ctypes.c_uint32, ctypes.c_uint64,
-                                          ctypes.c_uint32, _u8p, ctypes.c_uint64]
+        L.oracle_export_block.argtypes = [pp, _u64p, ctypes.c_uint32, ctypes.c_uint32, _u8p]
+        L.oracle_export_block.restype = None
+        L.oracle_import_block.argtypes = [pp, _u64p, ctypes.c_uint32, ctypes.c_uint32, _u8p,
+                                          ctypes.c_uint64]
         L.oracle_import_block.restype = ctypes.c_int
-        L.oracle_copy_blocks.argtypes = [pp, pp, ctypes.c_uint32, ctypes.c_uint64,
-                                         _u32p, ctypes.c_uint32]
+        L.oracle_copy_blocks.argtypes = [pp, _u64p, ctypes.c_uint32, _u32p, ctypes.c_uint32]
+        L.oracle_copy_blocks.restype = None
         _LIB = L
     return _LIB
 
@@ -169,37 +171,50 @@ def dense_attention_f64(q, k, v, scale, sliding_window=None, window_right=0):
 
 
 def block_bytes(layers, block_size, kvh, d, elt):
-    return lib().oracle_block_bytes(layers, block_size, kvh, d, elt)
+    """block_bytes (backend.rs:695-708) of a uniform cache."""
+    per = np.full(2 * layers, block_size * kvh * d * elt, dtype=np.uint64)
+    return lib().oracle_block_bytes(_p(per, _u64p), per.size)
 
 
-def _layer_ptrs(pools):
-    arr = (_u8p * len(pools))(*[_p(p.view(np.uint8).reshape(-1), _u8p) for p in pools])
-    return arr
+def _buffers(k_layers, v_layers):
+    """The reference's buffer order k[0..L] ++ v[0..L] as (pointers, per-block
+    bytes, count); a V layer that is None or empty (a rows layer) is
+    skipped, as the reference skips buffers of rank < 2."""
+    bufs = list(k_layers) + list(v_layers)
+    real = [b is not None and b.ndim >= 2 and b.size > 0 for b in bufs]
+    ptrs = (_u8p * len(bufs))(*[_p(b.view(np.uint8).reshape(-1), _u8p) if r else None
+                                for b, r in zip(bufs, real)])
+    per = np.array([b[0].nbytes if r else 0 for b, r in zip(bufs, real)], dtype=np.uint64)
+    return ptrs, per, len(bufs)
+
+
+def cache_block_bytes(k_layers, v_layers) -> int:
+    """block_bytes (backend.rs:695-708) of per-layer pools of any shapes."""
+    _, per, n = _buffers(k_layers, v_layers)
+    return lib().oracle_block_bytes(_p(per, _u64p), n)
 
 
 def export_block(k_layers, v_layers, block_id) -> bytes:
-    """export_block (backend.rs:718-734). k_layers/v_layers: per-layer pools."""
-    blk = k_layers[0][0].nbytes
-    out = np.zeros(2 * len(k_layers) * blk, dtype=np.uint8)
-    lib().oracle_export_block(_layer_ptrs(k_layers), _layer_ptrs(v_layers),
-                              len(k_layers), blk, block_id, _p(out, _u8p))
-    return out.tobytes()
+    """export_block (backend.rs:718-734). k_layers/v_layers: per-layer pools
+    (None or an empty array for a rows layer's V)."""
+    ptrs, per, n = _buffers(k_layers, v_layers)
+    out = np.zeros(max(int(per.sum()), 1), dtype=np.uint8)
+    lib().oracle_export_block(ptrs, _p(per, _u64p), n, block_id, _p(out, _u8p))
+    return out[:int(per.sum())].tobytes()
 
 
 def import_block(k_layers, v_layers, block_id, data: bytes) -> None:
     """import_block (backend.rs:738-773), in place."""
-    blk = k_layers[0][0].nbytes
+    ptrs, per, n = _buffers(k_layers, v_layers)
     buf = np.frombuffer(data, dtype=np.uint8).copy()
-    rc = lib().oracle_import_block(_layer_ptrs(k_layers), _layer_ptrs(v_layers),
-                                   len(k_layers), blk, block_id, _p(buf, _u8p), buf.size)
+    rc = lib().oracle_import_block(ptrs, _p(per, _u64p), n, block_id, _p(buf, _u8p), buf.size)
     if rc != 0:
         raise ValueError(f"spilled block is {buf.size} bytes, this cache wants "
-                         f"{2 * len(k_layers) * blk}")
+                         f"{int(per.sum())}")
 
 
 def copy_blocks(k_layers, v_layers, pairs) -> None:
     """copy_blocks (backend.rs:781-797), in place."""
     pairs = np.ascontiguousarray(np.asarray(pairs, dtype=np.uint32).reshape(-1, 2))
-    blk = k_layers[0][0].nbytes
-    lib().oracle_copy_blocks(_layer_ptrs(k_layers), _layer_ptrs(v_layers), len(k_layers),
-                             blk, _p(pairs, _u32p), pairs.shape[0])
+    ptrs, per, n = _buffers(k_layers, v_layers)
+    lib().oracle_copy_blocks(ptrs, _p(per, _u64p), n, _p(pairs, _u32p), pairs.shape[0])

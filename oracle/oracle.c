@@ -243,54 +243,59 @@ void oracle_dense_attention_f64(const double* q, const double* k,
   free(w);
 }
 
-/* block_bytes (backend.rs:695-708): sum over K and V buffers of every layer
- * of the per-block bytes. */
-uint64_t oracle_block_bytes(uint32_t layers, uint32_t block_size, uint32_t kvh,
-                            uint32_t d, uint32_t elt) {
-  return (uint64_t)layers * 2 * block_size * kvh * d * elt;
+/* The block methods below take the cache's buffers in the reference's
+ * iteration order, k[0..L] ++ v[0..L] (backend.rs:697-700, 720, 751-757),
+ * as `nbuf` pointers with each buffer's per-block byte count (the product of
+ * its dims past the first, times the element size). A buffer that is not
+ * at least rank 2 (a rows layer's empty V, cache.rs:96) is passed as NULL
+ * with 0 bytes and skipped, as the reference skips it. */
+
+/* block_bytes (backend.rs:695-708): the sum of the per-block bytes. */
+uint64_t oracle_block_bytes(const uint64_t* blk_bytes, uint32_t nbuf) {
+  uint64_t sum = 0;
+  for (uint32_t i = 0; i < nbuf; ++i) sum += blk_bytes[i];
+  return sum;
 }
 
-/* export_block (backend.rs:718-734): for each buffer in k[0..L] ++ v[0..L],
- * the block's (bs, kvh, d) bytes, concatenated. k_layers/v_layers: arrays
- * of L pointers to per-layer pools. */
-void oracle_export_block(uint8_t* const* k_layers, uint8_t* const* v_layers,
-                         uint32_t layers, uint64_t blk_bytes, uint32_t id,
-                         uint8_t* out) {
+/* export_block (backend.rs:718-734): each buffer's block `id`, flattened,
+ * concatenated in buffer order. */
+void oracle_export_block(uint8_t* const* bufs, const uint64_t* blk_bytes, uint32_t nbuf,
+                         uint32_t id, uint8_t* out) {
   uint64_t at = 0;
-  for (uint32_t i = 0; i < 2 * layers; ++i) {
-    const uint8_t* buf = i < layers ? k_layers[i] : v_layers[i - layers];
-    memcpy(out + at, buf + (uint64_t)id * blk_bytes, blk_bytes);
-    at += blk_bytes;
+  for (uint32_t i = 0; i < nbuf; ++i) {
+    if (!bufs[i] || !blk_bytes[i]) continue;
+    memcpy(out + at, bufs[i] + (uint64_t)id * blk_bytes[i], blk_bytes[i]);
+    at += blk_bytes[i];
   }
 }
 
-/* import_block (backend.rs:738-773): length must equal block_bytes, then the
- * same order is sliced back. Returns -1 on a length mismatch. */
-int oracle_import_block(uint8_t* const* k_layers, uint8_t* const* v_layers,
-                        uint32_t layers, uint64_t blk_bytes, uint32_t id,
-                        const uint8_t* bytes, uint64_t len) {
-  if (len != 2ull * layers * blk_bytes) return -1;
+/* import_block (backend.rs:738-773): the length must equal block_bytes,
+ * then the same order is sliced back. Returns -1 on a length mismatch. */
+int oracle_import_block(uint8_t* const* bufs, const uint64_t* blk_bytes, uint32_t nbuf,
+                        uint32_t id, const uint8_t* bytes, uint64_t len) {
+  if (len != oracle_block_bytes(blk_bytes, nbuf)) return -1;
   uint64_t at = 0;
-  for (uint32_t i = 0; i < 2 * layers; ++i) {
-    uint8_t* buf = i < layers ? k_layers[i] : v_layers[i - layers];
-    memcpy(buf + (uint64_t)id * blk_bytes, bytes + at, blk_bytes);
-    at += blk_bytes;
+  for (uint32_t i = 0; i < nbuf; ++i) {
+    if (!bufs[i] || !blk_bytes[i]) continue;
+    memcpy(bufs[i] + (uint64_t)id * blk_bytes[i], bytes + at, blk_bytes[i]);
+    at += blk_bytes[i];
   }
   return 0;
 }
 
 /* copy_blocks (backend.rs:781-797): pairs in order; for each, every layer,
- * K then V, dst := src. */
-void oracle_copy_blocks(uint8_t* const* k_layers, uint8_t* const* v_layers,
-                        uint32_t layers, uint64_t blk_bytes,
+ * K then V (`nbuf` = 2L, k[l] at l and v[l] at L + l), dst := src. */
+void oracle_copy_blocks(uint8_t* const* bufs, const uint64_t* blk_bytes, uint32_t nbuf,
                         const uint32_t* pairs, uint32_t n_pairs) {
+  const uint32_t layers = nbuf / 2;
   for (uint32_t p = 0; p < n_pairs; ++p) {
     const uint32_t src = pairs[2 * p], dst = pairs[2 * p + 1];
-    for (uint32_t l = 0; l < layers; ++l) {
-      memmove(k_layers[l] + (uint64_t)dst * blk_bytes,
-              k_layers[l] + (uint64_t)src * blk_bytes, blk_bytes);
-      memmove(v_layers[l] + (uint64_t)dst * blk_bytes,
-              v_layers[l] + (uint64_t)src * blk_bytes, blk_bytes);
-    }
+    for (uint32_t l = 0; l < layers; ++l)
+      for (uint32_t kv = 0; kv < 2; ++kv) {
+        const uint32_t i = kv * layers + l;
+        if (!bufs[i] || !blk_bytes[i]) continue;
+        memmove(bufs[i] + (uint64_t)dst * blk_bytes[i], bufs[i] + (uint64_t)src * blk_bytes[i],
+                blk_bytes[i]);
+      }
   }
 }

@@ -164,3 +164,37 @@ def test_the_workloads_have_the_baseline_shapes():
     w4 = workload.config4_block_ops()
     assert w4.pairs.shape == (2048, 2) and len(w4.swap_ids) == 4096
     assert not set(w4.pairs[:, 1]) & set(w4.pairs[:, 0])
+
+
+def test_block_bytes_walks_a_pool_chain_and_k_only_pools_count_k():
+    """A cache whose layers differ is a chain of pools: block_bytes sums
+    them (backend.rs:695-708), a K-only pool (a rows layer, v NULL) counts
+    its K alone. Checked against the oracle's sum over the same buffers."""
+    L = _lib.lib()
+    a = pool(num_layers=2, num_kv_heads=2, head_dim=64)
+    rows = pool(num_layers=1, num_kv_heads=1, head_dim=40)
+    rows.v = None
+    b = pool(num_layers=3, num_kv_heads=4, head_dim=128)
+    a.next = ctypes.addressof(rows)
+    rows.next = ctypes.addressof(b)
+    k = [np.zeros((1, 16, 2, 64), np.uint16)] * 2 + [np.zeros((1, 16, 1, 40), np.uint16)] + \
+        [np.zeros((1, 16, 4, 128), np.uint16)] * 3
+    v = [np.zeros((1, 16, 2, 64), np.uint16)] * 2 + [None] + \
+        [np.zeros((1, 16, 4, 128), np.uint16)] * 3
+    assert L.vapi_kv_block_bytes(ctypes.byref(a)) == oracle.cache_block_bytes(k, v)
+    assert L.vapi_kv_block_bytes(ctypes.byref(rows)) == 16 * 40 * 2 + 3 * 2 * 16 * 4 * 128 * 2
+
+
+def test_a_chain_of_pools_on_different_blocks_is_an_error():
+    L = _lib.lib()
+    a = pool(num_layers=1)
+    b = pool(num_layers=1, num_blocks=7)
+    a.next = ctypes.addressof(b)
+    pairs = (ctypes.c_uint32 * 2)(0, 1)
+    assert L.vapi_kv_copy_blocks(ctypes.byref(a), pairs, 1, None) == _lib.EINVAL
+    assert b"chained pool" in L.vapi_kv_last_error()
+    # A K-only pool refuses V rows.
+    k = pool(num_layers=1)
+    k.v = None
+    assert L.vapi_kv_append(ctypes.byref(k), 0, 1, 1, 1, 1, None) == _lib.EINVAL
+    assert b"K-only" in L.vapi_kv_last_error()

@@ -435,3 +435,126 @@ def test_async_spills_in_flight_on_a_ring_of_buffers_all_arrive_intact():
     assert store.stats()["ram_blocks"] == 5 * per
     for h, w in want.items():
         assert store.get(h, bb) == w
+
+
+# ---- rows layers and caches whose layers differ -------------------------------------------
+
+def _np_layers(c):
+    """Per-layer pools as the reference's [nb, bs, kvh, d] numpy arrays (None
+    for a rows layer's V)."""
+    ks = [as_np(c.reference_view(l, "k").contiguous()) for l in range(c.num_layers)]
+    vs = [as_np(c.reference_view(l, "v").contiguous()) if c.v[l].dim() == 4 else None
+          for l in range(c.num_layers)]
+    return ks, vs
+
+
+@pytest.mark.gpu
+def test_a_rows_layer_stores_one_row_per_token_and_no_v():
+    """cache.rs:414-436 on the device: rows 0..9 written at slots 9, 10 of a
+    Rows(5) layer come back from block 2 after an untouched slot 8; the K/V
+    layer beside it stays zero; V rows or a V gather on it are errors."""
+    from vapi_amd.cache import HybridKvCache, write_k_to_cache
+    c = HybridKvCache([("kv", 2, 3), ("rows", 5)], 4, 4, torch.float32, "NHD")
+    assert tuple(c.k[1].shape) == (4, 4, 1, 5) and c.v[1].numel() == 0
+    rows_ = torch.arange(10, dtype=torch.float32, device=DEV).reshape(2, 1, 5)
+    write_k_to_cache(c, 1, rows_, [9, 10])
+    got = gather_kv(c, 1, [2], 3).reshape(3, 5).cpu().tolist()
+    assert got == [[0.0] * 5, [0.0, 1.0, 2.0, 3.0, 4.0], [5.0, 6.0, 7.0, 8.0, 9.0]]
+    assert float(c.k[0].abs().sum()) == 0.0
+    with pytest.raises(ValueError):
+        write_kv_to_cache(c, 1, rows_, rows_, [0, 1])
+    with pytest.raises(ValueError):
+        gather_kv(c, 1, [2], 3, which="v")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("layout", ["HND", "NHD"])
+def test_a_mixed_cache_moves_blocks_like_the_reference(layout):
+    """A cache of layers Kv(4, 128), Rows(40), Kv(4, 128), Rows(24), Kv(2, 64)
+    (a hybrid model's attention and short-convolution layers), bf16: its
+    block bytes, export, import, copy_blocks and swap through pinned memory
+    against the oracle's per-buffer restatement of backend.rs:695-797,
+    bit-exact; single-buffer writes (write_k_to_cache on a K/V layer,
+    write_v_rows_indexed) touch only their buffer."""
+    from vapi_amd.cache import HybridKvCache, write_k_to_cache, write_v_rows_indexed
+    specs = [("kv", 4, 128), ("rows", 40), ("kv", 4, 128), ("rows", 24), ("kv", 2, 64)]
+    nb = 40
+    c = HybridKvCache(specs, nb, 16, torch.bfloat16, layout)
+    g = torch.Generator(device=DEV).manual_seed(7)
+    for t in c.k + c.v:
+        if t.numel():
+            t.copy_(torch.randn(t.shape, generator=g, device=DEV).to(t.dtype))
+    be = KvBlockBackend(c)
+    ks, vs = _np_layers(c)
+    assert be.block_bytes() == oracle.cache_block_bytes(ks, vs)
+    ids = [3, 17, 0, 39, 22]
+    blob = be.export_blocks(ids)
+    bb = be.block_bytes()
+    for j, b in enumerate(ids):
+        assert blob[j * bb:(j + 1) * bb].cpu().numpy().tobytes() == oracle.export_block(ks, vs, b)
+    # Import into other blocks: they equal the sources, nothing else moves.
+    before = [t.clone() for t in c.k + c.v]
+    dst = [5, 6, 30, 31, 8]
+    be.import_blocks(dst, blob)
+    torch.cuda.synchronize()
+    for t, t0 in zip(c.k + c.v, before):
+        if t.numel():
+            assert torch.equal(t[dst], t0[ids])
+            keep = [i for i in range(nb) if i not in dst]
+            assert torch.equal(t[keep], t0[keep])
+    # copy_blocks against the oracle.
+    ks, vs = _np_layers(c)
+    pairs = [(1, 10), (2, 11), (39, 12)]
+    be.copy_blocks(pairs)
+    oracle.copy_blocks(ks, vs, pairs)
+    got_k, got_v = _np_layers(c)
+    for a, b in zip(ks + vs, got_k + got_v):
+        if a is not None:
+            np.testing.assert_array_equal(a.view(np.uint16), b.view(np.uint16))
+    # Swap out through pinned memory and back into other blocks.
+    ids_dev = torch.tensor([4, 9], dtype=torch.int32, device=DEV)
+    host = torch.empty(2 * bb, dtype=torch.uint8, pin_memory=True)
+    staging = torch.empty(bb, dtype=torch.uint8, device=DEV)
+    be.swap_out(ids_dev, host, staging)
+    back = torch.tensor([13, 14], dtype=torch.int32, device=DEV)
+    be.swap_in(back, host, staging)
+    torch.cuda.synchronize()
+    assert be.export_block(13) == be.export_block(4) and be.export_block(14) == be.export_block(9)
+    # Single-buffer writes.
+    k0 = c.k[0].clone()
+    v0 = c.v[0].clone()
+    rows_k = torch.randn(3, 4, 128, generator=g, device=DEV).to(torch.bfloat16)
+    write_k_to_cache(c, 0, rows_k, [16 * 20, 16 * 20 + 1, 16 * 21])
+    assert torch.equal(c.v[0], v0)
+    idx = torch.tensor([16 * 25 + 3], dtype=torch.int32, device=DEV)
+    write_v_rows_indexed(c, 0, rows_k[:1], idx)
+    ref_k = c.reference_view(0, "k")
+    ref_v = c.reference_view(0, "v")
+    assert torch.equal(ref_k[20, 0], rows_k[0]) and torch.equal(ref_k[21, 0], rows_k[2])
+    assert torch.equal(ref_v[25, 3], rows_k[0])
+    changed = (c.k[0] != k0).flatten(1).any(1).nonzero().flatten().tolist()
+    assert changed == [20, 21]
+
+
+@pytest.mark.gpu
+def test_a_mixed_cache_spills_and_promotes_bit_exact():
+    """The spill tier over a chained cache: blobs are the whole chain's
+    blocks in the reference byte order and come back intact."""
+    import hashlib
+    from vapi_amd.cache import HybridKvCache
+    from vapi_amd.spill import SpillStore, pinned_buffer, promote, spill_evicted
+    c = HybridKvCache([("rows", 48), ("kv", 2, 128), ("rows", 48)], 32, 16, torch.bfloat16)
+    for t in c.k + c.v:
+        if t.numel():
+            workload.fill_normal(t, 11)
+    be = KvBlockBackend(c)
+    ks, vs = _np_layers(c)
+    hs = [hashlib.sha256(b"mixed %d" % i).digest() for i in range(6)]
+    store = SpillStore(None, 1 << 30, 0)
+    pinned = pinned_buffer(c, 4)
+    assert spill_evicted(store, c, zip(hs, range(6)), pinned) == 6
+    for i, h in enumerate(hs):
+        assert store.get(h, be.block_bytes()) == oracle.export_block(ks, vs, i)
+    assert promote(store, c, hs, list(range(20, 26)), pinned) == 6
+    for i in range(6):
+        assert be.export_block(20 + i) == be.export_block(i)

@@ -323,3 +323,63 @@ def test_block_sizing_matches_hand_arithmetic():
     per_block = oracle.block_bytes(16, 32, 8, 64, 2)
     assert (1 << 30) // per_block == 1024
     assert (1 << 30) // oracle.block_bytes(16, 32, 8, 64, 4) == 512
+
+
+# ---- rows layers and caches whose layers differ --------------------------------------
+
+def test_a_rows_layer_stores_one_row_per_token_and_no_v():
+    """cache.rs:414-436: a Kv(2, 3) layer and a Rows(5) layer; the rows layer
+    is [4, BS, 1, 5], K only; rows 0..9 at slots 9, 10 come back from block 2
+    (slots 8..11) after an untouched slot 8."""
+    k0 = np.zeros((4, BS, 2, 3), np.float32)
+    k1 = np.zeros((4, BS, 1, 5), np.float32)
+    assert k1.shape == (4, BS, 1, 5)
+    assert (2 * 2 * 3) + 5 == 17  # elems_per_token of the two layouts
+    rows_ = np.arange(10, dtype=np.float32).reshape(2, 1, 5)
+    oracle.write_rows(k1, rows_, [9, 10])
+    got = oracle.gather_kv(k1, [2], 3).reshape(3, 5)
+    np.testing.assert_array_equal(got[0], np.zeros(5))
+    np.testing.assert_array_equal(got[1], [0, 1, 2, 3, 4])
+    np.testing.assert_array_equal(got[2], [5, 6, 7, 8, 9])
+    assert k0.sum() == 0
+
+
+def test_a_mixed_cache_exports_k_of_every_layer_then_the_v_that_exist():
+    """backend.rs:695-773 over layers Kv(2, 3), Rows(5), Kv(1, 4): buffers of
+    rank < 2 (the rows layer's V) are skipped. Each buffer is stamped with
+    its own constant, so the blob order and segment sizes are read off
+    directly; block_bytes is the hand sum; import inverts export; a length
+    mismatch is an error; copy_blocks moves every real buffer."""
+    nb = 6
+    shapes = [(nb, BS, 2, 3), (nb, BS, 1, 5), (nb, BS, 1, 4)]
+    kc = [np.full(s, 10 + i, np.float32) for i, s in enumerate(shapes)]
+    vc = [np.full(shapes[0], 20, np.float32), np.zeros((0,), np.float32),
+          np.full(shapes[2], 22, np.float32)]
+    segs = [(BS * 2 * 3, 10), (BS * 5, 11), (BS * 4, 12), (BS * 2 * 3, 20), (BS * 4, 22)]
+    want_bytes = 4 * sum(n for n, _ in segs)
+    assert oracle.cache_block_bytes(kc, vc) == want_bytes == 4 * (24 + 20 + 16 + 24 + 16)
+    blob = np.frombuffer(oracle.export_block(kc, vc, 3), np.float32)
+    assert blob.nbytes == want_bytes
+    at = 0
+    for n, stamp in segs:
+        assert (blob[at:at + n] == stamp).all(), stamp
+        at += n
+    rng = np.random.default_rng(2)
+    for p in kc + vc:
+        p[...] = rng.standard_normal(p.shape)
+    data = oracle.export_block(kc, vc, 1)
+    k2 = [np.zeros_like(p) for p in kc]
+    v2 = [np.zeros_like(p) for p in vc]
+    oracle.import_block(k2, v2, 5, data)
+    for a, b in zip(kc + vc, k2 + v2):
+        if a.size:
+            np.testing.assert_array_equal(a[1], b[5])
+            assert np.count_nonzero(b[:5]) == 0
+    with pytest.raises(ValueError):
+        oracle.import_block(k2, v2, 0, data + b"\0" * 4)
+    before = [p.copy() for p in kc + vc]
+    oracle.copy_blocks(kc, vc, [(2, 0)])
+    for a, b in zip(before, kc + vc):
+        if a.size:
+            np.testing.assert_array_equal(b[0], a[2])
+            np.testing.assert_array_equal(b[1:], a[1:])

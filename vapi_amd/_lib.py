@@ -54,6 +54,7 @@ class Pool(ctypes.Structure):
         ("head_dim", ctypes.c_uint32),
         ("dtype", ctypes.c_uint32),
         ("layout", ctypes.c_uint32),
+        ("next", ctypes.c_void_p),
     ]
 
 

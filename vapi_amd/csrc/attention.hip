@@ -81,6 +81,7 @@ int vapi_paged_attention_append(const vapi_kv_pool* pool, uint32_t layer, const 
                                 int32_t window_left, int32_t window_right, void* workspace,
                                 size_t workspace_bytes, vapi_stream_t stream) {
   if (int rc = check_pool(pool, "vapi_paged_attention_append")) return rc;
+  if (!pool->v) VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention_append: a K-only pool has no V to attend over");
   const bool fused = n_tokens > 0 && batch > 0 && max_seqlen_q == 1 && num_heads > 0 &&
                      num_heads % pool->num_kv_heads == 0 && mfma_ok(pool, num_heads);
   if (!fused) {
@@ -110,6 +111,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
                                 size_t workspace_bytes, vapi_stream_t stream,
                                 const NewRows* fuse) {
   if (int rc = check_pool(pool, "vapi_paged_attention")) return rc;
+  if (!pool->v) VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: a K-only pool has no V to attend over");
   if (layer >= pool->num_layers)
     VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: layer %u of %u", layer,
             pool->num_layers);

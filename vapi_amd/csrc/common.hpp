@@ -50,7 +50,9 @@ inline size_t dtype_size(uint32_t dt) {
 }
 
 // Validates a pool descriptor; returns 0 or an error code with a message.
+// Validates a pool and every pool chained to it through `next`.
 int check_pool(const vapi_kv_pool* p, const char* who);
+constexpr uint32_t kMaxPoolChain = 4096;  // chained pools beyond the first
 
 // ---- geometry -------------------------------------------------------------
 

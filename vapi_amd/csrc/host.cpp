@@ -49,6 +49,7 @@ int vapi_cache_new(uint32_t num_layers, uint32_t num_blocks,
   p.head_dim = head_dim;
   p.dtype = dtype;
   p.layout = layout;
+  p.next = nullptr;
   const size_t layer_bytes = vapi_kv_layer_bytes(&p);
   // Align each layer buffer to 256 bytes.
   p.layer_stride_bytes = (layer_bytes + 255) & ~(size_t)255;

@@ -46,9 +46,31 @@ int check_pool(const vapi_kv_pool* p, const char* who) {
     VK_FAIL(VAPI_KV_EINVAL, "%s: layer stride %llu < layer size %llu", who,
             (unsigned long long)p->layer_stride_bytes,
             (unsigned long long)layer_bytes);
-  if (p->num_blocks > 0 && (!p->k || !p->v))
-    VK_FAIL(VAPI_KV_EINVAL, "%s: null K or V base pointer", who);
+  if (p->num_blocks > 0 && !p->k) VK_FAIL(VAPI_KV_EINVAL, "%s: null K base pointer", who);
+  // Further layer groups of the same cache (block-level calls walk them):
+  // each is a pool of its own, on the same blocks.
+  uint32_t links = 0;
+  for (const vapi_kv_pool* q = p->next; q; q = q->next) {
+    if (++links > kMaxPoolChain)
+      VK_FAIL(VAPI_KV_EINVAL, "%s: more than %u chained pools (a cycle?)", who, kMaxPoolChain);
+    if (q->num_blocks != p->num_blocks || q->block_size != p->block_size)
+      VK_FAIL(VAPI_KV_EINVAL,
+              "%s: chained pool %u has %u blocks of %u slots, the first %u of %u", who, links,
+              q->num_blocks, q->block_size, p->num_blocks, p->block_size);
+    vapi_kv_pool head = *q;
+    head.next = nullptr;
+    if (int rc = check_pool(&head, who)) return rc;
+  }
   return 0;
+}
+
+// Bytes of one block in the K buffers (or V buffers) of a pool's layers.
+static uint64_t pool_k_block_bytes(const vapi_kv_pool* p) {
+  return (uint64_t)p->num_layers * p->block_size * p->num_kv_heads * p->head_dim *
+         dtype_size(p->dtype);
+}
+static uint64_t pool_v_block_bytes(const vapi_kv_pool* p) {
+  return p->v ? pool_k_block_bytes(p) : 0;
 }
 
 // ---- append ---------------------------------------------------------------
@@ -59,8 +81,9 @@ struct AppendArgs {
   char* k_dst;
   char* v_dst;
   const uint32_t* slots;
-  uint32_t total;  // n_tokens * 2 * kvh * upr
+  uint32_t total;  // n_tokens * (2 or 1) * kvh * upr
   uint32_t num_slots;
+  uint32_t kv_shift;  // 1: K and V rows interleaved per token; 0: K only
   FastDiv upr, kvh, bs;
   uint32_t row_bytes;  // head_dim * elt
   uint64_t blk_b, head_b, tok_b;  // byte strides
@@ -88,7 +111,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
       const uint32_t u = i - r * a.upr.d;
       const uint32_t r2 = a.kvh.div(r);
       const uint32_t h = r - r2 * a.kvh.d;
-      const uint32_t kv = r2 & 1u, t = r2 >> 1;
+      const uint32_t kv = r2 & a.kv_shift, t = r2 >> a.kv_shift;
       // The source row and the slot are loaded together (the source address
       // does not depend on the slot), so one memory round trip precedes the
       // store.
@@ -208,7 +231,7 @@ __global__ __launch_bounds__(256) void kv_copy_kernel(CopyArgs a) {
       const uint32_t r = a.upb.div(i);
       const uint32_t u = i - r * a.upb.d;
       const uint32_t p = a.two_l.div(r);
-      const uint32_t s = r - p * a.two_l.d;  // 0..2L-1: K layers then V layers
+      const uint32_t s = r - p * a.two_l.d;  // K layers, then V layers (if any)
       const uint32_t kv = s >= a.num_layers;
       const uint32_t layer = kv ? s - a.num_layers : s;
       const uint32_t src_blk = a.pairs[2 * p], dst_blk = a.pairs[2 * p + 1];
@@ -225,16 +248,20 @@ __global__ __launch_bounds__(256) void kv_copy_kernel(CopyArgs a) {
 
 // ---- export / import (reference blob order) ----------------------------------
 
-// Blob of block i: segments s = 0..2L-1 (K layers then V layers), each NHD
-// [bs, kvh, d]. Item index = (((i*2L + s)*bs + t)*kvh + h)*upr + u, so the
-// blob side is walked contiguously.
+// Blob of block i: the K block of every layer of the cache in order, then
+// the V block of every layer that has V, each NHD [bs, kvh, d]. One launch
+// covers one pool of the chain: its segments s = 0..nbuf*L-1 (K layers, then
+// V layers) sit at k_off + l*seg_bytes and v_off + l*seg_bytes of each blob.
+// Item index = (((i*nbuf*L + s)*bs + t)*kvh + h)*upr + u, so a segment's blob
+// side is walked contiguously.
 struct BlobArgs {
   char* k;
   char* v;
   char* blob;
   const uint32_t* ids;
   uint64_t layer_b, blk_b, head_b, tok_b;
-  uint64_t block_bytes;
+  uint64_t block_bytes;  // blob stride: one block of the whole pool chain
+  uint64_t k_off, v_off; // this pool's first K and first V segment in a blob
   uint32_t total;
   FastDiv upr, kvh, bs, two_l;
   uint32_t num_layers, row_bytes, seg_bytes;
@@ -264,7 +291,8 @@ __global__ __launch_bounds__(256) void kv_blob_kernel(BlobArgs a) {
       const uint32_t blk = a.ids[bi];
       char* pool = (kv ? a.v : a.k) + layer * a.layer_b + blk * a.blk_b +
                    h * a.head_b + t * a.tok_b + (uint64_t)u * C;
-      char* blob = a.blob + bi * a.block_bytes + (uint64_t)s * a.seg_bytes +
+      char* blob = a.blob + bi * a.block_bytes + (kv ? a.v_off : a.k_off) +
+                   (uint64_t)layer * a.seg_bytes +
                    ((uint64_t)t * a.kvh.d + h) * a.row_bytes + (uint64_t)u * C;
       if (EXPORT) {
         val[j] = *(const V*)pool;
@@ -301,9 +329,11 @@ const char* vapi_kv_last_error(void) { return g_err.c_str(); }
 const char* vapi_kv_version(void) { return "vapi_kv 0.1.0 gfx950"; }
 
 size_t vapi_kv_block_bytes(const vapi_kv_pool* p) {
-  if (!p) return 0;
-  return (size_t)p->num_layers * 2 * p->block_size * p->num_kv_heads *
-         p->head_dim * dtype_size(p->dtype);
+  size_t bytes = 0;
+  uint32_t links = 0;
+  for (; p && links <= kMaxPoolChain; p = p->next, ++links)
+    bytes += pool_k_block_bytes(p) + pool_v_block_bytes(p);
+  return bytes;
 }
 
 size_t vapi_kv_layer_bytes(const vapi_kv_pool* p) {
@@ -323,7 +353,10 @@ static int append_impl(const char* who, const vapi_kv_pool* pool, uint32_t layer
     VK_FAIL(VAPI_KV_EINVAL, "%s: layers %u..%u of %u", who, layer0, layer0 + n_layers,
             pool->num_layers);
   if (n_tokens == 0) return 0;
-  if (!k_src || !v_src || !slot_mapping)
+  const bool has_v = pool->v != nullptr;
+  if (!has_v && v_src)
+    VK_FAIL(VAPI_KV_EINVAL, "%s: V rows for a K-only pool (a rows layer stores K only)", who);
+  if (!k_src || (has_v && !v_src) || !slot_mapping)
     VK_FAIL(VAPI_KV_EINVAL, "%s: null source or slot_mapping", who);
   if (n_layers > 65535) VK_FAIL(VAPI_KV_EUNSUP, "%s: %u layers in one call", who, n_layers);
   const Geom g = make_geom(pool);
@@ -335,18 +368,19 @@ static int append_impl(const char* who, const vapi_kv_pool* pool, uint32_t layer
   // Chunk size: the largest power of two up to 16 B that divides the row,
   // the source addresses and (several layers) both layer strides.
   int c = chunk_bytes_for(row_bytes);
-  const uint64_t align = (uint64_t)(uintptr_t)k_src | (uint64_t)(uintptr_t)v_src |
+  const uint64_t align = (uint64_t)(uintptr_t)k_src | (uint64_t)(uintptr_t)(has_v ? v_src : k_src) |
                          (n_layers > 1 ? src_layer_stride | pool->layer_stride_bytes : 0);
   while (c > 1 && align % c) c >>= 1;
-  const uint64_t total = (uint64_t)n_tokens * 2 * g.kvh * (row_bytes / c);
+  const uint64_t total = (uint64_t)n_tokens * (has_v ? 2 : 1) * g.kvh * (row_bytes / c);
   if (total >= (1ull << 31))
     VK_FAIL(VAPI_KV_EUNSUP, "%s: %u tokens is too many for one call", who, n_tokens);
   LayerPtrs lp = layer_ptrs(pool, layer0);
   AppendArgs a;
   a.k_src = (const char*)k_src;
-  a.v_src = (const char*)v_src;
+  a.v_src = (const char*)(has_v ? v_src : k_src);
   a.k_dst = lp.k;
-  a.v_dst = lp.v;
+  a.v_dst = has_v ? lp.v : lp.k;
+  a.kv_shift = has_v ? 1u : 0u;
   a.slots = slot_mapping;
   a.total = (uint32_t)total;
   a.num_slots = g.num_blocks * g.block_size;
@@ -393,6 +427,8 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
     VK_FAIL(VAPI_KV_EINVAL,
             "vapi_kv_gather: len_k %u exceeds %u blocks of %u slots", len_k,
             n_table, pool->block_size);
+  if (!pool->v && v_out)
+    VK_FAIL(VAPI_KV_EINVAL, "vapi_kv_gather: V output for a K-only pool");
   if (len_k == 0 || (!k_out && !v_out)) return 0;
   if (!block_table)
     VK_FAIL(VAPI_KV_EINVAL, "vapi_kv_gather: null block_table");
@@ -400,7 +436,7 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
   const uint32_t elt = dtype_size(pool->dtype);
   const uint32_t row_bytes = g.d * elt;
   const int c = chunk_bytes_for(row_bytes);
-  const uint64_t total = (uint64_t)2 * len_k * g.kvh * (row_bytes / c);
+  const uint64_t total = (uint64_t)(pool->v ? 2 : 1) * len_k * g.kvh * (row_bytes / c);
   if (total >= (1ull << 31))
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_kv_gather: len_k %u too large", len_k);
   LayerPtrs lp = layer_ptrs(pool, layer);
@@ -431,17 +467,16 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
   return 0;
 }
 
-int vapi_kv_copy_blocks(const vapi_kv_pool* pool, const uint32_t* pairs,
-                        uint32_t n_pairs, vapi_stream_t stream) {
-  if (int rc = check_pool(pool, "vapi_kv_copy_blocks")) return rc;
-  if (n_pairs == 0) return 0;
-  if (!pairs) VK_FAIL(VAPI_KV_EINVAL, "vapi_kv_copy_blocks: null pairs");
+// One pool of the chain: every layer's K and (if present) V block.
+static int copy_pool(const vapi_kv_pool* pool, const uint32_t* pairs, uint32_t n_pairs,
+                     hipStream_t stream) {
   const Geom g = make_geom(pool);
   const uint32_t elt = dtype_size(pool->dtype);
   const uint64_t blk_b = g.blk * elt;
   const int c = chunk_bytes_for(blk_b);
   const uint64_t upb = blk_b / c;
-  const uint64_t per_pair = (uint64_t)pool->num_layers * 2 * upb;
+  const uint32_t nbuf = pool->v ? 2 : 1;
+  const uint64_t per_pair = (uint64_t)pool->num_layers * nbuf * upb;
   if (per_pair >= (1ull << 31))
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_kv_copy_blocks: block too large");
   const uint32_t pairs_per_launch =
@@ -452,7 +487,7 @@ int vapi_kv_copy_blocks(const vapi_kv_pool* pool, const uint32_t* pairs,
   a.layer_b = pool->layer_stride_bytes;
   a.blk_b = blk_b;
   a.upb = FastDiv((uint32_t)upb);
-  a.two_l = FastDiv(2 * pool->num_layers);
+  a.two_l = FastDiv(nbuf * pool->num_layers);  // segment s >= num_layers is V
   a.num_layers = pool->num_layers;
   constexpr int ITEMS = 4;
   for (uint32_t p0 = 0; p0 < n_pairs; p0 += pairs_per_launch) {
@@ -462,7 +497,7 @@ int vapi_kv_copy_blocks(const vapi_kv_pool* pool, const uint32_t* pairs,
     const uint32_t grid = (a.total + 256 * ITEMS - 1) / (256 * ITEMS);
 #define L_COPY(C)                                                        \
   hipLaunchKernelGGL((kv_copy_kernel<C, ITEMS>), dim3(grid), dim3(256), 0, \
-                     hs(stream), a)
+                     stream, a)
     VK_DISPATCH_CHUNK(c, L_COPY)
 #undef L_COPY
     VK_LAUNCHED("kv_copy_blocks");
@@ -470,17 +505,25 @@ int vapi_kv_copy_blocks(const vapi_kv_pool* pool, const uint32_t* pairs,
   return 0;
 }
 
-static int blob_move(const vapi_kv_pool* pool, const uint32_t* ids, uint32_t n,
-                     char* blob, bool do_export, hipStream_t stream,
-                     const char* who) {
-  if (int rc = check_pool(pool, who)) return rc;
-  if (n == 0) return 0;
-  if (!ids || !blob) VK_FAIL(VAPI_KV_EINVAL, "%s: null ids or buffer", who);
+int vapi_kv_copy_blocks(const vapi_kv_pool* pool, const uint32_t* pairs,
+                        uint32_t n_pairs, vapi_stream_t stream) {
+  if (int rc = check_pool(pool, "vapi_kv_copy_blocks")) return rc;
+  if (n_pairs == 0) return 0;
+  if (!pairs) VK_FAIL(VAPI_KV_EINVAL, "vapi_kv_copy_blocks: null pairs");
+  for (const vapi_kv_pool* p = pool; p; p = p->next)
+    if (int rc = copy_pool(p, pairs, n_pairs, hs(stream))) return rc;
+  return 0;
+}
+
+static int blob_pool(const vapi_kv_pool* pool, const uint32_t* ids, uint32_t n, char* blob,
+                     uint64_t blob_stride, uint64_t k_off, uint64_t v_off, bool do_export,
+                     hipStream_t stream, const char* who) {
   const Geom g = make_geom(pool);
   const uint32_t elt = dtype_size(pool->dtype);
   const uint32_t row_bytes = g.d * elt;
   const int c = chunk_bytes_for(row_bytes);
-  const uint64_t per_block = (uint64_t)2 * pool->num_layers * g.block_size *
+  const uint32_t nbuf = pool->v ? 2 : 1;
+  const uint64_t per_block = (uint64_t)nbuf * pool->num_layers * g.block_size *
                              g.kvh * (row_bytes / c);
   if (per_block >= (1ull << 31))
     VK_FAIL(VAPI_KV_EUNSUP, "%s: block too large", who);
@@ -493,11 +536,13 @@ static int blob_move(const vapi_kv_pool* pool, const uint32_t* ids, uint32_t n,
   a.blk_b = g.blk * elt;
   a.head_b = g.head * elt;
   a.tok_b = g.tok * elt;
-  a.block_bytes = vapi_kv_block_bytes(pool);
+  a.block_bytes = blob_stride;
+  a.k_off = k_off;
+  a.v_off = v_off;
   a.upr = FastDiv(row_bytes / c);
   a.kvh = FastDiv(g.kvh);
   a.bs = FastDiv(g.block_size);
-  a.two_l = FastDiv(2 * pool->num_layers);
+  a.two_l = FastDiv(nbuf * pool->num_layers);
   a.num_layers = pool->num_layers;
   a.row_bytes = row_bytes;
   a.seg_bytes = (uint32_t)(g.blk * elt);
@@ -505,7 +550,7 @@ static int blob_move(const vapi_kv_pool* pool, const uint32_t* ids, uint32_t n,
   for (uint32_t b0 = 0; b0 < n; b0 += blocks_per_launch) {
     const uint32_t nb = std::min(blocks_per_launch, n - b0);
     a.ids = ids + b0;
-    a.blob = blob + (uint64_t)b0 * a.block_bytes;
+    a.blob = blob + (uint64_t)b0 * blob_stride;
     a.total = (uint32_t)(nb * per_block);
     const uint32_t grid = (a.total + 256 * ITEMS - 1) / (256 * ITEMS);
     if (do_export) {
@@ -522,6 +567,27 @@ static int blob_move(const vapi_kv_pool* pool, const uint32_t* ids, uint32_t n,
 #undef L_IMP
     }
     VK_LAUNCHED(who);
+  }
+  return 0;
+}
+
+// Export or import over the whole pool chain: one launch per pool, each
+// placing its segments at their offsets in the blob (backend.rs:718-773
+// order: K of every layer, then V of every layer with V).
+static int blob_move(const vapi_kv_pool* pool, const uint32_t* ids, uint32_t n,
+                     char* blob, bool do_export, hipStream_t stream,
+                     const char* who) {
+  if (int rc = check_pool(pool, who)) return rc;
+  if (n == 0) return 0;
+  if (!ids || !blob) VK_FAIL(VAPI_KV_EINVAL, "%s: null ids or buffer", who);
+  const uint64_t stride = vapi_kv_block_bytes(pool);
+  uint64_t k_off = 0, v_off = 0;
+  for (const vapi_kv_pool* p = pool; p; p = p->next) v_off += pool_k_block_bytes(p);
+  for (const vapi_kv_pool* p = pool; p; p = p->next) {
+    if (int rc = blob_pool(p, ids, n, blob, stride, k_off, v_off, do_export, stream, who))
+      return rc;
+    k_off += pool_k_block_bytes(p);
+    v_off += pool_v_block_bytes(p);
   }
   return 0;
 }
