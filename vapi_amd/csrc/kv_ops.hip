@@ -83,14 +83,14 @@ struct AppendArgs {
   const uint32_t* slots;
   uint32_t total;  // n_tokens * (2 or 1) * kvh * upr
   uint32_t num_slots;
-  uint32_t kv_shift;  // 1: K and V rows interleaved per token; 0: K only
+  uint32_t has_v;  // 0: a K-only pool (kernel template kKV = false)
   FastDiv upr, kvh, bs;
   uint32_t row_bytes;  // head_dim * elt
   uint64_t blk_b, head_b, tok_b;  // byte strides
   uint64_t src_layer_b, dst_layer_b;  // layer strides (grid y = layer)
 };
 
-template <int C, int ITEMS, bool kStream>
+template <int C, int ITEMS, bool kStream, bool kKV>
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   using V = typename Chunk<C>::T;
   // Layer blockIdx.y of a multi-layer append (0 for one layer).
@@ -111,7 +111,8 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
       const uint32_t u = i - r * a.upr.d;
       const uint32_t r2 = a.kvh.div(r);
       const uint32_t h = r - r2 * a.kvh.d;
-      const uint32_t kv = r2 & a.kv_shift, t = r2 >> a.kv_shift;
+      // kKV: K and V rows of a token interleave; else K only.
+      const uint32_t kv = kKV ? r2 & 1u : 0u, t = kKV ? r2 >> 1 : r2;
       // The source row and the slot are loaded together (the source address
       // does not depend on the slot), so one memory round trip precedes the
       // store.
@@ -141,11 +142,14 @@ template <int C>
 static void launch_append(const AppendArgs& a, uint32_t layers, hipStream_t s) {
   constexpr int ITEMS = 1;
   uint32_t grid = (a.total + 256 * ITEMS - 1) / (256 * ITEMS);
-  if (layers == 1)
-    hipLaunchKernelGGL((kv_append_kernel<C, ITEMS, true>), dim3(grid), dim3(256), 0, s, a);
+  if (!a.has_v)
+    hipLaunchKernelGGL((kv_append_kernel<C, ITEMS, false, false>), dim3(grid, layers), dim3(256),
+                       0, s, a);
+  else if (layers == 1)
+    hipLaunchKernelGGL((kv_append_kernel<C, ITEMS, true, true>), dim3(grid), dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((kv_append_kernel<C, ITEMS, false>), dim3(grid, layers), dim3(256), 0, s,
-                       a);
+    hipLaunchKernelGGL((kv_append_kernel<C, ITEMS, false, true>), dim3(grid, layers), dim3(256),
+                       0, s, a);
 }
 
 // ---- gather -----------------------------------------------------------------
@@ -380,7 +384,7 @@ static int append_impl(const char* who, const vapi_kv_pool* pool, uint32_t layer
   a.v_src = (const char*)(has_v ? v_src : k_src);
   a.k_dst = lp.k;
   a.v_dst = has_v ? lp.v : lp.k;
-  a.kv_shift = has_v ? 1u : 0u;
+  a.has_v = has_v ? 1u : 0u;
   a.slots = slot_mapping;
   a.total = (uint32_t)total;
   a.num_slots = g.num_blocks * g.block_size;
