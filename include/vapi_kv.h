@@ -143,7 +143,9 @@ int vapi_kv_append_layers(const vapi_kv_pool* pool, uint32_t layer0, uint32_t n_
 /*
  * Block-table gather into logical order. Replaces gather_kv (cache.rs:283-290).
  * block_table: device u32[n_table]; out: device [len_k, num_kv_heads,
- * head_dim] for K and for V (either may be NULL). len_k <= n_table*block_size.
+ * head_dim] for K and for V (either may be NULL; V must be NULL for a
+ * K-only pool). len_k <= n_table*block_size. Rows of a table entry past the
+ * pool are gathered as zeros.
  */
 int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
                    const uint32_t* block_table, uint32_t n_table,
@@ -236,7 +238,8 @@ int vapi_paged_attention_append(const vapi_kv_pool* pool, uint32_t layer,
  * Replaces CandleBackend::copy_blocks (backend.rs:781-797), which the
  * engine calls with Scheduler::fork's pairs (scheduler.rs:217-281).
  * pairs: device u32[n_pairs][2] = (src, dst). A dst must not also be a src
- * or another pair's dst in the same call.
+ * or another pair's dst in the same call. A pair naming a block past the
+ * pool is skipped (device ids are not checked on the host).
  */
 int vapi_kv_copy_blocks(const vapi_kv_pool* pool, const uint32_t* pairs,
                         uint32_t n_pairs, vapi_stream_t stream);
@@ -248,9 +251,10 @@ int vapi_kv_copy_blocks(const vapi_kv_pool* pool, const uint32_t* pairs,
  * in native little-endian element bytes, whatever the pool layout. Over a
  * pool chain the layers are those of every pool in order, and K-only
  * pools contribute no V segments (rank-1 V buffers are skipped there).
- * ids: device u32[n]. dst/src: n blobs back to back; device memory or
- * host-mapped pinned memory (hipHostMalloc), either is read/written directly
- * by the kernel.
+ * ids: device u32[n]; an id past the pool moves nothing (its blob is left
+ * as it was). dst/src: n blobs back to back; device memory or host-mapped
+ * pinned memory (hipHostMalloc), either is read/written directly by the
+ * kernel.
  */
 int vapi_kv_export_blocks(const vapi_kv_pool* pool, const uint32_t* ids,
                           uint32_t n, void* dst, vapi_stream_t stream);

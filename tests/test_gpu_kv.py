@@ -558,3 +558,43 @@ def test_a_mixed_cache_spills_and_promotes_bit_exact():
     assert promote(store, c, hs, list(range(20, 26)), pinned) == 6
     for i in range(6):
         assert be.export_block(20 + i) == be.export_block(i)
+
+
+@pytest.mark.gpu
+def test_block_ids_past_the_pool_move_nothing():
+    """Device-side ids the host never checked: an id past the pool is
+    skipped by copy and import, leaves its blob untouched on export, and a
+    table entry past the pool gathers zeros; host-side ids (the spill
+    calls) past the pool are errors."""
+    from vapi_amd._lib import VapiKvError, check, lib
+    from vapi_amd.backend import _dev_u32
+    from vapi_amd.spill import SpillStore, pinned_buffer, spill_evicted
+    c = PagedKvCache(2, 8, 16, 2, 64, torch.bfloat16, "HND")
+    workload.fill_normal(c._slab, 4)
+    be = KvBlockBackend(c)
+    bb = be.block_bytes()
+    before = c._slab.clone()
+    pairs = _dev_u32([1, 2, 100, 3, 4, 100], DEV)
+    check(lib().vapi_kv_copy_blocks(c.pool, pairs.data_ptr(), 3, None))
+    torch.cuda.synchronize()
+    assert torch.equal(c.k[0][2], before[0, 0].view(c.k[0].shape)[1])
+    assert torch.equal(c.k[0][3], before[0, 0].view(c.k[0].shape)[3])  # skipped pair
+    blob = torch.full((2 * bb,), 7, dtype=torch.uint8, device=DEV)
+    ids = _dev_u32([5, 1 << 20], DEV)
+    check(lib().vapi_kv_export_blocks(c.pool, ids.data_ptr(), 2, blob.data_ptr(), None))
+    torch.cuda.synchronize()
+    assert blob[:bb].cpu().numpy().tobytes() == be.export_block(5)
+    assert bool((blob[bb:] == 7).all())
+    snap = c._slab.clone()
+    check(lib().vapi_kv_import_blocks(c.pool, ids.data_ptr(), 2, blob.data_ptr(), None))
+    torch.cuda.synchronize()
+    assert torch.equal(c._slab, snap)
+    table = _dev_u32([0, 99], DEV)
+    out = torch.full((32, 2, 64), 3.0, dtype=torch.bfloat16, device=DEV)
+    check(lib().vapi_kv_gather(c.pool, 0, table.data_ptr(), 2, 32, out.data_ptr(), None, None))
+    torch.cuda.synchronize()
+    assert torch.equal(out[:16], ref_pool(c, 0, "k")[0].to(DEV))
+    assert bool((out[16:] == 0).all())
+    store = SpillStore(None, 1 << 30, 0)
+    with pytest.raises(VapiKvError, match="block 8 of 8"):
+        spill_evicted(store, c, [(bytes(32), 8)], pinned_buffer(c, 1))

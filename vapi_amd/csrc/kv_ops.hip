@@ -161,7 +161,7 @@ struct GatherArgs {
   char* v_out;
   const uint32_t* table;
   uint32_t total;  // 2 * len_k * kvh * upr
-  uint32_t len_k;
+  uint32_t len_k, num_blocks;
   FastDiv upr, kvh, bs, len;
   uint32_t row_bytes;
   uint64_t blk_b, head_b, tok_b;
@@ -195,7 +195,8 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(GatherArgs a) {
         const uint32_t blk = a.table[bi];
         const char* src = (kv ? a.v_src : a.k_src) + blk * a.blk_b +
                           h * a.head_b + off * a.tok_b + (uint64_t)u * C;
-        val[j] = *(const V*)src;
+        // A table entry past the pool reads nothing and gathers zeros.
+        val[j] = blk < a.num_blocks ? *(const V*)src : V{};
         dst[j] = out + ((uint64_t)t * a.kvh.d + h) * a.row_bytes +
                  (uint64_t)u * C;
       }
@@ -215,7 +216,7 @@ struct CopyArgs {
   uint64_t layer_b, blk_b;
   uint32_t total;  // n_pairs * L * 2 * upb
   FastDiv upb, two_l;
-  uint32_t num_layers;
+  uint32_t num_layers, num_blocks;
 };
 
 // Measured on config 4a (3.76 GB, 28 layers): 4.99 TB/s, about 88% of a
@@ -241,8 +242,10 @@ __global__ __launch_bounds__(256) void kv_copy_kernel(CopyArgs a) {
       const uint32_t src_blk = a.pairs[2 * p], dst_blk = a.pairs[2 * p + 1];
       char* buf = (kv ? a.v : a.k) + layer * a.layer_b;
       const uint64_t o = (uint64_t)u * C;
-      val[j] = *(const V*)(buf + src_blk * a.blk_b + o);
-      dst[j] = buf + dst_blk * a.blk_b + o;
+      if (src_blk < a.num_blocks && dst_blk < a.num_blocks) {  // else skipped
+        val[j] = *(const V*)(buf + src_blk * a.blk_b + o);
+        dst[j] = buf + dst_blk * a.blk_b + o;
+      }
     }
   }
 #pragma unroll
@@ -268,7 +271,7 @@ struct BlobArgs {
   uint64_t k_off, v_off; // this pool's first K and first V segment in a blob
   uint32_t total;
   FastDiv upr, kvh, bs, two_l;
-  uint32_t num_layers, row_bytes, seg_bytes;
+  uint32_t num_layers, row_bytes, seg_bytes, num_blocks;
 };
 
 template <int C, int ITEMS, bool EXPORT>
@@ -293,6 +296,7 @@ __global__ __launch_bounds__(256) void kv_blob_kernel(BlobArgs a) {
       const uint32_t kv = s >= a.num_layers;
       const uint32_t layer = kv ? s - a.num_layers : s;
       const uint32_t blk = a.ids[bi];
+      if (blk >= a.num_blocks) continue;  // an id past the pool moves nothing
       char* pool = (kv ? a.v : a.k) + layer * a.layer_b + blk * a.blk_b +
                    h * a.head_b + t * a.tok_b + (uint64_t)u * C;
       char* blob = a.blob + bi * a.block_bytes + (kv ? a.v_off : a.k_off) +
@@ -452,6 +456,7 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
   a.table = block_table;
   a.total = (uint32_t)total;
   a.len_k = len_k;
+  a.num_blocks = pool->num_blocks;
   a.upr = FastDiv(row_bytes / c);
   a.kvh = FastDiv(g.kvh);
   a.bs = FastDiv(g.block_size);
@@ -493,6 +498,7 @@ static int copy_pool(const vapi_kv_pool* pool, const uint32_t* pairs, uint32_t n
   a.upb = FastDiv((uint32_t)upb);
   a.two_l = FastDiv(nbuf * pool->num_layers);  // segment s >= num_layers is V
   a.num_layers = pool->num_layers;
+  a.num_blocks = pool->num_blocks;
   constexpr int ITEMS = 4;
   for (uint32_t p0 = 0; p0 < n_pairs; p0 += pairs_per_launch) {
     const uint32_t np = std::min(pairs_per_launch, n_pairs - p0);
@@ -550,6 +556,7 @@ static int blob_pool(const vapi_kv_pool* pool, const uint32_t* ids, uint32_t n, 
   a.num_layers = pool->num_layers;
   a.row_bytes = row_bytes;
   a.seg_bytes = (uint32_t)(g.blk * elt);
+  a.num_blocks = pool->num_blocks;
   constexpr int ITEMS = 4;
   for (uint32_t b0 = 0; b0 < n; b0 += blocks_per_launch) {
     const uint32_t nb = std::min(blocks_per_launch, n - b0);

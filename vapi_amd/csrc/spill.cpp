@@ -131,6 +131,15 @@ void parallel_for(uint32_t n, F f) {
 
 }  // namespace
 
+// Block ids from the host must name blocks of the pool (the kernels would
+// otherwise skip them silently).
+static int check_ids(const vapi_kv_pool* pool, const uint32_t* ids, uint32_t n, const char* who) {
+  for (uint32_t i = 0; i < n; ++i)
+    if (ids[i] >= pool->num_blocks)
+      VK_FAIL(VAPI_KV_EINVAL, "%s: block %u of %u", who, ids[i], pool->num_blocks);
+  return 0;
+}
+
 constexpr size_t kMaxInflight = 16;  // asynchronous exports in flight per store
 
 struct vapi_spill_store {
@@ -393,6 +402,7 @@ int64_t vapi_spill_evicted(vapi_spill_store* s, const vapi_kv_pool* pool, const 
   if (int rc = check_pool(pool, "vapi_spill_evicted")) return rc;
   if (!s || (n && (!ids || !hashes || !pinned)))
     VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_evicted: null argument");
+  if (int rc = check_ids(pool, ids, n, "vapi_spill_evicted")) return rc;
   if (int64_t rc = s->drain(true); rc < 0) return rc;
   const size_t bb = vapi_kv_block_bytes(pool);
   const size_t head = 4096;  // id staging, 1,024 ids per round at most
@@ -438,6 +448,7 @@ int64_t vapi_spill_evicted_async(vapi_spill_store* s, const vapi_kv_pool* pool,
   if (int rc = check_pool(pool, "vapi_spill_evicted_async")) return rc;
   if (!s || (n && (!ids || !hashes || !pinned || !staging)))
     VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_evicted_async: null argument");
+  if (int rc = check_ids(pool, ids, n, "vapi_spill_evicted_async")) return rc;
   const size_t bb = vapi_kv_block_bytes(pool);
   const size_t head = 4096;
   // Exports whose copies have completed enter the store now; the ones using
@@ -519,6 +530,7 @@ int64_t vapi_spill_promote(vapi_spill_store* s, const vapi_kv_pool* pool, const 
   if (int rc = check_pool(pool, "vapi_spill_promote")) return rc;
   if (!s || (n && (!ids || !hashes || !pinned)))
     VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_promote: null argument");
+  if (int rc = check_ids(pool, ids, n, "vapi_spill_promote")) return rc;
   if (int64_t rc = s->drain(true); rc < 0) return rc;
   const size_t bb = vapi_kv_block_bytes(pool);
   const size_t head = 4096;
