@@ -374,3 +374,25 @@ def test_one_very_long_context_matches_the_oracle(lens_q, lens_k):
     want = oracle_out(q, c, 0, batch, 128 ** -0.5)
     got = paged_attention(q, c, 0, batch, 128 ** -0.5)
     assert max_abs(got, want) <= 2e-2 * float(want.abs().max())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_table_entries_past_the_pool_read_the_last_block_instead_of_faulting(dtype):
+    """A block table is device data the call cannot check on the host:
+    entries past the pool are clamped to the last block (ForwardBatch::
+    validate, backend.rs:96-204, is where a bad table is refused), so the
+    result equals the same batch with those entries replaced by it. Decode
+    and prefill rows, MFMA (bf16) and VALU (f32) paths."""
+    c, q, batch = mixed(dtype)
+    nb = c.num_blocks
+    bad = ForwardBatch(cu_seqlens_q=batch.cu_seqlens_q, cu_seqlens_k=batch.cu_seqlens_k,
+                       block_tables=[[5, nb + 3, 6], [7, 1 << 30]],
+                       max_seqlen_q=batch.max_seqlen_q, max_seqlen_k=batch.max_seqlen_k)
+    clamped = ForwardBatch(cu_seqlens_q=batch.cu_seqlens_q, cu_seqlens_k=batch.cu_seqlens_k,
+                           block_tables=[[5, nb - 1, 6], [7, nb - 1]],
+                           max_seqlen_q=batch.max_seqlen_q, max_seqlen_k=batch.max_seqlen_k)
+    scale = HEAD_DIM ** -0.5
+    got = paged_attention(q, c, 0, bad, scale)
+    want = paged_attention(q, c, 0, clamped, scale)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)

@@ -122,6 +122,8 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   if (batch == 0 || max_seqlen_q == 0) return 0;
   if (!q || !out || !cu_seqlens_q || !cu_seqlens_k || !block_table)
     VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: null device pointer");
+  if (pool->num_blocks == 0 && max_seqlen_k > 0)
+    VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: keys to attend over in an empty pool");
   if (max_blocks == 0)
     VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: block table width 0");
   if (num_heads > 65535 || (batch > 65535 && !mfma_ok(pool, num_heads)))
@@ -153,6 +155,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   a.slots = fuse ? fuse->slots : nullptr;
   a.n_new = fuse ? fuse->n : 0;
   a.num_slots = g.num_blocks * g.block_size;
+  a.last_blk = g.num_blocks ? g.num_blocks - 1 : 0;
   a.blk_e = g.blk;
   a.head_e = g.head;
   a.tok_e = (uint32_t)g.tok;

@@ -56,6 +56,7 @@ struct AttnArgs {
   const char* v_new;
   const uint32_t* slots;
   uint32_t n_new, num_slots;
+  uint32_t last_blk;  // num_blocks - 1: table entries are clamped to it
   uint64_t blk_e, head_e;  // element strides in the pool
   uint32_t tok_e;
   uint32_t max_blocks, batch, num_heads, kvh, group, block_size, bs_shift;
@@ -205,7 +206,9 @@ __device__ __forceinline__ const char* tile_base(const uint32_t* __restrict__ ta
   // written by a kernel, and this keeps the load scalar wherever it is
   // inlined (a restrict qualifier does not survive every inlining).
   using ConstU32 = const __attribute__((address_space(4))) uint32_t;
-  const uint32_t blk = ((ConstU32*)tab)[(uint32_t)ts >> a.bs_shift];
+  // Clamped: a table entry past the pool reads the last block instead of
+  // faulting (ForwardBatch::validate is where bad tables are refused).
+  const uint32_t blk = min(((ConstU32*)tab)[(uint32_t)ts >> a.bs_shift], a.last_blk);
   const uint32_t off0 = (uint32_t)ts & (a.block_size - 1);
   return (const char*)(base + (uint64_t)blk * a.blk_e + (uint64_t)off0 * a.tok_e);
 }
