@@ -164,8 +164,9 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
  *   prefix and len_q <= len_k. Query j of a sequence sits at absolute
  *   position p = len_k - len_q + j (bottom-right aligned).
  * block_table: device u32[batch, max_blocks] (pack_block_tables layout,
- *   attention.rs:42-62). Entries past the pool are clamped to its last block
- *   (no fault); ForwardBatch::validate is where bad tables are refused.
+ *   attention.rs:42-62). Entries past the pool are clamped to its last block,
+ *   and keys past a row's max_blocks * block_size read the row's last entry
+ *   (no fault); ForwardBatch::validate is where bad batches are refused.
  * max_seqlen_q, max_seqlen_k: upper bounds of len_q and len_k.
  * window_left: keys k < p - window_left are hidden; -1 = unlimited. A sliding
  *   window of w (HF q - k < w) is window_left = w - 1 (attention.rs:179-194).

@@ -396,3 +396,23 @@ def test_table_entries_past_the_pool_read_the_last_block_instead_of_faulting(dty
     want = paged_attention(q, c, 0, clamped, scale)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_keys_past_the_table_row_read_its_last_entry_instead_of_faulting(dtype):
+    """cu_seqlens_k is device data too: a sequence longer than its table row
+    (len_k > max_blocks * block_size) reads the row's last entry for the keys
+    past it rather than another row or memory past the table. The call must
+    finish; the rows within the table are unaffected."""
+    c, q, batch = mixed(dtype)
+    # B's table has 2 blocks (64 keys) in a [2, 3] table; claim 100 keys.
+    over = ForwardBatch(cu_seqlens_q=batch.cu_seqlens_q, cu_seqlens_k=[0, 90, 190],
+                        block_tables=batch.block_tables, max_seqlen_q=batch.max_seqlen_q,
+                        max_seqlen_k=100)
+    prep = PreparedAttention.from_batch(over, DEV)  # no host check of table coverage
+    scale = HEAD_DIM ** -0.5
+    got = paged_attention_prepared(q, c, 0, prep, scale)
+    want = paged_attention(q, c, 0, batch, scale)
+    torch.cuda.synchronize()
+    assert torch.equal(got[:20], want[:20])
+    assert bool(torch.isfinite(got.float()).all())

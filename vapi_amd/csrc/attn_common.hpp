@@ -206,9 +206,12 @@ __device__ __forceinline__ const char* tile_base(const uint32_t* __restrict__ ta
   // written by a kernel, and this keeps the load scalar wherever it is
   // inlined (a restrict qualifier does not survive every inlining).
   using ConstU32 = const __attribute__((address_space(4))) uint32_t;
-  // Clamped: a table entry past the pool reads the last block instead of
-  // faulting (ForwardBatch::validate is where bad tables are refused).
-  const uint32_t blk = min(((ConstU32*)tab)[(uint32_t)ts >> a.bs_shift], a.last_blk);
+  // Clamped: a table entry past the pool reads the last block, and keys
+  // past the table's row (len_k beyond max_blocks * block_size) its last
+  // entry, instead of faulting (ForwardBatch::validate is where bad tables
+  // are refused).
+  const uint32_t col = min((uint32_t)ts >> a.bs_shift, a.max_blocks - 1);
+  const uint32_t blk = min(((ConstU32*)tab)[col], a.last_blk);
   const uint32_t off0 = (uint32_t)ts & (a.block_size - 1);
   return (const char*)(base + (uint64_t)blk * a.blk_e + (uint64_t)off0 * a.tok_e);
 }

@@ -42,7 +42,7 @@ __global__ __launch_bounds__(64) void paged_attn_generic(AttnArgs a,
     const int32_t key = c0 + (int32_t)lane;
     float s = -INFINITY;
     if (key <= hi) {
-      const uint32_t blk = min(table[key / a.block_size], a.last_blk);
+      const uint32_t blk = min(table[min((uint32_t)key / a.block_size, a.max_blocks - 1)], a.last_blk);
       const uint32_t off = key % a.block_size;
       const T* krow = kb + blk * a.blk_e + off * a.tok_e;
       float dot = 0.f;
@@ -67,7 +67,7 @@ __global__ __launch_bounds__(64) void paged_attn_generic(AttnArgs a,
     const int32_t nk = min(64, hi - c0 + 1);
     for (int32_t kk = 0; kk < nk; ++kk) {
       const int32_t key2 = c0 + kk;
-      const uint32_t blk = min(table[key2 / a.block_size], a.last_blk);
+      const uint32_t blk = min(table[min((uint32_t)key2 / a.block_size, a.max_blocks - 1)], a.last_blk);
       const uint32_t off = key2 % a.block_size;
       const T* vrow = vb + blk * a.blk_e + off * a.tok_e;
       const float pk = ps[kk];

@@ -84,8 +84,10 @@ __device__ __forceinline__ void pf_load(PfStage<D>& st, const uint32_t* __restri
   // by a kernel).
   using ConstU32 = const __attribute__((address_space(4))) uint32_t;
   const int32_t ts0 = min(s0, last & ~15), ts1 = min(s0 + 16, last & ~15);
-  const uint32_t blk0 = min(((ConstU32*)tab)[(uint32_t)ts0 >> a.bs_shift], a.last_blk);
-  const uint32_t blk1 = min(((ConstU32*)tab)[(uint32_t)ts1 >> a.bs_shift], a.last_blk);
+  const uint32_t c0 = min((uint32_t)ts0 >> a.bs_shift, a.max_blocks - 1);
+  const uint32_t c1 = min((uint32_t)ts1 >> a.bs_shift, a.max_blocks - 1);
+  const uint32_t blk0 = min(((ConstU32*)tab)[c0], a.last_blk);
+  const uint32_t blk1 = min(((ConstU32*)tab)[c1], a.last_blk);
   const uint64_t off0 = (uint64_t)blk0 * a.blk_e + (uint64_t)((uint32_t)ts0 & (a.block_size - 1)) * a.tok_e;
   const uint64_t off1 = (uint64_t)blk1 * a.blk_e + (uint64_t)((uint32_t)ts1 & (a.block_size - 1)) * a.tok_e;
 #pragma unroll
