@@ -360,6 +360,21 @@ def bench_blocks(steps, warmup, decode):
         f"({spill['export_gbs']:.1f} GB/s), back {spill['import_us_per_block']:.0f} us/block "
         f"({spill['import_gbs']:.1f} GB/s)")
     store.close()
+    # A full store (host memory for 128 blocks, no disk): every put evicts,
+    # and the evicted buffers take the next blobs, as in a long-running
+    # server whose spill tier has filled.
+    store = SpillStore(None, 128 * bb, 0)
+    spill_evicted(store, cache, zip(hs[:128], w.swap_ids[:128].tolist()), pin)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    spill_evicted(store, cache, zip(hs[128:ns], w.swap_ids[128:ns].tolist()), pin)
+    t1 = time.perf_counter()
+    spill.update(full_store_export_us_per_block=(t1 - t0) * 1e6 / (ns - 128),
+                 full_store_export_gbs=(ns - 128) * bb / (t1 - t0) / 1e9)
+    log(f"spill tier, full store: {ns - 128} blocks out "
+        f"{spill['full_store_export_us_per_block']:.0f} us/block "
+        f"({spill['full_store_export_gbs']:.1f} GB/s)")
+    store.close()
     # The same spill overlapped with the forward: the pack into device
     # staging is all the model's stream waits for; the copy to host runs on
     # a side stream and the drain puts the blobs into the store. The event

@@ -185,6 +185,33 @@ struct vapi_spill_store {
     }
   }
 
+  // Buffers of entries that left host memory, kept for the next copies in
+  // (a fresh buffer costs a page fault per 4 KiB on first touch; a full
+  // store recycles its evictions instead). Bounded by kSpareMax bytes and
+  // by the host-memory cap.
+  static constexpr uint64_t kSpareMax = 256ull << 20;
+  std::vector<std::vector<uint8_t>> spare;
+  uint64_t spare_bytes = 0;
+
+  void recycle(std::vector<uint8_t>&& b) {
+    if (spare_bytes + b.capacity() > std::min(kSpareMax, ram_max)) return;
+    spare_bytes += b.capacity();
+    spare.push_back(std::move(b));
+  }
+
+  // `n` buffers of `len` bytes (contents undefined): recycled ones first.
+  std::vector<std::vector<uint8_t>> buffers(uint32_t n, size_t len) {
+    std::vector<std::vector<uint8_t>> out(n);
+    for (uint32_t j = 0; j < n && !spare.empty(); ++j) {
+      if (spare.back().capacity() < len) break;
+      spare_bytes -= spare.back().capacity();
+      out[j] = std::move(spare.back());
+      spare.pop_back();
+      out[j].resize(len);
+    }
+    return out;
+  }
+
   // Push host-memory entries out to disk until the cap is met.
   void evict_ram() {
     Hash h;
@@ -193,6 +220,7 @@ struct vapi_spill_store {
       ram_bytes -= bytes.size();
       if (!has_dir || bytes.size() > disk_max) {
         ++st.drops;
+        recycle(std::move(bytes));
         continue;
       }
       std::ofstream f(path(h), std::ios::binary | std::ios::trunc);
@@ -205,6 +233,7 @@ struct vapi_spill_store {
       disk_bytes += bytes.size();
       disk.push(h, bytes.size());
       evict_disk();
+      recycle(std::move(bytes));
     }
   }
 
@@ -273,9 +302,10 @@ struct vapi_spill_store {
       }
       if (force) --force;
       const uint32_t m = (uint32_t)e.hashes.size();
-      std::vector<std::vector<uint8_t>> copies(m);
+      std::vector<std::vector<uint8_t>> copies = buffers(m, e.bb);
       parallel_for(m, [&](uint32_t j) {
-        copies[j].assign(e.blobs + (size_t)j * e.bb, e.blobs + (size_t)(j + 1) * e.bb);
+        if (copies[j].size() == e.bb) std::memcpy(copies[j].data(), e.blobs + (size_t)j * e.bb, e.bb);
+        else copies[j].assign(e.blobs + (size_t)j * e.bb, e.blobs + (size_t)(j + 1) * e.bb);
       });
       for (uint32_t j = 0; j < m; ++j) {
         put(e.hashes[j], std::move(copies[j]));
@@ -393,8 +423,10 @@ void vapi_spill_get_stats(const vapi_spill_store* s, vapi_spill_stats* out) {
 // the store does not hold yet are exported with vapi_kv_export_blocks into
 // `pinned` (hipHostMalloc memory the kernel writes directly; the block ids
 // are staged at its start) in as many rounds as it needs, and each blob is
-// put into the store. Returns the number exported; the blocks may be
-// overwritten once it returns.
+// put into the store; with room for two blocks the buffer is used in two
+// halves, so one round's export overlaps the previous round's copies.
+// Returns the number exported; the blocks may be overwritten once it
+// returns.
 int64_t vapi_spill_evicted(vapi_spill_store* s, const vapi_kv_pool* pool, const uint32_t* ids,
                            const uint8_t* hashes, uint32_t n, void* pinned, size_t pinned_bytes,
                            vapi_stream_t stream) {
@@ -409,25 +441,81 @@ int64_t vapi_spill_evicted(vapi_spill_store* s, const vapi_kv_pool* pool, const 
   if (pinned_bytes < head + bb)
     VK_FAIL(VAPI_KV_ESPACE, "vapi_spill_evicted: %zu pinned bytes < %zu (one block)",
             pinned_bytes, head + bb);
-  const uint32_t per = (uint32_t)std::min<size_t>((pinned_bytes - head) / bb, head / 4);
-  uint32_t* id_stage = (uint32_t*)pinned;
-  uint8_t* blobs = (uint8_t*)pinned + head;
   std::vector<uint32_t> todo;
   for (uint32_t i = 0; i < n; ++i)
     if (!vapi_spill_contains(s, hashes + 32ull * i)) todo.push_back(i);
+  if (todo.empty()) return 0;
+  // Two halves of the pinned buffer when it holds two blocks: the export
+  // of round r + 1 runs on the GPU while round r is copied into the store.
+  const size_t room = (pinned_bytes - head) / bb;
+  const uint32_t halves = room >= 2 ? 2 : 1;
+  const uint32_t per = (uint32_t)std::min<size_t>(room / halves, head / 4 / halves);
   const hipStream_t st = hs(stream);
-  for (size_t at = 0; at < todo.size(); at += per) {
+  hipEvent_t ev[2] = {s->event(), halves == 2 ? s->event() : nullptr};
+  auto give_back = [&] {
+    for (hipEvent_t e : ev)
+      if (e) s->spare_events.push_back(e);
+  };
+  if (!ev[0] || (halves == 2 && !ev[1])) {
+    give_back();
+    VK_FAIL(VAPI_KV_EHIP, "vapi_spill_evicted: hipEventCreate failed");
+  }
+  auto stage_ids = [&](uint32_t half) { return (uint32_t*)pinned + half * (head / 4 / halves); };
+  auto stage_blobs = [&](uint32_t half) {
+    return (uint8_t*)pinned + head + (size_t)half * per * bb;
+  };
+  const size_t rounds = (todo.size() + per - 1) / per;
+  auto issue = [&](size_t r) -> int {
+    const uint32_t half = (uint32_t)(r % halves);
+    const size_t at = r * per;
     const uint32_t m = (uint32_t)std::min<size_t>(per, todo.size() - at);
+    uint32_t* id_stage = stage_ids(half);
     for (uint32_t j = 0; j < m; ++j) id_stage[j] = ids[todo[at + j]];
-    if (int rc = vapi_kv_export_blocks(pool, id_stage, m, blobs, stream)) return rc;
-    VK_HIP(hipStreamSynchronize(st));
-    std::vector<std::vector<uint8_t>> copies(m);
+    if (int rc = vapi_kv_export_blocks(pool, id_stage, m, stage_blobs(half), stream)) return rc;
+    const hipError_t e = hipEventRecord(ev[half], st);
+    if (e != hipSuccess) {
+      set_error("vapi_spill_evicted: %s", hipGetErrorString(e));
+      return VAPI_KV_EHIP;
+    }
+    return 0;
+  };
+  if (int rc = issue(0)) {
+    give_back();
+    return rc;
+  }
+  for (size_t r = 0; r < rounds; ++r) {
+    const uint32_t half = (uint32_t)(r % halves);
+    // Round r + 1 goes to the other half, whose previous round was copied
+    // out before this iteration began.
+    if (halves == 2 && r + 1 < rounds)
+      if (int rc = issue(r + 1)) {
+        (void)hipStreamSynchronize(st);
+        give_back();
+        return rc;
+      }
+    const hipError_t e = hipEventSynchronize(ev[half]);
+    if (e != hipSuccess) {
+      (void)hipStreamSynchronize(st);
+      give_back();
+      VK_FAIL(VAPI_KV_EHIP, "vapi_spill_evicted: %s", hipGetErrorString(e));
+    }
+    const size_t at = r * per;
+    const uint32_t m = (uint32_t)std::min<size_t>(per, todo.size() - at);
+    const uint8_t* blobs = stage_blobs(half);
+    std::vector<std::vector<uint8_t>> copies = s->buffers(m, bb);
     parallel_for(m, [&](uint32_t j) {
-      copies[j].assign(blobs + (size_t)j * bb, blobs + (size_t)(j + 1) * bb);
+      if (copies[j].size() == bb) std::memcpy(copies[j].data(), blobs + (size_t)j * bb, bb);
+      else copies[j].assign(blobs + (size_t)j * bb, blobs + (size_t)(j + 1) * bb);
     });
     for (uint32_t j = 0; j < m; ++j)
       s->put(to_hash(hashes + 32ull * todo[at + j]), std::move(copies[j]));
+    if (halves == 1 && r + 1 < rounds)
+      if (int rc = issue(r + 1)) {
+        give_back();
+        return rc;
+      }
   }
+  give_back();
   return (int64_t)todo.size();
 }
 
@@ -520,7 +608,8 @@ int64_t vapi_spill_drain(vapi_spill_store* s, int wait) {
 // are a prompt's block chain and ids[0..n) the blocks allocated for them.
 // Blobs are taken from the store in order up to the first it does not hold
 // (only a contiguous prefix is worth restoring) and imported with
-// vapi_kv_import_blocks through `pinned`. A blob whose length is not
+// vapi_kv_import_blocks through `pinned` (in two halves when it holds two
+// blocks, so one round's copies overlap the previous round's import). A blob whose length is not
 // vapi_kv_block_bytes is an error (backend.rs:739-745). Returns the number
 // restored.
 int64_t vapi_spill_promote(vapi_spill_store* s, const vapi_kv_pool* pool, const uint8_t* hashes,
@@ -537,13 +626,35 @@ int64_t vapi_spill_promote(vapi_spill_store* s, const vapi_kv_pool* pool, const 
   if (pinned_bytes < head + bb)
     VK_FAIL(VAPI_KV_ESPACE, "vapi_spill_promote: %zu pinned bytes < %zu (one block)",
             pinned_bytes, head + bb);
-  const uint32_t per = (uint32_t)std::min<size_t>((pinned_bytes - head) / bb, head / 4);
-  uint32_t* id_stage = (uint32_t*)pinned;
-  uint8_t* blobs = (uint8_t*)pinned + head;
+  // Two halves of the pinned buffer when it holds two blocks: round r is
+  // copied into one half while the GPU imports round r - 1 from the other.
+  const size_t room = (pinned_bytes - head) / bb;
+  const uint32_t halves = room >= 2 ? 2 : 1;
+  const uint32_t per = (uint32_t)std::min<size_t>(room / halves, head / 4 / halves);
   const hipStream_t st = hs(stream);
-  uint32_t done = 0;
+  hipEvent_t ev[2] = {s->event(), halves == 2 ? s->event() : nullptr};
+  struct Events {  // handed back to the store on every return
+    vapi_spill_store* s;
+    hipEvent_t* ev;
+    ~Events() {
+      for (int i = 0; i < 2; ++i)
+        if (ev[i]) s->spare_events.push_back(ev[i]);
+    }
+  } events_guard{s, ev};
+  if (!ev[0] || (halves == 2 && !ev[1]))
+    VK_FAIL(VAPI_KV_EHIP, "vapi_spill_promote: hipEventCreate failed");
+  uint32_t done = 0, round = 0;
   bool more = true;
   while (more && done < n) {
+    const uint32_t half = round % halves;
+    uint32_t* id_stage = (uint32_t*)pinned + half * (head / 4 / halves);
+    uint8_t* blobs = (uint8_t*)pinned + head + (size_t)half * per * bb;
+    // This half's previous import must have read its blobs.
+    if (round >= halves) {
+      const hipError_t e = hipEventSynchronize(ev[half]);
+      if (e != hipSuccess)
+        VK_FAIL(VAPI_KV_EHIP, "vapi_spill_promote: %s", hipGetErrorString(e));
+    }
     // Resolve this round's chain entries in order, copy (or read from disk)
     // their blobs into the pinned slots on several threads, then account
     // in order as a get() per entry would: LRU touch and hit, or for an
@@ -565,9 +676,11 @@ int64_t vapi_spill_promote(vapi_spill_store* s, const vapi_kv_pool* pool, const 
         break;
       }
       const uint64_t len = r ? r->size() : *d;
-      if (len != bb)
+      if (len != bb) {
+        (void)hipStreamSynchronize(st);  // earlier rounds' imports finish first
         VK_FAIL(VAPI_KV_EINVAL, "vapi_spill_promote: blob of %llu bytes, blocks are %zu",
                 (unsigned long long)len, bb);
+      }
       src.push_back(Src{h, r, false});
     }
     parallel_for((uint32_t)src.size(), [&](uint32_t k) {
@@ -603,10 +716,15 @@ int64_t vapi_spill_promote(vapi_spill_store* s, const vapi_kv_pool* pool, const 
       more = false;
     }
     if (!m) break;
-    if (int rc = vapi_kv_import_blocks(pool, id_stage, m, blobs, stream)) return rc;
-    VK_HIP(hipStreamSynchronize(st));
+    if (int rc = vapi_kv_import_blocks(pool, id_stage, m, blobs, stream)) {
+      (void)hipStreamSynchronize(st);
+      return rc;
+    }
+    VK_HIP(hipEventRecord(ev[half], st));
     done += m;
+    ++round;
   }
+  VK_HIP(hipStreamSynchronize(st));
   return done;
 }
 
