@@ -198,3 +198,23 @@ def test_a_chain_of_pools_on_different_blocks_is_an_error():
     k.v = None
     assert L.vapi_kv_append(ctypes.byref(k), 0, 1, 1, 1, 1, None) == _lib.EINVAL
     assert b"K-only" in L.vapi_kv_last_error()
+
+
+def test_a_c_program_uses_the_library_through_the_header(tmp_path):
+    """tests/c_consumer.c: the header compiles as C11 (-Wall -Werror) and a
+    C program links libvapi_kv.so and runs the host-side calls, as a Rust
+    -sys crate or any other FFI would bind them."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no gcc")
+    root = Path(__file__).resolve().parents[1]
+    lib_dir = _lib.LIB_PATH.parent
+    exe = tmp_path / "c_consumer"
+    subprocess.run([gcc, "-std=c11", "-Wall", "-Wextra", "-Werror", "-I", str(root / "include"),
+                    str(root / "tests" / "c_consumer.c"), "-o", str(exe), f"-L{lib_dir}",
+                    "-lvapi_kv", f"-Wl,-rpath,{lib_dir}"], check=True)
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert res.returncode == 0, res.stdout + res.stderr
+    assert "all checks passed" in res.stdout
