@@ -124,7 +124,22 @@ def bench_decode(steps, warmup):
     gms = timed_graph(d["step"], steps, warmup)
     log(f"decode cfg2 in a graph: {gms * 1e3:.1f} us/step, "
         f"{d['alg_bytes'] / (gms * 1e-3) / 1e9:.0f} GB/s")
-    d.update(ms=ms, wall=wall, gbs=gbs, graph_ms=gms)
+    # Per-call spread: each of `steps` calls between its own pair of events
+    # on the stream the kernels run on (median, 10th and 90th percentile).
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    for a, b in evs:
+        a.record()
+        d["step"]()
+        b.record()
+    torch.cuda.synchronize()
+    per = np.array([a.elapsed_time(b) * 1e3 for a, b in evs])
+    spread = dict(median_us=float(np.median(per)), p10_us=float(np.percentile(per, 10)),
+                  p90_us=float(np.percentile(per, 90)), calls=int(steps),
+                  graph_us=gms * 1e3)
+    log(f"decode cfg2 per call: median {spread['median_us']:.1f} us "
+        f"(p10 {spread['p10_us']:.1f}, p90 {spread['p90_us']:.1f})")
+    d.update(ms=ms, wall=wall, gbs=gbs, graph_ms=gms, spread=spread)
     return d
 
 
@@ -589,7 +604,7 @@ def main():
     dec = bench_decode(args.steps, args.warmup)
     if args.only == "decode":
         return
-    extras = {}
+    extras = {"decode_cfg2_calls": dec["spread"]}
     extras["gather_cfg2"] = bench_gather(dec, args.steps, args.warmup)
     extras["fused_step_cfg2"] = bench_fused_step(dec, args.steps, args.warmup)
     if args.only in (None,):
