@@ -2,19 +2,15 @@
 //
 // Rows are the (query token, head) pairs of one kv head, r = j*G + h_local,
 // so the G query heads of a group share every K/V byte. A workgroup owns 256
-// rows (8 waves x 2 tiles of 16; one workgroup per CU, two waves per SIMD,
-// measured 5% faster than two workgroups of 4 waves) and walks the keys they
-// can see in 32-key steps. Each step's K and V are loaded once per workgroup into LDS (double
-// buffered in LDS, with the global loads issued two steps ahead into
-// registers) and every K/V fragment read from LDS feeds both row tiles of a
-// wave. V is written to LDS transposed, with the keys of a step permuted so
-// that the 8 keys one lane group feeds to an MFMA are contiguous (each V^T
-// fragment is a single ds_read_b128), and with its rows and the staging
-// threads arranged so that neither the writes nor the reads collide on LDS
-// banks (measured with SQ_LDS_BANK_CONFLICT: 20% -> 28% MFMA utilisation). The math per row
-// tile is attend_qk / attend_pv (S^T = K Q^T, online softmax, O^T += V^T P^T)
-// with the bottom-right causal mask and left window per row; row tiles
-// whose rows cannot see any key of a step skip it. Rows with len_q < 2 are
+// rows (8 waves x 2 tiles of 16; one workgroup per CU, two waves per SIMD)
+// and walks the keys they can see in 32-key steps. Each step's K and V rows
+// are copied from HBM straight into LDS by direct loads (global_load_lds:
+// no staging registers, no LDS store instructions) into a ring of three
+// step buffers, issued two steps ahead, and every fragment read from LDS
+// feeds both row tiles of a wave. The math per row tile is the decode's
+// operand scheme (S^T = K Q^T, online softmax, O^T += V^T P^T) with the
+// bottom-right causal mask and left window per row, applied only on steps
+// that some row of the workgroup cannot fully see. Rows with len_q < 2 are
 // left to the decode kernel.
 #include <type_traits>
 
@@ -27,118 +23,6 @@ namespace vk {
 #endif
 constexpr int kPfWaves = VK_PF_WAVES;
 constexpr int kPfThreads = 64 * kPfWaves;
-// 16-byte K chunks of one 32-key step per thread.
-template <int D>
-constexpr int kKIter = (32 * D / 8 + kPfThreads - 1) / kPfThreads;
-constexpr int kKPad = 8;  // elements of padding per K row in LDS
-constexpr int kVPad = 8;  // elements of padding per V^T row in LDS
-
-// Column of key k (0..31 within a step) in a V^T row: keys 4g..4g+3 of both
-// 16-key tiles (one lane group's MFMA k-slots) land in 8 contiguous columns.
-__device__ __forceinline__ uint32_t vt_col(uint32_t k) {
-  const uint32_t tt = k >> 4, r = k & 15;
-  return 8 * (r >> 2) + 4 * tt + (r & 3);
-}
-
-// V staging: thread -> (key pair kp, 16-byte d chunk c). Key pairs run
-// fastest across the lanes, so the 16 lanes of a group write 16 different
-// columns of one V^T row (d chunks fastest put them on rows 8 apart, which
-// share LDS banks).
-__device__ __forceinline__ uint32_t vkp(uint32_t tid, uint32_t cpk) {
-  return (tid % 16) + 16 * (tid / (16 * cpk));
-}
-__device__ __forceinline__ uint32_t vchunk(uint32_t tid, uint32_t cpk) { return (tid / 16) % cpk; }
-
-// LDS row of V^T row d: the rows the 16 lanes of a lane group read together
-// (d = DPL*col + k, col = 0..15) are stored consecutively, which the 80-byte
-// row pitch spreads over the banks (rows DPL apart would share two).
-template <int D>
-__device__ __forceinline__ uint32_t vrow(uint32_t d) {
-  constexpr uint32_t DPL = D / 16;
-  return (d % DPL) * 16 + d / DPL;
-}
-
-template <int D>
-struct alignas(16) PfSmem {
-  uint16_t k[2][32][D + kKPad];
-  uint16_t vt[2][D][32 + kVPad];
-};
-
-// One step's global loads, held in registers between issue and LDS store.
-// Plain members rather than arrays: a register copy between stages must not
-// turn the stage into a stack object.
-template <int D>
-struct PfStage {
-  uint4 k0, k1;  // K chunks (16 B) tid and tid + 256 of the step's 32 x D tile (k1: D = 128)
-  uint4 v0, v1;  // V of keys 2kp and 2kp+1 at d = 8c .. 8c+7 (tid < 2*D)
-};
-
-template <typename T, int D>
-__device__ __forceinline__ void pf_load(PfStage<D>& st, const uint32_t* __restrict__ tab,
-                                        const T* kb, const T* vb, const AttnArgs& a, int32_t s0,
-                                        int32_t last, uint32_t tid) {
-  constexpr uint32_t CPK = D / 8;  // 16-byte chunks per key row
-  // The step's two 16-key tiles (a tile past the last key re-reads the
-  // tile holding it): both block-table entries are read once, back to back,
-  // for K and V alike, through the scalar cache (the table is never written
-  // by a kernel).
-  using ConstU32 = const __attribute__((address_space(4))) uint32_t;
-  const int32_t ts0 = min(s0, last & ~15), ts1 = min(s0 + 16, last & ~15);
-  const uint32_t c0 = min((uint32_t)ts0 >> a.bs_shift, a.max_blocks - 1);
-  const uint32_t c1 = min((uint32_t)ts1 >> a.bs_shift, a.max_blocks - 1);
-  const uint32_t blk0 = min(((ConstU32*)tab)[c0], a.last_blk);
-  const uint32_t blk1 = min(((ConstU32*)tab)[c1], a.last_blk);
-  const uint64_t off0 = (uint64_t)blk0 * a.blk_e + (uint64_t)((uint32_t)ts0 & (a.block_size - 1)) * a.tok_e;
-  const uint64_t off1 = (uint64_t)blk1 * a.blk_e + (uint64_t)((uint32_t)ts1 & (a.block_size - 1)) * a.tok_e;
-#pragma unroll
-  for (int j = 0; j < kKIter<D>; ++j) {
-    const uint32_t ci = min(tid + kPfThreads * j, 32 * CPK - 1);
-    const uint32_t key = ci / CPK, part = ci % CPK;
-    // Uniform per wave: the 64 lanes cover 64 / CPK keys of one tile.
-    const bool second = __builtin_amdgcn_readfirstlane(key >> 4) != 0;
-    const T* base = kb + (second ? off1 : off0);
-    const int32_t lim = last - (second ? ts1 : ts0);
-    const uint32_t kk = (uint32_t)min((int32_t)(key & 15), lim);
-    const uint4 x = *(const uint4*)(base + kk * a.tok_e + 8 * part);
-    if (j == 0) st.k0 = x; else st.k1 = x;
-  }
-  if (tid < 2 * D) {
-    const uint32_t kp = vkp(tid, CPK), c = vchunk(tid, CPK);
-    // Key pairs 0..7 sit in the first tile, 8..15 in the second: selected
-    // per lane.
-    const bool second = kp >= 8;
-    const T* base = vb + (second ? off1 : off0);
-    const int32_t lim = last - (second ? ts1 : ts0);
-    const uint32_t k0 = (uint32_t)min((int32_t)((2 * kp) & 15), lim);
-    const uint32_t k1 = (uint32_t)min((int32_t)((2 * kp + 1) & 15), lim);
-    st.v0 = *(const uint4*)(base + k0 * a.tok_e + 8 * c);
-    st.v1 = *(const uint4*)(base + k1 * a.tok_e + 8 * c);
-  }
-}
-
-template <int D>
-__device__ __forceinline__ void pf_store(PfSmem<D>& sm, int buf, const PfStage<D>& st,
-                                         uint32_t tid) {
-  constexpr uint32_t CPK = D / 8;
-#pragma unroll
-  for (int j = 0; j < kKIter<D>; ++j) {
-    const uint32_t ci = tid + kPfThreads * j;
-    if (ci < 32 * CPK) *(uint4*)&sm.k[buf][ci / CPK][8 * (ci % CPK)] = j == 0 ? st.k0 : st.k1;
-  }
-  if (tid < 2 * D) {
-    const uint32_t kp = vkp(tid, CPK), c = vchunk(tid, CPK);
-    const uint32_t col = vt_col(2 * kp);  // even; key 2kp+1 sits next to it
-    const uint32_t x[4] = {st.v0.x, st.v0.y, st.v0.z, st.v0.w};
-    const uint32_t y[4] = {st.v1.x, st.v1.y, st.v1.z, st.v1.w};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t w =
-          __builtin_amdgcn_perm(y[e >> 1], x[e >> 1], (e & 1) ? 0x07060302u : 0x05040100u);
-      *(uint32_t*)&sm.vt[buf][vrow<D>(8 * c + e)][col] = w;
-    }
-  }
-}
-
 // Workgroup -> work item. The hardware deals workgroups round-robin to the
 // 8 XCDs (linear id % 8); each XCD here gets a contiguous range of work
 // items, so the q-tiles of one (sequence, kv head), which read the same K/V,
@@ -150,15 +34,127 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t lin, uint32_t n) {
   return x * per + min(x, extra) + i;
 }
 
+// ---- K and V staged by direct global-to-LDS loads --------------------------
+//
+// Rows keep the pool's order (key rows of D elements); each row's 16-byte
+// chunks are XOR-swizzled by the row index so that the fragment reads below
+// spread over the LDS banks. V^T fragments for O^T = V^T P^T are read
+// transposed from the V rows with ds_read_b64_tr_b16: for a 16-lane group,
+// lane i receives element i % 4 of the 64-bit chunk addressed by lane
+// 4 j + i / 4, for j = 0..3 (measured on gfx950), so lane 4 j + q pointing
+// at key row k0 + j, columns 4 q .. 4 q + 3 hands lane i the column of d
+// (i) over keys k0 .. k0 + 3. A d tile of 16 columns then lands in the
+// MFMA's A rows in order (d = 16 t + m), and the output O^T holds row col
+// at d = 16 t + 4 g + i.
+using LdsVoid = __attribute__((address_space(3))) void;
+
+
+// Element offset of 16-byte chunk p of key row r (0..31) in a step buffer.
+template <int D>
+__device__ __forceinline__ uint32_t pf_chunk(uint32_t r, uint32_t p) {
+  constexpr uint32_t CPR = D / 8;  // chunks per row
+  return (r * CPR + (p ^ (r & (CPR - 1)))) * 8;
+}
+
+// Issues the step at s0 into buffer b: each thread moves one 16-byte chunk
+// of K and one of V (D = 128), or one of K or V (D = 64: waves 0-3 K,
+// waves 4-7 V). LDS slot t of a tensor holds the chunk its swizzled
+// position names; a wave's 64 slots are contiguous, as the load writes them.
+template <typename T, int D>
+__device__ __forceinline__ void pf_dma(uint16_t* kdst, uint16_t* vdst, const uint32_t* __restrict__ tab,
+                                       const T* kb, const T* vb, const AttnArgs& a, int32_t s0,
+                                       int32_t last, uint32_t tid, uint32_t wave) {
+  constexpr uint32_t CPR = D / 8;
+  using ConstU32 = const __attribute__((address_space(4))) uint32_t;
+  const int32_t ts0 = min(s0, last & ~15), ts1 = min(s0 + 16, last & ~15);
+  const uint32_t c0 = min((uint32_t)ts0 >> a.bs_shift, a.max_blocks - 1);
+  const uint32_t c1 = min((uint32_t)ts1 >> a.bs_shift, a.max_blocks - 1);
+  const uint32_t blk0 = min(((ConstU32*)tab)[c0], a.last_blk);
+  const uint32_t blk1 = min(((ConstU32*)tab)[c1], a.last_blk);
+  const uint64_t off0 = (uint64_t)blk0 * a.blk_e + (uint64_t)((uint32_t)ts0 & (a.block_size - 1)) * a.tok_e;
+  const uint64_t off1 = (uint64_t)blk1 * a.blk_e + (uint64_t)((uint32_t)ts1 & (a.block_size - 1)) * a.tok_e;
+  auto one = [&](const T* base_t, uint16_t* buf, uint32_t slot, uint32_t wslot0)
+                 __attribute__((always_inline)) {
+    const uint32_t r = slot / CPR, pos = slot % CPR;
+    const uint32_t p = pos ^ (r & (CPR - 1));
+    // A wave's slots cover 64 / CPR whole rows of one 16-key tile.
+    const bool second = __builtin_amdgcn_readfirstlane(r) >= 16;
+    const T* base = base_t + (second ? off1 : off0);
+    const int32_t lim = last - (second ? ts1 : ts0);
+    const uint32_t kk = (uint32_t)min((int32_t)(r & 15), lim);
+    __builtin_amdgcn_global_load_lds((const void*)(base + kk * a.tok_e + 8 * p),
+                                     (LdsVoid*)(buf + wslot0 * 8), 16, 0, 0);
+  };
+  if constexpr (D == 128) {
+    one(kb, kdst, tid, 64 * wave);
+    one(vb, vdst, tid, 64 * wave);
+  } else {
+    if (wave < 4) one(kb, kdst, tid, 64 * wave);
+    else one(vb, vdst, tid - 256, 64 * (wave - 4));
+  }
+}
+
+// Waits until at most n of this wave's vector memory loads are in flight
+// (s_waitcnt: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(n >= 0 && n < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(n | (0x7 << 4) | (0xF << 8));
+}
+
+// The workgroup barrier of the ring: this wave's loads of the next step
+// have landed (the caller's wait_vmcnt), then s_barrier alone. A
+// __syncthreads() would add a release fence, which waits for every load
+// in flight into LDS, including the step issued two ahead.
+__device__ __forceinline__ void ring_barrier() {
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const uint16_t* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)p;
+}
+
+// Eight ds_read_b64_tr_b16 (four V^T fragments) as one inline-assembly
+// block that also waits for them: the compiler does not see these LDS
+// reads, so it neither waits for the direct loads in flight into the other
+// ring buffers before them nor could it track their results.
+__device__ __forceinline__ void ds_read_tr16_x8(uint2 (&r)[8], const uint32_t (&addr)[8]) {
+  __asm__ volatile(
+      "ds_read_b64_tr_b16 %0, %8\n\t"
+      "ds_read_b64_tr_b16 %1, %9\n\t"
+      "ds_read_b64_tr_b16 %2, %10\n\t"
+      "ds_read_b64_tr_b16 %3, %11\n\t"
+      "ds_read_b64_tr_b16 %4, %12\n\t"
+      "ds_read_b64_tr_b16 %5, %13\n\t"
+      "ds_read_b64_tr_b16 %6, %14\n\t"
+      "ds_read_b64_tr_b16 %7, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]),
+        "=&v"(r[6]), "=&v"(r[7])
+      : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]),
+        "v"(addr[6]), "v"(addr[7])
+      : "memory");
+}
+
 template <typename T, int D, int RT, int OCC>
 __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
     AttnArgs a, const uint32_t* __restrict__ cu_q, const uint32_t* __restrict__ cu_k,
     const uint32_t* __restrict__ table, uint32_t qtiles) {
+  static_assert(kPfWaves == 8, "the step's K and V are 8 waves' loads");
   constexpr int KC = D / 32;
-  constexpr int DPL = D / 16;
+  constexpr int DT = D / 16;  // 16-column d tiles
   constexpr int kPfRT = RT;
   constexpr uint32_t kPfRows = 16 * RT * kPfWaves;
-  __shared__ PfSmem<D> sm;
+  constexpr int kLoadsPerStep = D == 128 ? 2 : 1;
+  // The ring's three buffers per tensor are separate LDS objects, each
+  // named by a compile-time index where it is used: the compiler's wait
+  // insertion then knows that a direct load into one buffer cannot alias
+  // the reads of another, and does not wait for the loads in flight before
+  // every LDS read.
+  __shared__ __attribute__((aligned(16))) uint16_t k0[32 * D], k1[32 * D], k2[32 * D];
+  __shared__ __attribute__((aligned(16))) uint16_t v0[32 * D], v1[32 * D], v2[32 * D];
   const uint32_t n_items = gridDim.x;
   const uint32_t item = xcd_remap(blockIdx.x, n_items);
   const uint32_t qt = item % qtiles, rest = item / qtiles;
@@ -177,22 +173,19 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
   const int32_t offset = len_k - (int32_t)len_q;
   const int32_t last = len_k - 1;
 
-  // Keys the whole workgroup can see.
   const uint32_t wg_last = min(row_base + kPfRows, nrows) - 1;
   const int32_t wg_pmin = offset + (int32_t)(row_base / G);
   const int32_t wg_pmax = offset + (int32_t)(wg_last / G);
   const int32_t klo = a.wl >= 0 ? max(0, wg_pmin - a.wl) : 0;
   const int32_t khi = a.wr >= 0 ? min(last, wg_pmax + a.wr) : last;
 
-  // This wave's rows: Q^T operands, per-lane query position, per-tile range.
   const uint32_t row0 = row_base + wave * 16 * kPfRT;
   uint4 qf[kPfRT][KC];
-  // Per lane: visible keys lo..hi of its row, as key - lo < cnt (unsigned).
   int32_t lo[kPfRT], cnt[kPfRT];
 #pragma unroll
   for (int t = 0; t < kPfRT; ++t) {
     const uint32_t r = row0 + 16 * t + col;
-    const uint32_t rr = r < nrows ? r : 0;  // padding rows copy row 0, never stored
+    const uint32_t rr = r < nrows ? r : 0;
     const uint32_t j = rr / G, hl = rr % G;
     int32_t hi;
     key_range(offset + (int32_t)j, len_k, a.wl, a.wr, lo[t], hi);
@@ -211,51 +204,55 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
   const T* vb = (const T*)a.v + kh * a.head_e;
 
   float m_run[kPfRT], l_run[kPfRT];
-  floatx4 o[kPfRT][DPL];
+  floatx4 o[kPfRT][DT];
 #pragma unroll
   for (int t = 0; t < kPfRT; ++t) {
     m_run[t] = kNegBig;
     l_run[t] = 0.f;
 #pragma unroll
-    for (int k = 0; k < DPL; ++k) o[t][k] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < DT; ++k) o[t][k] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // Keys every row of the workgroup sees (ranges move right with the row):
-  // steps inside [full_lo, full_hi] need no mask.
   int32_t full_lo, full_hi, unused;
   key_range(wg_pmax, len_k, a.wl, a.wr, full_lo, unused);
   key_range(wg_pmin, len_k, a.wl, a.wr, unused, full_hi);
 
-  // Two register stages: the global loads of step s+2 are issued before
-  // step s is computed from LDS, and those of step s+1 (issued a whole step
-  // earlier) are stored to the other LDS buffer after it, so a step's global
-  // latency hides behind two steps of compute. Loads are unconditional
-  // (steps past the last re-read it).
-  PfStage<D> stA, stB;
+  // Per-lane fragment offsets (elements within a step buffer).
+  uint32_t k_off[2][KC];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int c = 0; c < KC; ++c) k_off[tt][c] = pf_chunk<D>(16 * tt + col, 4 * c + g);
+  const uint32_t vj = col >> 2, vq = col & 3;
+  uint32_t v_off[DT][2];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      v_off[t][h] = pf_chunk<D>(16 * h + 4 * g + vj, 2 * t + (vq >> 1)) + 4 * (vq & 1);
+
   int32_t s0_ = klo & ~31;
   const int32_t s_last = khi & ~31;
-  pf_load<T, D>(stA, tab, kb, vb, a, s0_, last, tid);
-  pf_store<D>(sm, 0, stA, tid);
-  pf_load<T, D>(stA, tab, kb, vb, a, min(s0_ + 32, s_last), last, tid);
-  __syncthreads();
-  int buf = 0;
-  // `ready` holds step s+1 (in flight since the previous step), `next`
-  // receives step s+2.
-  auto step = [&](auto masked, PfStage<D>& ready, PfStage<D>& next) __attribute__((always_inline)) {
-    // s0 is uniform; saying so keeps the table reads on the scalar unit.
+  pf_dma<T, D>(k0, v0, tab, kb, vb, a, s0_, last, tid, wave);
+  pf_dma<T, D>(k1, v1, tab, kb, vb, a, min(s0_ + 32, s_last), last, tid, wave);
+  wait_vmcnt<kLoadsPerStep>();
+  ring_barrier();
+  // Step s reads buffer s % 3 and issues step s + 2 into (s + 2) % 3.
+  auto step = [&](auto cur) __attribute__((always_inline)) {
+    constexpr int B = decltype(cur)::value;
+    uint16_t* const kbuf = B == 0 ? k0 : B == 1 ? k1 : k2;
+    uint16_t* const vbuf = B == 0 ? v0 : B == 1 ? v1 : v2;
+    uint16_t* const knext = B == 0 ? k2 : B == 1 ? k0 : k1;
+    uint16_t* const vnext = B == 0 ? v2 : B == 1 ? v0 : v1;
     const int32_t s0 = __builtin_amdgcn_readfirstlane(s0_);
-    pf_load<T, D>(next, tab, kb, vb, a, min(s0 + 64, s_last), last, tid);
+    pf_dma<T, D>(knext, vnext, tab, kb, vb, a, min(s0 + 64, s_last), last, tid, wave);
+    // Steps inside [full_lo, full_hi] need no mask (a uniform branch).
+    const bool masked = !(s0 >= full_lo && s0 + 31 <= full_hi);
     KTile<D> kt;
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-      for (int c = 0; c < KC; ++c)
-        kt.k[tt][c] = *(const uint4*)&sm.k[buf][16 * tt + col][32 * c + 8 * g];
-    // Every row tile runs every step: a tile whose rows see no key of the
-    // step gets P = 0 (all scores -inf). The scores of all row tiles are
-    // issued first (independent MFMA chains), then their maxima share one
-    // rescale branch, so no branch sits between a tile's MFMAs and the
-    // next tile's.
+      for (int c = 0; c < KC; ++c) kt.k[tt][c] = *(const uint4*)(kbuf + k_off[tt][c]);
     float sc[kPfRT][8];
     {
       floatx4 acc[kPfRT][2];
@@ -267,10 +264,14 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const bool vis = !decltype(masked)::value || base + 16 * tt + i < n;
-            sc[t][4 * tt + i] = vis ? acc[t][tt][i] : -INFINITY;
-          }
+          for (int i = 0; i < 4; ++i) sc[t][4 * tt + i] = acc[t][tt][i];
+        if (masked) {
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (!(base + 16 * tt + i < n)) sc[t][4 * tt + i] = -INFINITY;
+        }
       }
     }
     float mx[kPfRT];
@@ -288,44 +289,56 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
     uint4 pf[kPfRT];
 #pragma unroll
     for (int t = 0; t < kPfRT; ++t) pf[t] = exp_pack<T>(sc[t], m_run[t], l_run[t], a.scale_log2);
+    // V^T fragments four d tiles at a time; a batch's MFMAs run while the
+    // next batch's reads wait.
+    const uint32_t vbase = lds_addr(vbuf);
 #pragma unroll
-    for (int k = 0; k < DPL; ++k) {
-      const uint4 vf = *(const uint4*)&sm.vt[buf][vrow<D>(DPL * col + k)][8 * g];
+    for (int k0 = 0; k0 < DT; k0 += 4) {
+      uint32_t ad[8];
+      uint2 r[8];
 #pragma unroll
-      for (int t = 0; t < kPfRT; ++t) o[t][k] = mfma16x16x32<T>(vf, pf[t], o[t][k]);
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) ad[2 * k + h] = vbase + 2 * v_off[k0 + k][h];
+      ds_read_tr16_x8(r, ad);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint4 vf = make_uint4(r[2 * k].x, r[2 * k].y, r[2 * k + 1].x, r[2 * k + 1].y);
+#pragma unroll
+        for (int t = 0; t < kPfRT; ++t)
+          o[t][k0 + k] = mfma16x16x32<T>(vf, pf[t], o[t][k0 + k]);
+      }
     }
-    pf_store<D>(sm, buf ^ 1, ready, tid);
-    __syncthreads();
-    buf ^= 1;
+    // Step s + 1's chunks (issued a step ago) are in LDS once this wave's
+    // loads older than step s + 2's have landed; the barrier makes that
+    // hold for every wave.
+    wait_vmcnt<kLoadsPerStep>();
+    ring_barrier();
     s0_ += 32;
   };
-  using Masked = std::integral_constant<bool, true>;
-  using Full = std::integral_constant<bool, false>;
-  // Steps alternate the stage roles (unrolled by two); a loop that ends on
-  // an odd step moves the in-flight stage back to stA, the invariant between
-  // loops.
-  auto loop = [&](auto masked, auto more) __attribute__((always_inline)) {
-    while (more()) {
-      step(masked, stA, stB);
-      if (!more()) {
-        stA = stB;
-        return;
-      }
-      step(masked, stB, stA);
-    }
-  };
-  loop(Masked{}, [&] { return s0_ <= khi && s0_ < full_lo; });
-  loop(Full{}, [&] { return s0_ <= khi && s0_ + 31 <= full_hi; });
-  loop(Masked{}, [&] { return s0_ <= khi; });
+  while (true) {
+    if (s0_ > khi) break;
+    step(std::integral_constant<int, 0>{});
+    if (s0_ > khi) break;
+    step(std::integral_constant<int, 1>{});
+    if (s0_ > khi) break;
+    step(std::integral_constant<int, 2>{});
+  }
+  wait_vmcnt<0>();  // no load may land in LDS after the workgroup ends
 
 #pragma unroll
   for (int t = 0; t < kPfRT; ++t) {
     const float lt = wave_sum_g(l_run[t]);
-    const uint32_t r = row0 + 16 * t + col;  // this lane's query row
+    const uint32_t r = row0 + 16 * t + col;
     if (r >= nrows) continue;
     const uint32_t j = r / G, hl = r % G;
     T* orow = (T*)a.out + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * D;
-    store_row<T, D>(orow, o[t], lt > 0.f ? 1.f / lt : 0.f, g);
+    const float sc = lt > 0.f ? 1.f / lt : 0.f;
+#pragma unroll
+    for (int k = 0; k < DT; ++k)
+      *(uint2*)(orow + 16 * k + 4 * g) =
+          make_uint2(pack2<T>(o[t][k][0] * sc, o[t][k][1] * sc),
+                     pack2<T>(o[t][k][2] * sc, o[t][k][3] * sc));
   }
 }
 
