@@ -116,27 +116,22 @@ __device__ __forceinline__ uint32_t lds_addr(const uint16_t* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)p;
 }
 
-// Eight ds_read_b64_tr_b16 (four V^T fragments) as one inline-assembly
-// block that also waits for them: the compiler does not see these LDS
-// reads, so it neither waits for the direct loads in flight into the other
-// ring buffers before them nor could it track their results.
-__device__ __forceinline__ void ds_read_tr16_x8(uint2 (&r)[8], const uint32_t (&addr)[8]) {
+// Four ds_read_b64_tr_b16 (two V^T fragments, reads 4h .. 4h + 3) as one
+// inline-assembly block that also waits for them: the compiler does not
+// see these LDS reads, so it neither waits for the direct loads in flight
+// into the other ring buffers before them nor could it track their results.
+__device__ __forceinline__ void ds_read_tr16_x4(uint2 (&r)[8], const uint32_t (&addr)[8], int h) {
   __asm__ volatile(
-      "ds_read_b64_tr_b16 %0, %8\n\t"
-      "ds_read_b64_tr_b16 %1, %9\n\t"
-      "ds_read_b64_tr_b16 %2, %10\n\t"
-      "ds_read_b64_tr_b16 %3, %11\n\t"
-      "ds_read_b64_tr_b16 %4, %12\n\t"
-      "ds_read_b64_tr_b16 %5, %13\n\t"
-      "ds_read_b64_tr_b16 %6, %14\n\t"
-      "ds_read_b64_tr_b16 %7, %15\n\t"
+      "ds_read_b64_tr_b16 %0, %4\n\t"
+      "ds_read_b64_tr_b16 %1, %5\n\t"
+      "ds_read_b64_tr_b16 %2, %6\n\t"
+      "ds_read_b64_tr_b16 %3, %7\n\t"
       "s_waitcnt lgkmcnt(0)"
-      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]),
-        "=&v"(r[6]), "=&v"(r[7])
-      : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]),
-        "v"(addr[6]), "v"(addr[7])
+      : "=&v"(r[4 * h]), "=&v"(r[4 * h + 1]), "=&v"(r[4 * h + 2]), "=&v"(r[4 * h + 3])
+      : "v"(addr[4 * h]), "v"(addr[4 * h + 1]), "v"(addr[4 * h + 2]), "v"(addr[4 * h + 3])
       : "memory");
 }
+
 
 template <typename T, int D, int RT, int OCC>
 __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
@@ -289,8 +284,9 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
     uint4 pf[kPfRT];
 #pragma unroll
     for (int t = 0; t < kPfRT; ++t) pf[t] = exp_pack<T>(sc[t], m_run[t], l_run[t], a.scale_log2);
-    // V^T fragments four d tiles at a time; a batch's MFMAs run while the
-    // next batch's reads wait.
+    // V^T fragments two d tiles at a time; a batch's MFMAs run while the
+    // next batch's reads wait (measured: batches of two tiles 821-833
+    // TFLOP/s, of four 803-814, of one 794-805 on config 3).
     const uint32_t vbase = lds_addr(vbuf);
 #pragma unroll
     for (int k0 = 0; k0 < DT; k0 += 4) {
@@ -300,9 +296,17 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
       for (int k = 0; k < 4; ++k)
 #pragma unroll
         for (int h = 0; h < 2; ++h) ad[2 * k + h] = vbase + 2 * v_off[k0 + k][h];
-      ds_read_tr16_x8(r, ad);
+      ds_read_tr16_x4(r, ad, 0);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
+      for (int k = 0; k < 2; ++k) {
+        const uint4 vf = make_uint4(r[2 * k].x, r[2 * k].y, r[2 * k + 1].x, r[2 * k + 1].y);
+#pragma unroll
+        for (int t = 0; t < kPfRT; ++t)
+          o[t][k0 + k] = mfma16x16x32<T>(vf, pf[t], o[t][k0 + k]);
+      }
+      ds_read_tr16_x4(r, ad, 1);
+#pragma unroll
+      for (int k = 2; k < 4; ++k) {
         const uint4 vf = make_uint4(r[2 * k].x, r[2 * k].y, r[2 * k + 1].x, r[2 * k + 1].y);
 #pragma unroll
         for (int t = 0; t < kPfRT; ++t)
