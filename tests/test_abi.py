@@ -218,3 +218,15 @@ def test_a_c_program_uses_the_library_through_the_header(tmp_path):
     res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
     assert res.returncode == 0, res.stdout + res.stderr
     assert "all checks passed" in res.stdout
+
+
+def test_the_build_refuses_a_prefill_kernel_that_spills():
+    """The prefill ring's explicit vmcnt waits count only its direct loads;
+    the build parses the compiler's resource remarks and refuses scratch."""
+    from vapi_amd import build as b
+    ok = ("x: remark: Function Name: _ZN2vk19paged_prefill_tiledINS_6bf16_tE [-R]\n"
+          "x: remark:     ScratchSize [bytes/lane]: 0 [-R]\n")
+    b._check_no_scratch(Path("attn_prefill.hip"), ok)
+    with pytest.raises(RuntimeError, match="scratch"):
+        b._check_no_scratch(Path("attn_prefill.hip"), ok.replace(": 0 [", ": 16 ["))
+    b._check_no_scratch(Path("kv_ops.hip"), ok.replace(": 0 [", ": 16 ["))  # not checked

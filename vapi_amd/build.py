@@ -40,7 +40,29 @@ SOURCES = ["kv_ops.hip", "attention.hip", "attn_decode.hip", "attn_prefill.hip",
 # The MFMA attention kernels never produce NaN from finite K/V/Q (masked
 # scores are -inf, running maxima start finite), so fmaxf on MFMA results
 # needs no operand quieting: -fno-honor-nans drops one instruction per score.
-EXTRA_FLAGS = {"attn_decode.hip": ["-fno-honor-nans"], "attn_prefill.hip": ["-fno-honor-nans"]}
+EXTRA_FLAGS = {"attn_decode.hip": ["-fno-honor-nans"],
+               "attn_prefill.hip": ["-fno-honor-nans", "-Rpass-analysis=kernel-resource-usage"]}
+
+# The prefill kernel's step barrier counts its own vector-memory operations
+# (the direct loads into LDS) with an explicit vmcnt wait; a register spill
+# would add scratch loads and stores to that count, so a build whose prefill
+# kernels use scratch is refused.
+NO_SCRATCH = {"attn_prefill.hip": "paged_prefill_tiled"}
+
+
+def _check_no_scratch(src: Path, remarks: str) -> None:
+    kernel = NO_SCRATCH.get(src.name)
+    if not kernel:
+        return
+    current = None
+    for line in remarks.splitlines():
+        if "Function Name:" in line:
+            current = line.split("Function Name:")[1].split()[0]
+        elif "ScratchSize" in line and current and kernel in current:
+            size = int(line.split("ScratchSize [bytes/lane]:")[1].split()[0])
+            if size != 0:
+                raise RuntimeError(f"{current} uses {size} bytes of scratch per lane; its "
+                                   "explicit vmcnt waits assume it uses none")
 
 
 def _compile(src: Path, obj: Path) -> None:
@@ -53,6 +75,7 @@ def _compile(src: Path, obj: Path) -> None:
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError(f"hipcc failed on {src.name}")
+    _check_no_scratch(src, res.stderr)
 
 
 def build(verbose: bool = False) -> Path:

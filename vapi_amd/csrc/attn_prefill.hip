@@ -95,7 +95,9 @@ __device__ __forceinline__ void pf_dma(uint16_t* kdst, uint16_t* vdst, const uin
 }
 
 // Waits until at most n of this wave's vector memory loads are in flight
-// (s_waitcnt: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+// (s_waitcnt: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8). The
+// ring's waits count only its own direct loads, which holds while the
+// kernel uses no scratch (vapi_amd/build.py refuses a build where it does).
 template <int n>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(n >= 0 && n < 16, "vmcnt immediate");
