@@ -361,9 +361,15 @@ void launch_prefill(const AttnArgs& a, uint32_t max_q, uint32_t head_dim, bool b
   const uint32_t qtiles = (max_q * a.group + rows - 1) / rows;
   const uint64_t n = (uint64_t)qtiles * a.kvh * a.batch;
   const dim3 grid((uint32_t)n), block(kPfThreads);
+// head_dim 64 fits in 128 registers: two workgroups per CU (four waves per
+// SIMD) measured 1% faster than one on a config-3-shaped batch (676-678
+// against 669-673 TFLOP/s).
+#ifndef VK_PF_OCC64
+#define VK_PF_OCC64 2
+#endif
 #define VK_PF(T, DD)                                                                    \
-  hipLaunchKernelGGL((paged_prefill_tiled<T, DD, VK_PF_RT, VK_PF_OCC>), grid, block, 0, s, a, \
-                     a.cu_q, a.cu_k, a.table, qtiles)
+  hipLaunchKernelGGL((paged_prefill_tiled<T, DD, VK_PF_RT, DD == 64 ? VK_PF_OCC64 : VK_PF_OCC>), \
+                     grid, block, 0, s, a, a.cu_q, a.cu_k, a.table, qtiles)
   if (bf16) {
     if (head_dim == 128) VK_PF(bf16_t, 128);
     else VK_PF(bf16_t, 64);
