@@ -582,7 +582,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build's paged-KV path runs on a single "
-              "MI355X (see DESIGN.md for how it would shard); run with --gpus 1.",
+              "MI355X (across GPUs it would shard by kv head or by sequence, with no exchange); "
+              "run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
     torch.cuda.init()
