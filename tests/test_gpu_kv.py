@@ -598,3 +598,28 @@ def test_block_ids_past_the_pool_move_nothing():
     store = SpillStore(None, 1 << 30, 0)
     with pytest.raises(VapiKvError, match="block 8 of 8"):
         spill_evicted(store, c, [(bytes(32), 8)], pinned_buffer(c, 1))
+
+
+@pytest.mark.gpu
+def test_attention_over_a_layer_of_a_mixed_cache_matches_the_oracle():
+    """The K/V layers of a mixed cache attend like a uniform cache's (their
+    per-layer view is an ordinary pool); a rows layer is refused."""
+    from vapi_amd.attention import ForwardBatch, paged_attention
+    from vapi_amd.cache import HybridKvCache
+    c = HybridKvCache([("rows", 40), ("kv", 2, 64), ("rows", 40), ("kv", 2, 64)], 16, 16,
+                      torch.float32, "NHD")
+    g = torch.Generator(device=DEV).manual_seed(5)
+    for t in c.k + c.v:
+        if t.numel():
+            t.copy_(torch.randn(t.shape, generator=g, device=DEV))
+    batch = ForwardBatch(cu_seqlens_q=[0, 1, 6], cu_seqlens_k=[0, 40, 70],
+                         block_tables=[[3, 1, 7], [9, 2]], max_seqlen_q=5, max_seqlen_k=40)
+    q = torch.randn(6, 4, 64, generator=g, device=DEV)
+    for layer in (1, 3):
+        got = paged_attention(q, c, layer, batch, 0.125)
+        want = oracle.paged_attention(q.cpu().numpy(), as_np(c.reference_view(layer, "k")),
+                                      as_np(c.reference_view(layer, "v")), batch.cu_seqlens_q,
+                                      batch.cu_seqlens_k, batch.block_tables, 0.125, None, 0)
+        assert float(np.abs(got.cpu().numpy() - want).max()) <= 1e-5
+    with pytest.raises(Exception):
+        paged_attention(q, c, 0, batch, 0.125)

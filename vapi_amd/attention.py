@@ -15,7 +15,7 @@ import numpy as np
 import torch
 
 from ._lib import check, lib
-from .cache import PagedKvCache, stream_handle
+from .cache import PagedKvCache, _per_layer, stream_handle
 
 _u32p = ctypes.POINTER(ctypes.c_uint32)
 
@@ -135,7 +135,10 @@ def paged_attention_prepared(q: torch.Tensor, cache: PagedKvCache, layer: int,
                              window_size_right: int | None = 0,
                              out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """attention.rs:262-288 on libvapi_kv.so. None for a window side means
-    unlimited (flash convention); the default right window 0 is causal."""
+    unlimited (flash convention); the default right window 0 is causal.
+    `cache` may be a HybridKvCache: `layer` then names one of its K/V
+    layers."""
+    cache, layer = _per_layer(cache, layer)
     if q.dim() != 3 or q.shape[2] != cache.head_dim:
         raise ValueError(f"q must be (tokens, heads, {cache.head_dim}), got {tuple(q.shape)}")
     if q.dtype != cache.dtype:
@@ -191,6 +194,7 @@ def paged_attention_append_prepared(q: torch.Tensor, k: torch.Tensor, v: torch.T
     k, v: [n, num_kv_heads, head_dim] in the cache dtype; slot_mapping: a
     device u32 (int32 view) tensor of n slots.
     """
+    cache, layer = _per_layer(cache, layer)
     if q.dim() != 3 or q.shape[2] != cache.head_dim:
         raise ValueError(f"q must be (tokens, heads, {cache.head_dim}), got {tuple(q.shape)}")
     if q.dtype != cache.dtype or k.dtype != cache.dtype or v.dtype != cache.dtype:
