@@ -323,7 +323,10 @@ def write_kv_to_cache_layers(cache: PagedKvCache, layer0: int, k: torch.Tensor,
     """One step's K/V for layers layer0 .. layer0 + L - 1 in one launch: k, v
     are [L, n, num_kv_heads, head_dim] (any common stride between layers,
     rows contiguous within one) and idx a device u32 (int32 view) slot per
-    row. Equals L single-layer appends."""
+    row. Equals L single-layer appends. (A HybridKvCache's layers are
+    separate pools: append to them one layer at a time.)"""
+    if isinstance(cache, HybridKvCache):
+        raise ValueError("a mixed cache's layers are separate pools: append per layer")
     if k.dim() != 4 or tuple(k.shape) != tuple(v.shape):
         raise ValueError(f"k/v must be (layers, n, heads, width), got {tuple(k.shape)} "
                          f"and {tuple(v.shape)}")
