@@ -69,6 +69,10 @@ typedef enum {
  * block*block_size + offset, the addressing of ForwardBatch::slot_mapping
  * (crates/vapi-engine/src/backend.rs:62-64).
  *
+ * k and v must be 16-byte aligned and layer_stride_bytes a multiple of 16
+ * (the kernels move 16-byte chunks; vapi_cache_new and the Python cache pad
+ * layers to 256 bytes); anything else is VAPI_KV_EINVAL.
+ *
  * v == NULL makes a K-only pool: LayerLayout::Rows layers (cache.rs:24-33,
  * 89-96), one (1, width) row per token, num_kv_heads 1 and head_dim width.
  * Appends and gathers then move K only; attention rejects the pool.
@@ -203,6 +207,33 @@ int vapi_paged_attention(const vapi_kv_pool* pool, uint32_t layer,
                          vapi_stream_t stream);
 
 /*
+ * vapi_paged_attention with flags (0 = vapi_paged_attention itself). No
+ * counterpart in the reference, whose flash call takes no such options
+ * (attention.rs:272-287); they are host knowledge a caller can pass on:
+ *
+ * VAPI_ATTN_NO_DECODE_ROWS: the caller knows no row has len_q == 1 (a
+ *   prefill-only step; PreparedAttention knows it from its host
+ *   cu_seqlens). The call then launches the prefill kernel alone, which
+ *   takes every row, so a wrong hint costs time, never correctness. Such a
+ *   call needs no workspace (workspace may be NULL, workspace_bytes 0).
+ * VAPI_ATTN_DETERMINISTIC: the decode splits its work with fixed equal
+ *   per-XCD shares instead of the shares the previous call measured, and
+ *   does not update them: two calls on identical inputs give bit-identical
+ *   outputs, whatever ran on the workspace before. Costs the XCD balancing
+ *   (a few percent of decode time).
+ * Unknown flag bits are VAPI_KV_EINVAL.
+ */
+#define VAPI_ATTN_DETERMINISTIC 0x1u
+#define VAPI_ATTN_NO_DECODE_ROWS 0x2u
+int vapi_paged_attention_ex(const vapi_kv_pool* pool, uint32_t layer, const void* q, void* out,
+                            const uint32_t* cu_seqlens_q, const uint32_t* cu_seqlens_k,
+                            const uint32_t* block_table, uint32_t batch, uint32_t max_blocks,
+                            uint32_t max_seqlen_q, uint32_t max_seqlen_k, uint32_t num_heads,
+                            float scale, int32_t window_left, int32_t window_right,
+                            uint32_t flags, void* workspace, size_t workspace_bytes,
+                            vapi_stream_t stream);
+
+/*
  * One decode step's K/V append and paged attention in one call: the result
  * is that of vapi_kv_append(k_src, v_src, slot_mapping, n_tokens) followed
  * by vapi_paged_attention(...) with the same arguments. It fuses the
@@ -233,6 +264,19 @@ int vapi_paged_attention_append(const vapi_kv_pool* pool, uint32_t layer,
                                 float scale, int32_t window_left,
                                 int32_t window_right, void* workspace,
                                 size_t workspace_bytes, vapi_stream_t stream);
+
+/* vapi_paged_attention_append with the flags of vapi_paged_attention_ex
+ * (VAPI_ATTN_NO_DECODE_ROWS has no effect on a fused decode step). */
+int vapi_paged_attention_append_ex(const vapi_kv_pool* pool, uint32_t layer, const void* k_src,
+                                   const void* v_src, const uint32_t* slot_mapping,
+                                   uint32_t n_tokens, const void* q, void* out,
+                                   const uint32_t* cu_seqlens_q, const uint32_t* cu_seqlens_k,
+                                   const uint32_t* block_table, uint32_t batch,
+                                   uint32_t max_blocks, uint32_t max_seqlen_q,
+                                   uint32_t max_seqlen_k, uint32_t num_heads, float scale,
+                                   int32_t window_left, int32_t window_right, uint32_t flags,
+                                   void* workspace, size_t workspace_bytes,
+                                   vapi_stream_t stream);
 
 /*
  * Copy-on-write block copy over every layer, K and V, in one launch (one

@@ -33,7 +33,7 @@ def test_every_declared_symbol_is_exported():
 
 
 def pool(**kw):
-    p = dict(k=1, v=2, layer_stride_bytes=1 << 20, num_layers=1, num_blocks=8, block_size=16,
+    p = dict(k=1 << 12, v=1 << 13, layer_stride_bytes=1 << 20, num_layers=1, num_blocks=8, block_size=16,
              num_kv_heads=2, head_dim=64, dtype=_lib.BF16, layout=_lib.LAYOUT_HND)
     p.update(kw)
     return _lib.Pool(**p)
@@ -73,6 +73,41 @@ def test_bad_arguments_are_errors_not_crashes():
     assert b"null source" in L.vapi_kv_last_error()
     args = [1, 1, 1, 1, 1, 1, 2, 320, 1, 5000, 8, 0.1, -1, 0, None, 0, None]
     assert L.vapi_paged_attention_append(pool(), 0, 1, 1, 1, *args) == _lib.ESPACE
+
+
+def test_misaligned_pools_and_unknown_flags_are_refused():
+    """Pools whose bases or layer stride are not 16-byte multiples are
+    refused before any launch (the kernels move 16-byte chunks), and so are
+    flag bits the attention call does not know."""
+    L = _lib.lib()
+    assert L.vapi_kv_append(pool(k=(1 << 12) + 8), 0, 1, 1, 1, 1, None) == _lib.EINVAL
+    assert b"16-byte aligned" in L.vapi_kv_last_error()
+    assert L.vapi_kv_append(pool(v=(1 << 13) + 2), 0, 1, 1, 1, 1, None) == _lib.EINVAL
+    two = pool(num_layers=2, layer_stride_bytes=(1 << 20) + 8)
+    assert L.vapi_kv_copy_blocks(two, 1, 1, None) == _lib.EINVAL
+    assert b"multiple of 16" in L.vapi_kv_last_error()
+    assert L.vapi_kv_export_blocks(two, 1, 1, 1, None) == _lib.EINVAL
+    args = [1, 1, 1, 1, 1, 2, 4, 1, 100, 8, 0.1, -1, 0]
+    assert L.vapi_paged_attention_ex(pool(), 0, *args, 0x80, None, 0, None) == _lib.EINVAL
+    assert b"flags" in L.vapi_kv_last_error()
+    # The flags call keeps vapi_paged_attention's own checks.
+    need = L.vapi_paged_attention_workspace_size(pool(), 2, 8, 1, 5000)
+    args = [1, 1, 1, 1, 1, 2, 320, 1, 5000, 8, 0.1, -1, 0]
+    assert L.vapi_paged_attention_ex(pool(), 0, *args, _lib.ATTN_DETERMINISTIC, None, 0,
+                                     None) == _lib.ESPACE
+    assert need > 0
+
+
+def test_prepared_attention_flags_follow_the_host_lengths():
+    from vapi_amd.attention import ATTN_DETERMINISTIC, ATTN_NO_DECODE_ROWS, PreparedAttention
+    mk = lambda lq, lk: ForwardBatch(cu_seqlens_q=np.concatenate([[0], np.cumsum(lq)]).tolist(),
+                                     cu_seqlens_k=np.concatenate([[0], np.cumsum(lk)]).tolist(),
+                                     block_tables=[[i] for i in range(len(lq))],
+                                     max_seqlen_q=max(lq), max_seqlen_k=max(lk))
+    assert PreparedAttention.from_batch(mk([5, 7], [9, 9]), "cpu").flags == ATTN_NO_DECODE_ROWS
+    assert PreparedAttention.from_batch(mk([5, 1], [9, 9]), "cpu").flags == 0
+    assert PreparedAttention.from_batch(mk([1, 1], [9, 9]), "cpu",
+                                        deterministic=True).flags == ATTN_DETERMINISTIC
 
 
 def test_block_bytes_is_layers_times_kv_times_block():

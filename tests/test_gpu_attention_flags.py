@@ -1,0 +1,137 @@
+"""GPU checks of vapi_paged_attention_ex's flags and of the fused append's
+bounded table read.
+
+  * VAPI_ATTN_NO_DECODE_ROWS: a prefill-only batch runs the prefill kernel
+    alone; its output equals the two-kernel call bit for bit (the decode
+    kernel never writes a prefill row). Forced onto a batch that does have
+    decode rows, the prefill kernel takes them too: checked against the
+    oracle (bf16 max-abs <= 2e-2 * max|reference|, as every attention test).
+  * VAPI_ATTN_DETERMINISTIC: repeated calls on identical inputs are
+    bit-identical, also after other batches moved the workspace's shares.
+  * The fused append's per-row check reads the block table with the same
+    column clamp as every other table read: a row whose len_k runs past its
+    table row finishes, and pool and output equal the two-call sequence.
+"""
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_append_attention import clone, dev_slots
+from test_gpu_attention import max_abs, oracle_out, random_case
+from vapi_amd import _lib
+from vapi_amd.attention import (ATTN_DETERMINISTIC, ATTN_NO_DECODE_ROWS, ForwardBatch,
+                                PreparedAttention, paged_attention_append_prepared,
+                                paged_attention_prepared)
+from vapi_amd.cache import stream_handle, write_rows_indexed
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def call_ex(q, cache, prep, scale, flags, window_left=-1, ws=None):
+    """vapi_paged_attention_ex straight through the C ABI with `flags`."""
+    out = torch.full_like(q, float("nan"))
+    b = prep.seqlens_q.shape[0] - 1
+    max_q, max_k = max(prep.max_seqlen_q, 1), max(prep.max_seqlen_k, 1)
+    need = _lib.lib().vapi_paged_attention_workspace_size(cache.pool, b, q.shape[1], max_q,
+                                                          max_k)
+    if ws is None and not (flags & ATTN_NO_DECODE_ROWS):
+        ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=DEV)
+    _lib.check(_lib.lib().vapi_paged_attention_ex(
+        cache.pool, 0, q.data_ptr(), out.data_ptr(), prep.seqlens_q.data_ptr(),
+        prep.seqlens_k.data_ptr(), prep.block_table.data_ptr(), b, prep.block_table.shape[1],
+        max_q, max_k, q.shape[1], float(scale), window_left, 0, flags,
+        ws.data_ptr() if ws is not None else None, need if ws is not None else 0,
+        stream_handle()))
+    return out
+
+
+@pytest.mark.parametrize("heads,kvh,d,window", [(32, 8, 128, None), (16, 2, 64, 40),
+                                                (8, 8, 128, None)])
+def test_a_prefill_only_batch_runs_one_kernel_with_the_same_output(heads, kvh, d, window):
+    rng = np.random.default_rng(heads * 131 + d)
+    c, q, batch = random_case(rng, torch.bfloat16, heads, kvh, d, 16, [37, 64, 5, 2],
+                              [300, 700, 40, 2], "HND")
+    prep = PreparedAttention.from_batch(batch, DEV)
+    assert prep.flags == ATTN_NO_DECODE_ROWS
+    scale = d ** -0.5
+    wl = -1 if window is None else window - 1
+    one = call_ex(q, c, prep, scale, ATTN_NO_DECODE_ROWS, wl)  # no workspace at all
+    two = call_ex(q, c, prep, scale, 0, wl)
+    torch.cuda.synchronize()
+    assert torch.equal(one, two)
+    want = oracle_out(q, c, 0, batch, scale, window)
+    assert max_abs(one, want) <= 2e-2 * float(want.abs().max())
+
+
+@pytest.mark.parametrize("heads,kvh,d", [(32, 8, 128), (16, 2, 64)])
+def test_a_wrong_no_decode_hint_still_gives_every_row(heads, kvh, d):
+    """Decode rows under VAPI_ATTN_NO_DECODE_ROWS go to the prefill kernel."""
+    rng = np.random.default_rng(heads + d)
+    c, q, batch = random_case(rng, torch.bfloat16, heads, kvh, d, 16, [1, 19, 1, 3, 1],
+                              [900, 300, 1, 40, 2049], "NHD")
+    prep = PreparedAttention.from_batch(batch, DEV)
+    assert prep.flags == 0
+    got = call_ex(q, c, prep, d ** -0.5, ATTN_NO_DECODE_ROWS)
+    want = oracle_out(q, c, 0, batch, d ** -0.5)
+    assert max_abs(got, want) <= 2e-2 * float(want.abs().max())
+
+
+def test_deterministic_decode_is_bit_identical_across_calls():
+    rng = np.random.default_rng(64)
+    lens_k = np.clip(np.exp(rng.normal(np.log(1500), 0.75, 64)), 64, 6000).astype(int).tolist()
+    c, q, batch = random_case(rng, torch.bfloat16, 32, 8, 128, 16, [1] * 64, lens_k, "HND")
+    _, q2, other = random_case(np.random.default_rng(3), torch.bfloat16, 32, 8, 128, 16,
+                               [1] * 7, [5000, 20, 3000, 1, 800, 4000, 64], "HND",
+                               nb=c.num_blocks)
+    prep = PreparedAttention.from_batch(batch, DEV, deterministic=True)
+    assert prep.flags == ATTN_DETERMINISTIC
+    adaptive = PreparedAttention.from_batch(other, DEV)
+    scale = 128 ** -0.5
+    first = paged_attention_prepared(q, c, 0, prep, scale).clone()
+    outs = []
+    for _ in range(3):
+        # Other work on the same workspace moves the adaptive shares.
+        adaptive.workspace = prep.workspace
+        for _ in range(3):
+            paged_attention_prepared(q2, c, 0, adaptive, scale)
+        outs.append(paged_attention_prepared(q, c, 0, prep, scale).clone())
+    torch.cuda.synchronize()
+    for o in outs:
+        assert torch.equal(o, first)
+    want = oracle_out(q, c, 0, batch, scale)
+    assert max_abs(first, want) <= 2e-2 * float(want.abs().max())
+
+
+def test_fused_append_with_len_k_past_the_table_stays_in_bounds():
+    """ForwardBatch::validate refuses such a batch on the host; on the device
+    the fused path's table read is clamped like the others, so the call
+    finishes and matches the two-call sequence on the same inputs."""
+    rng = np.random.default_rng(77)
+    c, q, batch = random_case(rng, torch.bfloat16, 32, 8, 128, 16, [1, 1, 1],
+                              [300, 33, 700], "HND")
+    # Row 1 claims 1,000 keys over a 3-block table row; the packed table is
+    # 44 columns wide (700 keys), so its new key's column (62) is past the row.
+    over = ForwardBatch(cu_seqlens_q=batch.cu_seqlens_q, cu_seqlens_k=[0, 300, 1300, 2000],
+                        block_tables=batch.block_tables, max_seqlen_q=1, max_seqlen_k=1000)
+    k_new = torch.randn(3, 8, 128, device=DEV).to(torch.bfloat16)
+    v_new = torch.randn_like(k_new)
+    # Row 1's new row goes to a block no table names: the fused path's
+    # contract is that no row reads a slot the call writes other than its own
+    # new key, and row 1's over-long keys re-read its padded last entry.
+    spare = sorted(set(range(c.num_blocks)) - {b for t in batch.block_tables for b in t})[0]
+    slots = [batch.block_tables[0][299 // 16] * 16 + 299 % 16,
+             spare * 16 + 5,
+             batch.block_tables[2][699 // 16] * 16 + 699 % 16]
+    s = dev_slots(slots)
+    scale = 128 ** -0.5
+    c2 = clone(c)
+    write_rows_indexed(c2, 0, k_new, v_new, s)
+    out2 = paged_attention_prepared(q, c2, 0, PreparedAttention.from_batch(over, DEV), scale)
+    c1 = clone(c)
+    out1 = paged_attention_append_prepared(q, k_new, v_new, s, c1, 0,
+                                           PreparedAttention.from_batch(over, DEV), scale)
+    torch.cuda.synchronize()
+    assert torch.equal(c1._slab, c2._slab)
+    assert bool(torch.isfinite(out1.float()).all())
+    assert torch.equal(out1, out2)

@@ -16,6 +16,7 @@ LAYOUT_HND, LAYOUT_NHD = 0, 1
 SLOT_SKIP = 0xFFFFFFFF
 
 OK, EINVAL, EUNSUP, EHIP, ESPACE = 0, -1, -2, -3, -4
+ATTN_DETERMINISTIC, ATTN_NO_DECODE_ROWS = 0x1, 0x2
 
 # Every symbol include/vapi_kv.h declares.
 EXPORTS = (
@@ -32,6 +33,7 @@ EXPORTS = (
     "vapi_spill_open", "vapi_spill_close", "vapi_spill_contains", "vapi_spill_put",
     "vapi_spill_get", "vapi_spill_get_stats", "vapi_spill_evicted", "vapi_spill_promote",
     "vapi_spill_evicted_async", "vapi_spill_drain",
+    "vapi_paged_attention_ex", "vapi_paged_attention_append_ex",
 )
 
 
@@ -100,6 +102,12 @@ def lib():
     L.vapi_paged_attention_append.argtypes = [
         _poolp, _u32, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
         _u32, ctypes.c_float, _i32, _i32, _vp, _sz, _vp]
+    L.vapi_paged_attention_ex.argtypes = [
+        _poolp, _u32, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,
+        ctypes.c_float, _i32, _i32, _u32, _vp, _sz, _vp]
+    L.vapi_paged_attention_append_ex.argtypes = [
+        _poolp, _u32, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
+        _u32, ctypes.c_float, _i32, _i32, _u32, _vp, _sz, _vp]
     L.vapi_kv_append_layers.argtypes = [_poolp, _u32, _u32, _vp, _vp, ctypes.c_uint64, _vp,
                                          _u32, _vp]
     L.vapi_kv_copy_blocks.argtypes = [_poolp, _vp, _u32, _vp]

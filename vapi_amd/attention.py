@@ -90,25 +90,57 @@ def cu_seqlens(values, device) -> torch.Tensor:
     return torch.from_numpy(_u32(values).view(np.int32)).to(device)
 
 
+ATTN_DETERMINISTIC = 0x1
+ATTN_NO_DECODE_ROWS = 0x2
+
+
 @dataclass
 class PreparedAttention:
     """Per-step device inputs, built once per step rather than per layer
     (attention.rs:237-256). Also holds the decode workspace (per-XCD shares
-    and split-context partials), reused by every layer of the step."""
+    and split-context partials), reused by every layer of the step, and the
+    call flags the host lengths allow: a batch with no decode row (len_q ==
+    1) runs the prefill kernel alone (ATTN_NO_DECODE_ROWS); `deterministic`
+    freezes the decode's work split so repeated calls are bit-identical."""
     block_table: torch.Tensor
     seqlens_q: torch.Tensor
     seqlens_k: torch.Tensor
     max_seqlen_q: int
     max_seqlen_k: int
     workspace: torch.Tensor | None = None
+    flags: int = 0
 
     @classmethod
-    def from_batch(cls, batch: ForwardBatch, device) -> "PreparedAttention":
-        return cls(block_table=pack_block_tables(batch, device),
+    def from_batch(cls, batch: ForwardBatch, device, cache=None, num_heads: int | None = None,
+                   deterministic: bool = False) -> "PreparedAttention":
+        """With `cache` and `num_heads`, the workspace is sized here for the
+        largest attention layer of the cache (a HybridKvCache's layers may
+        differ in heads and head_dim), so no layer of the step allocates."""
+        cq = np.asarray(batch.cu_seqlens_q, dtype=np.int64)
+        lens_q = np.diff(cq) if cq.size > 1 else np.zeros(0, np.int64)
+        flags = ATTN_DETERMINISTIC if deterministic else 0
+        if lens_q.size and not np.any(lens_q == 1):
+            flags |= ATTN_NO_DECODE_ROWS
+        prep = cls(block_table=pack_block_tables(batch, device),
                    seqlens_q=cu_seqlens(batch.cu_seqlens_q, device),
                    seqlens_k=cu_seqlens(batch.cu_seqlens_k, device),
                    max_seqlen_q=int(batch.max_seqlen_q),
-                   max_seqlen_k=int(batch.max_seqlen_k))
+                   max_seqlen_k=int(batch.max_seqlen_k), flags=flags)
+        if cache is not None and num_heads is not None:
+            prep.reserve(cache, num_heads, device)
+        return prep
+
+    def reserve(self, cache, num_heads: int, device) -> None:
+        """Allocate (zeroed) the workspace the largest attention layer of
+        `cache` needs for this step."""
+        from .cache import HybridKvCache
+        b = self.seqlens_q.shape[0] - 1
+        max_q, max_k = max(self.max_seqlen_q, 1), max(self.max_seqlen_k, 1)
+        layers = ([cache.layer_view(l) for l, s in enumerate(cache.layouts) if s[0] == "kv"]
+                  if isinstance(cache, HybridKvCache) else [cache])
+        need = max(workspace_bytes(c, b, num_heads, max_q, max_k) for c in layers)
+        if need and (self.workspace is None or self.workspace.numel() < need):
+            self.workspace = torch.zeros(need, dtype=torch.uint8, device=device)
 
 
 def workspace_bytes(cache: PagedKvCache, batch: int, num_heads: int, max_q: int,
@@ -123,7 +155,9 @@ def _workspace(cache, prepared: PreparedAttention, b: int, num_heads: int, max_q
     ws = prepared.workspace
     if need and (ws is None or ws.numel() < need):
         # Zero-filled once: a zeroed workspace starts the decode from equal
-        # per-XCD shares; later calls carry the shares over.
+        # per-XCD shares; later calls carry the shares over. (A step whose
+        # layers differ in geometry sizes it up front with reserve(), so that
+        # no layer allocates mid-step or inside a captured graph.)
         ws = torch.zeros(need, dtype=torch.uint8, device=device)
         prepared.workspace = ws
     return need, ws
@@ -151,12 +185,12 @@ def paged_attention_prepared(q: torch.Tensor, cache: PagedKvCache, layer: int,
     max_q = max(int(prepared.max_seqlen_q), 1)
     max_k = max(int(prepared.max_seqlen_k), 1)
     need, ws = _workspace(cache, prepared, b, num_heads, max_q, max_k, q.device)
-    check(lib().vapi_paged_attention(
+    check(lib().vapi_paged_attention_ex(
         cache.pool, layer, q.data_ptr(), out.data_ptr(), prepared.seqlens_q.data_ptr(),
         prepared.seqlens_k.data_ptr(), prepared.block_table.data_ptr(), b,
         prepared.block_table.shape[1], max_q, max_k, num_heads, float(softmax_scale),
         -1 if window_size_left is None else int(window_size_left),
-        -1 if window_size_right is None else int(window_size_right),
+        -1 if window_size_right is None else int(window_size_right), prepared.flags,
         ws.data_ptr() if need else None, need, stream_handle(stream)))
     return out
 
@@ -213,12 +247,12 @@ def paged_attention_append_prepared(q: torch.Tensor, k: torch.Tensor, v: torch.T
     max_q = max(int(prepared.max_seqlen_q), 1)
     max_k = max(int(prepared.max_seqlen_k), 1)
     need, ws = _workspace(cache, prepared, b, num_heads, max_q, max_k, q.device)
-    check(lib().vapi_paged_attention_append(
+    check(lib().vapi_paged_attention_append_ex(
         cache.pool, layer, k.data_ptr(), v.data_ptr(), slot_mapping.data_ptr(), k.shape[0],
         q.data_ptr(), out.data_ptr(), prepared.seqlens_q.data_ptr(),
         prepared.seqlens_k.data_ptr(), prepared.block_table.data_ptr(), b,
         prepared.block_table.shape[1], max_q, max_k, num_heads, float(softmax_scale),
         -1 if window_size_left is None else int(window_size_left),
-        -1 if window_size_right is None else int(window_size_right),
+        -1 if window_size_right is None else int(window_size_right), prepared.flags,
         ws.data_ptr() if need else None, need, stream_handle(stream)))
     return out

@@ -38,7 +38,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
                                 uint32_t max_seqlen_k, uint32_t num_heads, float scale,
                                 int32_t window_left, int32_t window_right, void* workspace,
                                 size_t workspace_bytes, vapi_stream_t stream,
-                                const NewRows* fuse);
+                                const NewRows* fuse, uint32_t flags);
 
 extern "C" {
 
@@ -65,10 +65,23 @@ int vapi_paged_attention(const vapi_kv_pool* pool, uint32_t layer,
                          int32_t window_left, int32_t window_right,
                          void* workspace, size_t workspace_bytes,
                          vapi_stream_t stream) {
+  return vapi_paged_attention_ex(pool, layer, q, out, cu_seqlens_q, cu_seqlens_k, block_table,
+                                 batch, max_blocks, max_seqlen_q, max_seqlen_k, num_heads, scale,
+                                 window_left, window_right, 0u, workspace, workspace_bytes,
+                                 stream);
+}
+
+int vapi_paged_attention_ex(const vapi_kv_pool* pool, uint32_t layer, const void* q, void* out,
+                            const uint32_t* cu_seqlens_q, const uint32_t* cu_seqlens_k,
+                            const uint32_t* block_table, uint32_t batch, uint32_t max_blocks,
+                            uint32_t max_seqlen_q, uint32_t max_seqlen_k, uint32_t num_heads,
+                            float scale, int32_t window_left, int32_t window_right,
+                            uint32_t flags, void* workspace, size_t workspace_bytes,
+                            vapi_stream_t stream) {
   return paged_attention_impl(pool, layer, q, out, cu_seqlens_q, cu_seqlens_k, block_table,
                               batch, max_blocks, max_seqlen_q, max_seqlen_k, num_heads, scale,
                               window_left, window_right, workspace, workspace_bytes, stream,
-                              nullptr);
+                              nullptr, flags);
 }
 
 int vapi_paged_attention_append(const vapi_kv_pool* pool, uint32_t layer, const void* k_src,
@@ -80,6 +93,23 @@ int vapi_paged_attention_append(const vapi_kv_pool* pool, uint32_t layer, const 
                                 uint32_t max_seqlen_k, uint32_t num_heads, float scale,
                                 int32_t window_left, int32_t window_right, void* workspace,
                                 size_t workspace_bytes, vapi_stream_t stream) {
+  return vapi_paged_attention_append_ex(pool, layer, k_src, v_src, slot_mapping, n_tokens, q,
+                                        out, cu_seqlens_q, cu_seqlens_k, block_table, batch,
+                                        max_blocks, max_seqlen_q, max_seqlen_k, num_heads, scale,
+                                        window_left, window_right, 0u, workspace,
+                                        workspace_bytes, stream);
+}
+
+int vapi_paged_attention_append_ex(const vapi_kv_pool* pool, uint32_t layer, const void* k_src,
+                                   const void* v_src, const uint32_t* slot_mapping,
+                                   uint32_t n_tokens, const void* q, void* out,
+                                   const uint32_t* cu_seqlens_q, const uint32_t* cu_seqlens_k,
+                                   const uint32_t* block_table, uint32_t batch,
+                                   uint32_t max_blocks, uint32_t max_seqlen_q,
+                                   uint32_t max_seqlen_k, uint32_t num_heads, float scale,
+                                   int32_t window_left, int32_t window_right, uint32_t flags,
+                                   void* workspace, size_t workspace_bytes,
+                                   vapi_stream_t stream) {
   if (int rc = check_pool(pool, "vapi_paged_attention_append")) return rc;
   if (!pool->v) VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention_append: a K-only pool has no V to attend over");
   const bool fused = n_tokens > 0 && batch > 0 && max_seqlen_q == 1 && num_heads > 0 &&
@@ -87,9 +117,10 @@ int vapi_paged_attention_append(const vapi_kv_pool* pool, uint32_t layer, const 
   if (!fused) {
     if (int rc = vapi_kv_append(pool, layer, k_src, v_src, slot_mapping, n_tokens, stream))
       return rc;
-    return vapi_paged_attention(pool, layer, q, out, cu_seqlens_q, cu_seqlens_k, block_table,
-                                batch, max_blocks, max_seqlen_q, max_seqlen_k, num_heads, scale,
-                                window_left, window_right, workspace, workspace_bytes, stream);
+    return vapi_paged_attention_ex(pool, layer, q, out, cu_seqlens_q, cu_seqlens_k, block_table,
+                                   batch, max_blocks, max_seqlen_q, max_seqlen_k, num_heads,
+                                   scale, window_left, window_right, flags, workspace,
+                                   workspace_bytes, stream);
   }
   if (!k_src || !v_src || !slot_mapping)
     VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention_append: null source or slot_mapping");
@@ -97,7 +128,7 @@ int vapi_paged_attention_append(const vapi_kv_pool* pool, uint32_t layer, const 
   return paged_attention_impl(pool, layer, q, out, cu_seqlens_q, cu_seqlens_k, block_table,
                               batch, max_blocks, max_seqlen_q, max_seqlen_k, num_heads, scale,
                               window_left, window_right, workspace, workspace_bytes, stream,
-                              &rows);
+                              &rows, flags);
 }
 
 }  // extern "C"
@@ -109,7 +140,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
                                 uint32_t max_seqlen_k, uint32_t num_heads, float scale,
                                 int32_t window_left, int32_t window_right, void* workspace,
                                 size_t workspace_bytes, vapi_stream_t stream,
-                                const NewRows* fuse) {
+                                const NewRows* fuse, uint32_t flags) {
   if (int rc = check_pool(pool, "vapi_paged_attention")) return rc;
   if (!pool->v) VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: a K-only pool has no V to attend over");
   if (layer >= pool->num_layers)
@@ -126,11 +157,23 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
     VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: keys to attend over in an empty pool");
   if (max_blocks == 0)
     VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: block table width 0");
+  if (flags & ~(uint32_t)(VAPI_ATTN_DETERMINISTIC | VAPI_ATTN_NO_DECODE_ROWS))
+    VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: unknown flags 0x%x", flags);
   if (num_heads > 65535 || (batch > 65535 && !mfma_ok(pool, num_heads)))
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: batch %u / heads %u too large",
             batch, num_heads);
-  const size_t need = vapi_paged_attention_workspace_size(pool, batch, num_heads,
-                                                          max_seqlen_q, max_seqlen_k);
+  // Refused before anything is launched (a refused call writes nothing).
+  if (mfma_ok(pool, num_heads) && max_seqlen_q > 1 && batch > 65535)
+    VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: %u prefill sequences > 65535", batch);
+  // A batch the caller says has no decode rows (and which is not a fused
+  // decode step) runs one kernel: the prefill kernel then takes every row,
+  // len_q == 1 included, so the result does not depend on the hint. It needs
+  // no workspace.
+  const bool skip_decode = (flags & VAPI_ATTN_NO_DECODE_ROWS) && !fuse && max_seqlen_q > 1 &&
+                           mfma_ok(pool, num_heads);
+  const size_t need = skip_decode ? 0
+                                  : vapi_paged_attention_workspace_size(pool, batch, num_heads,
+                                                                        max_seqlen_q, max_seqlen_k);
   if (workspace_bytes < need || (need && !workspace))
     VK_FAIL(VAPI_KV_ESPACE, "vapi_paged_attention: workspace %zu bytes < %zu",
             workspace_bytes, need);
@@ -174,17 +217,16 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   a.q_sign = scale < 0.f ? 0x80008000u : 0u;
   a.wl = window_left < 0 ? -1 : window_left;
   a.wr = window_right < 0 ? -1 : window_right;
+  a.deterministic = (flags & VAPI_ATTN_DETERMINISTIC) ? 1u : 0u;
+  a.pf_min_q = 2;
   const hipStream_t s = hs(stream);
 
   if (mfma_ok(pool, num_heads)) {
     const bool bf16 = pool->dtype == VAPI_KV_BF16;
     a.num_waves = decode_num_waves();
-    launch_decode(a, workspace, g.d, bf16, s);
-    if (max_seqlen_q > 1) {
-      if (batch > 65535)
-        VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: %u prefill sequences > 65535", batch);
-      launch_prefill(a, max_seqlen_q, g.d, bf16, s);
-    }
+    if (skip_decode) a.pf_min_q = 1;
+    else launch_decode(a, workspace, g.d, bf16, s);
+    if (max_seqlen_q > 1) launch_prefill(a, max_seqlen_q, g.d, bf16, s);
   } else {
     if (g.d > 256)
       VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: head_dim %u > 256", g.d);

@@ -65,6 +65,8 @@ struct AttnArgs {
   float scale;
   uint32_t q_sign;     // 0x80008000 when scale < 0: XOR into packed 16-bit Q words
   int32_t wl, wr;
+  uint32_t deterministic;  // decode: fixed equal XCD shares, no share update
+  uint32_t pf_min_q;       // prefill: rows with len_q >= this (2, or 1 when no decode launch)
 };
 
 __device__ __forceinline__ void key_range(int32_t p, int32_t len_k, int32_t wl,

@@ -77,7 +77,7 @@ __device__ __forceinline__ uint32_t group_offset(uint32_t nwg, uint32_t x) {
 // The shares of this launch: 8 positive f32, uniform when the workspace
 // holds none yet (all zero) or anything unusable; 0 for groups without waves.
 __device__ __forceinline__ void load_shares(const AttnArgs& a, uint32_t nwg, float (&w)[kGroups]) {
-  bool ok = true;
+  bool ok = !a.deterministic;
 #pragma unroll
   for (uint32_t x = 0; x < kGroups; ++x) {
     w[x] = __uint_as_float(a.bal[x]);
@@ -253,7 +253,10 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
         if (ns) {
           const uint32_t q0 = cu_q[s], last = cu_k[s + 1] - cu_k[s] - 1;
           const uint32_t slot = q0 < a.n_new ? a.slots[q0] : 0xFFFFFFFFu;
-          const uint32_t blk = table[(uint64_t)s * a.max_blocks + (last >> a.bs_shift)];
+          // Column clamped like every other table read: len_k past the row's
+          // max_blocks * block_size reads the row's last entry.
+          const uint32_t blk =
+              table[(uint64_t)s * a.max_blocks + min(last >> a.bs_shift, a.max_blocks - 1)];
           f = slot < a.num_slots && slot == blk * a.block_size + (last & (a.block_size - 1));
         }
         FZ[s] = f;
@@ -465,7 +468,7 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_merge(AttnArgs 
   const uint32_t segi =
       blockIdx.x * kMergeWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (segi == nseg) {
-    update_shares(a, nwg, lane);
+    if (!a.deterministic) update_shares(a, nwg, lane);
     return;
   }
   if (segi > nseg) return;

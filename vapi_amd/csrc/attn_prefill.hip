@@ -11,7 +11,8 @@
 // operand scheme (S^T = K Q^T, online softmax, O^T += V^T P^T) with the
 // bottom-right causal mask and left window per row, applied only on steps
 // that some row of the workgroup cannot fully see. Rows with len_q < 2 are
-// left to the decode kernel.
+// left to the decode kernel, unless the call launches no decode kernel (the
+// caller said the batch has no decode rows): then every row is done here.
 #include <type_traits>
 
 #include "attn_common.hpp"
@@ -158,7 +159,7 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
   const uint32_t kh = rest % a.kvh, seq = rest / a.kvh;
   const uint32_t q0 = cu_q[seq];
   const uint32_t len_q = cu_q[seq + 1] - q0;
-  if (len_q < 2) return;
+  if (len_q < a.pf_min_q || len_q == 0) return;
   const uint32_t G = a.group;
   const uint32_t nrows = len_q * G;
   const uint32_t row_base = qt * kPfRows;

@@ -47,6 +47,13 @@ int check_pool(const vapi_kv_pool* p, const char* who) {
             (unsigned long long)p->layer_stride_bytes,
             (unsigned long long)layer_bytes);
   if (p->num_blocks > 0 && !p->k) VK_FAIL(VAPI_KV_EINVAL, "%s: null K base pointer", who);
+  // Every kernel moves 16-byte chunks of rows that start at these bases
+  // (the attention kernels load 16 bytes per lane, also into LDS).
+  if (((uintptr_t)p->k | (uintptr_t)p->v) & 15)
+    VK_FAIL(VAPI_KV_EINVAL, "%s: K/V base pointers must be 16-byte aligned", who);
+  if (p->num_layers > 1 && (p->layer_stride_bytes & 15))
+    VK_FAIL(VAPI_KV_EINVAL, "%s: layer stride %llu is not a multiple of 16 bytes", who,
+            (unsigned long long)p->layer_stride_bytes);
   // Further layer groups of the same cache (block-level calls walk them):
   // each is a pool of its own, on the same blocks.
   uint32_t links = 0;
