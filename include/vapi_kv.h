@@ -234,6 +234,30 @@ int vapi_paged_attention_ex(const vapi_kv_pool* pool, uint32_t layer, const void
                             vapi_stream_t stream);
 
 /*
+ * vapi_paged_attention_ex without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. The decode workspace is the library's own device array of
+ * VAPI_ATTN_SCRATCH_BYTES bytes, one per GPU, held until the process ends;
+ * the call allocates nothing. A batch whose workspace
+ * (vapi_paged_attention_workspace_size) exceeds it is refused with
+ * VAPI_KV_ESPACE before anything is launched. Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (different streams not
+ * ordered against each other) race and must not be issued. The first call
+ * on a device resolves the array's address and clears its XCD shares with a
+ * small kernel on `stream`; later calls carry the shares over, as a kept
+ * workspace does.
+ */
+#define VAPI_ATTN_SCRATCH_BYTES (16u << 20)
+int vapi_paged_attention_noalloc(const vapi_kv_pool* pool, uint32_t layer, const void* q,
+                                 void* out, const uint32_t* cu_seqlens_q,
+                                 const uint32_t* cu_seqlens_k, const uint32_t* block_table,
+                                 uint32_t batch, uint32_t max_blocks, uint32_t max_seqlen_q,
+                                 uint32_t max_seqlen_k, uint32_t num_heads, float scale,
+                                 int32_t window_left, int32_t window_right, uint32_t flags,
+                                 vapi_stream_t stream);
+
+/*
  * One decode step's K/V append and paged attention in one call: the result
  * is that of vapi_kv_append(k_src, v_src, slot_mapping, n_tokens) followed
  * by vapi_paged_attention(...) with the same arguments. It fuses the

@@ -17,6 +17,7 @@ SLOT_SKIP = 0xFFFFFFFF
 
 OK, EINVAL, EUNSUP, EHIP, ESPACE = 0, -1, -2, -3, -4
 ATTN_DETERMINISTIC, ATTN_NO_DECODE_ROWS = 0x1, 0x2
+ATTN_SCRATCH_BYTES = 16 << 20  # VAPI_ATTN_SCRATCH_BYTES
 
 # Every symbol include/vapi_kv.h declares.
 EXPORTS = (
@@ -34,6 +35,7 @@ EXPORTS = (
     "vapi_spill_get", "vapi_spill_get_stats", "vapi_spill_evicted", "vapi_spill_promote",
     "vapi_spill_evicted_async", "vapi_spill_drain",
     "vapi_paged_attention_ex", "vapi_paged_attention_append_ex",
+    "vapi_paged_attention_noalloc",
 )
 
 
@@ -108,6 +110,9 @@ def lib():
     L.vapi_paged_attention_append_ex.argtypes = [
         _poolp, _u32, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
         _u32, ctypes.c_float, _i32, _i32, _u32, _vp, _sz, _vp]
+    L.vapi_paged_attention_noalloc.argtypes = [
+        _poolp, _u32, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,
+        ctypes.c_float, _i32, _i32, _u32, _vp]
     L.vapi_kv_append_layers.argtypes = [_poolp, _u32, _u32, _vp, _vp, ctypes.c_uint64, _vp,
                                          _u32, _vp]
     L.vapi_kv_copy_blocks.argtypes = [_poolp, _vp, _u32, _vp]

@@ -7,6 +7,8 @@
 // (f32 pools included) runs the VALU kernel (attn_generic.hip).
 // Replaces paged_attention_cuda/_windowed/_prepared (vapi
 // crates/vapi-backend-candle/src/attention.rs:170-288).
+#include <mutex>
+
 #include "attn_common.hpp"
 
 namespace vk {
@@ -26,6 +28,51 @@ struct NewRows {
   const uint32_t* slots;
   uint32_t n;
 };
+
+// ---- allocation-free variant: the decode workspace in a device array ------
+//
+// `scratch` is this library's own copy of the decode workspace (XCD shares,
+// per-segment ranges, split partials) for callers that cannot allocate.
+// Every GPU the library runs on holds one copy, at its own address, until
+// the process ends. The host uses `scratch` only through the address
+// hipGetSymbolAddress returns on that device: in host code the array's name
+// is a host-side stand-in, not device memory.
+static __device__ __align__(256) unsigned char scratch[VAPI_ATTN_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];  // per device, set once
+
+// Zeroes the balance block at the start of the scratch (the shares a fresh
+// workspace starts from). A kernel, not hipMemsetAsync, so that a call
+// recorded into a HIP graph replays it correctly.
+__global__ void scratch_clear_kernel(uint32_t* p, uint32_t n_words) {
+  for (uint32_t i = threadIdx.x; i < n_words; i += blockDim.x) p[i] = 0u;
+}
+
+// The current device's scratch address; resolved (and its balance block
+// cleared on `stream`) by the first call on each device.
+static int scratch_for_device(void** out, hipStream_t stream) {
+  int dev = 0;
+  VK_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices)
+    VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention_noalloc: device %d of at most %d", dev,
+            kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      VK_FAIL(VAPI_KV_EHIP, "vapi_paged_attention_noalloc: hipGetSymbolAddress(scratch): %s",
+              hipGetErrorString(e));
+    hipLaunchKernelGGL(scratch_clear_kernel, dim3(1), dim3(256), 0, stream, (uint32_t*)ptr,
+                       (uint32_t)(kDecodeBalanceBytes / sizeof(uint32_t)));
+    VK_LAUNCHED("scratch_clear_kernel");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
 
 }  // namespace vk
 
@@ -129,6 +176,31 @@ int vapi_paged_attention_append_ex(const vapi_kv_pool* pool, uint32_t layer, con
                               batch, max_blocks, max_seqlen_q, max_seqlen_k, num_heads, scale,
                               window_left, window_right, workspace, workspace_bytes, stream,
                               &rows, flags);
+}
+
+int vapi_paged_attention_noalloc(const vapi_kv_pool* pool, uint32_t layer, const void* q,
+                                 void* out, const uint32_t* cu_seqlens_q,
+                                 const uint32_t* cu_seqlens_k, const uint32_t* block_table,
+                                 uint32_t batch, uint32_t max_blocks, uint32_t max_seqlen_q,
+                                 uint32_t max_seqlen_k, uint32_t num_heads, float scale,
+                                 int32_t window_left, int32_t window_right, uint32_t flags,
+                                 vapi_stream_t stream) {
+  if (int rc = check_pool(pool, "vapi_paged_attention_noalloc")) return rc;
+  // Sized before anything is resolved or launched: a call past the limit is
+  // refused and changes nothing.
+  const size_t need = vapi_paged_attention_workspace_size(pool, batch, num_heads, max_seqlen_q,
+                                                          max_seqlen_k);
+  if (need > VAPI_ATTN_SCRATCH_BYTES)
+    VK_FAIL(VAPI_KV_ESPACE,
+            "vapi_paged_attention_noalloc: this batch needs %zu bytes of decode workspace, more "
+            "than the library's %u-byte scratch (use vapi_paged_attention_ex with a workspace)",
+            need, (unsigned)VAPI_ATTN_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (int rc = scratch_for_device(&ws, hs(stream))) return rc;
+  return paged_attention_impl(pool, layer, q, out, cu_seqlens_q, cu_seqlens_k, block_table,
+                              batch, max_blocks, max_seqlen_q, max_seqlen_k, num_heads, scale,
+                              window_left, window_right, ws, VAPI_ATTN_SCRATCH_BYTES, stream,
+                              nullptr, flags);
 }
 
 }  // extern "C"

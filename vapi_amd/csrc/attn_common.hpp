@@ -423,5 +423,8 @@ void launch_generic(const AttnArgs& a, uint32_t max_q, uint32_t head_dim,
                     uint32_t dtype, hipStream_t s);
 // Persistent decode waves for the current device (CUs x 8).
 uint32_t decode_num_waves();
+// Bytes at the start of a decode workspace that carry over between calls
+// (the balance block: XCD shares and per-wave timings); zero = equal shares.
+extern const size_t kDecodeBalanceBytes;
 
 }  // namespace vk

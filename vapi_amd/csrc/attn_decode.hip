@@ -554,6 +554,10 @@ uint32_t decode_num_waves() {
 
 static size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// The words before the per-wave timings: the shares (words 0..7) and
+// reserved words. Only these carry over between launches.
+const size_t kDecodeBalanceBytes = kBalStats * sizeof(uint32_t);
+
 // Workspace: the balance block (shares and per-wave timings; the shares
 // carry over between launches, so the block leads the workspace whatever
 // the batch), the first and last range of every segment, and the partials:
