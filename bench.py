@@ -221,6 +221,24 @@ def bench_append(steps, warmup):
     gbs = alg / (ms * 1e-3) / 1e9
     log(f"append cfg1: {alg / 1e6:.1f} MB, {ms * 1e3:.2f} us/append in a graph "
         f"({gbs:.0f} GB/s), {ms_host * 1e3:.1f} us/append host-launched")
+    # Cold sources: the graph's appends rotate over 24 source sets (384 MB,
+    # more than the 256 MB last-level cache), as a fresh layer's K/V rows
+    # would arrive, so the reads come from HBM.
+    n_sets = 24
+    ks = torch.randn(n_sets, w.n_tokens, 8, 128, generator=g, device=DEV).to(torch.bfloat16)
+    vs = torch.randn_like(ks)
+    it = [0]
+
+    def append_cold():
+        i = it[0] % n_sets
+        it[0] += 1
+        write_rows_indexed(cache, 0, ks[i], vs[i], idx)
+
+    ms_cold = timed_graph(append_cold, max(steps, n_sets), warmup)
+    gbs_cold = alg / (ms_cold * 1e-3) / 1e9
+    log(f"append cfg1, sources rotated over {n_sets} sets: {ms_cold * 1e3:.2f} us/append "
+        f"({gbs_cold:.0f} GB/s)")
+    del ks, vs
     del cache
     # The same step's rows for 4 layers in one launch (vapi_kv_append_layers).
     L = 4
@@ -234,6 +252,7 @@ def bench_append(steps, warmup):
         f"({ms_l * 1e3 / L:.2f} us/layer, {gbs_l:.0f} GB/s)")
     del cache, kl, vl
     return dict(us=ms * 1e3, gbs=gbs, frac=gbs / HBM_PEAK_GBS, bytes=alg,
+                cold_us=ms_cold * 1e3, cold_gbs=gbs_cold, cold_frac=gbs_cold / HBM_PEAK_GBS,
                 us_host_launched=ms_host * 1e3,
                 gbs_host_launched=alg / (ms_host * 1e-3) / 1e9,
                 layers4_one_launch_us=ms_l * 1e3, layers4_gbs=gbs_l)
@@ -301,6 +320,7 @@ def bench_blocks(steps, warmup, decode):
     src = torch.from_numpy(w.pairs[:, 0].astype(np.int64)).to(DEV)
     dst = torch.from_numpy(w.pairs[:, 1].astype(np.int64)).to(DEV)
     copy_ok = all(torch.equal(t[src], t[dst]) for t in cache.k + cache.v)
+    copy_probes = probes_copy(w, cache)
 
     # Swap: 4,096 blocks out to pinned host and back into other blocks.
     n = len(w.swap_ids)
@@ -419,7 +439,9 @@ def bench_blocks(steps, warmup, decode):
     store.close()
     del pin, pin_all, staging
     res = dict(copy_ms=ms, copy_gbs=copy_gbs, copy_frac=copy_gbs / HBM_PEAK_GBS,
-               copy_bit_exact=bool(copy_ok),
+               copy_frac_of_runs_probe=copy_gbs / copy_probes["copy_runs16k_gbs"],
+               copy_frac_of_seq_copy_probe=copy_gbs / copy_probes["copy_seq_gbs"],
+               probes=copy_probes, copy_bit_exact=bool(copy_ok),
                swap_out_gbs=gb / (out_ms * 1e-3), swap_in_gbs=gb / (in_ms * 1e-3),
                swap_round_trip_bit_exact=bool(swap_ok),
                swap_out_overlapped_gbs=gb / (overlap_out_ms * 1e-3),
@@ -455,11 +477,122 @@ def _copy_on(stream, dst, src):
         dst.copy_(src, non_blocking=True)
 
 
-def hbm_probe():
-    a = torch.empty(4 << 30, dtype=torch.uint8, device=DEV)
+# ---- HBM ceiling probes (libvapi_probe.so) ---------------------------------------
+
+_PROBE = None
+
+
+def probe_lib():
+    """The benchmark's probe kernels (vapi_amd/csrc/probes.hip), built by
+    vapi_amd.build next to libvapi_kv.so."""
+    global _PROBE
+    if _PROBE is None:
+        import ctypes
+        path = ROOT / "vapi_amd" / "libvapi_probe.so"
+        if not path.exists():
+            raise ImportError(f"{path} is missing: build with `python -m vapi_amd.build`")
+        L = ctypes.CDLL(str(path))
+        vp, u32, u64 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64
+        L.vapi_probe_read.argtypes = [vp, u64, vp, vp]
+        L.vapi_probe_read_tiles.argtypes = [vp, vp, u32, u32, vp, vp]
+        L.vapi_probe_copy.argtypes = [vp, vp, u64, vp]
+        L.vapi_probe_copy_runs.argtypes = [vp, vp, u32, u32, vp]
+        _PROBE = L
+    return _PROBE
+
+
+def _probe_time(fn, reps=20, warmup=3):
+    ms, _ = timed(lambda: _chk_probe(fn()), reps, warmup)
+    return ms
+
+
+def _chk_probe(rc):
+    if rc != 0:
+        raise RuntimeError(f"probe launch failed ({rc})")
+
+
+def decode_tiles(d):
+    """The 4 KiB K and V tiles config 2's decode reads, as tile indices of
+    its pool slab, in the decode's order (sequence, kv head, block, K/V)."""
+    w, cache = d["w"], d["cache"]
+    tile = w.block_size * w.head_dim * 2
+    k0 = cache.pool.k
+    v_off = (cache.pool.v - k0) // tile
+    ids = []
+    for t, l in zip(w.tables, w.lens):
+        blocks = np.asarray(t[: -(-int(l) // w.block_size)], dtype=np.int64)
+        for h in range(w.num_kv_heads):
+            kt = blocks * w.num_kv_heads + h
+            ids.append(np.stack([kt, kt + v_off], 1).reshape(-1))
+    return np.concatenate(ids).astype(np.uint32), k0, tile
+
+
+def probes_decode(dec):
+    """Ceilings for the decode, measured on this box on its access pattern
+    (same bytes, same granularity; GB/s of bytes read):
+      read_seq:     a sequential read of the decode's K/V byte count;
+      read_tiles4k: the decode's own 4 KiB K/V tiles of config 2's pool, in
+                    its order (the decode kernel's reads without its math);
+      read_runs8k:  the same bytes as random 8 KiB runs of the pool."""
+    from vapi_amd.cache import stream_handle
+    L, sh = probe_lib(), stream_handle()
+    sink = torch.zeros(1024, dtype=torch.int32, device=DEV)
+    out = {}
+    ids, base, tile = decode_tiles(dec)
+    nbytes = int(ids.size) * tile
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    ms = _probe_time(lambda: L.vapi_probe_read(buf.data_ptr(), nbytes, sink.data_ptr(), sh))
+    out["read_seq_gbs"] = nbytes / (ms * 1e-3) / 1e9
+    del buf
+    dids = torch.from_numpy(ids.view(np.int32)).to(DEV)
+    ms = _probe_time(lambda: L.vapi_probe_read_tiles(base, dids.data_ptr(), ids.size, 4096,
+                                                      sink.data_ptr(), sh))
+    out["read_tiles4k_gbs"] = nbytes / (ms * 1e-3) / 1e9
+    slab_bytes = dec["cache"]._slab.numel() * 2
+    n8 = nbytes // 8192
+    r8 = np.random.default_rng(8).permutation(slab_bytes // 8192)[:n8].astype(np.uint32)
+    d8 = torch.from_numpy(r8.view(np.int32)).to(DEV)
+    ms = _probe_time(lambda: L.vapi_probe_read_tiles(base, d8.data_ptr(), n8, 8192,
+                                                      sink.data_ptr(), sh))
+    out["read_runs8k_gbs"] = n8 * 8192 / (ms * 1e-3) / 1e9
+    out["decode_kv_bytes"] = nbytes
+    log("probes (decode): " + ", ".join(f"{k} {v:.0f}" for k, v in out.items()
+                                        if k.endswith("gbs")))
+    return out
+
+
+def probes_copy(w, cache):
+    """Ceilings for the block copy (GB/s of bytes read + written):
+      copy_runs16k: config 4a's own (src, dst) 16 KiB runs over its pool,
+                    every layer, K and V (the block copy's pattern);
+      copy_seq:     a sequential device copy of the same byte count."""
+    from vapi_amd.cache import stream_handle
+    L, sh = probe_lib(), stream_handle()
+    out = {}
+    run = w.block_size * w.num_kv_heads * w.head_dim * 2
+    kbase = cache.pool.k
+    lstride = cache.pool.layer_stride_bytes // run
+    voff = (cache.pool.v - kbase) // run
+    pr = []
+    for l in range(w.num_layers):
+        for off in (0, voff):
+            pr.append(np.stack([w.pairs[:, 0].astype(np.int64) + l * lstride + off,
+                                w.pairs[:, 1].astype(np.int64) + l * lstride + off], 1))
+    pr = np.concatenate(pr).astype(np.uint32)
+    dpr = torch.from_numpy(pr.reshape(-1).view(np.int32)).to(DEV)
+    cbytes = pr.shape[0] * run
+    ms = _probe_time(lambda: L.vapi_probe_copy_runs(kbase, dpr.data_ptr(), pr.shape[0], run, sh),
+                     reps=10)
+    out["copy_runs16k_gbs"] = 2 * cbytes / (ms * 1e-3) / 1e9
+    a = torch.empty(cbytes, dtype=torch.uint8, device=DEV)
     b = torch.empty_like(a)
-    ms, _ = timed(lambda: b.copy_(a), 10, 3)
-    return 2 * a.numel() / (ms * 1e-3) / 1e9
+    ms = _probe_time(lambda: L.vapi_probe_copy(b.data_ptr(), a.data_ptr(), cbytes, sh), reps=10)
+    out["copy_seq_gbs"] = 2 * cbytes / (ms * 1e-3) / 1e9
+    out["copy_bytes_each_way"] = cbytes
+    del a, b
+    log("probes (copy): " + ", ".join(f"{k} {v:.0f}" for k, v in out.items()
+                                      if k.endswith("gbs")))
+    return out
 
 
 # ---- CPU baseline ------------------------------------------------------------------
@@ -478,7 +611,8 @@ def cpu_baseline(decode, budget_s=12.0):
     vc = cache.reference_view(0, "v")[idx].float().cpu().numpy()
     tables = [[remap[int(b)] for b in t] for t in w.tables]
     q = decode["q"].float().cpu().numpy()
-    threads = min(len(os.sched_getaffinity(0)), 16)
+    # Every core this process may run on (the box's share of the host).
+    threads = len(os.sched_getaffinity(0))
     cu_q, cu_k = w.cu_q(), w.cu_k()
     reps, t0 = 0, time.perf_counter()
     while True:
@@ -489,7 +623,7 @@ def cpu_baseline(decode, budget_s=12.0):
     sec = (time.perf_counter() - t0) / reps
     gbs = decode["alg_bytes"] / sec / 1e9
     log(f"cpu baseline: {sec * 1e3:.1f} ms per config-2 step on {threads} threads, {gbs:.2f} GB/s")
-    return dict(value=gbs, unit="GB/s", cores=threads, kind="port",
+    return dict(value=gbs, unit="GB/s", cores=threads, nproc=os.cpu_count(), kind="port",
                 sample=f"full config-2 decode batch (64 seqs, sum_len {w.lens.sum()}), "
                        f"{reps} passes, C oracle with OpenMP over sequences, f32 math on "
                        f"bf16-valued K/V", ms_per_step=sec * 1e3)
@@ -616,7 +750,10 @@ def main():
     extras["blocks_cfg4"] = bench_blocks(max(args.steps // 5, 3), 2, dec)
     if args.only == "blocks":
         return
-    extras["hbm_copy_probe_gbs"] = hbm_probe()
+    pd = probes_decode(dec)
+    extras["probes_decode"] = dict(
+        pd, decode_call_frac_of_tiles4k=dec["graph_gbs"] / pd["read_tiles4k_gbs"],
+        decode_call_frac_of_read_seq=dec["graph_gbs"] / pd["read_seq_gbs"])
     traffic = load_traffic()
     cpu = None if args.no_cpu else cpu_baseline(dec)
     if not args.no_cpu:
@@ -643,6 +780,10 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(dec["graph_gbs"], 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dec["graph_gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": traffic.get("bytes_per_call") if traffic else None,
+                     "traffic_source": ("profiles/paged_decode_config2_traffic.json: FETCH_SIZE "
+                                        "and WRITE_SIZE of a rocprofv3 --pmc run of this call, "
+                                        "calibrated on a copy of known size; read from the "
+                                        "committed file, not measured in this run"),
                      "kernel": "paged_decode_stream + paged_decode_merge (one vapi_paged_attention call)"},
         "cpu_baseline": cpu,
         "kv_append_gbs": round(extras["append_cfg1"]["gbs"], 1) if "append_cfg1" in extras else None,

@@ -18,6 +18,9 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 ROOT = HERE.parent
 LIB = HERE / "libvapi_kv.so"
+# The benchmark's HBM ceiling probes, outside the product library.
+PROBE_LIB = HERE / "libvapi_probe.so"
+PROBE_SOURCES = ["probes.hip"]
 OBJ_DIR = HERE / "_build"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -78,26 +81,28 @@ def _compile(src: Path, obj: Path) -> None:
     _check_no_scratch(src, res.stderr)
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every source and link libvapi_kv.so. Always rebuilds."""
-    OBJ_DIR.mkdir(exist_ok=True)
-    jobs = []
-    for name in SOURCES:
-        src = CSRC / name
-        obj = OBJ_DIR / (src.stem + ".o")
-        jobs.append((src, obj))
-    with ThreadPoolExecutor(max_workers=min(len(jobs), 4)) as ex:
-        list(ex.map(lambda j: _compile(*j), jobs))
-    tmp = LIB.with_suffix(".so.tmp")
+def _link(objs, out: Path) -> None:
+    tmp = out.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
-           *[str(o) for _, o in jobs]]
+           *[str(o) for o in objs]]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError("link of libvapi_kv.so failed")
-    os.replace(tmp, LIB)
+        raise RuntimeError(f"link of {out.name} failed")
+    os.replace(tmp, out)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every source and link libvapi_kv.so (and the benchmark's
+    libvapi_probe.so). Always rebuilds."""
+    OBJ_DIR.mkdir(exist_ok=True)
+    jobs = [(CSRC / n, OBJ_DIR / (Path(n).stem + ".o")) for n in SOURCES + PROBE_SOURCES]
+    with ThreadPoolExecutor(max_workers=min(len(jobs), 4)) as ex:
+        list(ex.map(lambda j: _compile(*j), jobs))
+    _link([o for s, o in jobs if s.name in SOURCES], LIB)
+    _link([o for s, o in jobs if s.name in PROBE_SOURCES], PROBE_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {PROBE_LIB}")
     return LIB
 
 

@@ -1,0 +1,145 @@
+// HBM ceiling probes for the benchmark (libvapi_probe.so, not part of the
+// product library): what this GPU's memory system delivers for the access
+// patterns of the paged-KV kernels, measured in the same run as the kernels
+// they bound.
+//
+//  * vapi_probe_read:       sequential read of a buffer (every byte once).
+//  * vapi_probe_read_tiles: reads of `tile_bytes` runs at given tile indices
+//                           (the decode's 4 KiB K or V tile of one (block,
+//                           head), or an 8 KiB run).
+//  * vapi_probe_copy:       sequential device-to-device copy.
+//  * vapi_probe_copy_runs:  copies of `run_bytes` runs between given run
+//                           indices (the block copy's 16 KiB (block, layer,
+//                           K or V) run).
+//
+// Each lane moves 16-byte chunks with all of its loads issued before any use;
+// reads fold their data into one word per workgroup so they cannot be
+// dropped. Grids are large (>> 256 workgroups) and one-shot.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 8;  // 16-byte loads in flight per lane
+
+__global__ __launch_bounds__(kThreads) void probe_read_kernel(const uint4* __restrict__ src,
+                                                              uint64_t n16,
+                                                              uint32_t* __restrict__ sink) {
+  const uint64_t base = (uint64_t)blockIdx.x * kThreads * kUnroll + threadIdx.x;
+  uint4 v[kUnroll];
+#pragma unroll
+  for (int i = 0; i < kUnroll; ++i) {
+    const uint64_t j = base + (uint64_t)i * kThreads;
+    v[i] = j < n16 ? src[j] : make_uint4(0, 0, 0, 0);
+  }
+  uint32_t x = 0;
+#pragma unroll
+  for (int i = 0; i < kUnroll; ++i) x ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+  // A data-dependent store no compiler can prove dead; almost never taken.
+  if (x == 0x9E3779B9u) sink[blockIdx.x & 1023] = x;
+}
+
+// One wave per tile: tile_bytes / 1024 loads of 16 B per lane.
+template <int LOADS>
+__global__ __launch_bounds__(kThreads) void probe_tiles_kernel(const char* __restrict__ base,
+                                                               const uint32_t* __restrict__ ids,
+                                                               uint32_t n_tiles,
+                                                               uint32_t* __restrict__ sink) {
+  const uint32_t wave = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63;
+  if (wave >= n_tiles) return;
+  const uint4* t = (const uint4*)(base + (uint64_t)ids[wave] * (LOADS * 1024u));
+  uint4 v[LOADS];
+#pragma unroll
+  for (int i = 0; i < LOADS; ++i) v[i] = t[i * 64 + lane];
+  uint32_t x = 0;
+#pragma unroll
+  for (int i = 0; i < LOADS; ++i) x ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+  if (x == 0x9E3779B9u) sink[wave & 1023] = x;
+}
+
+__global__ __launch_bounds__(kThreads) void probe_copy_kernel(uint4* __restrict__ dst,
+                                                              const uint4* __restrict__ src,
+                                                              uint64_t n16) {
+  const uint64_t base = (uint64_t)blockIdx.x * kThreads * kUnroll + threadIdx.x;
+  uint4 v[kUnroll];
+#pragma unroll
+  for (int i = 0; i < kUnroll; ++i) {
+    const uint64_t j = base + (uint64_t)i * kThreads;
+    if (j < n16) v[i] = src[j];
+  }
+#pragma unroll
+  for (int i = 0; i < kUnroll; ++i) {
+    const uint64_t j = base + (uint64_t)i * kThreads;
+    if (j < n16) dst[j] = v[i];
+  }
+}
+
+// One workgroup per run: run_bytes / 4096 chunks of 16 B per thread.
+template <int ITEMS>
+__global__ __launch_bounds__(kThreads) void probe_runs_kernel(char* __restrict__ base,
+                                                              const uint32_t* __restrict__ pairs,
+                                                              uint32_t n_runs) {
+  const uint32_t r = blockIdx.x;
+  if (r >= n_runs) return;
+  constexpr uint64_t kRun = ITEMS * kThreads * 16ull;
+  const uint4* s = (const uint4*)(base + (uint64_t)pairs[2 * r] * kRun);
+  uint4* d = (uint4*)(base + (uint64_t)pairs[2 * r + 1] * kRun);
+  uint4 v[ITEMS];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) v[i] = s[i * kThreads + threadIdx.x];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) d[i * kThreads + threadIdx.x] = v[i];
+}
+
+}  // namespace
+
+extern "C" {
+
+// Sequential read of `bytes` (a multiple of 16) at src. sink: device
+// u32[1024] (written only by a sentinel the data never hits).
+int vapi_probe_read(const void* src, uint64_t bytes, void* sink, hipStream_t stream) {
+  const uint64_t n16 = bytes / 16;
+  const uint64_t grid = (n16 + kThreads * kUnroll - 1) / (kThreads * kUnroll);
+  hipLaunchKernelGGL(probe_read_kernel, dim3((uint32_t)grid), dim3(kThreads), 0, stream,
+                     (const uint4*)src, n16, (uint32_t*)sink);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+// Reads of n_tiles runs of tile_bytes (4096 or 8192) at base + ids[i] *
+// tile_bytes (ids: device u32[n_tiles]).
+int vapi_probe_read_tiles(const void* base, const uint32_t* ids, uint32_t n_tiles,
+                          uint32_t tile_bytes, void* sink, hipStream_t stream) {
+  const uint32_t grid = (n_tiles + kThreads / 64 - 1) / (kThreads / 64);
+  if (tile_bytes == 4096)
+    hipLaunchKernelGGL(probe_tiles_kernel<4>, dim3(grid), dim3(kThreads), 0, stream,
+                       (const char*)base, ids, n_tiles, (uint32_t*)sink);
+  else if (tile_bytes == 8192)
+    hipLaunchKernelGGL(probe_tiles_kernel<8>, dim3(grid), dim3(kThreads), 0, stream,
+                       (const char*)base, ids, n_tiles, (uint32_t*)sink);
+  else
+    return -1;
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+// Sequential copy of `bytes` (a multiple of 16).
+int vapi_probe_copy(void* dst, const void* src, uint64_t bytes, hipStream_t stream) {
+  const uint64_t n16 = bytes / 16;
+  const uint64_t grid = (n16 + kThreads * kUnroll - 1) / (kThreads * kUnroll);
+  hipLaunchKernelGGL(probe_copy_kernel, dim3((uint32_t)grid), dim3(kThreads), 0, stream,
+                     (uint4*)dst, (const uint4*)src, n16);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+// Copies n_runs runs of run_bytes (16384) from base + pairs[2i] * run_bytes
+// to base + pairs[2i + 1] * run_bytes (pairs: device u32[n_runs][2]).
+int vapi_probe_copy_runs(void* base, const uint32_t* pairs, uint32_t n_runs, uint32_t run_bytes,
+                         hipStream_t stream) {
+  if (run_bytes != 16384) return -1;
+  hipLaunchKernelGGL(probe_runs_kernel<4>, dim3(n_runs), dim3(kThreads), 0, stream,
+                     (char*)base, pairs, n_runs);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+}  // extern "C"
