@@ -142,12 +142,19 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
     }
 }
 
-// One chunk per thread: measured on config 1 (4,096 tokens), 1 chunk per
-// thread ran 12.3 us per call against 20.7 / 21 / 12.7 / 16.5 us for
-// 2 / 4 / 8 / 16.
+// Two chunks per thread (both loads issued before either store). Config 1
+// replayed from a graph, sources warm (in the last-level cache, as the rows
+// a projection just wrote are) / cold (rotated over 384 MB of sources):
+// 1 chunk 4.1-4.2 / 9.2 us, 2 chunks 4.2-4.4 / 8.1 us, 4 chunks 4.8-4.9 /
+// 8.9 us. Two chunks make the grid one wave of resident workgroups (2,048
+// of 256 threads, 8 per CU), so a cold source costs one HBM round trip
+// per thread instead of two rounds of them.
 template <int C>
 static void launch_append(const AppendArgs& a, uint32_t layers, hipStream_t s) {
-  constexpr int ITEMS = 1;
+#ifndef VK_APPEND_ITEMS
+#define VK_APPEND_ITEMS 2
+#endif
+  constexpr int ITEMS = VK_APPEND_ITEMS;
   uint32_t grid = (a.total + 256 * ITEMS - 1) / (256 * ITEMS);
   if (!a.has_v)
     hipLaunchKernelGGL((kv_append_kernel<C, ITEMS, false, false>), dim3(grid, layers), dim3(256),
