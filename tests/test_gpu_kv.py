@@ -623,3 +623,66 @@ def test_attention_over_a_layer_of_a_mixed_cache_matches_the_oracle():
         assert float(np.abs(got.cpu().numpy() - want).max()) <= 1e-5
     with pytest.raises(Exception):
         paged_attention(q, c, 0, batch, 0.125)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_a_bf16_mixed_cache_runs_the_mfma_kernels_per_layer(layout):
+    """bf16 K/V layers of different geometry (head_dim 64 and 128, 2 and 4
+    kv heads) beside rows layers: each layer's attention (decode and
+    prefill rows, so both MFMA kernels) and the fused append + attention
+    through one PreparedAttention whose workspace is sized up front for the
+    largest layer (no layer reallocates it), against the oracle (bf16
+    max-abs <= 2e-2 * max|reference|) and the two-call sequence."""
+    from test_gpu_append_attention import dev_slots
+    from vapi_amd.attention import (ForwardBatch, PreparedAttention,
+                                    paged_attention_append_prepared, paged_attention_prepared)
+    from vapi_amd.cache import HybridKvCache, write_rows_indexed
+    spec = [("rows", 48), ("kv", 2, 64), ("kv", 4, 128), ("rows", 48), ("kv", 4, 64)]
+    c = HybridKvCache(spec, 64, 16, torch.bfloat16, layout)
+    g = torch.Generator(device=DEV).manual_seed(11)
+    for t in c.k + c.v:
+        if t.numel():
+            t.copy_(torch.randn(t.shape, generator=g, device=DEV).to(torch.bfloat16))
+    tables = [[3, 1, 7, 20, 21, 22], [9, 2, 40], [50, 51, 52, 53, 54, 55, 56, 57]]
+    lens_k, lens_q = [90, 40, 128], [1, 7, 1]
+    batch = ForwardBatch(cu_seqlens_q=np.concatenate([[0], np.cumsum(lens_q)]).tolist(),
+                         cu_seqlens_k=np.concatenate([[0], np.cumsum(lens_k)]).tolist(),
+                         block_tables=tables, max_seqlen_q=7, max_seqlen_k=128)
+    heads = 8
+    prep = PreparedAttention.from_batch(batch, DEV, cache=c, num_heads=heads)
+    ws = prep.workspace
+    assert ws is not None
+    for layer in (1, 2, 4):
+        d = spec[layer][2]
+        q = torch.randn(sum(lens_q), heads, d, generator=g, device=DEV).to(torch.bfloat16)
+        got = paged_attention_prepared(q, c, layer, prep, d ** -0.5)
+        assert prep.workspace is ws, "a layer reallocated the step's workspace"
+        want = oracle.paged_attention(q.float().cpu().numpy(),
+                                      c.reference_view(layer, "k").float().cpu().numpy(),
+                                      c.reference_view(layer, "v").float().cpu().numpy(),
+                                      batch.cu_seqlens_q, batch.cu_seqlens_k, tables, d ** -0.5)
+        want = torch.from_numpy(want).to(torch.bfloat16).float()
+        assert float((got.float().cpu() - want).abs().max()) <= 2e-2 * float(want.abs().max())
+    # Fused append + attention on a decode batch, per layer, against the two calls.
+    dec = ForwardBatch(cu_seqlens_q=[0, 1, 2], cu_seqlens_k=[0, 90, 218],
+                       block_tables=[tables[0], tables[1] + tables[2][:6]], max_seqlen_q=1,
+                       max_seqlen_k=128)
+    slots = [tables[0][89 // 16] * 16 + 89 % 16, dec.block_tables[1][127 // 16] * 16 + 127 % 16]
+    s = dev_slots(slots)
+    for layer in (1, 2):
+        kvh, d = spec[layer][1], spec[layer][2]
+        q = torch.randn(2, heads, d, generator=g, device=DEV).to(torch.bfloat16)
+        k_new = torch.randn(2, kvh, d, generator=g, device=DEV).to(torch.bfloat16)
+        v_new = torch.randn_like(k_new)
+        before_k = c.k[layer].clone(), c.v[layer].clone()
+        p1 = PreparedAttention.from_batch(dec, DEV, cache=c, num_heads=heads)
+        fused = paged_attention_append_prepared(q, k_new, v_new, s, c, layer, p1, d ** -0.5)
+        after = c.k[layer].clone(), c.v[layer].clone()
+        c.k[layer].copy_(before_k[0]), c.v[layer].copy_(before_k[1])
+        write_rows_indexed(c, layer, k_new, v_new, s)
+        assert torch.equal(c.k[layer], after[0]) and torch.equal(c.v[layer], after[1])
+        p2 = PreparedAttention.from_batch(dec, DEV, cache=c, num_heads=heads)
+        two = paged_attention_prepared(q, c, layer, p2, d ** -0.5)
+        torch.cuda.synchronize()
+        assert torch.equal(fused, two)

@@ -43,14 +43,15 @@ SOURCES = ["kv_ops.hip", "attention.hip", "attn_decode.hip", "attn_prefill.hip",
 # The MFMA attention kernels never produce NaN from finite K/V/Q (masked
 # scores are -inf, running maxima start finite), so fmaxf on MFMA results
 # needs no operand quieting: -fno-honor-nans drops one instruction per score.
-EXTRA_FLAGS = {"attn_decode.hip": ["-fno-honor-nans"],
+EXTRA_FLAGS = {"attn_decode.hip": ["-fno-honor-nans", "-Rpass-analysis=kernel-resource-usage"],
                "attn_prefill.hip": ["-fno-honor-nans", "-Rpass-analysis=kernel-resource-usage"]}
 
 # The prefill kernel's step barrier counts its own vector-memory operations
-# (the direct loads into LDS) with an explicit vmcnt wait; a register spill
-# would add scratch loads and stores to that count, so a build whose prefill
-# kernels use scratch is refused.
-NO_SCRATCH = {"attn_prefill.hip": "paged_prefill_tiled"}
+# (the direct loads into LDS) with an explicit vmcnt wait, and the decode
+# publishes its partials after an explicit vmcnt(0); a register spill would
+# add scratch traffic to those counts (and slow the stream), so a build
+# whose attention kernels use scratch is refused.
+NO_SCRATCH = {"attn_prefill.hip": "paged_prefill_tiled", "attn_decode.hip": "paged_decode_stream"}
 
 
 def _check_no_scratch(src: Path, remarks: str) -> None:
