@@ -186,9 +186,11 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
  *   split merge. Calls sharing one workspace must not overlap (same stream,
  *   or ordered streams).
  * max_seqlen_q/k must bound every sequence's len_q/len_k (as in
- *   flash-attention); max_seqlen_q sizes the prefill grid. The workspace
- *   size depends on the batch, the heads and the GPU's CU count, not on the
- *   lengths.
+ *   flash-attention); max_seqlen_q sizes the prefill grid. On the MFMA path
+ *   (bf16/f16, head_dim 64 or 128) the workspace size depends on the batch,
+ *   the heads and the GPU's CU count, not on the lengths; on the VALU path
+ *   (f32 pools, other head dims) it holds the split-context partials and
+ *   grows with max_seqlen_q * max_seqlen_k (0 while max_seqlen_k <= 512).
  */
 size_t vapi_paged_attention_workspace_size(const vapi_kv_pool* pool,
                                            uint32_t batch, uint32_t num_heads,

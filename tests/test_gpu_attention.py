@@ -184,6 +184,12 @@ CASES = [
     (torch.bfloat16, 32, 1, 128, 16, [1, 9, 1], [300, 40, 77], None, "HND"),
     (torch.float16, 8, 4, 256, 16, [1, 6], [500, 70], 30, "NHD"),
     (torch.bfloat16, 16, 8, 128, 8, [1, 12], [210, 50], None, "HND"),
+    # The VALU kernel's split contexts (more than 512 visible keys: chunks
+    # combined by its merge), odd head dims on its scalar dot path.
+    (torch.float32, 12, 4, 80, 16, [1, 20, 1], [3000, 1500, 700], None, "HND"),
+    (torch.float32, 4, 2, 3, 4, [1, 5], [1100, 600], 100, "NHD"),
+    (torch.float32, 8, 8, 128, 16, [1, 37], [2100, 1100], 700, "HND"),
+    (torch.bfloat16, 16, 4, 256, 16, [1, 9], [2000, 800], None, "HND"),
 ]
 
 

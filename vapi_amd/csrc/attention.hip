@@ -93,13 +93,15 @@ size_t vapi_paged_attention_workspace_size(const vapi_kv_pool* pool,
                                            uint32_t batch, uint32_t num_heads,
                                            uint32_t max_seqlen_q,
                                            uint32_t max_seqlen_k) {
-  (void)max_seqlen_q;
-  (void)max_seqlen_k;
-  if (!pool || pool->num_kv_heads == 0 || num_heads % pool->num_kv_heads ||
-      !mfma_ok(pool, num_heads) || batch == 0)
+  if (!pool || pool->num_kv_heads == 0 || num_heads % pool->num_kv_heads || batch == 0 ||
+      num_heads == 0)
     return 0;
-  return decode_workspace_bytes(batch, pool->num_kv_heads, num_heads / pool->num_kv_heads,
-                                pool->head_dim, decode_num_waves());
+  const uint32_t group = num_heads / pool->num_kv_heads;
+  if (!mfma_ok(pool, num_heads))
+    return generic_workspace_bytes(batch, pool->num_kv_heads, group, pool->head_dim,
+                                   std::max(max_seqlen_q, 1u), max_seqlen_k);
+  return decode_workspace_bytes(batch, pool->num_kv_heads, group, pool->head_dim,
+                                decode_num_waves());
 }
 
 int vapi_paged_attention(const vapi_kv_pool* pool, uint32_t layer,
@@ -302,7 +304,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   } else {
     if (g.d > 256)
       VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: head_dim %u > 256", g.d);
-    launch_generic(a, max_seqlen_q, g.d, pool->dtype, s);
+    launch_generic(a, max_seqlen_q, max_seqlen_k, g.d, pool->dtype, workspace, s);
   }
   VK_LAUNCHED("paged_attention");
   return 0;

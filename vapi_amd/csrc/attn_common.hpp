@@ -418,9 +418,12 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, bool bf16, hi
 // Prefill rows (len_q > 1); same dtypes and head dims.
 void launch_prefill(const AttnArgs& a, uint32_t max_q, uint32_t head_dim, bool bf16,
                     hipStream_t s);
-// Any row, any dtype, head_dim <= 256 (VALU).
-void launch_generic(const AttnArgs& a, uint32_t max_q, uint32_t head_dim,
-                    uint32_t dtype, hipStream_t s);
+// Any row, any dtype, head_dim <= 256 (VALU); split contexts combine their
+// partials through `workspace` (generic_workspace_bytes).
+void launch_generic(const AttnArgs& a, uint32_t max_q, uint32_t max_k, uint32_t head_dim,
+                    uint32_t dtype, void* workspace, hipStream_t s);
+size_t generic_workspace_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t head_dim,
+                               uint32_t max_q, uint32_t max_k);
 // Persistent decode waves for the current device (CUs x 8).
 uint32_t decode_num_waves();
 // Bytes at the start of a decode workspace that carry over between calls

@@ -1,104 +1,359 @@
 // Generic VALU paged attention: any dtype (f32 included), any head_dim up
-// to 256 and any GQA ratio. One wave per (query token, query head); K rows
-// are dotted one key per lane, V rows are accumulated one d per lane.
+// to 256 and any GQA ratio, for the shapes the MFMA kernels do not take.
+//
+// One workgroup (4 waves) per 16 rows of one (sequence, kv head), a row
+// being a (query token, query head of the kv head's group) pair, r = j*G +
+// h. The rows share every K/V byte: 32-key tiles of K and V are staged in
+// LDS as f32 by coalesced loads (consecutive threads walk a key row), then
+//  * scores: thread (row, key) dots its row's Q (LDS broadcast) with the
+//    key's row (LDS, rows padded by one word against bank conflicts);
+//  * online softmax per row across the 32 lanes of its half-wave (shuffles),
+//    in f32 with the row's running max, exactly as the CPU path orders it
+//    up to summation order;
+//  * PV: thread (row, d-slice) accumulates P (LDS broadcast) times V.
+// Exact f32 arithmetic (no MFMA), which the f32 parity bar (max-abs 1e-5)
+// needs.
+//
+// Long contexts are split: workgroup (sequence, kv head, row tile, chunk)
+// takes keys [chunk * kGenChunk, (chunk + 1) * kGenChunk). When a row tile's
+// visible keys span more than one chunk, each chunk writes (m, l, o) per row
+// to the workspace and paged_attn_generic_merge combines them; a tile whose
+// keys fit one chunk writes its output directly.
+#include <algorithm>
+
 #include "attn_common.hpp"
 
 namespace vk {
 
-// ---------------------------------------------------------------------------
-// Generic VALU kernel: one wave per (query token, query head).
-// ---------------------------------------------------------------------------
+constexpr uint32_t kGenRows = 16;   // rows per workgroup
+constexpr uint32_t kGenKeys = 32;   // keys per LDS tile
+constexpr uint32_t kGenThreads = 256;
+#ifndef VK_GEN_CHUNK
+#define VK_GEN_CHUNK 512
+#endif
+constexpr uint32_t kGenChunk = VK_GEN_CHUNK;  // keys per workgroup
+// Dynamic LDS of the largest tile (head_dim 256: 84 KiB), past the 64 KiB
+// a launch gets without asking.
+constexpr size_t kGenMaxDynLds = 96 * 1024;
+// The partials start past the words a decode keeps at the start of a
+// workspace (its XCD shares), so one workspace serves both kinds of layer.
+constexpr size_t kGenPartOffset = 256;
 
-template <typename T, int DPL>  // DPL = ceil(head_dim / 64)
-__global__ __launch_bounds__(64) void paged_attn_generic(AttnArgs a,
-                                                         uint32_t head_dim) {
-  const uint32_t seq = blockIdx.z, h = blockIdx.y, j = blockIdx.x;
-  const uint32_t lane = threadIdx.x;
+__host__ __device__ __forceinline__ uint32_t gen_k_stride(uint32_t d) {
+  return (d & 3) ? d + 1 : d + 4;
+}
+
+// Chunks a tile with visible keys [klo, khi] spans: [c_first, c_last].
+__device__ __forceinline__ void tile_chunks(int32_t klo, int32_t khi, int32_t& c_first,
+                                            int32_t& c_last) {
+  c_first = klo / (int32_t)kGenChunk;
+  c_last = khi / (int32_t)kGenChunk;
+}
+
+// Partials of item i: (m, l) at part + i * kGenRows * (D + 2) + 2 r, then
+// o at + 2 kGenRows + r * D.
+template <typename T>
+__global__ __launch_bounds__(kGenThreads) void paged_attn_generic(AttnArgs a, uint32_t head_dim,
+                                                                  uint32_t row_tiles,
+                                                                  uint32_t n_chunks,
+                                                                  float* __restrict__ part) {
+  extern __shared__ float lds[];
+  // K rows padded against bank conflicts: by 4 words (keeping 16-byte
+  // alignment) when head_dim is a multiple of 4, else by one.
+  const uint32_t D = head_dim, KS = gen_k_stride(head_dim);
+  float* ks = lds;                              // [32][KS]
+  float* vs = ks + kGenKeys * KS;               // [32][D]
+  float* qs = vs + kGenKeys * D;                // [16][D]
+  float* ps = qs + kGenRows * D;                // [16][32]
+  float* m_s = ps + kGenRows * kGenKeys;        // [16] running max
+  float* l_s = m_s + kGenRows;                  // [16] running sum
+  float* al_s = l_s + kGenRows;                 // [16] this tile's rescale
+
+  const uint32_t tid = threadIdx.x;
+  const uint32_t item = blockIdx.x;
+  const uint32_t chunk = item % n_chunks;
+  const uint32_t rt = (item / n_chunks) % row_tiles, rest = item / n_chunks / row_tiles;
+  const uint32_t kh = rest % a.kvh, seq = rest / a.kvh;
   const uint32_t q0 = a.cu_q[seq], len_q = a.cu_q[seq + 1] - q0;
-  if (j >= len_q) return;
+  const uint32_t G = a.group;
+  const uint32_t nrows = len_q * G;
+  const uint32_t row0 = rt * kGenRows;
+  if (row0 >= nrows) return;
+  const uint32_t rows = min(kGenRows, nrows - row0);
   const int32_t len_k = (int32_t)(a.cu_k[seq + 1] - a.cu_k[seq]);
-  const int32_t p = len_k - (int32_t)len_q + (int32_t)j;
-  int32_t lo, hi;
-  key_range(p, len_k, a.wl, a.wr, lo, hi);
-  const uint32_t kh = h / a.group;
+  const int32_t offset = len_k - (int32_t)len_q;
 
-  __shared__ float qs[64 * DPL];
-  __shared__ float ps[64];
-  const T* qrow = (const T*)a.q + ((uint64_t)(q0 + j) * a.num_heads + h) * head_dim;
-  for (uint32_t d = lane; d < 64 * DPL; d += 64)
-    qs[d] = d < head_dim ? to_f32(qrow[d]) : 0.f;
-  __syncthreads();
+  // Keys any row of the tile can see, and this workgroup's chunk of them.
+  int32_t klo, khi, unused;
+  key_range(offset + (int32_t)(row0 / G), len_k, a.wl, a.wr, klo, unused);
+  key_range(offset + (int32_t)((row0 + rows - 1) / G), len_k, a.wl, a.wr, unused, khi);
+  int32_t c_first, c_last;
+  tile_chunks(klo, khi, c_first, c_last);
+  if (khi < klo || (int32_t)chunk < c_first || (int32_t)chunk > c_last) return;
+  const bool split = c_last > c_first;
+  klo = max(klo, (int32_t)(chunk * kGenChunk));
+  khi = min(khi, (int32_t)((chunk + 1) * kGenChunk) - 1);
+
+  for (uint32_t i = tid; i < kGenRows * D; i += kGenThreads) {
+    const uint32_t r = i / D, d = i - r * D;
+    float x = 0.f;
+    if (r < rows) {
+      const uint32_t rr = row0 + r, j = rr / G, hl = rr - j * G;
+      x = to_f32(((const T*)a.q)[((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * D + d]);
+    }
+    qs[i] = x;
+  }
+  if (tid < kGenRows) m_s[tid] = kNegBig, l_s[tid] = 0.f;
 
   const uint32_t* table = a.table + (uint64_t)seq * a.max_blocks;
   const T* kb = (const T*)a.k + kh * a.head_e;
   const T* vb = (const T*)a.v + kh * a.head_e;
-
-  float m = kNegBig, l = 0.f;
-  float acc[DPL];
+  // Score phase: thread -> (row sr + 8 i, key sk); PV phase: thread -> (row
+  // pr, d = pd + 16 i).
+  const uint32_t sk = tid & 31, sr = tid >> 5;  // 8 rows per pass, 2 passes
+  const uint32_t pr = tid >> 4, pd = tid & 15;  // 16 rows, d stride 16
+  constexpr int kMaxDPer = 256 / 16;
+  float acc[kMaxDPer];
 #pragma unroll
-  for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
+  for (int i = 0; i < kMaxDPer; ++i) acc[i] = 0.f;
 
-  for (int32_t c0 = lo; c0 <= hi; c0 += 64) {
-    const int32_t key = c0 + (int32_t)lane;
-    float s = -INFINITY;
-    if (key <= hi) {
-      const uint32_t blk = min(table[min((uint32_t)key / a.block_size, a.max_blocks - 1)], a.last_blk);
-      const uint32_t off = key % a.block_size;
-      const T* krow = kb + blk * a.blk_e + off * a.tok_e;
-      float dot = 0.f;
-      for (uint32_t d = 0; d < head_dim; ++d) dot += qs[d] * to_f32(krow[d]);
-      s = dot * a.scale;
+  // Staging map: thread tid moves elements i = tid + 256 u of the 32 x D
+  // tile, key i / D and column i % D, stepped without divisions.
+  const uint32_t k_step = kGenThreads / D, d_step = kGenThreads % D;
+  const uint32_t k_first = tid / D, d_first = tid % D;
+  const uint32_t n_el = (kGenKeys * D + kGenThreads - 1 - tid) / kGenThreads;  // this thread's
+  // The chunk's block ids (one table read per block, not per key) and each
+  // tile's per-key row offsets.
+  __shared__ uint32_t blk_ids[kGenChunk];
+  __shared__ uint64_t key_off[kGenKeys];
+  const uint32_t col0 = (uint32_t)klo / a.block_size;
+  const uint32_t n_cols = (uint32_t)khi / a.block_size - col0 + 1;
+  for (uint32_t c = tid; c < n_cols; c += kGenThreads)
+    blk_ids[c] = min(table[min(col0 + c, a.max_blocks - 1)], a.last_blk);
+  for (int32_t c0 = klo; c0 <= khi; c0 += (int32_t)kGenKeys) {
+    __syncthreads();  // the previous tile's K, V, P and key offsets are consumed
+    if (tid < kGenKeys) {
+      const int32_t key = c0 + (int32_t)tid;
+      key_off[tid] = key <= khi ? (uint64_t)blk_ids[(uint32_t)key / a.block_size - col0] * a.blk_e +
+                                      (uint64_t)((uint32_t)key % a.block_size) * a.tok_e
+                                : ~0ull;
     }
-    float cm = s;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o));
-    const float mn = fmaxf(m, cm);
-    const float alpha = __expf(m - mn);
-    const float pv = key <= hi ? __expf(s - mn) : 0.f;
-    float cs = pv;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) cs += __shfl_xor(cs, o);
-    l = l * alpha + cs;
-    m = mn;
-    ps[lane] = pv;
     __syncthreads();
+    // Stage keys c0 .. c0 + 31 (past khi: zeros, never visible), eight
+    // elements at a time: all eight loads are issued before their stores.
+    {
+      constexpr int kBatch = 8;
+      uint32_t k = k_first, d = d_first;
+      for (uint32_t u0 = 0; u0 < n_el; u0 += kBatch) {
+        float kx[kBatch], vx[kBatch];
+        uint32_t kk[kBatch], dd[kBatch];
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) acc[i] *= alpha;
-    const int32_t nk = min(64, hi - c0 + 1);
-    for (int32_t kk = 0; kk < nk; ++kk) {
-      const int32_t key2 = c0 + kk;
-      const uint32_t blk = min(table[min((uint32_t)key2 / a.block_size, a.max_blocks - 1)], a.last_blk);
-      const uint32_t off = key2 % a.block_size;
-      const T* vrow = vb + blk * a.blk_e + off * a.tok_e;
-      const float pk = ps[kk];
+        for (int u = 0; u < kBatch; ++u) {
+          kk[u] = k, dd[u] = d;
+          kx[u] = 0.f, vx[u] = 0.f;
+          if (u0 + u < n_el) {
+            const uint64_t off = key_off[k];
+            if (off != ~0ull) {
+              kx[u] = to_f32(kb[off + d]);
+              vx[u] = to_f32(vb[off + d]);
+            }
+          }
+          d += d_step, k += k_step;
+          if (d >= D) d -= D, ++k;
+        }
 #pragma unroll
-      for (int i = 0; i < DPL; ++i) {
-        const uint32_t d = lane + 64 * i;
-        if (d < head_dim) acc[i] += pk * to_f32(vrow[d]);
+        for (int u = 0; u < kBatch; ++u) {
+          if (u0 + u < n_el) {
+            ks[kk[u] * KS + dd[u]] = kx[u];
+            vs[kk[u] * D + dd[u]] = vx[u];
+          }
+        }
       }
     }
     __syncthreads();
-  }
-  T* orow = (T*)a.out + ((uint64_t)(q0 + j) * a.num_heads + h) * head_dim;
-  const float inv = l > 0.f ? 1.f / l : 0.f;
+    // Scores and the online softmax, two passes of 8 rows.
 #pragma unroll
-  for (int i = 0; i < DPL; ++i) {
-    const uint32_t d = lane + 64 * i;
-    if (d < head_dim) orow[d] = from_f32<T>(acc[i] * inv);
+    for (uint32_t pass = 0; pass < 2; ++pass) {
+      const uint32_t r = sr + 8 * pass;
+      const int32_t key = c0 + (int32_t)sk;
+      float s = -INFINITY;
+      if (r < rows) {
+        int32_t lo, hi;
+        key_range(offset + (int32_t)((row0 + r) / G), len_k, a.wl, a.wr, lo, hi);
+        // Keys past this chunk (khi) are staged as zeros and belong to the
+        // next chunk's workgroup, whatever the row's own range says.
+        if (key >= lo && key <= min(hi, khi)) {
+          const float* qr = qs + r * D;
+          const float* kr = ks + sk * KS;
+          float dot;
+          if ((D & 3) == 0) {  // 16-byte LDS reads, four independent sums
+            const float4* q4 = (const float4*)qr;
+            const float4* k4 = (const float4*)kr;
+            float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+            for (uint32_t d4 = 0; d4 < D / 4; ++d4) {
+              const float4 qv = q4[d4], kv = k4[d4];
+              s0 = __builtin_fmaf(qv.x, kv.x, s0);
+              s1 = __builtin_fmaf(qv.y, kv.y, s1);
+              s2 = __builtin_fmaf(qv.z, kv.z, s2);
+              s3 = __builtin_fmaf(qv.w, kv.w, s3);
+            }
+            dot = (s0 + s1) + (s2 + s3);
+          } else {
+            dot = 0.f;
+            for (uint32_t d = 0; d < D; ++d) dot = __builtin_fmaf(qr[d], kr[d], dot);
+          }
+          s = dot * a.scale;
+        }
+      }
+      float cm = s;
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o, 32));
+      const float m_old = m_s[r];
+      const float mn = fmaxf(m_old, cm);
+      const float p = s == -INFINITY ? 0.f : __expf(s - mn);
+      float cs = p;
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) cs += __shfl_xor(cs, o, 32);
+      ps[r * kGenKeys + sk] = p;
+      if (sk == 0) {
+        const float alpha = __expf(m_old - mn);
+        al_s[r] = alpha;
+        l_s[r] = l_s[r] * alpha + cs;
+        m_s[r] = mn;
+      }
+    }
+    __syncthreads();
+    // O = O * alpha + P V.
+    const float alpha = al_s[pr];
+    const float* pp = ps + pr * kGenKeys;
+#pragma unroll
+    for (int i = 0; i < kMaxDPer; ++i) acc[i] *= alpha;
+    for (uint32_t k = 0; k < kGenKeys; ++k) {
+      const float pk = pp[k];
+      const float* vk = vs + k * D + pd;
+#pragma unroll
+      for (int i = 0; i < kMaxDPer; ++i)
+        if (pd + 16 * i < D) acc[i] = __builtin_fmaf(pk, vk[16 * i], acc[i]);
+    }
+  }
+  __syncthreads();
+  if (split) {
+    float* pi = part + (uint64_t)item * kGenRows * (D + 2);
+    if (tid < kGenRows) {
+      pi[2 * tid] = m_s[tid];
+      pi[2 * tid + 1] = l_s[tid];
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxDPer; ++i) {
+      const uint32_t d = pd + 16 * i;
+      if (d < D) pi[2 * kGenRows + pr * D + d] = acc[i];
+    }
+    return;
+  }
+  if (pr < rows) {
+    const uint32_t rr = row0 + pr, j = rr / G, hl = rr - j * G;
+    T* orow = (T*)a.out + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * D;
+    const float l = l_s[pr];
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+    for (int i = 0; i < kMaxDPer; ++i) {
+      const uint32_t d = pd + 16 * i;
+      if (d < D) orow[d] = from_f32<T>(acc[i] * inv);
+    }
   }
 }
 
-void launch_generic(const AttnArgs& a, uint32_t max_q, uint32_t head_dim, uint32_t dtype,
-                    hipStream_t s) {
-  const dim3 grid(max_q, a.num_heads, a.batch);
-#define VK_GEN(T)                                                                         \
-  do {                                                                                    \
-    if (head_dim <= 64)                                                                   \
-      hipLaunchKernelGGL((paged_attn_generic<T, 1>), grid, dim3(64), 0, s, a, head_dim); \
-    else if (head_dim <= 128)                                                             \
-      hipLaunchKernelGGL((paged_attn_generic<T, 2>), grid, dim3(64), 0, s, a, head_dim); \
-    else                                                                                  \
-      hipLaunchKernelGGL((paged_attn_generic<T, 4>), grid, dim3(64), 0, s, a, head_dim); \
+// One workgroup per (sequence, kv head, row tile) whose keys were split:
+// thread (row, d-slice) combines the chunks' partials.
+template <typename T>
+__global__ __launch_bounds__(kGenThreads) void paged_attn_generic_merge(
+    AttnArgs a, uint32_t head_dim, uint32_t row_tiles, uint32_t n_chunks,
+    const float* __restrict__ part) {
+  const uint32_t D = head_dim;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t rt = blockIdx.x % row_tiles, rest = blockIdx.x / row_tiles;
+  const uint32_t kh = rest % a.kvh, seq = rest / a.kvh;
+  const uint32_t q0 = a.cu_q[seq], len_q = a.cu_q[seq + 1] - q0;
+  const uint32_t G = a.group;
+  const uint32_t nrows = len_q * G;
+  const uint32_t row0 = rt * kGenRows;
+  if (row0 >= nrows) return;
+  const uint32_t rows = min(kGenRows, nrows - row0);
+  const int32_t len_k = (int32_t)(a.cu_k[seq + 1] - a.cu_k[seq]);
+  const int32_t offset = len_k - (int32_t)len_q;
+  int32_t klo, khi, unused, c_first, c_last;
+  key_range(offset + (int32_t)(row0 / G), len_k, a.wl, a.wr, klo, unused);
+  key_range(offset + (int32_t)((row0 + rows - 1) / G), len_k, a.wl, a.wr, unused, khi);
+  tile_chunks(klo, khi, c_first, c_last);
+  if (khi < klo || c_last == c_first) return;
+  const uint32_t pr = tid >> 4, pd = tid & 15;
+  if (pr >= rows) return;
+  const uint64_t base = (uint64_t)blockIdx.x * n_chunks;
+  const uint64_t stride = (uint64_t)kGenRows * (D + 2);
+  float M = kNegBig;
+  for (int32_t c = c_first; c <= c_last; ++c) {
+    const float* pc = part + (base + c) * stride;
+    if (pc[2 * pr + 1] > 0.f) M = fmaxf(M, pc[2 * pr]);
+  }
+  float L = 0.f;
+  constexpr int kMaxDPer = 256 / 16;
+  float o[kMaxDPer];
+#pragma unroll
+  for (int i = 0; i < kMaxDPer; ++i) o[i] = 0.f;
+  for (int32_t c = c_first; c <= c_last; ++c) {
+    const float* pc = part + (base + c) * stride;
+    const float l = pc[2 * pr + 1];
+    if (!(l > 0.f)) continue;  // a chunk no key of this row is visible in
+    const float e = __expf(pc[2 * pr] - M);
+    L += l * e;
+#pragma unroll
+    for (int i = 0; i < kMaxDPer; ++i) {
+      const uint32_t d = pd + 16 * i;
+      if (d < D) o[i] += pc[2 * kGenRows + pr * D + d] * e;
+    }
+  }
+  const uint32_t rr = row0 + pr, j = rr / G, hl = rr - j * G;
+  T* orow = (T*)a.out + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * D;
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxDPer; ++i) {
+    const uint32_t d = pd + 16 * i;
+    if (d < D) orow[d] = from_f32<T>(o[i] * inv);
+  }
+}
+
+size_t generic_workspace_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t head_dim,
+                               uint32_t max_q, uint32_t max_k) {
+  const uint64_t n_chunks = ((uint64_t)max_k + kGenChunk - 1) / kGenChunk;
+  if (n_chunks <= 1) return 0;
+  const uint64_t row_tiles = ((uint64_t)max_q * group + kGenRows - 1) / kGenRows;
+  return kGenPartOffset +
+         (size_t)(row_tiles * kvh * batch * n_chunks * kGenRows * (head_dim + 2) * sizeof(float));
+}
+
+void launch_generic(const AttnArgs& a, uint32_t max_q, uint32_t max_k, uint32_t head_dim,
+                    uint32_t dtype, void* workspace, hipStream_t s) {
+  const uint32_t row_tiles = (max_q * a.group + kGenRows - 1) / kGenRows;
+  const uint32_t n_chunks = (uint32_t)(((uint64_t)max_k + kGenChunk - 1) / kGenChunk);
+  const uint64_t n = (uint64_t)row_tiles * a.kvh * a.batch * std::max(n_chunks, 1u);
+  float* part = (float*)((char*)workspace + kGenPartOffset);
+  const size_t lds = ((size_t)kGenKeys * gen_k_stride(head_dim) + (size_t)kGenKeys * head_dim +
+                      (size_t)kGenRows * head_dim + kGenRows * kGenKeys + 3 * kGenRows) *
+                     sizeof(float);
+#define VK_GEN(T)                                                                            \
+  do {                                                                                       \
+    static bool lds_set = false;                                                             \
+    if (lds > 64 * 1024 && !lds_set) {                                                       \
+      if (hipFuncSetAttribute((const void*)paged_attn_generic<T>,                            \
+                              hipFuncAttributeMaxDynamicSharedMemorySize,                    \
+                              (int)kGenMaxDynLds) == hipSuccess)                             \
+        lds_set = true;                                                                      \
+    }                                                                                        \
+    hipLaunchKernelGGL((paged_attn_generic<T>), dim3((uint32_t)n), dim3(kGenThreads), lds, s, \
+                       a, head_dim, row_tiles, std::max(n_chunks, 1u), part);                \
+    if (n_chunks > 1)                                                                        \
+      hipLaunchKernelGGL((paged_attn_generic_merge<T>), dim3(row_tiles * a.kvh * a.batch),   \
+                         dim3(kGenThreads), 0, s, a, head_dim, row_tiles, n_chunks, part);   \
   } while (0)
   switch (dtype) {
     case VAPI_KV_F32: VK_GEN(float); break;
