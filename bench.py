@@ -197,6 +197,33 @@ def bench_fused_step(d, steps, warmup):
     return {"two_calls_us": round(ms_two * 1e3, 2), "fused_us": round(ms_fused * 1e3, 2)}
 
 
+# ---- the VALU kernel (f32 pools, other head dims) ---------------------------------
+
+def bench_valu(steps, warmup):
+    """The VALU attention kernel that f32 pools and head dims other than 64 /
+    128 run on: config 0 (Qwen3-0.6B-shaped f32 decode, the reference's CPU
+    parity case) and config 2's batch over an f32 pool (1.5 GB of K/V)."""
+    out = {}
+    for name, w, heads, kvh in (("cfg0_f32", workload.config0_decode_small(), 16, 8),
+                                ("cfg2_shape_f32", workload.config2_decode(), 32, 8)):
+        cache = PagedKvCache(1, w.num_blocks, w.block_size, kvh, w.head_dim, torch.float32, "HND")
+        workload.fill_normal(cache._slab, workload.seed_for(0))
+        q = torch.randn(w.batch, heads, w.head_dim, device=DEV)
+        batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
+                             block_tables=[t.tolist() for t in w.tables], max_seqlen_q=1,
+                             max_seqlen_k=int(w.lens.max()))
+        prep = PreparedAttention.from_batch(batch, DEV)
+        o = torch.empty_like(q)
+        ms, _ = timed(lambda: paged_attention_prepared(q, cache, 0, prep, w.head_dim ** -0.5,
+                                                       out=o), max(steps // 5, 3), 2)
+        kv = int(w.lens.sum()) * 2 * kvh * w.head_dim * 4
+        out[name] = dict(us=ms * 1e3, kv_bytes=kv, gbs=kv / (ms * 1e-3) / 1e9)
+        log(f"VALU attention {name}: {ms * 1e3:.1f} us, {kv / 1e6:.1f} MB of K/V, "
+            f"{out[name]['gbs']:.0f} GB/s")
+        del cache
+    return out
+
+
 # ---- config 1: append --------------------------------------------------------------
 
 def bench_append(steps, warmup):
@@ -707,7 +734,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["decode", "append", "prefill", "copy", "blocks"],
+    ap.add_argument("--only", choices=["decode", "append", "prefill", "copy", "blocks", "valu"],
                     default=None)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate", action="store_true",
@@ -737,6 +764,9 @@ def main():
     if args.only == "prefill":
         bench_prefill(args.steps, args.warmup)
         return
+    if args.only == "valu":
+        bench_valu(args.steps, args.warmup)
+        return
     dec = bench_decode(args.steps, args.warmup)
     if args.only == "decode":
         return
@@ -747,6 +777,7 @@ def main():
     if args.only in (None,):
         extras["append_cfg1"] = bench_append(args.steps, args.warmup)
         extras["prefill_cfg3"] = bench_prefill(max(args.steps // 5, 3), 2)
+        extras["valu_attention"] = bench_valu(args.steps, args.warmup)
     extras["blocks_cfg4"] = bench_blocks(max(args.steps // 5, 3), 2, dec)
     if args.only == "blocks":
         return

@@ -142,28 +142,30 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
     }
 }
 
-// Two chunks per thread (both loads issued before either store). Config 1
-// replayed from a graph, sources warm (in the last-level cache, as the rows
-// a projection just wrote are) / cold (rotated over 384 MB of sources):
-// 1 chunk 4.1-4.2 / 9.2 us, 2 chunks 4.2-4.4 / 8.1 us, 4 chunks 4.8-4.9 /
-// 8.9 us. Two chunks make the grid one wave of resident workgroups (2,048
-// of 256 threads, 8 per CU), so a cold source costs one HBM round trip
-// per thread instead of two rounds of them.
+// A single-layer append moves two chunks per thread (both loads issued
+// before either store). Config 1 replayed from a graph, sources warm (in
+// the last-level cache, as the rows a projection just wrote are) / cold
+// (rotated over 384 MB of sources): 1 chunk 4.1-4.2 / 9.2 us, 2 chunks
+// 4.2-4.4 / 8.1 us, 4 chunks 4.8-4.9 / 8.9 us. Two chunks make the grid one
+// wave of resident workgroups (2,048 of 256 threads, 8 per CU), so a cold
+// source costs one HBM round trip per thread instead of two rounds of
+// them. A multi-layer append already has layers times that grid and keeps
+// one chunk per thread (4 layers: 21.2 us against 29.5 us with two).
 template <int C>
 static void launch_append(const AppendArgs& a, uint32_t layers, hipStream_t s) {
-#ifndef VK_APPEND_ITEMS
-#define VK_APPEND_ITEMS 2
-#endif
-  constexpr int ITEMS = VK_APPEND_ITEMS;
-  uint32_t grid = (a.total + 256 * ITEMS - 1) / (256 * ITEMS);
-  if (!a.has_v)
-    hipLaunchKernelGGL((kv_append_kernel<C, ITEMS, false, false>), dim3(grid, layers), dim3(256),
+  if (!a.has_v) {
+    const uint32_t grid = (a.total + 255) / 256;
+    hipLaunchKernelGGL((kv_append_kernel<C, 1, false, false>), dim3(grid, layers), dim3(256),
                        0, s, a);
-  else if (layers == 1)
+  } else if (layers == 1) {
+    constexpr int ITEMS = 2;
+    const uint32_t grid = (a.total + 256 * ITEMS - 1) / (256 * ITEMS);
     hipLaunchKernelGGL((kv_append_kernel<C, ITEMS, true, true>), dim3(grid), dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL((kv_append_kernel<C, ITEMS, false, true>), dim3(grid, layers), dim3(256),
+  } else {
+    const uint32_t grid = (a.total + 255) / 256;
+    hipLaunchKernelGGL((kv_append_kernel<C, 1, false, true>), dim3(grid, layers), dim3(256),
                        0, s, a);
+  }
 }
 
 // ---- gather -----------------------------------------------------------------

@@ -7,7 +7,8 @@
 //  * vapi_probe_read_tiles: reads of `tile_bytes` runs at given tile indices
 //                           (the decode's 4 KiB K or V tile of one (block,
 //                           head), or an 8 KiB run).
-//  * vapi_probe_copy:       sequential device-to-device copy.
+//  * vapi_probe_copy:       sequential device-to-device copy, one workgroup
+//                           per 16 KiB run.
 //  * vapi_probe_copy_runs:  copies of `run_bytes` runs between given run
 //                           indices (the block copy's 16 KiB (block, layer,
 //                           K or V) run).
@@ -59,18 +60,21 @@ __global__ __launch_bounds__(kThreads) void probe_tiles_kernel(const char* __res
   if (x == 0x9E3779B9u) sink[wave & 1023] = x;
 }
 
+// One workgroup per 16 KiB: the block copy's per-workgroup shape, on
+// consecutive runs.
 __global__ __launch_bounds__(kThreads) void probe_copy_kernel(uint4* __restrict__ dst,
                                                               const uint4* __restrict__ src,
                                                               uint64_t n16) {
-  const uint64_t base = (uint64_t)blockIdx.x * kThreads * kUnroll + threadIdx.x;
-  uint4 v[kUnroll];
+  constexpr int kItems = 4;
+  const uint64_t base = (uint64_t)blockIdx.x * kThreads * kItems + threadIdx.x;
+  uint4 v[kItems];
 #pragma unroll
-  for (int i = 0; i < kUnroll; ++i) {
+  for (int i = 0; i < kItems; ++i) {
     const uint64_t j = base + (uint64_t)i * kThreads;
     if (j < n16) v[i] = src[j];
   }
 #pragma unroll
-  for (int i = 0; i < kUnroll; ++i) {
+  for (int i = 0; i < kItems; ++i) {
     const uint64_t j = base + (uint64_t)i * kThreads;
     if (j < n16) dst[j] = v[i];
   }
@@ -126,7 +130,7 @@ int vapi_probe_read_tiles(const void* base, const uint32_t* ids, uint32_t n_tile
 // Sequential copy of `bytes` (a multiple of 16).
 int vapi_probe_copy(void* dst, const void* src, uint64_t bytes, hipStream_t stream) {
   const uint64_t n16 = bytes / 16;
-  const uint64_t grid = (n16 + kThreads * kUnroll - 1) / (kThreads * kUnroll);
+  const uint64_t grid = (n16 + kThreads * 4 - 1) / (kThreads * 4);
   hipLaunchKernelGGL(probe_copy_kernel, dim3((uint32_t)grid), dim3(kThreads), 0, stream,
                      (uint4*)dst, (const uint4*)src, n16);
   return hipGetLastError() == hipSuccess ? 0 : -3;
