@@ -236,8 +236,21 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
   wait_vmcnt<kLoadsPerStep>();
   ring_barrier();
   // Step s reads buffer s % 3 and issues step s + 2 into (s + 2) % 3.
+#ifdef VK_PF_TRACE
+  // Phase timestamps (shader clock) of every wave of workgroup item 100,
+  // steps 16..47: [step][wave][phase].
+  uint32_t tr_step = 0;
+  const bool tr_on = item == 100 && lane == 0;
+  auto TR = [&](int ph) {
+    if (tr_on && tr_step >= 16 && tr_step < 48)
+      a.trace[((tr_step - 16) * 8 + wave) * 5 + ph] = __builtin_amdgcn_s_memtime();
+  };
+#else
+  auto TR = [](int) {};
+#endif
   auto step = [&](auto cur) __attribute__((always_inline)) {
     constexpr int B = decltype(cur)::value;
+    TR(0);
     uint16_t* const kbuf = B == 0 ? k0 : B == 1 ? k1 : k2;
     uint16_t* const vbuf = B == 0 ? v0 : B == 1 ? v1 : v2;
     uint16_t* const knext = B == 0 ? k2 : B == 1 ? k0 : k1;
@@ -272,6 +285,7 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
         }
       }
     }
+    TR(1);
     float mx[kPfRT];
     bool grow = false;
 #pragma unroll
@@ -287,6 +301,7 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
     uint4 pf[kPfRT];
 #pragma unroll
     for (int t = 0; t < kPfRT; ++t) pf[t] = exp_pack<T>(sc[t], m_run[t], l_run[t], a.scale_log2);
+    TR(2);
     // V^T fragments two d tiles at a time; a batch's MFMAs run while the
     // next batch's reads wait (measured: batches of two tiles 821-833
     // TFLOP/s, of four 803-814, of one 794-805 on config 3).
@@ -319,8 +334,13 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
     // Step s + 1's chunks (issued a step ago) are in LDS once this wave's
     // loads older than step s + 2's have landed; the barrier makes that
     // hold for every wave.
+    TR(3);
     wait_vmcnt<kLoadsPerStep>();
     ring_barrier();
+    TR(4);
+#ifdef VK_PF_TRACE
+    ++tr_step;
+#endif
     s0_ += 32;
   };
   while (true) {
@@ -356,8 +376,24 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
 #define VK_PF_OCC 1
 #endif
 
-void launch_prefill(const AttnArgs& a, uint32_t max_q, uint32_t head_dim, bool bf16,
+#ifdef VK_PF_TRACE
+__device__ uint64_t pf_trace_buf[32 * 8 * 5];
+}  // namespace vk
+extern "C" int vapi_pf_trace_copy(void* host) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(vk::pf_trace_buf), sizeof(vk::pf_trace_buf)) ==
+                 hipSuccess ? 0 : -3;
+}
+namespace vk {
+#endif
+
+void launch_prefill(const AttnArgs& a_in, uint32_t max_q, uint32_t head_dim, bool bf16,
                     hipStream_t s) {
+  AttnArgs a = a_in;
+#ifdef VK_PF_TRACE
+  void* tp = nullptr;
+  (void)hipGetSymbolAddress(&tp, HIP_SYMBOL(pf_trace_buf));
+  a.trace = (uint64_t*)tp;
+#endif
   constexpr uint32_t rows = 16 * VK_PF_RT * kPfWaves;
   const uint32_t qtiles = (max_q * a.group + rows - 1) / rows;
   const uint64_t n = (uint64_t)qtiles * a.kvh * a.batch;
