@@ -658,11 +658,24 @@ def cpu_baseline(decode, budget_s=12.0):
 
 def cpu_baselines_more(decode, budget_s=4.0):
     """BASELINE.md's other CPU legs, each on a bounded sample with the C
-    oracle: config-2 decode on one thread, the config-1 append scatter
-    (write_rows) and the config-4a block copy (copy_blocks), single-threaded
-    as the reference's own loops are."""
+    oracle, on one core and on every core this process may use: config-2
+    decode on one core (the all-core figure is `cpu_baseline`), the config-1
+    append scatter (write_rows), the config-3 chunked prefill (the last 64
+    query rows of each sequence's chunk) and the config-4a block copy
+    (copy_blocks). The multi-core append and copy split the rows or pairs over
+    threads (config 1's slots and config 4's pairs never collide)."""
     import oracle  # checker/baseline only
+    threads = len(os.sched_getaffinity(0))
     out = {}
+
+    def rate(fn, min_reps, budget):
+        fn()  # untimed: first touch of the pages
+        reps, t0 = 0, time.perf_counter()
+        while reps < min_reps or time.perf_counter() - t0 < budget:
+            fn()
+            reps += 1
+        return (time.perf_counter() - t0) / reps, reps
+
     # Decode on one core: the same batch as the headline leg.
     w = decode["w"]
     cache = decode["cache"]
@@ -686,15 +699,35 @@ def cpu_baselines_more(decode, budget_s=4.0):
     row = a.num_kv_heads * a.head_dim * 2
     pool = np.zeros((a.num_blocks * a.block_size, row), dtype=np.uint8)
     src = np.random.default_rng(1).integers(0, 255, size=(a.n_tokens, row), dtype=np.uint8)
-    oracle.write_rows(pool, src, a.slots)  # untimed: first touch of the pool's pages
-    reps, t0 = 0, time.perf_counter()
-    while reps < 3 or time.perf_counter() - t0 < budget_s / 4:
-        oracle.write_rows(pool, src, a.slots)
-        reps += 1
-    sec = 2 * (time.perf_counter() - t0) / reps
     alg = a.n_valid * 2 * row * 2 + a.n_tokens * 4
-    out["append_cfg1_1core"] = dict(gbs=alg / sec / 1e9, us=sec * 1e6, reps=reps)
+    for tag, th in (("1core", 1), ("allcores", threads)):
+        sec, reps = rate(lambda: oracle.write_rows(pool, src, a.slots, threads=th), 3, budget_s / 4)
+        out[f"append_cfg1_{tag}"] = dict(gbs=alg / (2 * sec) / 1e9, us=2 * sec * 1e6, reps=reps,
+                                         threads=th)
     del pool
+    # Chunked prefill (config 3): the last 64 query rows of each sequence's
+    # 512-row chunk (positions 4032..4095 over 4,096 keys, bottom-right
+    # causal as in the full chunk); one sequence on one core, one sequence
+    # per thread on every core.
+    p = workload.config3_prefill()
+    rng = np.random.default_rng(3)
+    kp = rng.standard_normal((p.num_blocks, p.block_size, p.num_kv_heads, p.head_dim),
+                             dtype=np.float32)
+    vp = rng.standard_normal(kp.shape, dtype=np.float32)
+    lq = 64
+    for tag, nseq, th in (("1core", 1, 1), ("allcores", min(threads, p.batch), threads)):
+        qs = rng.standard_normal((nseq * lq, p.num_heads, p.head_dim), dtype=np.float32)
+        cu_q = np.arange(nseq + 1, dtype=np.uint32) * lq
+        cu_k = np.arange(nseq + 1, dtype=np.uint32) * p.len_k
+        tabs = [t.tolist() for t in p.tables[:nseq]]
+        flops = 4.0 * p.head_dim * p.num_heads * nseq * sum(
+            pos + 1 for pos in range(p.len_k - lq, p.len_k))
+        sec, reps = rate(lambda: oracle.paged_attention(qs, kp, vp, cu_q, cu_k, tabs,
+                                                        p.head_dim ** -0.5, threads=th),
+                         1, budget_s / 2)
+        out[f"prefill_cfg3_{tag}"] = dict(tflops=flops / sec / 1e12, ms=sec * 1e3, reps=reps,
+                                          threads=th, sample=f"{nseq} seq x {lq} query rows")
+    del kp, vp
     # Block copy (config 4a) over per-layer pools holding just the pairs'
     # blocks, renumbered densely.
     c = workload.config4_block_ops()
@@ -704,18 +737,19 @@ def cpu_baselines_more(decode, budget_s=4.0):
     blk = c.block_size * c.num_kv_heads * c.head_dim * 2
     ks = [np.zeros((len(blocks), blk), dtype=np.uint8) for _ in range(c.num_layers)]
     vs = [np.zeros((len(blocks), blk), dtype=np.uint8) for _ in range(c.num_layers)]
-    oracle.copy_blocks(ks, vs, pairs)  # untimed: first touch of the pools' pages
-    reps, t0 = 0, time.perf_counter()
-    while reps < 1 or time.perf_counter() - t0 < budget_s / 2:
-        oracle.copy_blocks(ks, vs, pairs)
-        reps += 1
-    sec = (time.perf_counter() - t0) / reps
     alg = len(pairs) * 2 * c.num_layers * blk * 2
-    out["copy_cfg4a_1core"] = dict(gbs=alg / sec / 1e9, ms=sec * 1e3, reps=reps)
+    for tag, th in (("1core", 1), ("allcores", threads)):
+        sec, reps = rate(lambda: oracle.copy_blocks(ks, vs, pairs, threads=th), 1, budget_s / 2)
+        out[f"copy_cfg4a_{tag}"] = dict(gbs=alg / sec / 1e9, ms=sec * 1e3, reps=reps, threads=th)
     del ks, vs
-    log("cpu baselines: decode 1 core {:.2f} GB/s, append {:.2f} GB/s, copy {:.2f} GB/s".format(
-        out["decode_cfg2_1core"]["gbs"], out["append_cfg1_1core"]["gbs"],
-        out["copy_cfg4a_1core"]["gbs"]))
+    out["threads_allcores"] = threads
+    out["nproc"] = os.cpu_count()
+    log("cpu baselines: decode 1 core {:.2f} GB/s; append {:.1f}/{:.1f} GB/s; prefill "
+        "{:.4f}/{:.4f} TFLOP/s; copy {:.1f}/{:.1f} GB/s (1 core / {} threads)".format(
+            out["decode_cfg2_1core"]["gbs"], out["append_cfg1_1core"]["gbs"],
+            out["append_cfg1_allcores"]["gbs"], out["prefill_cfg3_1core"]["tflops"],
+            out["prefill_cfg3_allcores"]["tflops"], out["copy_cfg4a_1core"]["gbs"],
+            out["copy_cfg4a_allcores"]["gbs"], threads))
     return out
 
 

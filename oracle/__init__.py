@@ -37,7 +37,7 @@ def lib():
             _b.build()
         L = ctypes.CDLL(str(path))
         L.oracle_write_rows.argtypes = [_u8p, ctypes.c_uint64, ctypes.c_uint64, _u8p,
-                                        _u32p, ctypes.c_uint32, ctypes.c_int, _u32p]
+                                        _u32p, ctypes.c_uint32, ctypes.c_int, _u32p, ctypes.c_int]
         L.oracle_write_rows.restype = ctypes.c_int
         L.oracle_gather_kv.argtypes = [_u8p, ctypes.c_uint64, ctypes.c_uint32, _u32p,
                                        ctypes.c_uint32, ctypes.c_uint32, _u8p]
@@ -63,7 +63,8 @@ def lib():
         L.oracle_import_block.argtypes = [pp, _u64p, ctypes.c_uint32, ctypes.c_uint32, _u8p,
                                           ctypes.c_uint64]
         L.oracle_import_block.restype = ctypes.c_int
-        L.oracle_copy_blocks.argtypes = [pp, _u64p, ctypes.c_uint32, _u32p, ctypes.c_uint32]
+        L.oracle_copy_blocks.argtypes = [pp, _u64p, ctypes.c_uint32, _u32p, ctypes.c_uint32,
+                                         ctypes.c_int]
         L.oracle_copy_blocks.restype = None
         _LIB = L
     return _LIB
@@ -74,10 +75,11 @@ def _p(a: np.ndarray, t):
     return a.ctypes.data_as(t)
 
 
-def write_rows(pool: np.ndarray, src: np.ndarray, slots, force_scatter=False):
+def write_rows(pool: np.ndarray, src: np.ndarray, slots, force_scatter=False, threads=1):
     """write_rows (cache.rs:217-273) in place on `pool` [nb, bs, kvh, d] (or
     any array whose leading dims flatten to slots). Returns the run count;
-    raises ValueError on the reference's error cases."""
+    raises ValueError on the reference's error cases. threads > 1 (CPU
+    baseline timing) is only for slot lists without repeats."""
     slots = np.ascontiguousarray(slots, dtype=np.uint32)
     n = src.shape[0]
     if n != slots.shape[0]:
@@ -91,7 +93,7 @@ def write_rows(pool: np.ndarray, src: np.ndarray, slots, force_scatter=False):
     rc = lib().oracle_write_rows(
         _p(pool.view(np.uint8).reshape(-1), _u8p), num_slots, row_bytes,
         _p(src.view(np.uint8).reshape(-1), _u8p), _p(slots, _u32p), n,
-        int(force_scatter), ctypes.byref(runs))
+        int(force_scatter), ctypes.byref(runs), int(threads))
     if rc != 0:
         raise ValueError("slot is past the end of the cache")
     return runs.value
@@ -213,8 +215,11 @@ def import_block(k_layers, v_layers, block_id, data: bytes) -> None:
                          f"{int(per.sum())}")
 
 
-def copy_blocks(k_layers, v_layers, pairs) -> None:
-    """copy_blocks (backend.rs:781-797), in place."""
+def copy_blocks(k_layers, v_layers, pairs, threads=1) -> None:
+    """copy_blocks (backend.rs:781-797), in place. threads > 1 (CPU baseline
+    timing) is only for pairs whose destinations are distinct and no pair's
+    source."""
     pairs = np.ascontiguousarray(np.asarray(pairs, dtype=np.uint32).reshape(-1, 2))
     ptrs, per, n = _buffers(k_layers, v_layers)
-    lib().oracle_copy_blocks(ptrs, _p(per, _u64p), n, _p(pairs, _u32p), pairs.shape[0])
+    lib().oracle_copy_blocks(ptrs, _p(per, _u64p), n, _p(pairs, _u32p), pairs.shape[0],
+                             int(threads))

@@ -28,10 +28,13 @@
  * padded-slot convention, not present in the reference; see slot_mapping
  * docs). Returns 0, -1 if a slot is past the end (cache.rs:236-240), or the
  * number of runs as a positive count via *runs_out. force_scatter selects
- * the scatter branch (cache.rs:265-272) regardless of the run count. */
+ * the scatter branch (cache.rs:265-272) regardless of the run count.
+ * nthreads > 1 spreads the copies over OpenMP threads (for timing the CPU
+ * baseline on every core); the result equals the serial one only when no
+ * two kept tokens share a slot, which is what callers passing it ensure. */
 int oracle_write_rows(uint8_t* pool, uint64_t num_slots, uint64_t row_bytes,
                       const uint8_t* src, const uint32_t* slots, uint32_t n,
-                      int force_scatter, uint32_t* runs_out) {
+                      int force_scatter, uint32_t* runs_out, int nthreads) {
   uint32_t* keep = (uint32_t*)malloc(sizeof(uint32_t) * (n ? n : 1));
   uint32_t m = 0;
   for (uint32_t i = 0; i < n; ++i)
@@ -68,6 +71,7 @@ int oracle_write_rows(uint8_t* pool, uint64_t num_slots, uint64_t row_bytes,
     }
   } else {
     /* cache.rs:265-272: one scatter of every row to its slot. */
+#pragma omp parallel for num_threads(nthreads > 0 ? nthreads : 1) schedule(static)
     for (uint32_t i = 0; i < m; ++i)
       memcpy(pool + (uint64_t)slots[keep[i]] * row_bytes,
              src + (uint64_t)keep[i] * row_bytes, row_bytes);
@@ -284,10 +288,14 @@ int oracle_import_block(uint8_t* const* bufs, const uint64_t* blk_bytes, uint32_
 }
 
 /* copy_blocks (backend.rs:781-797): pairs in order; for each, every layer,
- * K then V (`nbuf` = 2L, k[l] at l and v[l] at L + l), dst := src. */
+ * K then V (`nbuf` = 2L, k[l] at l and v[l] at L + l), dst := src.
+ * nthreads > 1 spreads the pairs over OpenMP threads (CPU-baseline timing);
+ * that equals the ordered result only when no destination is also a source
+ * or a second destination, which callers passing it ensure. */
 void oracle_copy_blocks(uint8_t* const* bufs, const uint64_t* blk_bytes, uint32_t nbuf,
-                        const uint32_t* pairs, uint32_t n_pairs) {
+                        const uint32_t* pairs, uint32_t n_pairs, int nthreads) {
   const uint32_t layers = nbuf / 2;
+#pragma omp parallel for num_threads(nthreads > 0 ? nthreads : 1) schedule(static)
   for (uint32_t p = 0; p < n_pairs; ++p) {
     const uint32_t src = pairs[2 * p], dst = pairs[2 * p + 1];
     for (uint32_t l = 0; l < layers; ++l)
