@@ -98,6 +98,22 @@ def test_misaligned_pools_and_unknown_flags_are_refused():
     assert need > 0
 
 
+def test_launches_too_large_for_one_grid_are_refused():
+    """A batch whose prefill or VALU grid would pass 2^32 workgroups is
+    refused before anything is launched, not truncated."""
+    L = _lib.lib()
+    # MFMA prefill: 65,535 sequences x 2^24 query rows x 4 heads per group.
+    args = [1, 1, 1, 1, 1, 65535, 1, 1 << 24, 1 << 24, 8, 0.1, -1, 0]
+    assert L.vapi_paged_attention_ex(pool(), 0, *args, _lib.ATTN_NO_DECODE_ROWS, None, 0,
+                                     None) == _lib.EUNSUP
+    assert b"too large" in L.vapi_kv_last_error()
+    # VALU path (f32 pool): row tiles x kv heads x sequences x key chunks.
+    args = [1, 1, 1, 1, 1, 60000, 1, 1 << 20, 1 << 20, 8, 0.1, -1, 0]
+    assert L.vapi_paged_attention_ex(pool(dtype=_lib.F32), 0, *args, 0, 1, 1 << 62,
+                                     None) == _lib.EUNSUP
+    assert b"too large" in L.vapi_kv_last_error()
+
+
 def test_prepared_attention_flags_follow_the_host_lengths():
     from vapi_amd.attention import ATTN_DETERMINISTIC, ATTN_NO_DECODE_ROWS, PreparedAttention
     mk = lambda lq, lk: ForwardBatch(cu_seqlens_q=np.concatenate([[0], np.cumsum(lq)]).tolist(),

@@ -239,6 +239,10 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   // Refused before anything is launched (a refused call writes nothing).
   if (mfma_ok(pool, num_heads) && max_seqlen_q > 1 && batch > 65535)
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: %u prefill sequences > 65535", batch);
+  if (mfma_ok(pool, num_heads) && max_seqlen_q > 1 &&
+      prefill_grid(batch, pool->num_kv_heads, num_heads / pool->num_kv_heads, max_seqlen_q) >
+          0xFFFFFFFFull)
+    VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: prefill batch too large for one launch");
   // A batch the caller says has no decode rows (and which is not a fused
   // decode step) runs one kernel: the prefill kernel then takes every row,
   // len_q == 1 included, so the result does not depend on the hint. It needs
@@ -304,6 +308,8 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   } else {
     if (g.d > 256)
       VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: head_dim %u > 256", g.d);
+    if (generic_grid(batch, g.kvh, num_heads / g.kvh, max_seqlen_q, max_seqlen_k) > 0xFFFFFFFFull)
+      VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: batch too large for one launch");
     launch_generic(a, max_seqlen_q, max_seqlen_k, g.d, pool->dtype, workspace, s);
   }
   VK_LAUNCHED("paged_attention");

@@ -416,12 +416,19 @@ size_t decode_workspace_bytes(uint32_t batch, uint32_t kvh, uint32_t group,
                               uint32_t head_dim, uint32_t num_waves);
 void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, bool bf16, hipStream_t s);
 // Prefill rows (len_q > 1); same dtypes and head dims.
+// Workgroups of the prefill launch (query tiles x kv heads x sequences); a
+// launch needs it below 2^32.
+uint64_t prefill_grid(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t max_q);
 void launch_prefill(const AttnArgs& a, uint32_t max_q, uint32_t head_dim, bool bf16,
                     hipStream_t s);
 // Any row, any dtype, head_dim <= 256 (VALU); split contexts combine their
 // partials through `workspace` (generic_workspace_bytes).
 void launch_generic(const AttnArgs& a, uint32_t max_q, uint32_t max_k, uint32_t head_dim,
                     uint32_t dtype, void* workspace, hipStream_t s);
+// Workgroups of the VALU kernel's launch (row tiles x kv heads x sequences
+// x key chunks); a launch needs it below 2^32.
+uint64_t generic_grid(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t max_q,
+                      uint32_t max_k);
 size_t generic_workspace_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t head_dim,
                                uint32_t max_q, uint32_t max_k);
 // Persistent decode waves for the current device (CUs x 8).

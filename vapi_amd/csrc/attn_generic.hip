@@ -322,6 +322,13 @@ __global__ __launch_bounds__(kGenThreads) void paged_attn_generic_merge(
   }
 }
 
+uint64_t generic_grid(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t max_q,
+                      uint32_t max_k) {
+  const uint64_t row_tiles = ((uint64_t)max_q * group + kGenRows - 1) / kGenRows;
+  const uint64_t n_chunks = std::max<uint64_t>(((uint64_t)max_k + kGenChunk - 1) / kGenChunk, 1);
+  return row_tiles * kvh * batch * n_chunks;
+}
+
 size_t generic_workspace_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t head_dim,
                                uint32_t max_q, uint32_t max_k) {
   const uint64_t n_chunks = ((uint64_t)max_k + kGenChunk - 1) / kGenChunk;
@@ -333,7 +340,7 @@ size_t generic_workspace_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uin
 
 void launch_generic(const AttnArgs& a, uint32_t max_q, uint32_t max_k, uint32_t head_dim,
                     uint32_t dtype, void* workspace, hipStream_t s) {
-  const uint32_t row_tiles = (max_q * a.group + kGenRows - 1) / kGenRows;
+  const uint32_t row_tiles = (uint32_t)(((uint64_t)max_q * a.group + kGenRows - 1) / kGenRows);
   const uint32_t n_chunks = (uint32_t)(((uint64_t)max_k + kGenChunk - 1) / kGenChunk);
   const uint64_t n = (uint64_t)row_tiles * a.kvh * a.batch * std::max(n_chunks, 1u);
   float* part = (float*)((char*)workspace + kGenPartOffset);

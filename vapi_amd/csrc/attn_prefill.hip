@@ -386,6 +386,11 @@ extern "C" int vapi_pf_trace_copy(void* host) {
 namespace vk {
 #endif
 
+uint64_t prefill_grid(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t max_q) {
+  constexpr uint64_t rows = 16 * VK_PF_RT * kPfWaves;
+  return ((uint64_t)max_q * group + rows - 1) / rows * kvh * batch;
+}
+
 void launch_prefill(const AttnArgs& a_in, uint32_t max_q, uint32_t head_dim, bool bf16,
                     hipStream_t s) {
   AttnArgs a = a_in;
@@ -395,7 +400,7 @@ void launch_prefill(const AttnArgs& a_in, uint32_t max_q, uint32_t head_dim, boo
   a.trace = (uint64_t*)tp;
 #endif
   constexpr uint32_t rows = 16 * VK_PF_RT * kPfWaves;
-  const uint32_t qtiles = (max_q * a.group + rows - 1) / rows;
+  const uint32_t qtiles = (uint32_t)(((uint64_t)max_q * a.group + rows - 1) / rows);
   const uint64_t n = (uint64_t)qtiles * a.kvh * a.batch;
   const dim3 grid((uint32_t)n), block(kPfThreads);
 // head_dim 64 fits in 128 registers: two workgroups per CU (four waves per
