@@ -38,8 +38,8 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t lin, uint32_t n) {
 // ---- K and V staged by direct global-to-LDS loads --------------------------
 //
 // Rows keep the pool's order (key rows of D elements); each row's 16-byte
-// chunks are XOR-swizzled by the row index so that the fragment reads below
-// spread over the LDS banks. V^T fragments for O^T = V^T P^T are read
+// chunks are XOR-swizzled by a function of the row index (pf_swz) so that
+// the fragment reads below spread over the LDS banks. V^T fragments for O^T = V^T P^T are read
 // transposed from the V rows with ds_read_b64_tr_b16: for a 16-lane group,
 // lane i receives element i % 4 of the 64-bit chunk addressed by lane
 // 4 j + i / 4, for j = 0..3 (measured on gfx950), so lane 4 j + q pointing
@@ -50,11 +50,28 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t lin, uint32_t n) {
 using LdsVoid = __attribute__((address_space(3))) void;
 
 
+// The XOR swizzle of key row r's 16-byte chunks. D = 128 (16 chunks, a row
+// is 256 bytes: every row starts at bank 0): the row index rotated left by
+// one bit, a bijection on 0..15, so the 16 rows a K fragment read touches
+// use 16 distinct chunk positions for any chunk, and the 8 rows of one
+// half-wave of a transposing V read (rows 0..7 or 8..15, chunks 2t, 2t + 1)
+// land on 8 distinct chunk pairs (XOR with r alone would put rows 2m and
+// 2m + 1 on the same pair: a 2-way bank conflict). D = 64: r mod 8.
+template <int D>
+__device__ __forceinline__ uint32_t pf_swz(uint32_t r) {
+  if constexpr (D == 128) {
+    const uint32_t x = r & 15;
+    return ((x << 1) | (x >> 3)) & 15;
+  } else {
+    return r & (D / 8 - 1);
+  }
+}
+
 // Element offset of 16-byte chunk p of key row r (0..31) in a step buffer.
 template <int D>
 __device__ __forceinline__ uint32_t pf_chunk(uint32_t r, uint32_t p) {
   constexpr uint32_t CPR = D / 8;  // chunks per row
-  return (r * CPR + (p ^ (r & (CPR - 1)))) * 8;
+  return (r * CPR + (p ^ pf_swz<D>(r))) * 8;
 }
 
 // Issues the step at s0 into buffer b: each thread moves one 16-byte chunk
@@ -77,7 +94,7 @@ __device__ __forceinline__ void pf_dma(uint16_t* kdst, uint16_t* vdst, const uin
   auto one = [&](const T* base_t, uint16_t* buf, uint32_t slot, uint32_t wslot0)
                  __attribute__((always_inline)) {
     const uint32_t r = slot / CPR, pos = slot % CPR;
-    const uint32_t p = pos ^ (r & (CPR - 1));
+    const uint32_t p = pos ^ pf_swz<D>(r);
     // A wave's slots cover 64 / CPR whole rows of one 16-key tile.
     const bool second = __builtin_amdgcn_readfirstlane(r) >= 16;
     const T* base = base_t + (second ? off1 : off0);
