@@ -55,8 +55,10 @@ using LdsVoid = __attribute__((address_space(3))) void;
 // one bit, a bijection on 0..15, so the 16 rows a K fragment read touches
 // use 16 distinct chunk positions for any chunk, and the 8 rows of one
 // half-wave of a transposing V read (rows 0..7 or 8..15, chunks 2t, 2t + 1)
-// land on 8 distinct chunk pairs (XOR with r alone would put rows 2m and
-// 2m + 1 on the same pair: a 2-way bank conflict). D = 64: r mod 8.
+// use 8 distinct chunk pairs (XOR with r alone puts rows 2m and 2m + 1 on
+// the same pair). Measured 0.5-1% faster than XOR with r; the bank-conflict
+// counter reads the same either way (2 cycles per transposing read).
+// D = 64: r mod 8.
 template <int D>
 __device__ __forceinline__ uint32_t pf_swz(uint32_t r) {
   if constexpr (D == 128) {
