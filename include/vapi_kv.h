@@ -190,7 +190,9 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
  *   (bf16/f16, head_dim 64 or 128) the workspace size depends on the batch,
  *   the heads and the GPU's CU count, not on the lengths; on the VALU path
  *   (f32 pools, other head dims) it holds the split-context partials and
- *   grows with max_seqlen_q * max_seqlen_k (0 while max_seqlen_k <= 512).
+ *   grows with the batch, max_seqlen_q and max_seqlen_k (0 while
+ *   max_seqlen_k <= 64; small batches split their keys into chunks of 64
+ *   to 512 keys to fill the GPU).
  */
 size_t vapi_paged_attention_workspace_size(const vapi_kv_pool* pool,
                                            uint32_t batch, uint32_t num_heads,

@@ -15,10 +15,13 @@
 // needs.
 //
 // Long contexts are split: workgroup (sequence, kv head, row tile, chunk)
-// takes keys [chunk * kGenChunk, (chunk + 1) * kGenChunk). When a row tile's
-// visible keys span more than one chunk, each chunk writes (m, l, o) per row
-// to the workspace and paged_attn_generic_merge combines them; a tile whose
-// keys fit one chunk writes its output directly.
+// takes keys [chunk * C, (chunk + 1) * C), C = 512 keys, or down to 64 when
+// that leaves fewer than two workgroups per CU (a few short decode rows).
+// When a row tile's visible keys span more than one chunk, each chunk writes
+// (m, l, o) per row to the workspace and paged_attn_generic_merge combines
+// them; a tile whose keys fit one chunk writes its output directly. Head
+// dims 64, 128 and 256 are compiled as constants (unrolled dot products,
+// 4-element staging loads); others take the runtime-D kernel.
 #include <algorithm>
 
 #include "attn_common.hpp"
@@ -28,10 +31,8 @@ namespace vk {
 constexpr uint32_t kGenRows = 16;   // rows per workgroup
 constexpr uint32_t kGenKeys = 32;   // keys per LDS tile
 constexpr uint32_t kGenThreads = 256;
-#ifndef VK_GEN_CHUNK
-#define VK_GEN_CHUNK 512
-#endif
-constexpr uint32_t kGenChunk = VK_GEN_CHUNK;  // keys per workgroup
+constexpr uint32_t kGenChunk = 512;  // keys per workgroup, at most
+constexpr uint32_t kGenMinChunk = 64;
 // Dynamic LDS of the largest tile (head_dim 256: 84 KiB), past the 64 KiB
 // a launch gets without asking.
 constexpr size_t kGenMaxDynLds = 96 * 1024;
@@ -44,23 +45,38 @@ __host__ __device__ __forceinline__ uint32_t gen_k_stride(uint32_t d) {
 }
 
 // Chunks a tile with visible keys [klo, khi] spans: [c_first, c_last].
-__device__ __forceinline__ void tile_chunks(int32_t klo, int32_t khi, int32_t& c_first,
-                                            int32_t& c_last) {
-  c_first = klo / (int32_t)kGenChunk;
-  c_last = khi / (int32_t)kGenChunk;
+__device__ __forceinline__ void tile_chunks(int32_t klo, int32_t khi, uint32_t chunk,
+                                            int32_t& c_first, int32_t& c_last) {
+  c_first = klo / (int32_t)chunk;
+  c_last = khi / (int32_t)chunk;
+}
+
+// Four consecutive elements as f32 (16 bytes of f32, 8 of bf16 / f16).
+template <typename T>
+__device__ __forceinline__ float4 load4(const T* p);
+template <>
+__device__ __forceinline__ float4 load4<float>(const float* p) {
+  return *(const float4*)p;
+}
+template <typename T>
+__device__ __forceinline__ float4 load4(const T* p) {
+  const uint2 x = *(const uint2*)p;
+  const T* h = (const T*)&x;
+  return make_float4(to_f32(h[0]), to_f32(h[1]), to_f32(h[2]), to_f32(h[3]));
 }
 
 // Partials of item i: (m, l) at part + i * kGenRows * (D + 2) + 2 r, then
 // o at + 2 kGenRows + r * D.
-template <typename T>
+template <typename T, int DT>
 __global__ __launch_bounds__(kGenThreads) void paged_attn_generic(AttnArgs a, uint32_t head_dim,
                                                                   uint32_t row_tiles,
                                                                   uint32_t n_chunks,
+                                                                  uint32_t chunk_keys,
                                                                   float* __restrict__ part) {
-  extern __shared__ float lds[];
+  extern __shared__ __attribute__((aligned(16))) float lds[];
   // K rows padded against bank conflicts: by 4 words (keeping 16-byte
   // alignment) when head_dim is a multiple of 4, else by one.
-  const uint32_t D = head_dim, KS = gen_k_stride(head_dim);
+  const uint32_t D = DT ? DT : head_dim, KS = gen_k_stride(D);
   float* ks = lds;                              // [32][KS]
   float* vs = ks + kGenKeys * KS;               // [32][D]
   float* qs = vs + kGenKeys * D;                // [16][D]
@@ -88,11 +104,11 @@ __global__ __launch_bounds__(kGenThreads) void paged_attn_generic(AttnArgs a, ui
   key_range(offset + (int32_t)(row0 / G), len_k, a.wl, a.wr, klo, unused);
   key_range(offset + (int32_t)((row0 + rows - 1) / G), len_k, a.wl, a.wr, unused, khi);
   int32_t c_first, c_last;
-  tile_chunks(klo, khi, c_first, c_last);
+  tile_chunks(klo, khi, chunk_keys, c_first, c_last);
   if (khi < klo || (int32_t)chunk < c_first || (int32_t)chunk > c_last) return;
   const bool split = c_last > c_first;
-  klo = max(klo, (int32_t)(chunk * kGenChunk));
-  khi = min(khi, (int32_t)((chunk + 1) * kGenChunk) - 1);
+  klo = max(klo, (int32_t)(chunk * chunk_keys));
+  khi = min(khi, (int32_t)((chunk + 1) * chunk_keys) - 1);
 
   for (uint32_t i = tid; i < kGenRows * D; i += kGenThreads) {
     const uint32_t r = i / D, d = i - r * D;
@@ -112,7 +128,7 @@ __global__ __launch_bounds__(kGenThreads) void paged_attn_generic(AttnArgs a, ui
   // pr, d = pd + 16 i).
   const uint32_t sk = tid & 31, sr = tid >> 5;  // 8 rows per pass, 2 passes
   const uint32_t pr = tid >> 4, pd = tid & 15;  // 16 rows, d stride 16
-  constexpr int kMaxDPer = 256 / 16;
+  constexpr int kMaxDPer = DT ? (DT + 15) / 16 : 256 / 16;
   float acc[kMaxDPer];
 #pragma unroll
   for (int i = 0; i < kMaxDPer; ++i) acc[i] = 0.f;
@@ -139,8 +155,38 @@ __global__ __launch_bounds__(kGenThreads) void paged_attn_generic(AttnArgs a, ui
                                 : ~0ull;
     }
     __syncthreads();
-    // Stage keys c0 .. c0 + 31 (past khi: zeros, never visible), eight
-    // elements at a time: all eight loads are issued before their stores.
+    // Stage keys c0 .. c0 + 31 (past khi: zeros, never visible).
+    if constexpr (DT > 0 && DT % 4 == 0) {
+      // Four consecutive elements per load; every load issued before the
+      // first store.
+      constexpr uint32_t kC4 = kGenKeys * DT / 4;
+      constexpr uint32_t kPer = (kC4 + kGenThreads - 1) / kGenThreads;
+      float4 kx[kPer], vx[kPer];
+#pragma unroll
+      for (uint32_t u = 0; u < kPer; ++u) {
+        const uint32_t c = tid + u * kGenThreads;
+        kx[u] = vx[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (c < kC4) {
+          const uint32_t key = c * 4 / DT, d = c * 4 % DT;
+          const uint64_t off = key_off[key];
+          if (off != ~0ull) {
+            kx[u] = load4<T>(kb + off + d);
+            vx[u] = load4<T>(vb + off + d);
+          }
+        }
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < kPer; ++u) {
+        const uint32_t c = tid + u * kGenThreads;
+        if (c < kC4) {
+          const uint32_t key = c * 4 / DT, d = c * 4 % DT;
+          *(float4*)(ks + key * KS + d) = kx[u];
+          *(float4*)(vs + key * DT + d) = vx[u];
+        }
+      }
+    } else
+    // Any head_dim: eight elements at a time, all eight loads issued before
+    // their stores.
     {
       constexpr int kBatch = 8;
       uint32_t k = k_first, d = d_first;
@@ -265,11 +311,11 @@ __global__ __launch_bounds__(kGenThreads) void paged_attn_generic(AttnArgs a, ui
 
 // One workgroup per (sequence, kv head, row tile) whose keys were split:
 // thread (row, d-slice) combines the chunks' partials.
-template <typename T>
+template <typename T, int DT>
 __global__ __launch_bounds__(kGenThreads) void paged_attn_generic_merge(
-    AttnArgs a, uint32_t head_dim, uint32_t row_tiles, uint32_t n_chunks,
+    AttnArgs a, uint32_t head_dim, uint32_t row_tiles, uint32_t n_chunks, uint32_t chunk_keys,
     const float* __restrict__ part) {
-  const uint32_t D = head_dim;
+  const uint32_t D = DT ? DT : head_dim;
   const uint32_t tid = threadIdx.x;
   const uint32_t rt = blockIdx.x % row_tiles, rest = blockIdx.x / row_tiles;
   const uint32_t kh = rest % a.kvh, seq = rest / a.kvh;
@@ -284,7 +330,7 @@ __global__ __launch_bounds__(kGenThreads) void paged_attn_generic_merge(
   int32_t klo, khi, unused, c_first, c_last;
   key_range(offset + (int32_t)(row0 / G), len_k, a.wl, a.wr, klo, unused);
   key_range(offset + (int32_t)((row0 + rows - 1) / G), len_k, a.wl, a.wr, unused, khi);
-  tile_chunks(klo, khi, c_first, c_last);
+  tile_chunks(klo, khi, chunk_keys, c_first, c_last);
   if (khi < klo || c_last == c_first) return;
   const uint32_t pr = tid >> 4, pd = tid & 15;
   if (pr >= rows) return;
@@ -296,7 +342,7 @@ __global__ __launch_bounds__(kGenThreads) void paged_attn_generic_merge(
     if (pc[2 * pr + 1] > 0.f) M = fmaxf(M, pc[2 * pr]);
   }
   float L = 0.f;
-  constexpr int kMaxDPer = 256 / 16;
+  constexpr int kMaxDPer = DT ? (DT + 15) / 16 : 256 / 16;
   float o[kMaxDPer];
 #pragma unroll
   for (int i = 0; i < kMaxDPer; ++i) o[i] = 0.f;
@@ -322,51 +368,73 @@ __global__ __launch_bounds__(kGenThreads) void paged_attn_generic_merge(
   }
 }
 
+// Keys per workgroup: 512, halved down to 64 while that leaves fewer than
+// two workgroups per CU of a 256-CU GPU (one rule for the launch and the
+// workspace size).
+static uint32_t gen_chunk_keys(uint64_t tiles, uint32_t max_k) {
+  uint32_t c = kGenChunk;
+  while (c > kGenMinChunk && tiles * (((uint64_t)max_k + c - 1) / c) < 512) c /= 2;
+  return c;
+}
+
 uint64_t generic_grid(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t max_q,
                       uint32_t max_k) {
   const uint64_t row_tiles = ((uint64_t)max_q * group + kGenRows - 1) / kGenRows;
-  const uint64_t n_chunks = std::max<uint64_t>(((uint64_t)max_k + kGenChunk - 1) / kGenChunk, 1);
-  return row_tiles * kvh * batch * n_chunks;
+  const uint64_t tiles = row_tiles * kvh * batch;
+  const uint32_t c = gen_chunk_keys(tiles, max_k);
+  return tiles * std::max<uint64_t>(((uint64_t)max_k + c - 1) / c, 1);
 }
 
 size_t generic_workspace_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t head_dim,
                                uint32_t max_q, uint32_t max_k) {
-  const uint64_t n_chunks = ((uint64_t)max_k + kGenChunk - 1) / kGenChunk;
-  if (n_chunks <= 1) return 0;
   const uint64_t row_tiles = ((uint64_t)max_q * group + kGenRows - 1) / kGenRows;
-  return kGenPartOffset +
-         (size_t)(row_tiles * kvh * batch * n_chunks * kGenRows * (head_dim + 2) * sizeof(float));
+  const uint64_t tiles = row_tiles * kvh * batch;
+  const uint32_t c = gen_chunk_keys(tiles, max_k);
+  const uint64_t n_chunks = ((uint64_t)max_k + c - 1) / c;
+  if (n_chunks <= 1) return 0;
+  return kGenPartOffset + (size_t)(tiles * n_chunks * kGenRows * (head_dim + 2) * sizeof(float));
 }
 
 void launch_generic(const AttnArgs& a, uint32_t max_q, uint32_t max_k, uint32_t head_dim,
                     uint32_t dtype, void* workspace, hipStream_t s) {
   const uint32_t row_tiles = (uint32_t)(((uint64_t)max_q * a.group + kGenRows - 1) / kGenRows);
-  const uint32_t n_chunks = (uint32_t)(((uint64_t)max_k + kGenChunk - 1) / kGenChunk);
-  const uint64_t n = (uint64_t)row_tiles * a.kvh * a.batch * std::max(n_chunks, 1u);
+  const uint64_t tiles = (uint64_t)row_tiles * a.kvh * a.batch;
+  const uint32_t chunk_keys = gen_chunk_keys(tiles, max_k);
+  const uint32_t n_chunks = (uint32_t)(((uint64_t)max_k + chunk_keys - 1) / chunk_keys);
+  const uint64_t n = tiles * std::max(n_chunks, 1u);
   float* part = (float*)((char*)workspace + kGenPartOffset);
   const size_t lds = ((size_t)kGenKeys * gen_k_stride(head_dim) + (size_t)kGenKeys * head_dim +
                       (size_t)kGenRows * head_dim + kGenRows * kGenKeys + 3 * kGenRows) *
                      sizeof(float);
-#define VK_GEN(T)                                                                            \
+#define VK_GEN(T, DT)                                                                        \
   do {                                                                                       \
     static bool lds_set = false;                                                             \
     if (lds > 64 * 1024 && !lds_set) {                                                       \
-      if (hipFuncSetAttribute((const void*)paged_attn_generic<T>,                            \
+      if (hipFuncSetAttribute((const void*)paged_attn_generic<T, DT>,                        \
                               hipFuncAttributeMaxDynamicSharedMemorySize,                    \
                               (int)kGenMaxDynLds) == hipSuccess)                             \
         lds_set = true;                                                                      \
     }                                                                                        \
-    hipLaunchKernelGGL((paged_attn_generic<T>), dim3((uint32_t)n), dim3(kGenThreads), lds, s, \
-                       a, head_dim, row_tiles, std::max(n_chunks, 1u), part);                \
+    hipLaunchKernelGGL((paged_attn_generic<T, DT>), dim3((uint32_t)n), dim3(kGenThreads), lds, \
+                       s, a, head_dim, row_tiles, std::max(n_chunks, 1u), chunk_keys, part); \
     if (n_chunks > 1)                                                                        \
-      hipLaunchKernelGGL((paged_attn_generic_merge<T>), dim3(row_tiles * a.kvh * a.batch),   \
-                         dim3(kGenThreads), 0, s, a, head_dim, row_tiles, n_chunks, part);   \
+      hipLaunchKernelGGL((paged_attn_generic_merge<T, DT>), dim3((uint32_t)tiles),           \
+                         dim3(kGenThreads), 0, s, a, head_dim, row_tiles, n_chunks,          \
+                         chunk_keys, part);                                                  \
+  } while (0)
+#define VK_GEN_D(T)                                  \
+  do {                                               \
+    if (head_dim == 128) VK_GEN(T, 128);             \
+    else if (head_dim == 64) VK_GEN(T, 64);          \
+    else if (head_dim == 256) VK_GEN(T, 256);        \
+    else VK_GEN(T, 0);                               \
   } while (0)
   switch (dtype) {
-    case VAPI_KV_F32: VK_GEN(float); break;
-    case VAPI_KV_BF16: VK_GEN(bf16_t); break;
-    default: VK_GEN(f16_t); break;
+    case VAPI_KV_F32: VK_GEN_D(float); break;
+    case VAPI_KV_BF16: VK_GEN_D(bf16_t); break;
+    default: VK_GEN_D(f16_t); break;
   }
+#undef VK_GEN_D
 #undef VK_GEN
 }
 
