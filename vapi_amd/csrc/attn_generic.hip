@@ -146,35 +146,36 @@ __global__ __launch_bounds__(kGenThreads) void paged_attn_generic(AttnArgs a, ui
   const uint32_t n_cols = (uint32_t)khi / a.block_size - col0 + 1;
   for (uint32_t c = tid; c < n_cols; c += kGenThreads)
     blk_ids[c] = min(table[min(col0 + c, a.max_blocks - 1)], a.last_blk);
+  // Constant head dims: each thread's 4-element chunks of the next tile are
+  // loaded into registers while the current tile is computed (one HBM round
+  // trip hidden per tile).
+  constexpr bool kVec = DT > 0 && DT % 4 == 0;
+  constexpr uint32_t kC4 = kVec ? kGenKeys * DT / 4 : 1;
+  constexpr uint32_t kPer = (kC4 + kGenThreads - 1) / kGenThreads;
+  float4 kx[kPer], vx[kPer];
+  auto fetch = [&](int32_t cs) __attribute__((always_inline)) {
+#pragma unroll
+    for (uint32_t u = 0; u < kPer; ++u) {
+      const uint32_t c = tid + u * kGenThreads;
+      kx[u] = vx[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      const int32_t key = cs + (int32_t)(c * 4 / D);
+      if (c < kC4 && key <= khi) {
+        const uint32_t d = c * 4 % D;
+        const uint64_t off = (uint64_t)blk_ids[(uint32_t)key / a.block_size - col0] * a.blk_e +
+                             (uint64_t)((uint32_t)key % a.block_size) * a.tok_e;
+        kx[u] = load4<T>(kb + off + d);
+        vx[u] = load4<T>(vb + off + d);
+      }
+    }
+  };
+  if constexpr (kVec) {
+    __syncthreads();  // blk_ids
+    fetch(klo);
+  }
   for (int32_t c0 = klo; c0 <= khi; c0 += (int32_t)kGenKeys) {
     __syncthreads();  // the previous tile's K, V, P and key offsets are consumed
-    if (tid < kGenKeys) {
-      const int32_t key = c0 + (int32_t)tid;
-      key_off[tid] = key <= khi ? (uint64_t)blk_ids[(uint32_t)key / a.block_size - col0] * a.blk_e +
-                                      (uint64_t)((uint32_t)key % a.block_size) * a.tok_e
-                                : ~0ull;
-    }
-    __syncthreads();
     // Stage keys c0 .. c0 + 31 (past khi: zeros, never visible).
-    if constexpr (DT > 0 && DT % 4 == 0) {
-      // Four consecutive elements per load; every load issued before the
-      // first store.
-      constexpr uint32_t kC4 = kGenKeys * DT / 4;
-      constexpr uint32_t kPer = (kC4 + kGenThreads - 1) / kGenThreads;
-      float4 kx[kPer], vx[kPer];
-#pragma unroll
-      for (uint32_t u = 0; u < kPer; ++u) {
-        const uint32_t c = tid + u * kGenThreads;
-        kx[u] = vx[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (c < kC4) {
-          const uint32_t key = c * 4 / DT, d = c * 4 % DT;
-          const uint64_t off = key_off[key];
-          if (off != ~0ull) {
-            kx[u] = load4<T>(kb + off + d);
-            vx[u] = load4<T>(vb + off + d);
-          }
-        }
-      }
+    if constexpr (kVec) {
 #pragma unroll
       for (uint32_t u = 0; u < kPer; ++u) {
         const uint32_t c = tid + u * kGenThreads;
@@ -184,39 +185,49 @@ __global__ __launch_bounds__(kGenThreads) void paged_attn_generic(AttnArgs a, ui
           *(float4*)(vs + key * DT + d) = vx[u];
         }
       }
-    } else
-    // Any head_dim: eight elements at a time, all eight loads issued before
-    // their stores.
-    {
-      constexpr int kBatch = 8;
-      uint32_t k = k_first, d = d_first;
-      for (uint32_t u0 = 0; u0 < n_el; u0 += kBatch) {
-        float kx[kBatch], vx[kBatch];
-        uint32_t kk[kBatch], dd[kBatch];
+      __syncthreads();
+      if (c0 + (int32_t)kGenKeys <= khi) fetch(c0 + (int32_t)kGenKeys);
+    } else {
+      if (tid < kGenKeys) {
+        const int32_t key = c0 + (int32_t)tid;
+        key_off[tid] = key <= khi ? (uint64_t)blk_ids[(uint32_t)key / a.block_size - col0] * a.blk_e +
+                                        (uint64_t)((uint32_t)key % a.block_size) * a.tok_e
+                                  : ~0ull;
+      }
+      __syncthreads();
+      // Any head_dim: eight elements at a time, all eight loads issued
+      // before their stores.
+      {
+        constexpr int kBatch = 8;
+        uint32_t k = k_first, d = d_first;
+        for (uint32_t u0 = 0; u0 < n_el; u0 += kBatch) {
+          float kx1[kBatch], vx1[kBatch];
+          uint32_t kk[kBatch], dd[kBatch];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-          kk[u] = k, dd[u] = d;
-          kx[u] = 0.f, vx[u] = 0.f;
-          if (u0 + u < n_el) {
-            const uint64_t off = key_off[k];
-            if (off != ~0ull) {
-              kx[u] = to_f32(kb[off + d]);
-              vx[u] = to_f32(vb[off + d]);
+          for (int u = 0; u < kBatch; ++u) {
+            kk[u] = k, dd[u] = d;
+            kx1[u] = 0.f, vx1[u] = 0.f;
+            if (u0 + u < n_el) {
+              const uint64_t off = key_off[k];
+              if (off != ~0ull) {
+                kx1[u] = to_f32(kb[off + d]);
+                vx1[u] = to_f32(vb[off + d]);
+              }
             }
+            d += d_step, k += k_step;
+            if (d >= D) d -= D, ++k;
           }
-          d += d_step, k += k_step;
-          if (d >= D) d -= D, ++k;
-        }
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-          if (u0 + u < n_el) {
-            ks[kk[u] * KS + dd[u]] = kx[u];
-            vs[kk[u] * D + dd[u]] = vx[u];
+          for (int u = 0; u < kBatch; ++u) {
+            if (u0 + u < n_el) {
+              ks[kk[u] * KS + dd[u]] = kx1[u];
+              vs[kk[u] * D + dd[u]] = vx1[u];
+            }
           }
         }
       }
+      __syncthreads();
     }
-    __syncthreads();
     // Scores and the online softmax, two passes of 8 rows.
 #pragma unroll
     for (uint32_t pass = 0; pass < 2; ++pass) {
