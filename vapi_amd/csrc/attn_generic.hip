@@ -23,6 +23,7 @@
 // dims 64, 128 and 256 are compiled as constants (unrolled dot products,
 // 4-element staging loads); others take the runtime-D kernel.
 #include <algorithm>
+#include <type_traits>
 
 #include "attn_common.hpp"
 
@@ -124,10 +125,15 @@ __global__ __launch_bounds__(kGenThreads) void paged_attn_generic(AttnArgs a, ui
   const uint32_t* table = a.table + (uint64_t)seq * a.max_blocks;
   const T* kb = (const T*)a.k + kh * a.head_e;
   const T* vb = (const T*)a.v + kh * a.head_e;
-  // Score phase: thread -> (row sr + 8 i, key sk); PV phase: thread -> (row
-  // pr, d = pd + 16 i).
-  const uint32_t sk = tid & 31, sr = tid >> 5;  // 8 rows per pass, 2 passes
-  const uint32_t pr = tid >> 4, pd = tid & 15;  // 16 rows, d stride 16
+  // Score phase: thread -> (row sr + 8 i, key sk), 8 rows per pass (one
+  // pass when the tile has at most 8 rows). PV phase: the tile's rows
+  // rounded up to R = 4, 8 or 16 share the threads, thread -> (row pr, d =
+  // pd + S i) with S = 256 / R d-slices, so a decode tile (G rows) keeps
+  // every thread on a real row.
+  const uint32_t sk = tid & 31, sr = tid >> 5;
+  const uint32_t pv_rows = rows <= 4 ? 4u : rows <= 8 ? 8u : 16u;
+  const uint32_t S = kGenThreads / pv_rows;
+  const uint32_t pr = tid / S, pd = tid % S;
   constexpr int kMaxDPer = DT ? (DT + 15) / 16 : 256 / 16;
   float acc[kMaxDPer];
 #pragma unroll
@@ -231,6 +237,7 @@ __global__ __launch_bounds__(kGenThreads) void paged_attn_generic(AttnArgs a, ui
     // Scores and the online softmax, two passes of 8 rows.
 #pragma unroll
     for (uint32_t pass = 0; pass < 2; ++pass) {
+      if (pass == 1 && rows <= 8) break;
       const uint32_t r = sr + 8 * pass;
       const int32_t key = c0 + (int32_t)sk;
       float s = -INFINITY;
@@ -285,13 +292,23 @@ __global__ __launch_bounds__(kGenThreads) void paged_attn_generic(AttnArgs a, ui
     const float* pp = ps + pr * kGenKeys;
 #pragma unroll
     for (int i = 0; i < kMaxDPer; ++i) acc[i] *= alpha;
-    for (uint32_t k = 0; k < kGenKeys; ++k) {
-      const float pk = pp[k];
-      const float* vk = vs + k * D + pd;
+    // One copy of the loop per slice count, so that its d offsets and trip
+    // count are constants.
+    auto pv = [&](auto s_c) __attribute__((always_inline)) {
+      constexpr uint32_t SC = decltype(s_c)::value;
+      constexpr int kN = DT ? (int)((DT + SC - 1) / SC) : kMaxDPer;
+      for (uint32_t k = 0; k < kGenKeys; ++k) {
+        const float pk = pp[k];
+        const float* vk = vs + k * D + pd;
 #pragma unroll
-      for (int i = 0; i < kMaxDPer; ++i)
-        if (pd + 16 * i < D) acc[i] = __builtin_fmaf(pk, vk[16 * i], acc[i]);
-    }
+        for (int i = 0; i < kN; ++i)
+          if ((DT && DT % SC == 0) || pd + SC * i < D)
+            acc[i] = __builtin_fmaf(pk, vk[SC * i], acc[i]);
+      }
+    };
+    if (S == 64) pv(std::integral_constant<uint32_t, 64>{});
+    else if (S == 32) pv(std::integral_constant<uint32_t, 32>{});
+    else pv(std::integral_constant<uint32_t, 16>{});
   }
   __syncthreads();
   if (split) {
@@ -302,7 +319,7 @@ __global__ __launch_bounds__(kGenThreads) void paged_attn_generic(AttnArgs a, ui
     }
 #pragma unroll
     for (int i = 0; i < kMaxDPer; ++i) {
-      const uint32_t d = pd + 16 * i;
+      const uint32_t d = pd + S * i;
       if (d < D) pi[2 * kGenRows + pr * D + d] = acc[i];
     }
     return;
@@ -314,7 +331,7 @@ __global__ __launch_bounds__(kGenThreads) void paged_attn_generic(AttnArgs a, ui
     const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
     for (int i = 0; i < kMaxDPer; ++i) {
-      const uint32_t d = pd + 16 * i;
+      const uint32_t d = pd + S * i;
       if (d < D) orow[d] = from_f32<T>(acc[i] * inv);
     }
   }
