@@ -190,6 +190,10 @@ CASES = [
     (torch.float32, 4, 2, 3, 4, [1, 5], [1100, 600], 100, "NHD"),
     (torch.float32, 8, 8, 128, 16, [1, 37], [2100, 1100], 700, "HND"),
     (torch.bfloat16, 16, 4, 256, 16, [1, 9], [2000, 800], None, "HND"),
+    # More head dims the VALU kernel compiles as constants (96, 32), and a
+    # block size that is not a power of two.
+    (torch.bfloat16, 16, 4, 96, 16, [1, 7], [900, 130], None, "HND"),
+    (torch.float16, 8, 2, 32, 12, [1, 3, 1], [260, 45, 1300], 40, "NHD"),
 ]
 
 

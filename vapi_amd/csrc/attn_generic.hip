@@ -20,8 +20,9 @@
 // When a row tile's visible keys span more than one chunk, each chunk writes
 // (m, l, o) per row to the workspace and paged_attn_generic_merge combines
 // them; a tile whose keys fit one chunk writes its output directly. Head
-// dims 64, 128 and 256 are compiled as constants (unrolled dot products,
-// 4-element staging loads); others take the runtime-D kernel.
+// dims 16, 32, 64, 80, 96, 128 and 256 are compiled as constants (unrolled
+// dot products, 4-element staging loads, the next tile loaded while the
+// current one is computed); others take the runtime-D kernel.
 #include <algorithm>
 #include <type_traits>
 
@@ -452,10 +453,16 @@ void launch_generic(const AttnArgs& a, uint32_t max_q, uint32_t max_k, uint32_t 
   } while (0)
 #define VK_GEN_D(T)                                  \
   do {                                               \
-    if (head_dim == 128) VK_GEN(T, 128);             \
-    else if (head_dim == 64) VK_GEN(T, 64);          \
-    else if (head_dim == 256) VK_GEN(T, 256);        \
-    else VK_GEN(T, 0);                               \
+    switch (head_dim) {                              \
+      case 16: VK_GEN(T, 16); break;                 \
+      case 32: VK_GEN(T, 32); break;                 \
+      case 64: VK_GEN(T, 64); break;                 \
+      case 80: VK_GEN(T, 80); break;                 \
+      case 96: VK_GEN(T, 96); break;                 \
+      case 128: VK_GEN(T, 128); break;               \
+      case 256: VK_GEN(T, 256); break;               \
+      default: VK_GEN(T, 0); break;                  \
+    }                                                \
   } while (0)
   switch (dtype) {
     case VAPI_KV_F32: VK_GEN_D(float); break;
