@@ -383,3 +383,28 @@ def test_a_mixed_cache_exports_k_of_every_layer_then_the_v_that_exist():
         if a.size:
             np.testing.assert_array_equal(b[0], a[2])
             np.testing.assert_array_equal(b[1:], a[1:])
+
+
+def test_threaded_scatter_and_copy_equal_the_serial_ones():
+    """The CPU baseline's multi-threaded write_rows (scatter branch) and
+    copy_blocks give the serial results for slot lists without repeats and
+    pairs whose destinations are distinct and never a source."""
+    rng = np.random.default_rng(11)
+    row = 64
+    slots = rng.permutation(4096)[:1500].astype(np.uint32)
+    slots[::37] = 0xFFFFFFFF
+    src = rng.integers(0, 255, size=(len(slots), row), dtype=np.uint8)
+    a = np.zeros((4096, row), dtype=np.uint8)
+    b = np.zeros_like(a)
+    oracle.write_rows(a, src, slots)
+    oracle.write_rows(b, src, slots, threads=4)
+    assert np.array_equal(a, b)
+    perm = rng.permutation(300).astype(np.uint32)
+    pairs = np.stack([perm[:100], perm[100:200]], 1)
+    ks = [rng.integers(0, 255, size=(300, 96), dtype=np.uint8) for _ in range(3)]
+    vs = [x.copy() for x in ks]
+    ks2, vs2 = [x.copy() for x in ks], [x.copy() for x in vs]
+    oracle.copy_blocks(ks, vs, pairs)
+    oracle.copy_blocks(ks2, vs2, pairs, threads=4)
+    assert all(np.array_equal(x, y) for x, y in zip(ks + vs, ks2 + vs2))
+    assert np.array_equal(ks[1][perm[100:200]], ks[1][perm[:100]])
