@@ -224,6 +224,43 @@ def bench_valu(steps, warmup):
     return out
 
 
+def bench_head_dim_64(steps, warmup):
+    """Configs 2 and 3 with head_dim 64 (LFM2's attention layers: 32 q / 8 kv
+    heads of 64), on the same MFMA kernels' head_dim-64 builds."""
+    w = workload.config2_decode()
+    cache = PagedKvCache(1, w.num_blocks, w.block_size, 8, 64, torch.bfloat16, "HND")
+    workload.fill_normal(cache._slab, workload.seed_for(2))
+    q = torch.randn(w.batch, 32, 64, device=DEV).to(torch.bfloat16)
+    batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
+                         block_tables=[t.tolist() for t in w.tables], max_seqlen_q=1,
+                         max_seqlen_k=int(w.lens.max()))
+    prep = PreparedAttention.from_batch(batch, DEV)
+    out = torch.empty_like(q)
+    gms = timed_graph(lambda: paged_attention_prepared(q, cache, 0, prep, 0.125, out=out),
+                      steps, warmup)
+    kv = int(w.lens.sum()) * 2 * 8 * 64 * 2
+    res = {"decode_cfg2_d64": dict(us=gms * 1e3, kv_bytes=kv, gbs=kv / (gms * 1e-3) / 1e9)}
+    del cache, q, out
+    p = workload.config3_prefill()
+    cache = PagedKvCache(1, p.num_blocks, p.block_size, 8, 64, torch.bfloat16, "HND")
+    workload.fill_normal(cache._slab, workload.seed_for(3))
+    q = torch.randn(p.batch * p.len_q, 32, 64, device=DEV).to(torch.bfloat16)
+    batch = ForwardBatch(cu_seqlens_q=p.cu_q().tolist(), cu_seqlens_k=p.cu_k().tolist(),
+                         block_tables=[t.tolist() for t in p.tables], max_seqlen_q=p.len_q,
+                         max_seqlen_k=p.len_k)
+    prep = PreparedAttention.from_batch(batch, DEV)
+    out = torch.empty_like(q)
+    ms, _ = timed(lambda: paged_attention_prepared(q, cache, 0, prep, 0.125, out=out),
+                  max(steps, 10), 30)
+    flops = p.flops() / 2  # head_dim 64
+    res["prefill_cfg3_d64"] = dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12)
+    log("head_dim 64: decode cfg2 {:.1f} us ({:.0f} GB/s), prefill cfg3 {:.3f} ms ({:.0f} "
+        "TFLOP/s)".format(res["decode_cfg2_d64"]["us"], res["decode_cfg2_d64"]["gbs"], ms,
+                          res["prefill_cfg3_d64"]["tflops"]))
+    del cache, q, out
+    return res
+
+
 # ---- config 1: append --------------------------------------------------------------
 
 def bench_append(steps, warmup):
@@ -815,6 +852,7 @@ def main():
         # box), so it warms up for 30 calls, as a serving loop's steady state.
         extras["prefill_cfg3"] = bench_prefill(max(args.steps, 10), 30)
         extras["valu_attention"] = bench_valu(args.steps, args.warmup)
+        extras["head_dim_64"] = bench_head_dim_64(args.steps, args.warmup)
     extras["blocks_cfg4"] = bench_blocks(max(args.steps // 5, 3), 2, dec)
     if args.only == "blocks":
         return
