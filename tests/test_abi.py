@@ -281,3 +281,18 @@ def test_the_build_refuses_a_prefill_kernel_that_spills():
     with pytest.raises(RuntimeError, match="scratch"):
         b._check_no_scratch(Path("attn_prefill.hip"), ok.replace(": 0 [", ": 16 ["))
     b._check_no_scratch(Path("kv_ops.hip"), ok.replace(": 0 [", ": 16 ["))  # not checked
+
+
+def test_the_valu_workspace_follows_its_key_chunks():
+    """f32 pools run the VALU kernel: keys split into chunks of 512, halved
+    down to 64 while the launch has fewer than 512 workgroups; a call whose
+    keys fit one chunk needs no workspace."""
+    L = _lib.lib()
+    f32 = pool(dtype=_lib.F32, num_kv_heads=8, head_dim=128)
+    # 64 rows x 8 kv heads = 512 row tiles: 512-key chunks, one chunk.
+    assert L.vapi_paged_attention_workspace_size(f32, 64, 32, 1, 512) == 0
+    # Two sequences: 16 tiles, so 64-key chunks (8 of them for 512 keys).
+    need = L.vapi_paged_attention_workspace_size(f32, 2, 32, 1, 512)
+    tiles, chunks = 2 * 8, 8
+    assert need == 256 + tiles * chunks * 16 * (128 + 2) * 4
+    assert L.vapi_paged_attention_workspace_size(f32, 2, 32, 1, 64) == 0
