@@ -456,25 +456,34 @@ __device__ __forceinline__ void copy_new_rows(const AttnArgs& a, uint32_t wg, ui
   }
 }
 
-template <typename T, int D, bool kFuse>
+// WPS waves per segment: 1 (four segments per workgroup) when segments are
+// many and each has a few pieces; 4 (one segment per workgroup) when they
+// are few, so that each has many pieces: wave v then combines pieces r0 +
+// v, r0 + v + 4, ..., 16 per round trip, and the four waves' results are
+// combined through LDS.
+template <typename T, int D, bool kFuse, int WPS>
 __global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_merge(AttnArgs a, uint32_t nwg,
                                                                       uint32_t merge_wgs) {
+  static_assert(WPS == 1 || WPS == kMergeWaves, "a wave or a workgroup per segment");
   if (kFuse && blockIdx.x >= merge_wgs) {
     copy_new_rows<T, D>(a, blockIdx.x - merge_wgs, gridDim.x - merge_wgs);
     return;
   }
   const uint32_t lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t nseg = a.batch * a.kvh;
-  const uint32_t segi =
-      blockIdx.x * kMergeWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  constexpr uint32_t kSegsPerWG = kMergeWaves / WPS;
+  const uint32_t segi = blockIdx.x * kSegsPerWG + wave / WPS;
+  const uint32_t v = wave % WPS;
   if (segi == nseg) {
-    if (!a.deterministic) update_shares(a, nwg, lane);
+    if (v == 0 && !a.deterministic) update_shares(a, nwg, lane);
     return;
   }
   if (segi > nseg) return;
   const uint32_t seq = segi / a.kvh, kh = segi - seq * a.kvh;
   // One round trip: the row's extents and the segment's ranges (stale for
-  // rows that are not decode rows, which return here).
+  // rows that are not decode rows, which return here; the same for all the
+  // waves of a segment).
   const uint32_t q0 = a.cu_q[seq], q1 = a.cu_q[seq + 1];
   const uint32_t k0 = a.cu_k[seq], k1 = a.cu_k[seq + 1];
   const uint32_t r0 = a.seg_ranges[2 * segi], r1 = a.seg_ranges[2 * segi + 1];
@@ -486,20 +495,22 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_merge(AttnArgs 
   const uint32_t e_lane = lane * E;
   const uint32_t h0 = e_lane / D, h1 = (e_lane + E - 1) / D;
   T* orow = (T*)a.out + ((uint64_t)q0 * a.num_heads + kh * G) * D;
-  // Up to 8 ranges per round trip; E is a multiple of 4 for G*D >= 256
+  // Up to R ranges per round trip; E is a multiple of 4 for G*D >= 256
   // (D is 64 or 128), so outputs move as float4.
-  constexpr int R = 8;
+  constexpr int R = WPS == 1 ? 8 : 16;
+  __shared__ float cmb[WPS > 1 ? WPS : 1][3][WPS > 1 ? 64 * 8 : 1];
   for (uint32_t j0 = 0; j0 < E; j0 += 8) {
     const uint32_t n = min(8u, E - j0);
     float M[8], L[8], O[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) M[j] = kNegBig, L[j] = 0.f, O[j] = 0.f;
-    for (uint32_t w = r0; w <= r1; w += R) {
+    for (uint32_t w = r0 + v; w <= r1; w += R * WPS) {
       float om[R][8], mm[R][2], ll[R][2];
 #pragma unroll
       for (int u = 0; u < R; ++u) {
-        const bool in = w + u <= r1;
-        const uint64_t sl = (uint64_t)(w + u + seg) * G;
+        const uint32_t pc = w + u * WPS;
+        const bool in = pc <= r1;
+        const uint64_t sl = (uint64_t)(pc + seg) * G;
         const float* po = a.ws_o + sl * D + e_lane + j0;
         if (in && n == 8) {
           const float4 v0 = *(const float4*)po, v1 = *(const float4*)(po + 4);
@@ -533,8 +544,39 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_merge(AttnArgs 
         M[j] = Mn, L[j] = Lj, O[j] = Oj;
       }
     }
-    for (uint32_t j = 0; j < n; ++j)
-      orow[e_lane + j0 + j] = from_f32<T>(L[j] > 0.f ? O[j] / L[j] : 0.f);
+    if constexpr (WPS > 1) {
+      // The segment's waves hand their (M, L, O) to wave 0 through LDS, in
+      // wave order, so the combination order is fixed.
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        cmb[v][0][lane * 8 + j] = M[j];
+        cmb[v][1][lane * 8 + j] = L[j];
+        cmb[v][2][lane * 8 + j] = O[j];
+      }
+      __syncthreads();
+      if (v == 0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float Mn = M[j];
+#pragma unroll
+          for (int x = 1; x < WPS; ++x) Mn = fmaxf(Mn, cmb[x][0][lane * 8 + j]);
+          float Lj = 0.f, Oj = 0.f;
+#pragma unroll
+          for (int x = 0; x < WPS; ++x) {
+            const float f = fast_exp2(cmb[x][0][lane * 8 + j] - Mn);
+            Lj += cmb[x][1][lane * 8 + j] * f;
+            Oj += cmb[x][2][lane * 8 + j] * f;
+          }
+          L[j] = Lj, O[j] = Oj;
+        }
+        for (uint32_t j = 0; j < n; ++j)
+          orow[e_lane + j0 + j] = from_f32<T>(L[j] > 0.f ? O[j] / L[j] : 0.f);
+      }
+      __syncthreads();  // cmb is reused by the next eight outputs
+    } else {
+      for (uint32_t j = 0; j < n; ++j)
+        orow[e_lane + j0 + j] = from_f32<T>(L[j] > 0.f ? O[j] / L[j] : 0.f);
+    }
   }
 }
 
@@ -612,7 +654,9 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, bool bf16,
     // Fused append: the first chunk's merge launch also writes the new rows
     // (every chunk's stream reads a row's new key from the new rows).
     const bool fuse = a.k_new != nullptr;
-    const uint32_t merge_wgs = (nb * a.kvh + kMergeWaves) / kMergeWaves;
+    // Few segments (each split over many waves): a workgroup per segment.
+    const bool wide = nb * a.kvh <= 256;
+    const uint32_t merge_wgs = wide ? nb * a.kvh + 1 : (nb * a.kvh + kMergeWaves) / kMergeWaves;
     uint32_t copy_wgs = 0;
     if (fuse && b0 == 0) {
       const uint64_t chunks = 2ull * a.n_new * a.kvh * (head_dim / 8);
@@ -623,8 +667,12 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, bool bf16,
   do {                                                                                          \
     hipLaunchKernelGGL((paged_decode_stream<T, DD, F>), dim3(nwg), dim3(64 * kDecodeWavesPerWG), \
                        lds, s, c, c.cu_q, c.cu_k, c.table);                                    \
-    hipLaunchKernelGGL((paged_decode_merge<T, DD, F>), dim3(merge_wgs + copy_wgs),             \
-                       dim3(64 * kMergeWaves), 0, s, c, nwg, merge_wgs);                        \
+    if (wide)                                                                                   \
+      hipLaunchKernelGGL((paged_decode_merge<T, DD, F, kMergeWaves>), dim3(merge_wgs + copy_wgs), \
+                         dim3(64 * kMergeWaves), 0, s, c, nwg, merge_wgs);                      \
+    else                                                                                        \
+      hipLaunchKernelGGL((paged_decode_merge<T, DD, F, 1>), dim3(merge_wgs + copy_wgs),         \
+                         dim3(64 * kMergeWaves), 0, s, c, nwg, merge_wgs);                      \
   } while (0)
 #define VK_DEC2(T, DD) \
   do {                 \
