@@ -501,9 +501,11 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_merge(AttnArgs 
   __shared__ float cmb[WPS > 1 ? WPS : 1][3][WPS > 1 ? 64 * 8 : 1];
   for (uint32_t j0 = 0; j0 < E; j0 += 8) {
     const uint32_t n = min(8u, E - j0);
-    float M[8], L[8], O[8];
+    // Running max and sum per head (a lane's eight outputs span at most two
+    // heads, and all outputs of a head share them), output sums per element.
+    float Mh[2] = {kNegBig, kNegBig}, Lh[2] = {0.f, 0.f}, O[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) M[j] = kNegBig, L[j] = 0.f, O[j] = 0.f;
+    for (int j = 0; j < 8; ++j) O[j] = 0.f;
     for (uint32_t w = r0 + v; w <= r1; w += R * WPS) {
       float om[R][8], mm[R][2], ll[R][2];
 #pragma unroll
@@ -526,23 +528,39 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_merge(AttnArgs 
         mm[u][0] = x0.y > 0.f ? x0.x : kNegBig, ll[u][0] = x0.y;
         mm[u][1] = x1.y > 0.f ? x1.x : kNegBig, ll[u][1] = x1.y;
       }
+      float f[2], e[R][2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float Mn = Mh[h];
+#pragma unroll
+        for (int u = 0; u < R; ++u) Mn = fmaxf(Mn, mm[u][h]);
+        f[h] = fast_exp2(Mh[h] - Mn);
+        float Ln = Lh[h] * f[h];
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+          e[u][h] = ll[u][h] > 0.f ? fast_exp2(mm[u][h] - Mn) : 0.f;
+          Ln += ll[u][h] * e[u][h];
+        }
+        Mh[h] = Mn, Lh[h] = Ln;
+      }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int hw = e_lane + j0 + j >= (h0 + 1) * D;  // the lane's second head
-        float Mn = M[j];
-#pragma unroll
-        for (int u = 0; u < R; ++u) Mn = fmaxf(Mn, mm[u][hw]);
-        const float f = fast_exp2(M[j] - Mn);
-        float Lj = L[j] * f, Oj = O[j] * f;
+        float Oj = O[j] * f[hw];
 #pragma unroll
         for (int u = 0; u < R; ++u) {
-          const bool live = ll[u][hw] > 0.f;
-          const float e = fast_exp2(mm[u][hw] - Mn);
-          Lj += live ? ll[u][hw] * e : 0.f;
-          Oj += live ? om[u][j] * e : 0.f;
+          // A zero weight takes nothing from the piece's o (an empty slice's
+          // slot holds whatever an earlier call left there).
+          Oj += e[u][hw] != 0.f ? om[u][j] * e[u][hw] : 0.f;
         }
-        M[j] = Mn, L[j] = Lj, O[j] = Oj;
+        O[j] = Oj;
       }
+    }
+    float M[8], L[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int hw = e_lane + j0 + j >= (h0 + 1) * D;
+      M[j] = Mh[hw], L[j] = Lh[hw];
     }
     if constexpr (WPS > 1) {
       // The segment's waves hand their (M, L, O) to wave 0 through LDS, in
