@@ -224,6 +224,33 @@ def bench_valu(steps, warmup):
     return out
 
 
+def bench_small_batches(steps, warmup):
+    """Decode latency at small batches (config 2's heads and pool, equal
+    contexts): where the call's fixed costs (the first loads, the merge)
+    weigh most. Per call, replayed from a HIP graph."""
+    cache = PagedKvCache(1, 32768, 16, 8, 128, torch.bfloat16, "HND")
+    workload.fill_normal(cache._slab, workload.seed_for(2))
+    rng = np.random.default_rng(workload.seed_for(2))
+    out = {}
+    for b, lk in ((1, 8192), (1, 32768), (4, 4096), (16, 2048)):
+        nb = (lk + 15) // 16
+        perm = rng.permutation(32768)
+        batch = ForwardBatch(cu_seqlens_q=list(range(b + 1)),
+                             cu_seqlens_k=[i * lk for i in range(b + 1)],
+                             block_tables=[perm[i * nb:(i + 1) * nb].tolist() for i in range(b)],
+                             max_seqlen_q=1, max_seqlen_k=lk)
+        prep = PreparedAttention.from_batch(batch, DEV)
+        q = torch.randn(b, 32, 128, device=DEV).to(torch.bfloat16)
+        o = torch.empty_like(q)
+        gms = timed_graph(lambda: paged_attention_prepared(q, cache, 0, prep, 128 ** -0.5, out=o),
+                          steps, warmup)
+        kv = b * lk * 8 * 128 * 2 * 2
+        out[f"b{b}_k{lk}"] = dict(us=gms * 1e3, gbs=kv / (gms * 1e-3) / 1e9)
+    log("decode small batches: " + ", ".join(f"{k} {v['us']:.1f} us" for k, v in out.items()))
+    del cache
+    return out
+
+
 def bench_head_dim_64(steps, warmup):
     """Configs 2 and 3 with head_dim 64 (LFM2's attention layers: 32 q / 8 kv
     heads of 64), on the same MFMA kernels' head_dim-64 builds."""
@@ -853,6 +880,7 @@ def main():
         extras["prefill_cfg3"] = bench_prefill(max(args.steps, 10), 30)
         extras["valu_attention"] = bench_valu(args.steps, args.warmup)
         extras["head_dim_64"] = bench_head_dim_64(args.steps, args.warmup)
+        extras["decode_small_batches"] = bench_small_batches(args.steps, args.warmup)
     extras["blocks_cfg4"] = bench_blocks(max(args.steps // 5, 3), 2, dec)
     if args.only == "blocks":
         return
