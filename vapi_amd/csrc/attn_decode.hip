@@ -22,7 +22,9 @@
 // whole segment writes the normalised output; the first and last piece of a
 // slice may be partial and write (m, l, o) to slot range + segment (ranges
 // and segments are both numbered in step order, so slots are unique), and
-// paged_decode_merge, one wave per split segment, combines them. Each
+// paged_decode_merge combines them: one wave per split segment, or, when a
+// launch has at most 256 segments (each then split into many pieces), one
+// workgroup per segment whose waves share its pieces. Each
 // segment's first and last range are recorded by the waves holding its first
 // and last step, and a wave whose slice is empty marks its slot empty, so
 // the merge needs no step arithmetic. The merge
