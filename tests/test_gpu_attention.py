@@ -16,10 +16,10 @@ import pytest
 import torch
 
 import oracle
-from vapi_amd import workload
+from vapi_amd import _lib, workload
 from vapi_amd.attention import (ForwardBatch, PreparedAttention, paged_attention,
                                 paged_attention_prepared, paged_attention_windowed)
-from vapi_amd.cache import PagedKvCache, write_kv_to_cache
+from vapi_amd.cache import PagedKvCache, stream_handle, write_kv_to_cache
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -426,3 +426,51 @@ def test_keys_past_the_table_row_read_its_last_entry_instead_of_faulting(dtype):
     torch.cuda.synchronize()
     assert torch.equal(got[:20], want[:20])
     assert bool(torch.isfinite(got.float()).all())
+
+
+# ---- small prefill batches: the keys split over more workgroups -------------
+
+SPLIT_CASES = [
+    # dtype, heads, kvh, d, bs, lens_q, lens_k, window, layout
+    (torch.bfloat16, 32, 8, 128, 16, [64], [4096], None, "HND"),
+    (torch.bfloat16, 32, 8, 128, 16, [40, 1, 100], [3000, 2500, 2100], None, "NHD"),
+    (torch.float16, 16, 4, 64, 32, [96, 1], [5000, 700], 1500, "HND"),
+    (torch.bfloat16, 28, 4, 128, 16, [300], [2600], 700, "HND"),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: f"{str(c[0])[6:]}-d{c[3]}-q{c[5]}-w{c[7]}")
+def test_small_prefill_batches_split_their_keys_and_match_the_oracle(case):
+    """A prefill batch too small to fill the GPU with query tiles splits each
+    tile's keys over up to 64 workgroups and merges their partials; with the
+    workspace vapi_paged_attention_workspace_size asks for it matches the
+    oracle, and so does the same call without a workspace (no split)."""
+    dtype, heads, kvh, d, bs, lens_q, lens_k, window, layout = case
+    rng = np.random.default_rng(zlib.crc32(str(case).encode()))
+    c, q, batch = random_case(rng, dtype, heads, kvh, d, bs, lens_q, lens_k, layout)
+    lib = _lib.lib()
+    full = lib.vapi_paged_attention_workspace_size(c.pool, len(lens_q), heads, max(lens_q),
+                                                   max(lens_k))
+    decode_only = lib.vapi_paged_attention_workspace_size(c.pool, len(lens_q), heads, 1,
+                                                          max(lens_k))
+    assert full > decode_only  # the split asks for room
+    wl = -1 if window is None else window - 1
+    want = oracle_out(q, c, 0, batch, d ** -0.5, window)
+    tol = (2e-2 if dtype == torch.bfloat16 else 1e-2) * float(want.abs().max())
+    prep = PreparedAttention.from_batch(batch, DEV, cache=c, num_heads=heads)
+    got = torch.full_like(q, float("nan"))
+    _lib.check(lib.vapi_paged_attention(
+        c.pool, 0, q.data_ptr(), got.data_ptr(), prep.seqlens_q.data_ptr(),
+        prep.seqlens_k.data_ptr(), prep.block_table.data_ptr(), len(lens_q),
+        prep.block_table.shape[1], max(lens_q), max(lens_k), heads, d ** -0.5, wl, 0,
+        prep.workspace.data_ptr(), prep.workspace.numel(), stream_handle()))
+    assert max_abs(got, want) <= tol
+    if 1 not in lens_q:  # prefill only: no workspace at all, no split
+        plain = torch.full_like(q, float("nan"))
+        _lib.check(lib.vapi_paged_attention_ex(
+            c.pool, 0, q.data_ptr(), plain.data_ptr(), prep.seqlens_q.data_ptr(),
+            prep.seqlens_k.data_ptr(), prep.block_table.data_ptr(), len(lens_q),
+            prep.block_table.shape[1], max(lens_q), max(lens_k), heads, d ** -0.5, wl, 0,
+            _lib.ATTN_NO_DECODE_ROWS, None, 0, stream_handle()))
+        assert max_abs(plain, want) <= tol
+        assert max_abs(plain, got) <= tol

@@ -2,8 +2,10 @@
 bounded table read.
 
   * VAPI_ATTN_NO_DECODE_ROWS: a prefill-only batch runs the prefill kernel
-    alone; its output equals the two-kernel call bit for bit (the decode
-    kernel never writes a prefill row). Forced onto a batch that does have
+    alone; given the same workspace (so the same key split) its output
+    equals the two-kernel call bit for bit (the decode kernel never writes a
+    prefill row); without a workspace (no split) it matches the oracle.
+    Forced onto a batch that does have
     decode rows, the prefill kernel takes them too: checked against the
     oracle (bf16 max-abs <= 2e-2 * max|reference|, as every attention test).
   * VAPI_ATTN_DETERMINISTIC: repeated calls on identical inputs are
@@ -56,12 +58,18 @@ def test_a_prefill_only_batch_runs_one_kernel_with_the_same_output(heads, kvh, d
     assert prep.flags == ATTN_NO_DECODE_ROWS
     scale = d ** -0.5
     wl = -1 if window is None else window - 1
-    one = call_ex(q, c, prep, scale, ATTN_NO_DECODE_ROWS, wl)  # no workspace at all
+    b = prep.seqlens_q.shape[0] - 1
+    need = _lib.lib().vapi_paged_attention_workspace_size(
+        c.pool, b, q.shape[1], max(prep.max_seqlen_q, 1), max(prep.max_seqlen_k, 1))
+    ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=DEV)
+    one = call_ex(q, c, prep, scale, ATTN_NO_DECODE_ROWS, wl, ws=ws)
     two = call_ex(q, c, prep, scale, 0, wl)
+    bare = call_ex(q, c, prep, scale, ATTN_NO_DECODE_ROWS, wl)  # no workspace at all
     torch.cuda.synchronize()
     assert torch.equal(one, two)
     want = oracle_out(q, c, 0, batch, scale, window)
     assert max_abs(one, want) <= 2e-2 * float(want.abs().max())
+    assert max_abs(bare, want) <= 2e-2 * float(want.abs().max())
 
 
 @pytest.mark.parametrize("heads,kvh,d", [(32, 8, 128), (16, 2, 64)])

@@ -87,12 +87,10 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
                                 size_t workspace_bytes, vapi_stream_t stream,
                                 const NewRows* fuse, uint32_t flags);
 
-extern "C" {
-
-size_t vapi_paged_attention_workspace_size(const vapi_kv_pool* pool,
-                                           uint32_t batch, uint32_t num_heads,
-                                           uint32_t max_seqlen_q,
-                                           uint32_t max_seqlen_k) {
+// The workspace a call cannot run without: the decode's (unless the call
+// launches no decode kernel) or the VALU kernel's split partials.
+static size_t required_workspace(const vapi_kv_pool* pool, uint32_t batch, uint32_t num_heads,
+                                 uint32_t max_seqlen_q, uint32_t max_seqlen_k, bool skip_decode) {
   if (!pool || pool->num_kv_heads == 0 || num_heads % pool->num_kv_heads || batch == 0 ||
       num_heads == 0)
     return 0;
@@ -100,8 +98,26 @@ size_t vapi_paged_attention_workspace_size(const vapi_kv_pool* pool,
   if (!mfma_ok(pool, num_heads))
     return generic_workspace_bytes(batch, pool->num_kv_heads, group, pool->head_dim,
                                    std::max(max_seqlen_q, 1u), max_seqlen_k);
-  return decode_workspace_bytes(batch, pool->num_kv_heads, group, pool->head_dim,
-                                decode_num_waves());
+  return skip_decode ? 0
+                     : decode_workspace_bytes(batch, pool->num_kv_heads, group, pool->head_dim,
+                                              decode_num_waves());
+}
+
+extern "C" {
+
+size_t vapi_paged_attention_workspace_size(const vapi_kv_pool* pool,
+                                           uint32_t batch, uint32_t num_heads,
+                                           uint32_t max_seqlen_q,
+                                           uint32_t max_seqlen_k) {
+  const size_t need =
+      required_workspace(pool, batch, num_heads, max_seqlen_q, max_seqlen_k, false);
+  if (!pool || pool->num_kv_heads == 0 || num_heads % pool->num_kv_heads || batch == 0 ||
+      num_heads == 0 || !mfma_ok(pool, num_heads))
+    return need;
+  // Past the decode's part: what a small prefill batch's key split uses
+  // (optional: a smaller workspace only means fewer splits).
+  return need + prefill_split_bytes(batch, pool->num_kv_heads, num_heads / pool->num_kv_heads,
+                                    pool->head_dim, max_seqlen_q, max_seqlen_k);
 }
 
 int vapi_paged_attention(const vapi_kv_pool* pool, uint32_t layer,
@@ -190,8 +206,9 @@ int vapi_paged_attention_noalloc(const vapi_kv_pool* pool, uint32_t layer, const
   if (int rc = check_pool(pool, "vapi_paged_attention_noalloc")) return rc;
   // Sized before anything is resolved or launched: a call past the limit is
   // refused and changes nothing.
-  const size_t need = vapi_paged_attention_workspace_size(pool, batch, num_heads, max_seqlen_q,
-                                                          max_seqlen_k);
+  const bool skip = (flags & VAPI_ATTN_NO_DECODE_ROWS) && max_seqlen_q > 1;
+  const size_t need =
+      required_workspace(pool, batch, num_heads, max_seqlen_q, max_seqlen_k, skip);
   if (need > VAPI_ATTN_SCRATCH_BYTES)
     VK_FAIL(VAPI_KV_ESPACE,
             "vapi_paged_attention_noalloc: this batch needs %zu bytes of decode workspace, more "
@@ -249,9 +266,8 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   // no workspace.
   const bool skip_decode = (flags & VAPI_ATTN_NO_DECODE_ROWS) && !fuse && max_seqlen_q > 1 &&
                            mfma_ok(pool, num_heads);
-  const size_t need = skip_decode ? 0
-                                  : vapi_paged_attention_workspace_size(pool, batch, num_heads,
-                                                                        max_seqlen_q, max_seqlen_k);
+  const size_t need =
+      required_workspace(pool, batch, num_heads, max_seqlen_q, max_seqlen_k, skip_decode);
   if (workspace_bytes < need || (need && !workspace))
     VK_FAIL(VAPI_KV_ESPACE, "vapi_paged_attention: workspace %zu bytes < %zu",
             workspace_bytes, need);
@@ -304,7 +320,15 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
     a.num_waves = decode_num_waves();
     if (skip_decode) a.pf_min_q = 1;
     else launch_decode(a, workspace, g.d, bf16, s);
-    if (max_seqlen_q > 1) launch_prefill(a, max_seqlen_q, g.d, bf16, s);
+    if (max_seqlen_q > 1) {
+      // The workspace past the decode's part serves the prefill's key split
+      // (never its first 256 bytes, which carry the decode's XCD shares
+      // from call to call).
+      const size_t off = std::max<size_t>((need + 255) & ~(size_t)255, 256);
+      const bool room = workspace && workspace_bytes > off;
+      launch_prefill(a, max_seqlen_q, max_seqlen_k, g.d, bf16,
+                     room ? (char*)workspace + off : nullptr, room ? workspace_bytes - off : 0, s);
+    }
   } else {
     if (g.d > 256)
       VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: head_dim %u > 256", g.d);

@@ -419,8 +419,13 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, bool bf16, hi
 // Workgroups of the prefill launch (query tiles x kv heads x sequences); a
 // launch needs it below 2^32.
 uint64_t prefill_grid(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t max_q);
-void launch_prefill(const AttnArgs& a, uint32_t max_q, uint32_t head_dim, bool bf16,
-                    hipStream_t s);
+// The prefill launch; with a workspace (`split_ws`, `split_ws_bytes`) a
+// batch too small to fill the GPU splits its keys over more workgroups.
+void launch_prefill(const AttnArgs& a, uint32_t max_q, uint32_t max_k, uint32_t head_dim,
+                    bool bf16, void* split_ws, size_t split_ws_bytes, hipStream_t s);
+// Workspace the prefill's key split wants for this shape (0: no split).
+size_t prefill_split_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t head_dim,
+                           uint32_t max_q, uint32_t max_k);
 // Any row, any dtype, head_dim <= 256 (VALU); split contexts combine their
 // partials through `workspace` (generic_workspace_bytes).
 void launch_generic(const AttnArgs& a, uint32_t max_q, uint32_t max_k, uint32_t head_dim,

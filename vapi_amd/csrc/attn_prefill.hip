@@ -13,6 +13,7 @@
 // that some row of the workgroup cannot fully see. Rows with len_q < 2 are
 // left to the decode kernel, unless the call launches no decode kernel (the
 // caller said the batch has no decode rows): then every row is done here.
+#include <algorithm>
 #include <type_traits>
 
 #include "attn_common.hpp"
@@ -155,10 +156,17 @@ __device__ __forceinline__ void ds_read_tr16_x4(uint2 (&r)[8], const uint32_t (&
 }
 
 
-template <typename T, int D, int RT, int OCC>
+// With n_split > 1 the keys a workgroup would walk are cut into n_split
+// contiguous runs of steps, one workgroup each (a batch too small to fill
+// the GPU with query tiles alone); each writes its rows' (m, l, o) to
+// `part` and paged_prefill_merge combines them.
+template <typename T, int D, int RT, int OCC, bool kSplit>
 __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
     AttnArgs a, const uint32_t* __restrict__ cu_q, const uint32_t* __restrict__ cu_k,
-    const uint32_t* __restrict__ table, uint32_t qtiles) {
+    const uint32_t* __restrict__ table, uint32_t qtiles, uint32_t n_split_arg,
+    float* __restrict__ part) {
+  // The unsplit launch compiles without the split's arithmetic.
+  const uint32_t n_split = kSplit ? n_split_arg : 1u;
   static_assert(kPfWaves == 8, "the step's K and V are 8 waves' loads");
   constexpr int KC = D / 32;
   constexpr int DT = D / 16;  // 16-column d tiles
@@ -174,7 +182,10 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
   __shared__ __attribute__((aligned(16))) uint16_t v0[32 * D], v1[32 * D], v2[32 * D];
   const uint32_t n_items = gridDim.x;
   const uint32_t item = xcd_remap(blockIdx.x, n_items);
-  const uint32_t qt = item % qtiles, rest = item / qtiles;
+  // Item order: query tile fastest, then key split, kv head, sequence (the
+  // q-tiles of one split read the same K/V and run on one XCD).
+  const uint32_t qt = item % qtiles, rest_s = item / qtiles;
+  const uint32_t split = rest_s % n_split, rest = rest_s / n_split;
   const uint32_t kh = rest % a.kvh, seq = rest / a.kvh;
   const uint32_t q0 = cu_q[seq];
   const uint32_t len_q = cu_q[seq + 1] - q0;
@@ -193,8 +204,17 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
   const uint32_t wg_last = min(row_base + kPfRows, nrows) - 1;
   const int32_t wg_pmin = offset + (int32_t)(row_base / G);
   const int32_t wg_pmax = offset + (int32_t)(wg_last / G);
-  const int32_t klo = a.wl >= 0 ? max(0, wg_pmin - a.wl) : 0;
-  const int32_t khi = a.wr >= 0 ? min(last, wg_pmax + a.wr) : last;
+  const int32_t klo_wg = a.wl >= 0 ? max(0, wg_pmin - a.wl) : 0;
+  const int32_t khi_wg = a.wr >= 0 ? min(last, wg_pmax + a.wr) : last;
+  // This workgroup's run of 32-key steps: all of them, or split's share.
+  int32_t klo = klo_wg, khi = khi_wg;
+  if (kSplit) {
+    const int32_t first = klo_wg & ~31;
+    const uint32_t steps = khi_wg >= klo_wg ? (uint32_t)(((khi_wg & ~31) - first) / 32 + 1) : 0u;
+    const uint32_t a0 = split * steps / n_split, a1 = (split + 1) * steps / n_split;
+    klo = max(klo_wg, first + 32 * (int32_t)a0);
+    khi = min(khi_wg, first + 32 * (int32_t)a1 - 1);  // < klo when the share is empty
+  }
 
   const uint32_t row0 = row_base + wave * 16 * kPfRT;
   uint4 qf[kPfRT][KC];
@@ -250,10 +270,12 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
 
   int32_t s0_ = klo & ~31;
   const int32_t s_last = khi & ~31;
-  pf_dma<T, D>(k0, v0, tab, kb, vb, a, s0_, last, tid, wave);
-  pf_dma<T, D>(k1, v1, tab, kb, vb, a, min(s0_ + 32, s_last), last, tid, wave);
-  wait_vmcnt<kLoadsPerStep>();
-  ring_barrier();
+  if (!kSplit || s0_ <= khi) {  // (uniform) an empty key split issues no loads
+    pf_dma<T, D>(k0, v0, tab, kb, vb, a, s0_, last, tid, wave);
+    pf_dma<T, D>(k1, v1, tab, kb, vb, a, min(s0_ + 32, s_last), last, tid, wave);
+    wait_vmcnt<kLoadsPerStep>();
+    ring_barrier();
+  }
   // Step s reads buffer s % 3 and issues step s + 2 into (s + 2) % 3.
 #ifdef VK_PF_TRACE
   // Phase timestamps (shader clock) of every wave of workgroup item 100,
@@ -372,6 +394,22 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
   }
   wait_vmcnt<0>();  // no load may land in LDS after the workgroup ends
 
+  if constexpr (kSplit) {
+    // Partials of this split: row (m in scaled log2 units, l, o[D]),
+    // unnormalised; an empty share leaves l = 0.
+    float* pb = part + ((uint64_t)(rest * qtiles + qt) * n_split + split) * kPfRows * (D + 2);
+#pragma unroll
+    for (int t = 0; t < kPfRT; ++t) {
+      const float lt = wave_sum_g(l_run[t]);
+      float* pr = pb + (uint64_t)(wave * 16 * kPfRT + 16 * t + col) * (D + 2);
+      if (g == 0) *(float2*)pr = make_float2(m_run[t], lt);
+#pragma unroll
+      for (int k = 0; k < DT; ++k)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pr[2 + 16 * k + 4 * g + i] = o[t][k][i];
+    }
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < kPfRT; ++t) {
     const float lt = wave_sum_g(l_run[t]);
@@ -386,6 +424,49 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
           make_uint2(pack2<T>(o[t][k][0] * sc, o[t][k][1] * sc),
                      pack2<T>(o[t][k][2] * sc, o[t][k][3] * sc));
   }
+}
+
+// Combines the key splits' partials of a prefill launch: thread (row, four
+// consecutive d) over the splits, in split order.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void paged_prefill_merge(AttnArgs a, uint32_t qtiles,
+                                                           uint32_t rows_per_item,
+                                                           uint32_t n_split,
+                                                           const float* __restrict__ part) {
+  constexpr uint32_t kTpr = D / 4;           // threads per row
+  constexpr uint32_t kRpw = 256 / kTpr;      // rows per workgroup
+  const uint32_t blocks_per_item = rows_per_item / kRpw;
+  const uint32_t base = blockIdx.x / blocks_per_item;
+  const uint32_t row_in = (blockIdx.x % blocks_per_item) * kRpw + threadIdx.x / kTpr;
+  const uint32_t dq = (threadIdx.x % kTpr) * 4;
+  const uint32_t qt = base % qtiles, rest = base / qtiles;
+  const uint32_t kh = rest % a.kvh, seq = rest / a.kvh;
+  const uint32_t q0 = a.cu_q[seq], len_q = a.cu_q[seq + 1] - q0;
+  if (len_q < a.pf_min_q || len_q == 0) return;
+  const uint32_t G = a.group;
+  const uint32_t row = qt * rows_per_item + row_in;
+  if (row >= len_q * G) return;
+  const uint64_t stride = (uint64_t)rows_per_item * (D + 2);
+  const float* p0 = part + (uint64_t)base * n_split * stride + (uint64_t)row_in * (D + 2);
+  float M = kNegBig;
+  for (uint32_t sp = 0; sp < n_split; ++sp) {
+    const float2 ml = *(const float2*)(p0 + sp * stride);
+    if (ml.y > 0.f) M = fmaxf(M, ml.x);
+  }
+  float L = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
+  for (uint32_t sp = 0; sp < n_split; ++sp) {
+    const float* pr = p0 + sp * stride;
+    const float2 ml = *(const float2*)pr;
+    if (!(ml.y > 0.f)) continue;  // a share with no visible key
+    const float e = fast_exp2(ml.x - M);
+    L += ml.y * e;
+    const float4 x = *(const float4*)(pr + 2 + dq);
+    o[0] += x.x * e, o[1] += x.y * e, o[2] += x.z * e, o[3] += x.w * e;
+  }
+  const uint32_t j = row / G, hl = row % G;
+  T* orow = (T*)a.out + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * D + dq;
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  *(uint2*)orow = make_uint2(pack2<T>(o[0] * inv, o[1] * inv), pack2<T>(o[2] * inv, o[3] * inv));
 }
 
 #ifndef VK_PF_RT
@@ -410,8 +491,42 @@ uint64_t prefill_grid(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t max
   return ((uint64_t)max_q * group + rows - 1) / rows * kvh * batch;
 }
 
-void launch_prefill(const AttnArgs& a_in, uint32_t max_q, uint32_t head_dim, bool bf16,
-                    hipStream_t s) {
+// Key splits for a launch of `base` workgroups (query tiles x kv heads x
+// sequences) over at most max_k keys: enough to give every CU of a 256-CU
+// GPU a workgroup (one workgroup per CU is the kernel's occupancy at
+// head_dim 128), each split keeping at least 8 steps of 32 keys, at most 64.
+static uint32_t pf_splits(uint64_t base, uint32_t max_k) {
+  constexpr uint64_t kTarget = 256;
+  if (base == 0 || base >= kTarget) return 1;
+  uint64_t n = (kTarget + base - 1) / base;
+  n = std::min<uint64_t>(n, std::max<uint32_t>(1u, max_k / 256));
+  return (uint32_t)std::min<uint64_t>(n, 64);
+}
+
+static uint64_t pf_split_bytes(uint64_t base, uint32_t n, uint32_t head_dim) {
+  constexpr uint64_t rows = 16 * VK_PF_RT * kPfWaves;
+  return n > 1 ? base * n * rows * (head_dim + 2) * sizeof(float) : 0;
+}
+
+// At most this much workspace for the partials (fewer splits beyond).
+constexpr uint64_t kPfSplitMaxBytes = 256ull << 20;
+
+static uint32_t pf_splits_within(uint64_t base, uint32_t max_k, uint32_t head_dim,
+                                 uint64_t bytes) {
+  uint32_t n = pf_splits(base, max_k);
+  while (n > 1 && pf_split_bytes(base, n, head_dim) > std::min(bytes, kPfSplitMaxBytes)) --n;
+  return n;
+}
+
+size_t prefill_split_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t head_dim,
+                           uint32_t max_q, uint32_t max_k) {
+  if (max_q <= 1) return 0;
+  const uint64_t base = prefill_grid(batch, kvh, group, max_q);
+  return (size_t)pf_split_bytes(base, pf_splits_within(base, max_k, head_dim, ~0ull), head_dim);
+}
+
+void launch_prefill(const AttnArgs& a_in, uint32_t max_q, uint32_t max_k, uint32_t head_dim,
+                    bool bf16, void* split_ws, size_t split_ws_bytes, hipStream_t s) {
   AttnArgs a = a_in;
 #ifdef VK_PF_TRACE
   void* tp = nullptr;
@@ -420,17 +535,35 @@ void launch_prefill(const AttnArgs& a_in, uint32_t max_q, uint32_t head_dim, boo
 #endif
   constexpr uint32_t rows = 16 * VK_PF_RT * kPfWaves;
   const uint32_t qtiles = (uint32_t)(((uint64_t)max_q * a.group + rows - 1) / rows);
-  const uint64_t n = (uint64_t)qtiles * a.kvh * a.batch;
-  const dim3 grid((uint32_t)n), block(kPfThreads);
+  const uint64_t base = (uint64_t)qtiles * a.kvh * a.batch;
+  // As many splits as the workspace given holds (none without one); a
+  // deterministic call does not split, so its output does not depend on
+  // the workspace it is given.
+  const uint32_t n_split = split_ws && !a.deterministic
+                               ? pf_splits_within(base, max_k, head_dim, split_ws_bytes)
+                               : 1;
+  float* part = n_split > 1 ? (float*)split_ws : nullptr;
+  const dim3 grid((uint32_t)(base * n_split)), block(kPfThreads);
 // head_dim 64 fits in 128 registers: two workgroups per CU (four waves per
 // SIMD) measured 1% faster than one on a config-3-shaped batch (676-678
 // against 669-673 TFLOP/s).
 #ifndef VK_PF_OCC64
 #define VK_PF_OCC64 2
 #endif
-#define VK_PF(T, DD)                                                                    \
-  hipLaunchKernelGGL((paged_prefill_tiled<T, DD, VK_PF_RT, DD == 64 ? VK_PF_OCC64 : VK_PF_OCC>), \
-                     grid, block, 0, s, a, a.cu_q, a.cu_k, a.table, qtiles)
+#define VK_PF(T, DD)                                                                             \
+  do {                                                                                           \
+    constexpr int occ = DD == 64 ? VK_PF_OCC64 : VK_PF_OCC;                                      \
+    if (n_split > 1) {                                                                           \
+      hipLaunchKernelGGL((paged_prefill_tiled<T, DD, VK_PF_RT, occ, true>), grid, block, 0, s, a, \
+                         a.cu_q, a.cu_k, a.table, qtiles, n_split, part);                        \
+      hipLaunchKernelGGL((paged_prefill_merge<T, DD>),                                           \
+                         dim3((uint32_t)(base * (rows / (256 / (DD / 4))))), dim3(256), 0, s, a, \
+                         qtiles, rows, n_split, part);                                           \
+    } else {                                                                                     \
+      hipLaunchKernelGGL((paged_prefill_tiled<T, DD, VK_PF_RT, occ, false>), grid, block, 0, s,  \
+                         a, a.cu_q, a.cu_k, a.table, qtiles, 1u, nullptr);                       \
+    }                                                                                            \
+  } while (0)
   if (bf16) {
     if (head_dim == 128) VK_PF(bf16_t, 128);
     else VK_PF(bf16_t, 64);
