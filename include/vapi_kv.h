@@ -187,8 +187,13 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
  *   or ordered streams).
  * max_seqlen_q/k must bound every sequence's len_q/len_k (as in
  *   flash-attention); max_seqlen_q sizes the prefill grid. On the MFMA path
- *   (bf16/f16, head_dim 64 or 128) the workspace size depends on the batch,
- *   the heads and the GPU's CU count, not on the lengths; on the VALU path
+ *   (bf16/f16, head_dim 64 or 128) the decode's part depends on the batch,
+ *   the heads and the GPU's CU count, not on the lengths; a prefill batch
+ *   with fewer query tiles than the GPU has CUs asks for more (up to 256
+ *   MiB) to split its keys over more workgroups. That part is optional: a
+ *   workspace holding only the decode's part (or none, for a call with
+ *   VAPI_ATTN_NO_DECODE_ROWS) runs the prefill unsplit, and a
+ *   VAPI_ATTN_DETERMINISTIC call never splits. On the VALU path
  *   (f32 pools, other head dims) it holds the split-context partials and
  *   grows with the batch, max_seqlen_q and max_seqlen_k (0 while
  *   max_seqlen_k <= 64; small batches split their keys into chunks of 64
