@@ -251,6 +251,36 @@ def bench_small_batches(steps, warmup):
     return out
 
 
+def bench_small_prefill(steps, warmup):
+    """Prefill latency at small batches (config 3's heads, one causal chunk
+    at the end of each context): fewer query tiles than CUs, so the kernel
+    splits each tile's keys over several workgroups. Per call, replayed
+    from a HIP graph."""
+    cache = PagedKvCache(1, 32768, 16, 8, 128, torch.bfloat16, "HND")
+    workload.fill_normal(cache._slab, workload.seed_for(3))
+    rng = np.random.default_rng(workload.seed_for(3))
+    out = {}
+    for b, lq, lk in ((1, 512, 4096), (1, 128, 8192), (2, 512, 4096), (4, 512, 4096)):
+        nb = (lk + 15) // 16
+        perm = rng.permutation(32768)
+        batch = ForwardBatch(cu_seqlens_q=[i * lq for i in range(b + 1)],
+                             cu_seqlens_k=[i * lk for i in range(b + 1)],
+                             block_tables=[perm[i * nb:(i + 1) * nb].tolist() for i in range(b)],
+                             max_seqlen_q=lq, max_seqlen_k=lk)
+        prep = PreparedAttention.from_batch(batch, DEV)
+        q = torch.randn(b * lq, 32, 128, device=DEV).to(torch.bfloat16)
+        o = torch.empty_like(q)
+        gms = timed_graph(lambda: paged_attention_prepared(q, cache, 0, prep, 128 ** -0.5, out=o),
+                          steps, warmup)
+        # causal chunk at the end of the context: query i sees lk - lq + i + 1 keys
+        flops = 4 * 32 * 128 * b * sum(lk - lq + i + 1 for i in range(lq))
+        out[f"b{b}_q{lq}_k{lk}"] = dict(us=gms * 1e3, tflops=flops / (gms * 1e-3) / 1e12)
+    log("prefill small batches: " + ", ".join(f"{k} {v['us']:.1f} us ({v['tflops']:.0f} TFLOP/s)"
+                                              for k, v in out.items()))
+    del cache
+    return out
+
+
 def bench_head_dim_64(steps, warmup):
     """Configs 2 and 3 with head_dim 64 (LFM2's attention layers: 32 q / 8 kv
     heads of 64), on the same MFMA kernels' head_dim-64 builds."""
@@ -881,6 +911,7 @@ def main():
         extras["valu_attention"] = bench_valu(args.steps, args.warmup)
         extras["head_dim_64"] = bench_head_dim_64(args.steps, args.warmup)
         extras["decode_small_batches"] = bench_small_batches(args.steps, args.warmup)
+        extras["prefill_small_batches"] = bench_small_prefill(args.steps, args.warmup)
     extras["blocks_cfg4"] = bench_blocks(max(args.steps // 5, 3), 2, dec)
     if args.only == "blocks":
         return
