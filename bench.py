@@ -87,9 +87,18 @@ def timed_graph(fn, steps, warmup):
 
 # ---- config 2: decode (headline) ---------------------------------------------
 
+# Decode calls rotate over this many layers of one pool (each config 2's
+# 32k blocks, filled with their own values), as a forward pass's layers
+# follow each other. Replaying one layer's call back to back lets the
+# 256 MB last-level cache keep some of the previous call's K/V (the adaptive
+# work split moves which wave reads a tile, and when), which no forward
+# sees: on one box 137 us per call on one layer against 143 us rotating.
+DECODE_LAYERS = 4
+
+
 def setup_decode():
     w = workload.config2_decode()
-    cache = PagedKvCache(1, w.num_blocks, w.block_size, w.num_kv_heads, w.head_dim,
+    cache = PagedKvCache(DECODE_LAYERS, w.num_blocks, w.block_size, w.num_kv_heads, w.head_dim,
                          torch.bfloat16, "HND")
     workload.fill_normal(cache._slab, workload.seed_for(2))
     g = torch.Generator(device=DEV).manual_seed(workload.seed_for(2) + 1)
@@ -106,10 +115,17 @@ def setup_decode():
     alg_bytes = (kv_bytes + 2 * w.batch * w.num_heads * w.head_dim * 2 + n_blocks * 4
                  + 2 * (w.batch + 1) * 4)
 
+    turn = [0]
+
     def step():
+        paged_attention_prepared(q, cache, turn[0] % DECODE_LAYERS, prep, scale, out=out)
+        turn[0] += 1
+
+    def step_same_layer():
         paged_attention_prepared(q, cache, 0, prep, scale, out=out)
 
-    return dict(w=w, cache=cache, q=q, batch=batch, prep=prep, step=step, scale=scale,
+    return dict(w=w, cache=cache, q=q, batch=batch, prep=prep, step=step,
+                step_same_layer=step_same_layer, scale=scale,
                 sum_len=sum_len, alg_bytes=alg_bytes, flops=4.0 * w.num_heads * w.head_dim * sum_len)
 
 
@@ -123,7 +139,11 @@ def bench_decode(steps, warmup):
     # captures its decode step runs it (GraphRunner, backend.rs:893-1216).
     gms = timed_graph(d["step"], steps, warmup)
     log(f"decode cfg2 in a graph: {gms * 1e3:.1f} us/step, "
-        f"{d['alg_bytes'] / (gms * 1e-3) / 1e9:.0f} GB/s")
+        f"{d['alg_bytes'] / (gms * 1e-3) / 1e9:.0f} GB/s (layers rotating)")
+    same = timed_graph(d["step_same_layer"], steps, warmup)
+    log(f"decode cfg2 in a graph, one layer replayed: {same * 1e3:.1f} us/step, "
+        f"{d['alg_bytes'] / (same * 1e-3) / 1e9:.0f} GB/s (not reported as the value: the "
+        "last-level cache keeps part of the previous call's K/V)")
     # Per-call spread: each of `steps` calls between its own pair of events
     # on the stream the kernels run on (median, 10th and 90th percentile).
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -136,7 +156,9 @@ def bench_decode(steps, warmup):
     per = np.array([a.elapsed_time(b) * 1e3 for a, b in evs])
     spread = dict(median_us=float(np.median(per)), p10_us=float(np.percentile(per, 10)),
                   p90_us=float(np.percentile(per, 90)), calls=int(steps),
-                  graph_us=gms * 1e3)
+                  graph_us=gms * 1e3, layers_rotated=DECODE_LAYERS,
+                  one_layer_replayed_graph_us=same * 1e3,
+                  one_layer_replayed_graph_gbs=d["alg_bytes"] / (same * 1e-3) / 1e9)
     log(f"decode cfg2 per call: median {spread['median_us']:.1f} us "
         f"(p10 {spread['p10_us']:.1f}, p90 {spread['p90_us']:.1f})")
     d.update(ms=ms, wall=wall, gbs=gbs, graph_ms=gms, spread=spread,
@@ -183,12 +205,19 @@ def bench_fused_step(d, steps, warmup):
     dslots = torch.from_numpy(slots.view(np.int32)).to(DEV)
     cache, q, prep, scale, out = d["cache"], d["q"], d["prep"], d["scale"], torch.empty_like(d["q"])
 
+    turn = [0]
+
     def two():
-        write_rows_indexed(cache, 0, k_new, v_new, dslots)
-        paged_attention_prepared(q, cache, 0, prep, scale, out=out)
+        layer = turn[0] % DECODE_LAYERS
+        turn[0] += 1
+        write_rows_indexed(cache, layer, k_new, v_new, dslots)
+        paged_attention_prepared(q, cache, layer, prep, scale, out=out)
 
     def fused():
-        paged_attention_append_prepared(q, k_new, v_new, dslots, cache, 0, prep, scale, out=out)
+        layer = turn[0] % DECODE_LAYERS
+        turn[0] += 1
+        paged_attention_append_prepared(q, k_new, v_new, dslots, cache, layer, prep, scale,
+                                        out=out)
 
     ms_two, _ = timed(two, steps, warmup)
     ms_fused, _ = timed(fused, steps, warmup)
@@ -227,7 +256,7 @@ def bench_valu(steps, warmup):
 def bench_small_batches(steps, warmup):
     """Decode latency at small batches (config 2's heads and pool, equal
     contexts): where the call's fixed costs (the first loads, the merge)
-    weigh most. Per call, replayed from a HIP graph."""
+    weigh most. Per call, replayed from a HIP graph over rotating tables."""
     cache = PagedKvCache(1, 32768, 16, 8, 128, torch.bfloat16, "HND")
     workload.fill_normal(cache._slab, workload.seed_for(2))
     rng = np.random.default_rng(workload.seed_for(2))
@@ -235,15 +264,28 @@ def bench_small_batches(steps, warmup):
     for b, lk in ((1, 8192), (1, 32768), (4, 4096), (16, 2048)):
         nb = (lk + 15) // 16
         perm = rng.permutation(32768)
-        batch = ForwardBatch(cu_seqlens_q=list(range(b + 1)),
-                             cu_seqlens_k=[i * lk for i in range(b + 1)],
-                             block_tables=[perm[i * nb:(i + 1) * nb].tolist() for i in range(b)],
-                             max_seqlen_q=1, max_seqlen_k=lk)
-        prep = PreparedAttention.from_batch(batch, DEV)
+        # Consecutive calls read disjoint blocks (up to 16 tables cut from one
+        # permutation of the pool), so no call finds the previous one's K/V
+        # in the last-level cache: at least 512 MB between reuses.
+        n_tab = min(16, 32768 // (b * nb))
+        preps = []
+        for j in range(n_tab):
+            part = perm[j * b * nb:(j + 1) * b * nb]
+            batch = ForwardBatch(cu_seqlens_q=list(range(b + 1)),
+                                 cu_seqlens_k=[i * lk for i in range(b + 1)],
+                                 block_tables=[part[i * nb:(i + 1) * nb].tolist() for i in range(b)],
+                                 max_seqlen_q=1, max_seqlen_k=lk)
+            preps.append(PreparedAttention.from_batch(batch, DEV))
         q = torch.randn(b, 32, 128, device=DEV).to(torch.bfloat16)
         o = torch.empty_like(q)
-        gms = timed_graph(lambda: paged_attention_prepared(q, cache, 0, prep, 128 ** -0.5, out=o),
-                          steps, warmup)
+        turn = [0]
+
+        def call():
+            prep = preps[turn[0] % n_tab]
+            turn[0] += 1
+            paged_attention_prepared(q, cache, 0, prep, 128 ** -0.5, out=o)
+
+        gms = timed_graph(call, max(steps, 2 * n_tab), warmup)
         kv = b * lk * 8 * 128 * 2 * 2
         out[f"b{b}_k{lk}"] = dict(us=gms * 1e3, gbs=kv / (gms * 1e-3) / 1e9)
     log("decode small batches: " + ", ".join(f"{k} {v['us']:.1f} us" for k, v in out.items()))
@@ -285,7 +327,8 @@ def bench_head_dim_64(steps, warmup):
     """Configs 2 and 3 with head_dim 64 (LFM2's attention layers: 32 q / 8 kv
     heads of 64), on the same MFMA kernels' head_dim-64 builds."""
     w = workload.config2_decode()
-    cache = PagedKvCache(1, w.num_blocks, w.block_size, 8, 64, torch.bfloat16, "HND")
+    cache = PagedKvCache(DECODE_LAYERS, w.num_blocks, w.block_size, 8, 64, torch.bfloat16,
+                         "HND")
     workload.fill_normal(cache._slab, workload.seed_for(2))
     q = torch.randn(w.batch, 32, 64, device=DEV).to(torch.bfloat16)
     batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
@@ -293,8 +336,13 @@ def bench_head_dim_64(steps, warmup):
                          max_seqlen_k=int(w.lens.max()))
     prep = PreparedAttention.from_batch(batch, DEV)
     out = torch.empty_like(q)
-    gms = timed_graph(lambda: paged_attention_prepared(q, cache, 0, prep, 0.125, out=out),
-                      steps, warmup)
+    turn = [0]
+
+    def call():
+        paged_attention_prepared(q, cache, turn[0] % DECODE_LAYERS, prep, 0.125, out=out)
+        turn[0] += 1
+
+    gms = timed_graph(call, steps, warmup)
     kv = int(w.lens.sum()) * 2 * 8 * 64 * 2
     res = {"decode_cfg2_d64": dict(us=gms * 1e3, kv_bytes=kv, gbs=kv / (gms * 1e-3) / 1e9)}
     del cache, q, out
