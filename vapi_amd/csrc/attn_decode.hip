@@ -13,8 +13,9 @@
 // XCD is slow differs between boxes), so the steps are split into 8 group
 // ranges, one per XCD (workgroup b runs on XCD b % 8), in proportion to
 // shares that each launch measures for the next: every wave records its
-// steps and elapsed time, and the merge kernel moves the shares halfway to
-// the measured per-group rates. Within a group each wave takes an
+// steps and its entry and end times, and the merge kernel moves the shares
+// halfway to the measured per-group rates, counted from the grid's first
+// entry (the XCDs start the grid up to ~2.5 us apart). Within a group each wave takes an
 // equal contiguous slice. Any shares give the same results up to the f32
 // merge order; the shares only move where the pieces split.
 //
@@ -52,8 +53,10 @@ constexpr uint32_t kMergeWaves = VK_MERGE_WAVES;  // merge: segments (waves) per
 constexpr uint32_t kMaxPlanSeqs = 4096;  // sequences per launch (host chunks beyond)
 
 // Balance block (u32 words, kept across launches at the start of the
-// workspace): shares f32[8] at 0, per-wave (steps, ticks) from kBalStats.
+// workspace): shares f32[8] at 0, per-wave (steps, entry tick, end tick, 0)
+// from kBalStats.
 constexpr uint32_t kBalStats = 64;
+constexpr uint32_t kStatWords = 4;
 
 // Steps of sequence s (0 for rows that are not decode rows).
 __device__ __forceinline__ uint32_t decode_steps(const AttnArgs& a,
@@ -225,6 +228,9 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t B = a.batch;
   const uint32_t nwg = gridDim.x;
+  // The shared 100 MHz clock at entry: XCDs start the grid up to ~2.5 us
+  // apart, and the shares account for it.
+  const uint32_t t_entry = (uint32_t)__builtin_amdgcn_s_memrealtime();
 
   // Step prefix sums over sequences (each sequence contributes kvh segments).
   {
@@ -280,9 +286,9 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
   const uint32_t t_end = F[x] + (uint32_t)(((uint64_t)(j + 1) * len) / nw);
   const uint32_t r = group_offset(nwg, x) + j;
   const uint32_t gw = blockIdx.x * kDecodeWavesPerWG + wave;
-  uint32_t* stat = a.bal + kBalStats + 2 * gw;
+  uint32_t* stat = a.bal + kBalStats + kStatWords * gw;
   if (t_begin >= t_end) {
-    if (lane == 0) stat[0] = 0u, stat[1] = 0u;
+    if (lane == 0) *(uint4*)stat = make_uint4(0u, t_entry, t_entry, 0u);
     // An empty slice between the first and last range of a segment: its
     // partial slot is marked empty (l = 0) for the merge.
     if (t_begin < S) {
@@ -292,7 +298,9 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
     }
     return;
   }
+#ifdef VK_DECODE_TRACE
   const uint64_t tr0 = __builtin_amdgcn_s_memrealtime();
+#endif
 
   uint32_t t = t_begin;
   const uint32_t col = lane & 15, g = lane >> 4;
@@ -365,25 +373,28 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
   }
   const uint64_t tr1 = __builtin_amdgcn_s_memrealtime();
   if (lane == 0) {
-    stat[0] = t_end - t_begin;
-    stat[1] = (uint32_t)min(tr1 - tr0, (uint64_t)0xFFFFFFFFu);
+    *(uint4*)stat = make_uint4(t_end - t_begin, t_entry, (uint32_t)tr1, 0u);
   }
 #ifdef VK_DECODE_TRACE
-  // Per wave: start/end (100 MHz ticks), steps done, HW_ID | XCC_ID << 32.
+  // Per wave: start/end (100 MHz ticks), steps done << 32 | entry tick,
+  // HW_ID | XCC_ID << 32.
   if (lane == 0) {
     uint64_t* tr = a.trace + 4ull * gw;
     tr[0] = tr0;
     tr[1] = tr1;
-    tr[2] = t_end - t_begin;
+    tr[2] = ((uint64_t)(t_end - t_begin) << 32) | t_entry;
     tr[3] = (uint64_t)__builtin_amdgcn_s_getreg((31 << 11) | 4) |
             ((uint64_t)__builtin_amdgcn_s_getreg((3 << 11) | 20) << 32);
   }
 #endif
 }
 
-// The next launch's shares from this launch's per-wave timings: groups that
-// ran keep their total and move halfway to their measured rates (steps per
-// tick per wave); groups without steps keep their share.
+// The next launch's shares from this launch's per-wave timings: each group
+// that ran keeps its total and moves halfway to its measured rate, steps
+// per tick per wave counted from the grid's first entry (so a group whose
+// XCD started late, or streamed slower, gets fewer steps and the groups end
+// together); groups without steps keep their share. Ticks are the low 32
+// bits of the shared 100 MHz clock, compared as differences.
 __device__ __forceinline__ void update_shares(const AttnArgs& a, uint32_t nwg, uint32_t lane) {
   float steps[kGroups], ticks[kGroups];
   const uint32_t W = nwg * kDecodeWavesPerWG;
@@ -392,27 +403,37 @@ __device__ __forceinline__ void update_shares(const AttnArgs& a, uint32_t nwg, u
   // All of a lane's loads are issued before the first is used (one memory
   // round trip instead of W / 64 dependent ones).
   constexpr uint32_t kBatch = 16;
-  float st = 0.f, tk = 0.f;
+  const uint32_t* stats = a.bal + kBalStats;
+  const uint32_t ref = __builtin_amdgcn_readfirstlane(stats[1]);  // wave 0's entry
+  float st = 0.f, tk = 0.f, cnt = 0.f;
+  int32_t first = 0;
   for (uint32_t base = 0; base < W; base += 64 * kBatch) {
-    uint2 v[kBatch];
+    uint4 v[kBatch];
 #pragma unroll
     for (uint32_t i = 0; i < kBatch; ++i) {
       const uint32_t gw = base + 64 * i + lane;
-      v[i] = gw < W ? *(const uint2*)(a.bal + kBalStats + 2 * gw) : make_uint2(0u, 0u);
+      v[i] = gw < W ? *(const uint4*)(stats + kStatWords * gw) : make_uint4(0u, ref, ref, 0u);
     }
 #pragma unroll
-    for (uint32_t i = 0; i < kBatch; ++i)
-      if (v[i].x) st += (float)v[i].x, tk += (float)v[i].y;
+    for (uint32_t i = 0; i < kBatch; ++i) {
+      first = min(first, (int32_t)(v[i].y - ref));
+      if (v[i].x) st += (float)v[i].x, tk += (float)(int32_t)(v[i].z - ref), cnt += 1.f;
+    }
   }
+  // tk holds end - ref summed over the lane's counted waves; the counts
+  // turn it into end - (grid entry) below.
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) first = min(first, __shfl_xor(first, o));
   // Sum over the lanes of each group: lanes with equal (l / 4) % 8 are
   // l ^ 32 and l ^ 1, l ^ 2 (same l / 4).
-  st += __shfl_xor(st, 1), tk += __shfl_xor(tk, 1);
-  st += __shfl_xor(st, 2), tk += __shfl_xor(tk, 2);
-  st += __shfl_xor(st, 32), tk += __shfl_xor(tk, 32);
+  st += __shfl_xor(st, 1), tk += __shfl_xor(tk, 1), cnt += __shfl_xor(cnt, 1);
+  st += __shfl_xor(st, 2), tk += __shfl_xor(tk, 2), cnt += __shfl_xor(cnt, 2);
+  st += __shfl_xor(st, 32), tk += __shfl_xor(tk, 32), cnt += __shfl_xor(cnt, 32);
 #pragma unroll
   for (uint32_t y = 0; y < kGroups; ++y) {
     steps[y] = __shfl(st, (int)(y * kDecodeWavesPerWG));
-    ticks[y] = __shfl(tk, (int)(y * kDecodeWavesPerWG));
+    ticks[y] = __shfl(tk, (int)(y * kDecodeWavesPerWG)) -
+               __shfl(cnt, (int)(y * kDecodeWavesPerWG)) * (float)first;
   }
   if (lane != 0) return;
   float w[kGroups], rate[kGroups], w_tot = 0.f, r_tot = 0.f;
@@ -634,7 +655,7 @@ static DecodeWs decode_ws(uint32_t b, uint32_t kvh, uint32_t group, uint32_t hea
   const size_t slots = (size_t)num_waves + (size_t)b * kvh;
   DecodeWs w;
   w.bal = 0;
-  w.ranges = up256((kBalStats + 2 * (size_t)num_waves) * sizeof(uint32_t));
+  w.ranges = up256((kBalStats + kStatWords * (size_t)num_waves) * sizeof(uint32_t));
   w.ml = w.ranges + up256((size_t)b * kvh * 2 * sizeof(uint32_t));
   w.o = w.ml + up256(slots * group * 2 * sizeof(float));
   w.trace = w.o + up256(slots * group * head_dim * sizeof(float));
