@@ -178,12 +178,26 @@ def bench_gather(d, steps, warmup):
     from vapi_amd._lib import check, lib
     from vapi_amd.cache import stream_handle
     cache = d["cache"]
+    # The timed calls rotate over the layers and over four tables of the
+    # same length cut from one permutation of the pool (the first is the
+    # sequence's own): 16 sources of 34 MB, so no call reads what the
+    # last-level cache kept from the one before.
+    nb = table.shape[0]
+    perm = np.random.default_rng(7).permutation(w.num_blocks)
+    tables = [table] + [torch.from_numpy(perm[j * nb:(j + 1) * nb].astype(np.int32)).to(DEV)
+                        for j in range(3)]
+    turn = [0]
 
     def gather():
-        check(lib().vapi_kv_gather(cache.pool, 0, table.data_ptr(), table.shape[0], lk,
+        t = tables[(turn[0] // DECODE_LAYERS) % len(tables)]
+        layer = turn[0] % DECODE_LAYERS
+        turn[0] += 1
+        check(lib().vapi_kv_gather(cache.pool, layer, t.data_ptr(), nb, lk,
                                    k_out.data_ptr(), v_out.data_ptr(), stream_handle()))
 
-    ms, _ = timed(gather, steps, warmup)
+    ms, _ = timed(gather, max(steps, 32), warmup)
+    turn[0] = 0
+    gather()
     alg = 2 * 2 * k_out.numel() * k_out.element_size() + table.numel() * 4
     gbs = alg / (ms * 1e-3) / 1e9
     ok = torch.equal(k_out[: w.block_size], cache.reference_view(0, "k")[int(w.tables[i][0])])
