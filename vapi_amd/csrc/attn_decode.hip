@@ -479,6 +479,22 @@ __device__ __forceinline__ void copy_new_rows(const AttnArgs& a, uint32_t wg, ui
   }
 }
 
+// n <= 8 merged outputs O / L at dst: one 16-byte store when there are
+// eight and dst is 16-byte aligned (output rows start 256-byte aligned),
+// else one store per element.
+template <typename T>
+__device__ __forceinline__ void store_outputs(T* dst, uint32_t n, const float (&O)[8],
+                                              const float (&L)[8]) {
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = L[j] > 0.f ? O[j] / L[j] : 0.f;
+  if (n == 8 && ((uintptr_t)dst & 15) == 0) {
+    *(uint4*)dst = pack8<T>(v);
+  } else {
+    for (uint32_t j = 0; j < n; ++j) dst[j] = from_f32<T>(v[j]);
+  }
+}
+
 // WPS waves per segment: 1 (four segments per workgroup) when segments are
 // many and each has a few pieces; 4 (one segment per workgroup) when they
 // are few, so that each has many pieces: wave v then combines pieces r0 +
@@ -507,12 +523,15 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_merge(AttnArgs 
   // One round trip: the row's extents and the segment's ranges (stale for
   // rows that are not decode rows, which return here; the same for all the
   // waves of a segment).
+  const uint2 rr = *(const uint2*)(a.seg_ranges + 2 * segi);
   const uint32_t q0 = a.cu_q[seq], q1 = a.cu_q[seq + 1];
   const uint32_t k0 = a.cu_k[seq], k1 = a.cu_k[seq + 1];
-  const uint32_t r0 = a.seg_ranges[2 * segi], r1 = a.seg_ranges[2 * segi + 1];
-  if (q1 - q0 != 1 || (int32_t)(k1 - k0) <= 0) return;
-  // r0 == r1: one range held the whole segment and wrote the output.
-  if (r0 >= r1 || r1 >= nwg * kDecodeWavesPerWG) return;
+  const uint32_t r0 = rr.x, r1 = rr.y;
+  // One test of all six words (r0 == r1: one range held the whole segment
+  // and wrote the output), so that the loads are issued together.
+  const bool skip = (q1 - q0 != 1) | ((int32_t)(k1 - k0) <= 0) | (r0 >= r1) |
+                    (r1 >= nwg * kDecodeWavesPerWG);
+  if (skip) return;
   const uint32_t G = a.group, seg = segi;
   const uint32_t E = G * D / 64;
   const uint32_t e_lane = lane * E;
@@ -610,13 +629,11 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_merge(AttnArgs 
           }
           L[j] = Lj, O[j] = Oj;
         }
-        for (uint32_t j = 0; j < n; ++j)
-          orow[e_lane + j0 + j] = from_f32<T>(L[j] > 0.f ? O[j] / L[j] : 0.f);
+        store_outputs<T>(orow + e_lane + j0, n, O, L);
       }
       __syncthreads();  // cmb is reused by the next eight outputs
     } else {
-      for (uint32_t j = 0; j < n; ++j)
-        orow[e_lane + j0 + j] = from_f32<T>(L[j] > 0.f ? O[j] / L[j] : 0.f);
+      store_outputs<T>(orow + e_lane + j0, n, O, L);
     }
   }
 }
