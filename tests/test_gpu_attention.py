@@ -212,6 +212,42 @@ def test_random_mixed_batches_match_the_oracle(case):
         assert d_abs <= 2e-2 * float(want.abs().max()), d_abs
 
 
+def drawn_case(seed):
+    """A batch drawn from a seed: dtype, GQA group (1-16), head_dim, block
+    size, layout, window, and 1-6 sequences mixing decode rows with prefill
+    chunks of up to 150 tokens over up to 2,500 keys."""
+    rng = np.random.default_rng(1000 + seed)
+    dtype = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(3))]
+    kvh = int(rng.choice([1, 2, 4, 8]))
+    group = int(rng.choice([1, 2, 4, 8, 16]))
+    d = int(rng.choice([64, 128, 128, 80])) if dtype == torch.float32 else int(rng.choice([64, 128]))
+    bs = int(rng.choice([16, 32, 64]))
+    layout = "HND" if rng.random() < 0.7 else "NHD"
+    window = None if rng.random() < 0.6 else int(rng.integers(1, 600))
+    n = int(rng.integers(1, 7))
+    lens_k = [int(x) for x in rng.integers(1, 2500, n)]
+    lens_q = [1 if rng.random() < 0.5 else int(rng.integers(0, min(lk, 150) + 1)) for lk in lens_k]
+    return dtype, kvh * group, kvh, d, bs, lens_q, lens_k, window, layout, rng
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_drawn_batches_match_the_oracle(seed):
+    dtype, heads, kvh, d, bs, lens_q, lens_k, window, layout, rng = drawn_case(seed)
+    print(f"drawn case {seed}: {dtype} h{heads} kv{kvh} d{d} bs{bs} {layout} w{window} "
+          f"q{lens_q} k{lens_k}", flush=True)
+    c, q, batch = random_case(rng, dtype, heads, kvh, d, bs, lens_q, lens_k, layout)
+    if q.shape[0] == 0:
+        pytest.skip("no query rows drawn")
+    scale = d ** -0.5
+    want = oracle_out(q, c, 0, batch, scale, window)
+    got = paged_attention(q, c, 0, batch, scale, window)
+    d_abs = max_abs(got, want)
+    if dtype == torch.float32:
+        assert d_abs <= 1e-5, d_abs
+    else:
+        assert d_abs <= 2e-2 * float(want.abs().max()), d_abs
+
+
 @pytest.mark.parametrize("scale", [-0.09, 0.0, 0.7])
 def test_negative_zero_and_large_scales_match_the_oracle(scale):
     """The MFMA kernels take the max on raw scores and fold |scale| into the
