@@ -16,6 +16,8 @@
  *   HipBackend::{num_blocks, block_bytes, export_block, import_block,
  *                copy_blocks}        backend.rs:339-367 as CandleBackend
  *                                    implements them (candle backend.rs:695-797)
+ *   fork_copy_pairs                  the copy pairs of Scheduler::fork
+ *                                    (crates/vapi-engine/src/scheduler.rs:217-281)
  *
  * Errors are values, never exceptions (shape, dtype and range violations are
  * errors, as cache.rs:438-445 tests). Tensors are device buffers with a
@@ -653,6 +655,37 @@ inline Result<Tensor> paged_attention(const Tensor& q, const PagedKvCache& cache
 // ---- the backend's block methods ---------------------------------------------
 
 using BlockId = uint32_t;
+
+/*
+ * The copy pairs Scheduler::fork hands to copy_blocks
+ * (crates/vapi-engine/src/scheduler.rs:217-281), for `extra` children of a
+ * sequence whose table is `parent` and whose prompt has `computed` tokens:
+ * the blocks the prompt fills completely are shared; the open block after
+ * them (if the parent has one) is replaced by a fresh block per child,
+ * `allocate()`, and a (parent's open block, child's block) pair is emitted
+ * only when the open block holds content (computed % block_size != 0).
+ */
+struct ForkPlan {
+  std::vector<std::vector<BlockId>> children;
+  std::vector<std::pair<BlockId, BlockId>> pairs;
+};
+template <class Allocate>
+ForkPlan fork_copy_pairs(const std::vector<BlockId>& parent, size_t computed, size_t block_size,
+                         size_t extra, Allocate allocate) {
+  const size_t full = computed / block_size;
+  const bool has_content = computed % block_size != 0;
+  ForkPlan plan;
+  for (size_t c = 0; c < extra; ++c) {
+    std::vector<BlockId> child(parent.begin(), parent.begin() + std::min(full, parent.size()));
+    if (parent.size() > full) {
+      const BlockId fresh = allocate();
+      if (has_content) plan.pairs.push_back({parent[full], fresh});
+      child.push_back(fresh);
+    }
+    plan.children.push_back(std::move(child));
+  }
+  return plan;
+}
 
 /*
  * ExecutionBackend's block methods (crates/vapi-engine/src/backend.rs:339-367)

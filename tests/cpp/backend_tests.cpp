@@ -4,8 +4,9 @@
 //   crates/vapi-backend-candle/src/cache.rs:292-446      (cache tests)
 //   crates/vapi-backend-candle/src/attention.rs:318-431  (CPU-path tests)
 //   crates/vapi-backend-candle/src/attention.rs:432-714  (GPU-vs-CPU tests)
-// plus the block methods (backend.rs:695-797) and ForwardBatch::validate
-// (crates/vapi-engine/src/backend.rs:96-204).
+// plus the block methods (backend.rs:695-797), ForwardBatch::validate
+// (crates/vapi-engine/src/backend.rs:96-204) and the fork's copy pairs
+// (crates/vapi-engine/tests/scheduler.rs:524-637).
 //
 // Usage: backend_tests [--host-only] [name-substring]
 //   --host-only runs the tests that touch no GPU (validate, table packing,
@@ -571,6 +572,58 @@ TEST(copy_blocks_copies_every_layer_k_and_v, true) {
   EXPECT(OK(be.export_block(1)) == b2);
   EXPECT(OK(be.export_block(5)) == b5);  // untouched
   EXPECT(be.copy_blocks({{0, 6}}).is_err());
+}
+
+// ---- Scheduler::fork's copy pairs (crates/vapi-engine/tests/scheduler.rs:524-637) ----
+
+std::function<BlockId()> counter(BlockId start) {
+  auto next = std::make_shared<BlockId>(start);
+  return [next] { return (*next)++; };
+}
+
+TEST(a_partial_prompt_block_is_copied_once_per_child, false) {
+  // 10 tokens over 4-token blocks, two forks: two full blocks shared, the
+  // partial third copied per fork.
+  const std::vector<BlockId> parent = {5, 9, 2};
+  const auto plan = fork_copy_pairs(parent, 10, 4, 2, counter(100));
+  EXPECT(plan.children.size() == 2 && plan.pairs.size() == 2);
+  for (size_t c = 0; c < plan.children.size(); ++c) {
+    EXPECT(plan.pairs[c].first == parent[2]);
+    EXPECT(plan.children[c][0] == parent[0] && plan.children[c][1] == parent[1]);
+    EXPECT(plan.children[c][2] == plan.pairs[c].second && plan.children[c][2] != parent[2]);
+  }
+  EXPECT(plan.pairs[0].second != plan.pairs[1].second);
+}
+
+TEST(a_block_aligned_prompt_copies_nothing_but_still_takes_a_private_open_block, false) {
+  const std::vector<BlockId> parent = {3, 4, 11};
+  const auto plan = fork_copy_pairs(parent, 8, 4, 1, counter(100));
+  EXPECT(plan.pairs.empty());
+  EXPECT(plan.children[0][0] == 3 && plan.children[0][1] == 4 && plan.children[0][2] != 11);
+}
+
+TEST(a_parent_without_an_open_block_shares_everything, false) {
+  int calls = 0;
+  const auto plan = fork_copy_pairs({7, 8}, 8, 4, 3, [&] { ++calls; return BlockId(99); });
+  EXPECT(plan.pairs.empty() && calls == 0);
+  for (const auto& child : plan.children) EXPECT((child == std::vector<BlockId>{7, 8}));
+}
+
+TEST(a_fork_copies_the_open_block_into_each_child_on_the_device, true) {
+  // The fork's pairs through copy_blocks: each child's private block holds
+  // the parent's open block, every layer, K and V; the shared blocks are
+  // untouched.
+  auto be = OK(filled_backend(3, 8));
+  const std::vector<BlockId> parent = {5, 1, 6};
+  const auto plan = fork_copy_pairs(parent, 10 * 16 / 4, 16, 2, counter(2));  // 40 tokens
+  EXPECT(plan.pairs.size() == 2);
+  const auto open = OK(be.export_block(6)), shared = OK(be.export_block(5));
+  OK_VOID(be.copy_blocks(plan.pairs));
+  for (const auto& child : plan.children) {
+    EXPECT(OK(be.export_block(child[2])) == open);
+    EXPECT(child[0] == 5 && child[1] == 1);
+  }
+  EXPECT(OK(be.export_block(5)) == shared);
 }
 
 // ---- ForwardBatch::validate (crates/vapi-engine/src/backend.rs:96-204) ----------
