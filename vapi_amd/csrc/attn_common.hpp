@@ -126,12 +126,12 @@ template <int DPL>
 __device__ __forceinline__ VRow<DPL> load_vrow(const void* p) {
   VRow<DPL> r;
   if constexpr (DPL == 4) {
-    const uint2 x = *(const uint2*)p;
+    const uint2 x = load_stream((const uint2*)p);
     r.w[0] = x.x; r.w[1] = x.y;
   } else {
 #pragma unroll
     for (int i = 0; i < DPL / 8; ++i) {
-      const uint4 x = ((const uint4*)p)[i];
+      const uint4 x = load_stream((const uint4*)p + i);
       r.w[4 * i] = x.x; r.w[4 * i + 1] = x.y; r.w[4 * i + 2] = x.z; r.w[4 * i + 3] = x.w;
     }
   }
@@ -234,7 +234,7 @@ __device__ __forceinline__ void load_k(KTile<D>& st, const uint32_t* __restrict_
     const char* src = kt + kr;
     if (knew != nullptr && (int32_t)col >= last - ts) src = knew + 8 * g * sizeof(T);
 #pragma unroll
-    for (int c = 0; c < KC; ++c) st.k[tt][c] = *(const uint4*)(src + 64u * c);
+    for (int c = 0; c < KC; ++c) st.k[tt][c] = load_stream((const uint4*)(src + 64u * c));
   }
 }
 

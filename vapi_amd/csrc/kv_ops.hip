@@ -212,7 +212,7 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(GatherArgs a) {
         const char* src = (kv ? a.v_src : a.k_src) + blk * a.blk_b +
                           h * a.head_b + off * a.tok_b + (uint64_t)u * C;
         // A table entry past the pool reads nothing and gathers zeros.
-        val[j] = blk < a.num_blocks ? *(const V*)src : V{};
+        val[j] = blk < a.num_blocks ? load_stream((const V*)src) : V{};
         dst[j] = out + ((uint64_t)t * a.kvh.d + h) * a.row_bytes +
                  (uint64_t)u * C;
       }
@@ -259,14 +259,14 @@ __global__ __launch_bounds__(256) void kv_copy_kernel(CopyArgs a) {
       char* buf = (kv ? a.v : a.k) + layer * a.layer_b;
       const uint64_t o = (uint64_t)u * C;
       if (src_blk < a.num_blocks && dst_blk < a.num_blocks) {  // else skipped
-        val[j] = *(const V*)(buf + src_blk * a.blk_b + o);
+        val[j] = load_stream((const V*)(buf + src_blk * a.blk_b + o));
         dst[j] = buf + dst_blk * a.blk_b + o;
       }
     }
   }
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j)
-    if (dst[j]) *(V*)dst[j] = val[j];
+    if (dst[j]) store_stream((V*)dst[j], val[j]);
 }
 
 // ---- export / import (reference blob order) ----------------------------------
@@ -319,7 +319,7 @@ __global__ __launch_bounds__(256) void kv_blob_kernel(BlobArgs a) {
                    (uint64_t)layer * a.seg_bytes +
                    ((uint64_t)t * a.kvh.d + h) * a.row_bytes + (uint64_t)u * C;
       if (EXPORT) {
-        val[j] = *(const V*)pool;
+        val[j] = load_stream((const V*)pool);
         dst[j] = blob;
       } else {
         val[j] = *(const V*)blob;

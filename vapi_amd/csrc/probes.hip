@@ -13,17 +13,33 @@
 //                           indices (the block copy's 16 KiB (block, layer,
 //                           K or V) run).
 //
-// Each lane moves 16-byte chunks with all of its loads issued before any use;
+// Each probe comes in two forms: ordinary loads and stores, and streaming
+// (non-temporal) ones, which the paged-KV kernels use for data they touch
+// once. Each lane moves 16-byte chunks with all of its loads issued before any use;
 // reads fold their data into one word per workgroup so they cannot be
 // dropped. Grids are large (>> 256 workgroups) and one-shot.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "common.hpp"
 
 namespace {
 
 constexpr int kThreads = 256;
 constexpr int kUnroll = 8;  // 16-byte loads in flight per lane
 
+template <bool NT>
+__device__ __forceinline__ uint4 ld(const uint4* p) {
+  if constexpr (NT) return vk::load_stream(p);
+  else return *p;
+}
+template <bool NT>
+__device__ __forceinline__ void st(uint4* p, uint4 v) {
+  if constexpr (NT) vk::store_stream(p, v);
+  else *p = v;
+}
+
+template <bool NT>
 __global__ __launch_bounds__(kThreads) void probe_read_kernel(const uint4* __restrict__ src,
                                                               uint64_t n16,
                                                               uint32_t* __restrict__ sink) {
@@ -32,7 +48,7 @@ __global__ __launch_bounds__(kThreads) void probe_read_kernel(const uint4* __res
 #pragma unroll
   for (int i = 0; i < kUnroll; ++i) {
     const uint64_t j = base + (uint64_t)i * kThreads;
-    v[i] = j < n16 ? src[j] : make_uint4(0, 0, 0, 0);
+    v[i] = j < n16 ? ld<NT>(src + j) : make_uint4(0, 0, 0, 0);
   }
   uint32_t x = 0;
 #pragma unroll
@@ -42,7 +58,7 @@ __global__ __launch_bounds__(kThreads) void probe_read_kernel(const uint4* __res
 }
 
 // One wave per tile: tile_bytes / 1024 loads of 16 B per lane.
-template <int LOADS>
+template <int LOADS, bool NT>
 __global__ __launch_bounds__(kThreads) void probe_tiles_kernel(const char* __restrict__ base,
                                                                const uint32_t* __restrict__ ids,
                                                                uint32_t n_tiles,
@@ -53,7 +69,7 @@ __global__ __launch_bounds__(kThreads) void probe_tiles_kernel(const char* __res
   const uint4* t = (const uint4*)(base + (uint64_t)ids[wave] * (LOADS * 1024u));
   uint4 v[LOADS];
 #pragma unroll
-  for (int i = 0; i < LOADS; ++i) v[i] = t[i * 64 + lane];
+  for (int i = 0; i < LOADS; ++i) v[i] = ld<NT>(t + i * 64 + lane);
   uint32_t x = 0;
 #pragma unroll
   for (int i = 0; i < LOADS; ++i) x ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
@@ -62,6 +78,7 @@ __global__ __launch_bounds__(kThreads) void probe_tiles_kernel(const char* __res
 
 // One workgroup per 16 KiB: the block copy's per-workgroup shape, on
 // consecutive runs.
+template <bool NT>
 __global__ __launch_bounds__(kThreads) void probe_copy_kernel(uint4* __restrict__ dst,
                                                               const uint4* __restrict__ src,
                                                               uint64_t n16) {
@@ -71,17 +88,17 @@ __global__ __launch_bounds__(kThreads) void probe_copy_kernel(uint4* __restrict_
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     const uint64_t j = base + (uint64_t)i * kThreads;
-    if (j < n16) v[i] = src[j];
+    if (j < n16) v[i] = ld<NT>(src + j);
   }
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     const uint64_t j = base + (uint64_t)i * kThreads;
-    if (j < n16) dst[j] = v[i];
+    if (j < n16) st<NT>(dst + j, v[i]);
   }
 }
 
 // One workgroup per run: run_bytes / 4096 chunks of 16 B per thread.
-template <int ITEMS>
+template <int ITEMS, bool NT>
 __global__ __launch_bounds__(kThreads) void probe_runs_kernel(char* __restrict__ base,
                                                               const uint32_t* __restrict__ pairs,
                                                               uint32_t n_runs) {
@@ -92,57 +109,80 @@ __global__ __launch_bounds__(kThreads) void probe_runs_kernel(char* __restrict__
   uint4* d = (uint4*)(base + (uint64_t)pairs[2 * r + 1] * kRun);
   uint4 v[ITEMS];
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) v[i] = s[i * kThreads + threadIdx.x];
+  for (int i = 0; i < ITEMS; ++i) v[i] = ld<NT>(s + i * kThreads + threadIdx.x);
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) d[i * kThreads + threadIdx.x] = v[i];
+  for (int i = 0; i < ITEMS; ++i) st<NT>(d + i * kThreads + threadIdx.x, v[i]);
 }
 
 }  // namespace
 
 extern "C" {
 
+// Every probe takes `streaming`: 0 for ordinary loads and stores, 1 for
+// non-temporal ones.
+
 // Sequential read of `bytes` (a multiple of 16) at src. sink: device
 // u32[1024] (written only by a sentinel the data never hits).
-int vapi_probe_read(const void* src, uint64_t bytes, void* sink, hipStream_t stream) {
+int vapi_probe_read(const void* src, uint64_t bytes, void* sink, uint32_t streaming,
+                    hipStream_t stream) {
   const uint64_t n16 = bytes / 16;
   const uint64_t grid = (n16 + kThreads * kUnroll - 1) / (kThreads * kUnroll);
-  hipLaunchKernelGGL(probe_read_kernel, dim3((uint32_t)grid), dim3(kThreads), 0, stream,
-                     (const uint4*)src, n16, (uint32_t*)sink);
+  if (streaming)
+    hipLaunchKernelGGL(probe_read_kernel<true>, dim3((uint32_t)grid), dim3(kThreads), 0, stream,
+                       (const uint4*)src, n16, (uint32_t*)sink);
+  else
+    hipLaunchKernelGGL(probe_read_kernel<false>, dim3((uint32_t)grid), dim3(kThreads), 0, stream,
+                       (const uint4*)src, n16, (uint32_t*)sink);
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 // Reads of n_tiles runs of tile_bytes (4096 or 8192) at base + ids[i] *
 // tile_bytes (ids: device u32[n_tiles]).
 int vapi_probe_read_tiles(const void* base, const uint32_t* ids, uint32_t n_tiles,
-                          uint32_t tile_bytes, void* sink, hipStream_t stream) {
+                          uint32_t tile_bytes, void* sink, uint32_t streaming,
+                          hipStream_t stream) {
   const uint32_t grid = (n_tiles + kThreads / 64 - 1) / (kThreads / 64);
-  if (tile_bytes == 4096)
-    hipLaunchKernelGGL(probe_tiles_kernel<4>, dim3(grid), dim3(kThreads), 0, stream,
-                       (const char*)base, ids, n_tiles, (uint32_t*)sink);
+#define VK_TILES(L, NT)                                                                   \
+  hipLaunchKernelGGL((probe_tiles_kernel<L, NT>), dim3(grid), dim3(kThreads), 0, stream, \
+                     (const char*)base, ids, n_tiles, (uint32_t*)sink)
+  if (tile_bytes == 4096 && streaming)
+    VK_TILES(4, true);
+  else if (tile_bytes == 4096)
+    VK_TILES(4, false);
+  else if (tile_bytes == 8192 && streaming)
+    VK_TILES(8, true);
   else if (tile_bytes == 8192)
-    hipLaunchKernelGGL(probe_tiles_kernel<8>, dim3(grid), dim3(kThreads), 0, stream,
-                       (const char*)base, ids, n_tiles, (uint32_t*)sink);
+    VK_TILES(8, false);
   else
     return -1;
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 // Sequential copy of `bytes` (a multiple of 16).
-int vapi_probe_copy(void* dst, const void* src, uint64_t bytes, hipStream_t stream) {
+int vapi_probe_copy(void* dst, const void* src, uint64_t bytes, uint32_t streaming,
+                    hipStream_t stream) {
   const uint64_t n16 = bytes / 16;
   const uint64_t grid = (n16 + kThreads * 4 - 1) / (kThreads * 4);
-  hipLaunchKernelGGL(probe_copy_kernel, dim3((uint32_t)grid), dim3(kThreads), 0, stream,
-                     (uint4*)dst, (const uint4*)src, n16);
+  if (streaming)
+    hipLaunchKernelGGL(probe_copy_kernel<true>, dim3((uint32_t)grid), dim3(kThreads), 0, stream,
+                       (uint4*)dst, (const uint4*)src, n16);
+  else
+    hipLaunchKernelGGL(probe_copy_kernel<false>, dim3((uint32_t)grid), dim3(kThreads), 0, stream,
+                       (uint4*)dst, (const uint4*)src, n16);
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 // Copies n_runs runs of run_bytes (16384) from base + pairs[2i] * run_bytes
 // to base + pairs[2i + 1] * run_bytes (pairs: device u32[n_runs][2]).
 int vapi_probe_copy_runs(void* base, const uint32_t* pairs, uint32_t n_runs, uint32_t run_bytes,
-                         hipStream_t stream) {
+                         uint32_t streaming, hipStream_t stream) {
   if (run_bytes != 16384) return -1;
-  hipLaunchKernelGGL(probe_runs_kernel<4>, dim3(n_runs), dim3(kThreads), 0, stream,
-                     (char*)base, pairs, n_runs);
+  if (streaming)
+    hipLaunchKernelGGL((probe_runs_kernel<4, true>), dim3(n_runs), dim3(kThreads), 0, stream,
+                       (char*)base, pairs, n_runs);
+  else
+    hipLaunchKernelGGL((probe_runs_kernel<4, false>), dim3(n_runs), dim3(kThreads), 0, stream,
+                       (char*)base, pairs, n_runs);
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
