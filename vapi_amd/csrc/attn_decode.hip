@@ -328,16 +328,24 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
     const bool more = t + 1 < t_end;
     const bool seg_ends = pos.key0 + 32 >= pos.len_k;
     const bool same_piece = more && !seg_ends;
-    // The next step's loads are issued unconditionally (the final step of a
-    // wave re-reads its own tiles, which hit in L2): a load inside a branch
-    // makes the waitcnt pass assume it may be the newest and wait for the
-    // prefetch before this step's MFMAs.
+    // The next step's loads are issued unconditionally: a load inside a
+    // branch makes the waitcnt pass assume it may be the newest and wait for
+    // the prefetch before this step's MFMAs. The final step of a wave points
+    // them at key 0 of sequence 0 (one row of one tile per kv head, the same
+    // for every wave, so they hit in L2): the K/V loads are streaming, and a
+    // re-read of the wave's own tiles would go to HBM again (16 KiB per wave)
+    // and hold the wave's end for a memory round trip.
     DecodePos nxt = pos;
     if (same_piece) {
       nxt.key0 += 32;
       nxt.seg_first = false;
     } else if (more) {
       nxt = locate(a, cu_q, cu_k, P, FZ, t + 1);
+    } else {
+      nxt.seq = 0;
+      nxt.key0 = 0;
+      nxt.len_k = 1;
+      nxt.fuse = 0;
     }
     load_step_k<T, D>(kn, a, table, nxt, col, g);
     load_step_v<T, D>(vn, a, table, nxt, col, g);
