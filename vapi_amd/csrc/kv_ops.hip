@@ -184,8 +184,8 @@ struct GatherArgs {
 };
 
 // Item i -> (kv, token t, head h, chunk u), walked in the output's order.
-// Streaming stores: 8,192 keys of K and V (67 MB) in 9.8 us against 22.4 us
-// with ordinary stores (walking an HND pool tile by tile instead measured the
+// Streaming loads and stores: 8,192 keys of K and V (67 MB) in 9.8 us
+// against 22.4 us with ordinary stores (walking an HND pool tile by tile instead measured the
 // same either way).
 template <int C, int ITEMS>
 __global__ __launch_bounds__(256) void kv_gather_kernel(GatherArgs a) {
@@ -235,9 +235,11 @@ struct CopyArgs {
   uint32_t num_layers, num_blocks;
 };
 
-// Measured on config 4a (3.76 GB, 28 layers): 4.99 TB/s, about 88% of a
-// plain device-to-device copy on the same box (5.6 TB/s); a persistent
-// grid-stride variant and non-temporal loads/stores measured no better.
+// Streaming loads and stores (each byte is moved once). Measured on config
+// 4a (3.76 GB, 28 layers): 5.0-5.1 TB/s, what a trivial copy of the same
+// random 16 KiB runs reaches and 85% of a sequential copy of the same
+// bytes; the order the runs are walked in, a persistent grid-stride
+// variant and two runs per workgroup measured no better.
 template <int C, int ITEMS>
 __global__ __launch_bounds__(256) void kv_copy_kernel(CopyArgs a) {
   using V = typename Chunk<C>::T;
