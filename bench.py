@@ -422,6 +422,28 @@ def bench_append(steps, warmup):
     log(f"append cfg1, sources rotated over {n_sets} sets: {ms_cold * 1e3:.2f} us/append "
         f"({gbs_cold:.0f} GB/s)")
     del ks, vs
+    # Ceiling for the cold leg: a trivial sequential copy of the same byte
+    # count (the valid rows' K and V), its source rotated over 24 buffers the
+    # same way, in ordinary and streaming form.
+    from vapi_amd.cache import stream_handle
+    plib = probe_lib()
+    half = w.n_valid * 2 * 8 * 128 * 2
+    half -= half % 16
+    srcs = torch.empty(n_sets, half, dtype=torch.uint8, device=DEV)
+    dst = torch.empty(half, dtype=torch.uint8, device=DEV)
+    cold_probe = {}
+    for nt, sfx in ((0, ""), (1, "_nt")):
+        def probe_cold(nt=nt):
+            i = it[0] % n_sets
+            it[0] += 1
+            _chk_probe(plib.vapi_probe_copy(dst.data_ptr(), srcs[i].data_ptr(), half, nt,
+                                         stream_handle()))
+        pms = timed_graph(probe_cold, max(steps, n_sets), warmup)
+        cold_probe["copy_seq_cold" + sfx + "_us"] = pms * 1e3
+        cold_probe["copy_seq_cold" + sfx + "_gbs"] = 2 * half / (pms * 1e-3) / 1e9
+    log("append cold-source ceiling: sequential copy of the same bytes " +
+        ", ".join(f"{k} {v:.1f}" for k, v in cold_probe.items()))
+    del srcs, dst
     del cache
     # The same step's rows for 4 layers in one launch (vapi_kv_append_layers).
     L = 4
@@ -436,6 +458,9 @@ def bench_append(steps, warmup):
     del cache, kl, vl
     return dict(us=ms * 1e3, gbs=gbs, frac=gbs / HBM_PEAK_GBS, bytes=alg,
                 cold_us=ms_cold * 1e3, cold_gbs=gbs_cold, cold_frac=gbs_cold / HBM_PEAK_GBS,
+                cold_frac_of_cold_copy_probe=gbs_cold / max(cold_probe["copy_seq_cold_gbs"],
+                                                            cold_probe["copy_seq_cold_nt_gbs"]),
+                cold_probe=cold_probe,
                 us_host_launched=ms_host * 1e3,
                 gbs_host_launched=alg / (ms_host * 1e-3) / 1e9,
                 layers4_one_launch_us=ms_l * 1e3, layers4_gbs=gbs_l)
