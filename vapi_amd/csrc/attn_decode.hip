@@ -300,6 +300,7 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
   }
 #ifdef VK_DECODE_TRACE
   const uint64_t tr0 = __builtin_amdgcn_s_memrealtime();
+  uint64_t tr_first = 0, tr_last = 0;
 #endif
 
   uint32_t t = t_begin;
@@ -358,6 +359,10 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
       return key >= lo && key < len_k;
     });
     attend_pv<T, D>(vc, pf, o);
+#ifdef VK_DECODE_TRACE
+    tr_last = __builtin_amdgcn_s_memrealtime();
+    if (!tr_first) tr_first = tr_last;
+#endif
     if (!same_piece) {
       const uint32_t seg = pos.seq * a.kvh + pos.kh;
       if (lane == 0) {
@@ -384,10 +389,13 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
     *(uint4*)stat = make_uint4(t_end - t_begin, t_entry, (uint32_t)tr1, 0u);
   }
 #ifdef VK_DECODE_TRACE
-  // Per wave: start/end (100 MHz ticks), steps done << 32 | entry tick,
-  // HW_ID | XCC_ID << 32.
+  // Per wave (8 words): start/end (100 MHz ticks), steps done << 32 | entry
+  // tick, HW_ID | XCC_ID << 32, the ends of the first and the last step's
+  // attention.
   if (lane == 0) {
-    uint64_t* tr = a.trace + 4ull * gw;
+    uint64_t* tr = a.trace + 8ull * gw;
+    tr[4] = tr_first;
+    tr[5] = tr_last;
     tr[0] = tr0;
     tr[1] = tr1;
     tr[2] = ((uint64_t)(t_end - t_begin) << 32) | t_entry;
@@ -686,7 +694,7 @@ static DecodeWs decode_ws(uint32_t b, uint32_t kvh, uint32_t group, uint32_t hea
   w.trace = w.o + up256(slots * group * head_dim * sizeof(float));
   w.total = w.trace;
 #ifdef VK_DECODE_TRACE
-  w.total += (size_t)num_waves * 4 * sizeof(uint64_t);
+  w.total += (size_t)num_waves * 8 * sizeof(uint64_t);
 #endif
   return w;
 }
