@@ -242,6 +242,52 @@ def bench_fused_step(d, steps, warmup):
 
 # ---- the VALU kernel (f32 pools, other head dims) ---------------------------------
 
+def bench_mixed_step(d, steps, warmup):
+    """A chunked-prefill serving step on config 2's pool: its first 63
+    sequences as decode rows plus one 512-token chunk at positions
+    1536..2047, in one call, replayed from a graph: through the prepared
+    call that names the step's prefill sequences (what PreparedAttention
+    issues) and through vapi_paged_attention_ex without the list (the prefill
+    grid then spans every sequence, and the chunk is not split)."""
+    from vapi_amd import _lib
+    from vapi_amd.cache import stream_handle
+    w, cache = d["w"], d["cache"]
+    nd = 63
+    lens_q = [1] * nd + [512]
+    lens_k = [int(x) for x in w.lens[:nd]] + [2048]
+    tables = [list(t) for t in w.tables[:nd]]
+    # The chunk's 128 blocks: pool blocks no decode row reads.
+    used = set(int(x) for t in tables for x in t)
+    tables.append([x for x in range(w.num_blocks) if x not in used][:128])
+    batch = ForwardBatch(cu_seqlens_q=np.concatenate([[0], np.cumsum(lens_q)]).tolist(),
+                         cu_seqlens_k=np.concatenate([[0], np.cumsum(lens_k)]).tolist(),
+                         block_tables=tables, max_seqlen_q=512, max_seqlen_k=max(lens_k))
+    prep = PreparedAttention.from_batch(batch, DEV)
+    q = torch.randn(sum(lens_q), w.num_heads, w.head_dim, device=DEV).to(torch.bfloat16)
+    o = torch.empty_like(q)
+    scale = w.head_dim ** -0.5
+    listed_ms = timed_graph(lambda: paged_attention_prepared(q, cache, 0, prep, scale, out=o),
+                            steps, warmup)
+    L = _lib.lib()
+    b = nd + 1
+    need = L.vapi_paged_attention_workspace_size(cache.pool, b, w.num_heads, 512, prep.max_seqlen_k)
+    ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
+
+    def unlisted():
+        _lib.check(L.vapi_paged_attention_ex(
+            cache.pool, 0, q.data_ptr(), o.data_ptr(), prep.seqlens_q.data_ptr(),
+            prep.seqlens_k.data_ptr(), prep.block_table.data_ptr(), b, prep.block_table.shape[1],
+            512, prep.max_seqlen_k, w.num_heads, scale, -1, 0, 0, ws.data_ptr(), need,
+            stream_handle()))
+
+    unlisted_ms = timed_graph(unlisted, steps, warmup)
+    res = dict(decode_rows=nd, prefill_chunk=512, prefill_context=2048,
+               us=listed_ms * 1e3, us_without_prefill_list=unlisted_ms * 1e3)
+    log(f"mixed step (63 decode rows + one 512-token chunk): {res['us']:.1f} us per call, "
+        f"{res['us_without_prefill_list']:.1f} us without the prefill list")
+    return res
+
+
 def bench_valu(steps, warmup):
     """The VALU attention kernel that f32 pools and head dims other than 64 /
     128 run on: config 0 (Qwen3-0.6B-shaped f32 decode, the reference's CPU
@@ -1000,6 +1046,7 @@ def main():
                                         host_launched_gbs=dec["gbs"])}
     extras["gather_cfg2"] = bench_gather(dec, args.steps, args.warmup)
     extras["fused_step_cfg2"] = bench_fused_step(dec, args.steps, args.warmup)
+    extras["mixed_step_cfg2"] = bench_mixed_step(dec, args.steps, args.warmup)
     if args.only in (None,):
         extras["append_cfg1"] = bench_append(args.steps, args.warmup)
         # Prefill runs 1.2 ms per call; its rate climbs over the first ~25

@@ -243,6 +243,37 @@ int vapi_paged_attention_ex(const vapi_kv_pool* pool, uint32_t layer, const void
                             vapi_stream_t stream);
 
 /*
+ * vapi_paged_attention_ex with the step's prefill sequences named by the
+ * host: prefill_seqs = device u32[n_prefill], the indices of every sequence
+ * with len_q > 1, in ascending order. It mirrors paged_attention_cuda_prepared
+ * (attention.rs:262-288), whose PreparedAttention the host builds once per
+ * step from the batch (attention.rs:234-256); the list is one more array of
+ * that kind. The prefill grid then covers those sequences only, and its key
+ * split is chosen for them: a chunked-prefill step of many decode rows and
+ * one prefill chunk runs that chunk over the whole GPU instead of one
+ * workgroup per query tile and kv head. A sequence with len_q > 1 missing
+ * from the list gets no output rows; the list is trusted like the block
+ * table. With VAPI_ATTN_NO_DECODE_ROWS the call covers every sequence and
+ * ignores the list. Same workspace contract as vapi_paged_attention, sized
+ * by vapi_paged_attention_prepared_workspace_size (the prefill's optional
+ * key-split part is sized for n_prefill sequences). n_prefill > batch, or a
+ * null list with n_prefill > 0, is VAPI_KV_EINVAL.
+ */
+size_t vapi_paged_attention_prepared_workspace_size(const vapi_kv_pool* pool, uint32_t batch,
+                                                    uint32_t n_prefill, uint32_t num_heads,
+                                                    uint32_t max_seqlen_q,
+                                                    uint32_t max_seqlen_k);
+int vapi_paged_attention_prepared(const vapi_kv_pool* pool, uint32_t layer, const void* q,
+                                  void* out, const uint32_t* cu_seqlens_q,
+                                  const uint32_t* cu_seqlens_k, const uint32_t* block_table,
+                                  uint32_t batch, uint32_t max_blocks, uint32_t max_seqlen_q,
+                                  uint32_t max_seqlen_k, uint32_t num_heads, float scale,
+                                  int32_t window_left, int32_t window_right, uint32_t flags,
+                                  const uint32_t* prefill_seqs, uint32_t n_prefill,
+                                  void* workspace, size_t workspace_bytes,
+                                  vapi_stream_t stream);
+
+/*
  * vapi_paged_attention_ex without a workspace argument, for callers that
  * cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc). No counterpart in the

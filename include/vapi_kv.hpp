@@ -525,8 +525,9 @@ inline Result<detail::DevicePtr> cu_seqlens(const std::vector<uint32_t>& values)
 /*
  * PreparedAttention (attention.rs:234-256): the step's device inputs, built
  * once per step and shared by every layer: the packed block table, the
- * cumulative lengths and the attention workspace (sized for the cache's
- * largest attention layer and `num_heads`, zeroed once).
+ * cumulative lengths, the sequences with prefill rows (len_q > 1, for
+ * vapi_paged_attention_prepared) and the attention workspace (sized for the
+ * cache's largest attention layer and `num_heads`, zeroed once).
  */
 class PreparedAttention {
  public:
@@ -546,8 +547,12 @@ class PreparedAttention {
       }
     }
     bool any_decode = false;
-    for (size_t i = 0; i < p.batch_; ++i)
-      any_decode |= batch.cu_seqlens_q[i + 1] - batch.cu_seqlens_q[i] == 1;
+    std::vector<uint32_t> pf;
+    for (size_t i = 0; i < p.batch_; ++i) {
+      const uint32_t lq = batch.cu_seqlens_q[i + 1] - batch.cu_seqlens_q[i];
+      any_decode |= lq == 1;
+      if (lq > 1) pf.push_back((uint32_t)i);
+    }
     p.flags_ = (deterministic ? VAPI_ATTN_DETERMINISTIC : 0u) |
                (!any_decode && p.max_q_ > 1 ? VAPI_ATTN_NO_DECODE_ROWS : 0u);
     auto tab = detail::device_alloc(std::max<size_t>(packed.first.size(), 1) * 4);
@@ -563,15 +568,21 @@ class PreparedAttention {
     if (ck.is_err()) return ck.error();
     p.cu_q_ = std::move(cq.value());
     p.cu_k_ = std::move(ck.value());
+    auto pfd = detail::device_alloc(std::max<size_t>(pf.size(), 1) * 4);
+    if (pfd.is_err()) return pfd.error();
+    if (!pf.empty())
+      VAPI_TRY(detail::hip(hipMemcpy(pfd.value().get(), pf.data(), pf.size() * 4,
+                                     hipMemcpyHostToDevice),
+                           "hipMemcpy"));
+    p.pf_ = std::move(pfd.value());
+    p.n_pf_ = pf.size();
     size_t ws = 0;
     for (size_t l = 0; l < cache.num_layers(); ++l) {
       if (cache.layout(l).kind != LayerLayout::Kind::Kv) continue;
       uint32_t lp = 0;
-      ws = std::max(ws, vapi_paged_attention_workspace_size(cache.pool_of(l, &lp),
-                                                            (uint32_t)p.batch_,
-                                                            (uint32_t)num_heads,
-                                                            (uint32_t)p.max_q_,
-                                                            (uint32_t)p.max_k_));
+      ws = std::max(ws, vapi_paged_attention_prepared_workspace_size(
+                            cache.pool_of(l, &lp), (uint32_t)p.batch_, (uint32_t)p.n_pf_,
+                            (uint32_t)num_heads, (uint32_t)p.max_q_, (uint32_t)p.max_k_));
     }
     auto w = detail::device_alloc(ws);
     if (w.is_err()) return w.error();
@@ -589,12 +600,14 @@ class PreparedAttention {
   size_t max_seqlen_q() const { return max_q_; }
   size_t max_seqlen_k() const { return max_k_; }
   uint32_t flags() const { return flags_; }
+  const uint32_t* prefill_seqs() const { return (const uint32_t*)pf_.get(); }
+  size_t n_prefill() const { return n_pf_; }
   void* workspace() const { return ws_.get(); }
   size_t workspace_bytes() const { return ws_bytes_; }
 
  private:
-  detail::DevicePtr table_, cu_q_, cu_k_, ws_;
-  size_t batch_ = 0, width_ = 0, max_q_ = 0, max_k_ = 0, ws_bytes_ = 0;
+  detail::DevicePtr table_, cu_q_, cu_k_, pf_, ws_;
+  size_t batch_ = 0, width_ = 0, max_q_ = 0, max_k_ = 0, ws_bytes_ = 0, n_pf_ = 0;
   uint32_t flags_ = 0;
 };
 
@@ -618,12 +631,13 @@ inline Result<Tensor> paged_attention_prepared(const Tensor& q, const PagedKvCac
   const vapi_kv_pool* pool = cache.pool_of(layer, &lp);
   const int32_t wl = window_size_left ? (int32_t)*window_size_left : -1;
   const int32_t wr = window_size_right ? (int32_t)*window_size_right : -1;
-  VAPI_TRY(detail::check(vapi_paged_attention_ex(
+  VAPI_TRY(detail::check(vapi_paged_attention_prepared(
       pool, lp, q.data(), out.value().data(), prepared.seqlens_q(), prepared.seqlens_k(),
       prepared.block_table(), (uint32_t)prepared.batch(), (uint32_t)prepared.width(),
       (uint32_t)prepared.max_seqlen_q(), (uint32_t)prepared.max_seqlen_k(),
-      (uint32_t)q.dims()[1], softmax_scale, wl, wr, prepared.flags(), prepared.workspace(),
-      prepared.workspace_bytes(), (vapi_stream_t)stream)));
+      (uint32_t)q.dims()[1], softmax_scale, wl, wr, prepared.flags(), prepared.prefill_seqs(),
+      (uint32_t)prepared.n_prefill(), prepared.workspace(), prepared.workspace_bytes(),
+      (vapi_stream_t)stream)));
   VAPI_TRY(detail::hip(hipStreamSynchronize(stream), "hipStreamSynchronize"));
   return out;
 }

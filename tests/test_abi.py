@@ -98,6 +98,33 @@ def test_misaligned_pools_and_unknown_flags_are_refused():
     assert need > 0
 
 
+def test_the_prepared_call_checks_its_prefill_list_and_sizes_its_split():
+    """vapi_paged_attention_prepared refuses a list longer than the batch or
+    a null list, before anything is launched; its workspace size covers the
+    key split of the listed sequences alone (a step of 63 decode rows and one
+    512-token chunk splits that chunk; counted over all 64 sequences it would
+    not)."""
+    L = _lib.lib()
+    args = [1, 1, 1, 1, 1, 2, 4, 512, 2048, 32, 0.1, -1, 0, 0]
+    assert L.vapi_paged_attention_prepared(pool(), 0, *args, 1, 3, None, 0,
+                                           None) == _lib.EINVAL
+    assert b"prefill sequences" in L.vapi_kv_last_error()
+    assert L.vapi_paged_attention_prepared(pool(), 0, *args, None, 1, None, 0,
+                                           None) == _lib.EINVAL
+    plain = L.vapi_paged_attention_workspace_size(pool(), 64, 32, 512, 2048)
+    listed = L.vapi_paged_attention_prepared_workspace_size(pool(), 64, 1, 32, 512, 2048)
+    decode_only = L.vapi_paged_attention_prepared_workspace_size(pool(), 64, 0, 32, 512, 2048)
+    assert listed > plain >= decode_only > 0
+
+
+def test_prepared_attention_lists_the_prefill_sequences():
+    from vapi_amd.attention import PreparedAttention
+    b = ForwardBatch(cu_seqlens_q=[0, 1, 6, 7, 7, 10], cu_seqlens_k=[0, 9, 18, 27, 30, 39],
+                     block_tables=[[i] for i in range(5)], max_seqlen_q=5, max_seqlen_k=9)
+    prep = PreparedAttention.from_batch(b, "cpu")
+    assert prep.n_prefill == 2 and prep.prefill_seqs.tolist() == [1, 4]
+
+
 def test_launches_too_large_for_one_grid_are_refused():
     """A batch whose prefill or VALU grid would pass 2^32 workgroups is
     refused before anything is launched, not truncated."""

@@ -143,3 +143,62 @@ def test_fused_append_with_len_k_past_the_table_stays_in_bounds():
     assert torch.equal(c1._slab, c2._slab)
     assert bool(torch.isfinite(out1.float()).all())
     assert torch.equal(out1, out2)
+
+
+def call_prepared(q, cache, prep, scale, flags, seqs, window_left=-1):
+    """vapi_paged_attention_prepared straight through the C ABI with the
+    prefill sequence list `seqs` (host ints), its workspace sized by
+    vapi_paged_attention_prepared_workspace_size."""
+    out = torch.full_like(q, float("nan"))
+    b = prep.seqlens_q.shape[0] - 1
+    max_q, max_k = max(prep.max_seqlen_q, 1), max(prep.max_seqlen_k, 1)
+    L = _lib.lib()
+    need = L.vapi_paged_attention_prepared_workspace_size(cache.pool, b, len(seqs), q.shape[1],
+                                                          max_q, max_k)
+    ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=DEV)
+    dseqs = torch.tensor(list(seqs) or [0], dtype=torch.int32, device=DEV)
+    _lib.check(L.vapi_paged_attention_prepared(
+        cache.pool, 0, q.data_ptr(), out.data_ptr(), prep.seqlens_q.data_ptr(),
+        prep.seqlens_k.data_ptr(), prep.block_table.data_ptr(), b, prep.block_table.shape[1],
+        max_q, max_k, q.shape[1], float(scale), window_left, 0, flags, dseqs.data_ptr(),
+        len(seqs), ws.data_ptr(), need, stream_handle()))
+    return out
+
+
+@pytest.mark.parametrize("d,window", [(128, None), (128, 300), (64, None)])
+def test_a_chunked_prefill_step_with_its_prefill_list_matches_the_oracle(d, window):
+    """A serving step of many decode rows and two prefill chunks: the prefill
+    grid covers the two chunks only (and splits their keys over the GPU);
+    the output matches the oracle, as does the same call without the list."""
+    rng = np.random.default_rng(d + (window or 0))
+    n_dec = 40
+    lens_q = [1] * 20 + [256] + [1] * 20 + [100]
+    lens_k = [int(x) for x in rng.integers(50, 3000, 20)] + [1024] + \
+             [int(x) for x in rng.integers(50, 3000, 20)] + [100]
+    c, q, batch = random_case(rng, torch.bfloat16, 32, 8, d, 16, lens_q, lens_k, "HND")
+    prep = PreparedAttention.from_batch(batch, DEV)
+    assert prep.n_prefill == 2 and prep.flags == 0
+    assert prep.prefill_seqs.cpu().tolist() == [20, 41]
+    scale = d ** -0.5
+    wl = -1 if window is None else window - 1
+    want = oracle_out(q, c, 0, batch, scale, window)  # the oracle takes the window w itself
+    tol = 2e-2 * float(want.abs().max())
+    listed = call_prepared(q, c, prep, scale, 0, [20, 41], wl)
+    assert max_abs(listed, want) <= tol
+    assert max_abs(call_ex(q, c, prep, scale, 0, wl), want) <= tol
+    # The Python wrapper takes the same path.
+    out = paged_attention_prepared(q, c, 0, prep, scale, None if window is None else wl)
+    assert max_abs(out, want) <= tol
+    assert n_dec + 2 == len(lens_q)
+
+
+def test_a_prefill_only_call_ignores_the_prefill_list():
+    """With VAPI_ATTN_NO_DECODE_ROWS the call covers every sequence whatever
+    the list names (here: none of them)."""
+    rng = np.random.default_rng(77)
+    c, q, batch = random_case(rng, torch.bfloat16, 32, 8, 128, 16, [40, 9], [500, 60], "HND")
+    prep = PreparedAttention.from_batch(batch, DEV)
+    scale = 128 ** -0.5
+    want = oracle_out(q, c, 0, batch, scale)
+    out = call_prepared(q, c, prep, scale, ATTN_NO_DECODE_ROWS, [])
+    assert max_abs(out, want) <= 2e-2 * float(want.abs().max())

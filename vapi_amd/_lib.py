@@ -36,6 +36,7 @@ EXPORTS = (
     "vapi_spill_evicted_async", "vapi_spill_drain",
     "vapi_paged_attention_ex", "vapi_paged_attention_append_ex",
     "vapi_paged_attention_noalloc",
+    "vapi_paged_attention_prepared", "vapi_paged_attention_prepared_workspace_size",
 )
 
 
@@ -110,6 +111,12 @@ def lib():
     L.vapi_paged_attention_append_ex.argtypes = [
         _poolp, _u32, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
         _u32, ctypes.c_float, _i32, _i32, _u32, _vp, _sz, _vp]
+    L.vapi_paged_attention_prepared_workspace_size.argtypes = [_poolp, _u32, _u32, _u32, _u32,
+                                                               _u32]
+    L.vapi_paged_attention_prepared_workspace_size.restype = _sz
+    L.vapi_paged_attention_prepared.argtypes = [
+        _poolp, _u32, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,
+        ctypes.c_float, _i32, _i32, _u32, _vp, _u32, _vp, _sz, _vp]
     L.vapi_paged_attention_noalloc.argtypes = [
         _poolp, _u32, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,
         ctypes.c_float, _i32, _i32, _u32, _vp]

@@ -101,7 +101,10 @@ class PreparedAttention:
     and split-context partials), reused by every layer of the step, and the
     call flags the host lengths allow: a batch with no decode row (len_q ==
     1) runs the prefill kernel alone (ATTN_NO_DECODE_ROWS); `deterministic`
-    freezes the decode's work split so repeated calls are bit-identical."""
+    freezes the decode's work split so repeated calls are bit-identical.
+    `prefill_seqs` lists the sequences with len_q > 1 (device u32), so that
+    the prefill grid of a mixed step covers its prefill chunks only
+    (vapi_paged_attention_prepared); None covers every sequence."""
     block_table: torch.Tensor
     seqlens_q: torch.Tensor
     seqlens_k: torch.Tensor
@@ -109,6 +112,8 @@ class PreparedAttention:
     max_seqlen_k: int
     workspace: torch.Tensor | None = None
     flags: int = 0
+    prefill_seqs: torch.Tensor | None = None
+    n_prefill: int = 0
 
     @classmethod
     def from_batch(cls, batch: ForwardBatch, device, cache=None, num_heads: int | None = None,
@@ -121,11 +126,14 @@ class PreparedAttention:
         flags = ATTN_DETERMINISTIC if deterministic else 0
         if lens_q.size and not np.any(lens_q == 1):
             flags |= ATTN_NO_DECODE_ROWS
+        pf = np.nonzero(lens_q > 1)[0]
         prep = cls(block_table=pack_block_tables(batch, device),
                    seqlens_q=cu_seqlens(batch.cu_seqlens_q, device),
                    seqlens_k=cu_seqlens(batch.cu_seqlens_k, device),
                    max_seqlen_q=int(batch.max_seqlen_q),
-                   max_seqlen_k=int(batch.max_seqlen_k), flags=flags)
+                   max_seqlen_k=int(batch.max_seqlen_k), flags=flags,
+                   prefill_seqs=cu_seqlens(pf if pf.size else [0], device),
+                   n_prefill=int(pf.size))
         if cache is not None and num_heads is not None:
             prep.reserve(cache, num_heads, device)
         return prep
@@ -138,20 +146,30 @@ class PreparedAttention:
         max_q, max_k = max(self.max_seqlen_q, 1), max(self.max_seqlen_k, 1)
         layers = ([cache.layer_view(l) for l, s in enumerate(cache.layouts) if s[0] == "kv"]
                   if isinstance(cache, HybridKvCache) else [cache])
-        need = max(workspace_bytes(c, b, num_heads, max_q, max_k) for c in layers)
+        need = max(workspace_bytes(c, b, num_heads, max_q, max_k, self.n_prefill_arg())
+                   for c in layers)
         if need and (self.workspace is None or self.workspace.numel() < need):
             self.workspace = torch.zeros(need, dtype=torch.uint8, device=device)
 
+    def n_prefill_arg(self) -> int | None:
+        """The prefill sequence count the calls pass (None: no list)."""
+        return self.n_prefill if self.prefill_seqs is not None else None
+
 
 def workspace_bytes(cache: PagedKvCache, batch: int, num_heads: int, max_q: int,
-                    max_k: int) -> int:
-    return lib().vapi_paged_attention_workspace_size(cache.pool, batch, num_heads,
-                                                      max_q, max_k)
+                    max_k: int, n_prefill: int | None = None) -> int:
+    """vapi_paged_attention_workspace_size, or with `n_prefill` (a call that
+    names its prefill sequences) vapi_paged_attention_prepared_workspace_size."""
+    if n_prefill is None:
+        return lib().vapi_paged_attention_workspace_size(cache.pool, batch, num_heads,
+                                                          max_q, max_k)
+    return lib().vapi_paged_attention_prepared_workspace_size(cache.pool, batch, n_prefill,
+                                                               num_heads, max_q, max_k)
 
 
 def _workspace(cache, prepared: PreparedAttention, b: int, num_heads: int, max_q: int,
                max_k: int, device):
-    need = workspace_bytes(cache, b, num_heads, max_q, max_k)
+    need = workspace_bytes(cache, b, num_heads, max_q, max_k, prepared.n_prefill_arg())
     ws = prepared.workspace
     if need and (ws is None or ws.numel() < need):
         # Zero-filled once: a zeroed workspace starts the decode from equal
@@ -185,13 +203,17 @@ def paged_attention_prepared(q: torch.Tensor, cache: PagedKvCache, layer: int,
     max_q = max(int(prepared.max_seqlen_q), 1)
     max_k = max(int(prepared.max_seqlen_k), 1)
     need, ws = _workspace(cache, prepared, b, num_heads, max_q, max_k, q.device)
-    check(lib().vapi_paged_attention_ex(
-        cache.pool, layer, q.data_ptr(), out.data_ptr(), prepared.seqlens_q.data_ptr(),
-        prepared.seqlens_k.data_ptr(), prepared.block_table.data_ptr(), b,
-        prepared.block_table.shape[1], max_q, max_k, num_heads, float(softmax_scale),
-        -1 if window_size_left is None else int(window_size_left),
-        -1 if window_size_right is None else int(window_size_right), prepared.flags,
-        ws.data_ptr() if need else None, need, stream_handle(stream)))
+    args = (cache.pool, layer, q.data_ptr(), out.data_ptr(), prepared.seqlens_q.data_ptr(),
+            prepared.seqlens_k.data_ptr(), prepared.block_table.data_ptr(), b,
+            prepared.block_table.shape[1], max_q, max_k, num_heads, float(softmax_scale),
+            -1 if window_size_left is None else int(window_size_left),
+            -1 if window_size_right is None else int(window_size_right), prepared.flags)
+    tail = (ws.data_ptr() if need else None, need, stream_handle(stream))
+    if prepared.prefill_seqs is None:
+        check(lib().vapi_paged_attention_ex(*args, *tail))
+    else:
+        check(lib().vapi_paged_attention_prepared(
+            *args, prepared.prefill_seqs.data_ptr(), prepared.n_prefill, *tail))
     return out
 
 
@@ -246,6 +268,15 @@ def paged_attention_append_prepared(q: torch.Tensor, k: torch.Tensor, v: torch.T
     num_heads = q.shape[1]
     max_q = max(int(prepared.max_seqlen_q), 1)
     max_k = max(int(prepared.max_seqlen_k), 1)
+    if max_q > 1 and prepared.prefill_seqs is not None:
+        # A step with prefill rows is not fused (the library runs the append
+        # and then the attention); run that pair here so that the attention
+        # gets the step's prefill list.
+        check(lib().vapi_kv_append(cache.pool, layer, k.data_ptr(), v.data_ptr(),
+                                   slot_mapping.data_ptr(), k.shape[0], stream_handle(stream)))
+        return paged_attention_prepared(q, cache, layer, prepared, softmax_scale,
+                                        window_size_left, window_size_right, out=out,
+                                        stream=stream)
     need, ws = _workspace(cache, prepared, b, num_heads, max_q, max_k, q.device)
     check(lib().vapi_paged_attention_append_ex(
         cache.pool, layer, k.data_ptr(), v.data_ptr(), slot_mapping.data_ptr(), k.shape[0],

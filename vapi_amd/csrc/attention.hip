@@ -21,6 +21,12 @@ static bool mfma_ok(const vapi_kv_pool* p, uint32_t num_heads) {
   return G >= 1 && G <= 16;
 }
 
+// The sequences with prefill rows, named by the host (vapi_paged_attention_prepared).
+struct PrefillSeqs {
+  const uint32_t* seqs;  // device u32[n]
+  uint32_t n;
+};
+
 // The fused append's new rows (decode batches on the MFMA path only).
 struct NewRows {
   const void* k;
@@ -85,7 +91,8 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
                                 uint32_t max_seqlen_k, uint32_t num_heads, float scale,
                                 int32_t window_left, int32_t window_right, void* workspace,
                                 size_t workspace_bytes, vapi_stream_t stream,
-                                const NewRows* fuse, uint32_t flags);
+                                const NewRows* fuse, uint32_t flags,
+                                const PrefillSeqs* pf = nullptr);
 
 // The workspace a call cannot run without: the decode's (unless the call
 // launches no decode kernel) or the VALU kernel's split partials.
@@ -118,6 +125,41 @@ size_t vapi_paged_attention_workspace_size(const vapi_kv_pool* pool,
   // (optional: a smaller workspace only means fewer splits).
   return need + prefill_split_bytes(batch, pool->num_kv_heads, num_heads / pool->num_kv_heads,
                                     pool->head_dim, max_seqlen_q, max_seqlen_k);
+}
+
+size_t vapi_paged_attention_prepared_workspace_size(const vapi_kv_pool* pool, uint32_t batch,
+                                                    uint32_t n_prefill, uint32_t num_heads,
+                                                    uint32_t max_seqlen_q,
+                                                    uint32_t max_seqlen_k) {
+  const size_t need =
+      required_workspace(pool, batch, num_heads, max_seqlen_q, max_seqlen_k, false);
+  if (!pool || pool->num_kv_heads == 0 || num_heads % pool->num_kv_heads || batch == 0 ||
+      num_heads == 0 || !mfma_ok(pool, num_heads))
+    return need;
+  return need + prefill_split_bytes(std::min(n_prefill, batch), pool->num_kv_heads,
+                                    num_heads / pool->num_kv_heads, pool->head_dim,
+                                    max_seqlen_q, max_seqlen_k);
+}
+
+int vapi_paged_attention_prepared(const vapi_kv_pool* pool, uint32_t layer, const void* q,
+                                  void* out, const uint32_t* cu_seqlens_q,
+                                  const uint32_t* cu_seqlens_k, const uint32_t* block_table,
+                                  uint32_t batch, uint32_t max_blocks, uint32_t max_seqlen_q,
+                                  uint32_t max_seqlen_k, uint32_t num_heads, float scale,
+                                  int32_t window_left, int32_t window_right, uint32_t flags,
+                                  const uint32_t* prefill_seqs, uint32_t n_prefill,
+                                  void* workspace, size_t workspace_bytes,
+                                  vapi_stream_t stream) {
+  if (n_prefill > batch)
+    VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention_prepared: %u prefill sequences in a batch of %u",
+            n_prefill, batch);
+  if (n_prefill && !prefill_seqs)
+    VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention_prepared: null prefill_seqs");
+  const PrefillSeqs pf{prefill_seqs, n_prefill};
+  return paged_attention_impl(pool, layer, q, out, cu_seqlens_q, cu_seqlens_k, block_table,
+                              batch, max_blocks, max_seqlen_q, max_seqlen_k, num_heads, scale,
+                              window_left, window_right, workspace, workspace_bytes, stream,
+                              nullptr, flags, &pf);
 }
 
 int vapi_paged_attention(const vapi_kv_pool* pool, uint32_t layer,
@@ -231,7 +273,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
                                 uint32_t max_seqlen_k, uint32_t num_heads, float scale,
                                 int32_t window_left, int32_t window_right, void* workspace,
                                 size_t workspace_bytes, vapi_stream_t stream,
-                                const NewRows* fuse, uint32_t flags) {
+                                const NewRows* fuse, uint32_t flags, const PrefillSeqs* pf) {
   if (int rc = check_pool(pool, "vapi_paged_attention")) return rc;
   if (!pool->v) VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: a K-only pool has no V to attend over");
   if (layer >= pool->num_layers)
@@ -253,19 +295,24 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   if (num_heads > 65535 || (batch > 65535 && !mfma_ok(pool, num_heads)))
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: batch %u / heads %u too large",
             batch, num_heads);
-  // Refused before anything is launched (a refused call writes nothing).
-  if (mfma_ok(pool, num_heads) && max_seqlen_q > 1 && batch > 65535)
-    VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: %u prefill sequences > 65535", batch);
-  if (mfma_ok(pool, num_heads) && max_seqlen_q > 1 &&
-      prefill_grid(batch, pool->num_kv_heads, num_heads / pool->num_kv_heads, max_seqlen_q) >
-          0xFFFFFFFFull)
-    VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: prefill batch too large for one launch");
   // A batch the caller says has no decode rows (and which is not a fused
   // decode step) runs one kernel: the prefill kernel then takes every row,
   // len_q == 1 included, so the result does not depend on the hint. It needs
   // no workspace.
   const bool skip_decode = (flags & VAPI_ATTN_NO_DECODE_ROWS) && !fuse && max_seqlen_q > 1 &&
                            mfma_ok(pool, num_heads);
+  // The sequences the prefill grid covers: those the host named (a mixed
+  // step's few prefill chunks among many decode rows), else all of them. A
+  // prefill-only call covers every row and ignores the list.
+  const bool listed = pf && !skip_decode;
+  const uint32_t pf_n = listed ? pf->n : batch;
+  // Refused before anything is launched (a refused call writes nothing).
+  if (mfma_ok(pool, num_heads) && max_seqlen_q > 1 && pf_n > 65535)
+    VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: %u prefill sequences > 65535", pf_n);
+  if (mfma_ok(pool, num_heads) && max_seqlen_q > 1 &&
+      prefill_grid(pf_n, pool->num_kv_heads, num_heads / pool->num_kv_heads, max_seqlen_q) >
+          0xFFFFFFFFull)
+    VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: prefill batch too large for one launch");
   const size_t need =
       required_workspace(pool, batch, num_heads, max_seqlen_q, max_seqlen_k, skip_decode);
   if (workspace_bytes < need || (need && !workspace))
@@ -313,6 +360,8 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   a.wr = window_right < 0 ? -1 : window_right;
   a.deterministic = (flags & VAPI_ATTN_DETERMINISTIC) ? 1u : 0u;
   a.pf_min_q = 2;
+  a.pf_seqs = listed ? pf->seqs : nullptr;
+  a.pf_seqs_n = pf_n;
   const hipStream_t s = hs(stream);
 
   if (mfma_ok(pool, num_heads)) {
@@ -320,7 +369,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
     a.num_waves = decode_num_waves();
     if (skip_decode) a.pf_min_q = 1;
     else launch_decode(a, workspace, g.d, bf16, s);
-    if (max_seqlen_q > 1) {
+    if (max_seqlen_q > 1 && pf_n > 0) {
       // The workspace past the decode's part serves the prefill's key split
       // (never its first 256 bytes, which carry the decode's XCD shares
       // from call to call).

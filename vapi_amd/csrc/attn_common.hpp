@@ -67,6 +67,10 @@ struct AttnArgs {
   int32_t wl, wr;
   uint32_t deterministic;  // decode: fixed equal XCD shares, no share update
   uint32_t pf_min_q;       // prefill: rows with len_q >= this (2, or 1 when no decode launch)
+  // prefill: the sequences its grid covers, u32[pf_seqs_n] (null: 0 ..
+  // batch - 1); the host names the sequences with prefill rows.
+  const uint32_t* pf_seqs;
+  uint32_t pf_seqs_n;
 };
 
 __device__ __forceinline__ void key_range(int32_t p, int32_t len_k, int32_t wl,
@@ -419,8 +423,9 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, bool bf16, hi
 // Workgroups of the prefill launch (query tiles x kv heads x sequences); a
 // launch needs it below 2^32.
 uint64_t prefill_grid(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t max_q);
-// The prefill launch; with a workspace (`split_ws`, `split_ws_bytes`) a
-// batch too small to fill the GPU splits its keys over more workgroups.
+// The prefill launch over a.pf_seqs_n sequences (those a.pf_seqs names, or
+// all a.batch); with a workspace (`split_ws`, `split_ws_bytes`) a batch too
+// small to fill the GPU splits its keys over more workgroups.
 void launch_prefill(const AttnArgs& a, uint32_t max_q, uint32_t max_k, uint32_t head_dim,
                     bool bf16, void* split_ws, size_t split_ws_bytes, hipStream_t s);
 // Workspace the prefill's key split wants for this shape (0: no split).

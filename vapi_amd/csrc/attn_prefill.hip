@@ -186,7 +186,9 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
   // q-tiles of one split read the same K/V and run on one XCD).
   const uint32_t qt = item % qtiles, rest_s = item / qtiles;
   const uint32_t split = rest_s % n_split, rest = rest_s / n_split;
-  const uint32_t kh = rest % a.kvh, seq = rest / a.kvh;
+  const uint32_t kh = rest % a.kvh;
+  const uint32_t seq = a.pf_seqs ? a.pf_seqs[rest / a.kvh] : rest / a.kvh;
+  if (seq >= a.batch) return;
   const uint32_t q0 = cu_q[seq];
   const uint32_t len_q = cu_q[seq + 1] - q0;
   if (len_q < a.pf_min_q || len_q == 0) return;
@@ -440,7 +442,9 @@ __global__ __launch_bounds__(256) void paged_prefill_merge(AttnArgs a, uint32_t 
   const uint32_t row_in = (blockIdx.x % blocks_per_item) * kRpw + threadIdx.x / kTpr;
   const uint32_t dq = (threadIdx.x % kTpr) * 4;
   const uint32_t qt = base % qtiles, rest = base / qtiles;
-  const uint32_t kh = rest % a.kvh, seq = rest / a.kvh;
+  const uint32_t kh = rest % a.kvh;
+  const uint32_t seq = a.pf_seqs ? a.pf_seqs[rest / a.kvh] : rest / a.kvh;
+  if (seq >= a.batch) return;
   const uint32_t q0 = a.cu_q[seq], len_q = a.cu_q[seq + 1] - q0;
   if (len_q < a.pf_min_q || len_q == 0) return;
   const uint32_t G = a.group;
@@ -535,7 +539,7 @@ void launch_prefill(const AttnArgs& a_in, uint32_t max_q, uint32_t max_k, uint32
 #endif
   constexpr uint32_t rows = 16 * VK_PF_RT * kPfWaves;
   const uint32_t qtiles = (uint32_t)(((uint64_t)max_q * a.group + rows - 1) / rows);
-  const uint64_t base = (uint64_t)qtiles * a.kvh * a.batch;
+  const uint64_t base = (uint64_t)qtiles * a.kvh * a.pf_seqs_n;
   // As many splits as the workspace given holds (none without one); a
   // deterministic call does not split, so its output does not depend on
   // the workspace it is given.
