@@ -862,36 +862,62 @@ def probes_copy(w, cache):
 
 # ---- CPU baseline ------------------------------------------------------------------
 
-def cpu_baseline(decode, budget_s=12.0):
-    """The C oracle (candle CPU path restated) on the same config-2 batch,
-    repeated until ~budget_s of CPU time; OpenMP over sequences."""
+def cpu_baseline(decode, budget_s=8.0):
+    """The candle CPU path on the same config-2 batch, in two restatements,
+    each repeated until ~budget_s: the C oracle (OpenMP over sequences,
+    scalar f32 loops) and oracle/candle_np.py (candle's own steps: gather,
+    cast, repeat_kv, BLAS matmuls, host-built mask, softmax). The faster is
+    the reported baseline; both are in the line."""
     import oracle  # checker/baseline only
+    from oracle import candle_np  # baseline only
     w = decode["w"]
     cache = decode["cache"]
     # Host copy of just the blocks the batch uses, renumbered densely.
     used = np.concatenate(w.tables).astype(np.int64)
     remap = {int(b): i for i, b in enumerate(used)}
     idx = torch.from_numpy(used).to(DEV)
-    kc = cache.reference_view(0, "k")[idx].float().cpu().numpy()
-    vc = cache.reference_view(0, "v")[idx].float().cpu().numpy()
+    kd = cache.reference_view(0, "k")[idx]
+    vd = cache.reference_view(0, "v")[idx]
+    kc, vc = kd.float().cpu().numpy(), vd.float().cpu().numpy()
+    kbits = kd.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    vbits = vd.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
     tables = [[remap[int(b)] for b in t] for t in w.tables]
     q = decode["q"].float().cpu().numpy()
+    qbits = decode["q"].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
     # Every core this process may run on (the box's share of the host).
     threads = len(os.sched_getaffinity(0))
     cu_q, cu_k = w.cu_q(), w.cu_k()
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        oracle.paged_attention(q, kc, vc, cu_q, cu_k, tables, decode["scale"], threads=threads)
-        reps += 1
-        if time.perf_counter() - t0 > budget_s or reps >= 50:
-            break
-    sec = (time.perf_counter() - t0) / reps
-    gbs = decode["alg_bytes"] / sec / 1e9
-    log(f"cpu baseline: {sec * 1e3:.1f} ms per config-2 step on {threads} threads, {gbs:.2f} GB/s")
-    return dict(value=gbs, unit="GB/s", cores=threads, nproc=os.cpu_count(), kind="port",
-                sample=f"full config-2 decode batch (64 seqs, sum_len {w.lens.sum()}), "
-                       f"{reps} passes, C oracle with OpenMP over sequences, f32 math on "
-                       f"bf16-valued K/V", ms_per_step=sec * 1e3)
+
+    def rate(fn):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            if time.perf_counter() - t0 > budget_s or reps >= 50:
+                break
+        return (time.perf_counter() - t0) / reps, reps
+
+    legs = {}
+    sec, reps = rate(lambda: oracle.paged_attention(q, kc, vc, cu_q, cu_k, tables,
+                                                    decode["scale"], threads=threads))
+    legs["c_oracle"] = dict(
+        value=decode["alg_bytes"] / sec / 1e9, ms_per_step=sec * 1e3, reps=reps,
+        sample=f"full config-2 decode batch (64 seqs, sum_len {w.lens.sum()}), {reps} passes, "
+               f"C oracle with OpenMP over sequences, f32 math on bf16-valued K/V")
+    sec, reps = rate(lambda: candle_np.paged_attention(qbits, kbits, vbits, cu_q, cu_k, tables,
+                                                       decode["scale"]))
+    legs["candle_numpy"] = dict(
+        value=decode["alg_bytes"] / sec / 1e9, ms_per_step=sec * 1e3, reps=reps,
+        sample=f"full config-2 decode batch (64 seqs, sum_len {w.lens.sum()}), {reps} passes, "
+               f"candle's steps in numpy (gather, f32 cast, repeat_kv, BLAS matmuls, mask, "
+               f"softmax) on bf16 K/V, BLAS threads as the process allows")
+    for k, v in legs.items():
+        log(f"cpu baseline ({k}): {v['ms_per_step']:.1f} ms per config-2 step, "
+            f"{v['value']:.2f} GB/s")
+    best = max(legs, key=lambda k: legs[k]["value"])
+    b = legs[best]
+    return dict(value=b["value"], unit="GB/s", cores=threads, nproc=os.cpu_count(), kind="port",
+                sample=b["sample"], ms_per_step=b["ms_per_step"], legs=legs)
 
 
 def cpu_baselines_more(decode, budget_s=4.0):

@@ -408,3 +408,31 @@ def test_threaded_scatter_and_copy_equal_the_serial_ones():
     oracle.copy_blocks(ks2, vs2, pairs, threads=4)
     assert all(np.array_equal(x, y) for x, y in zip(ks + vs, ks2 + vs2))
     assert np.array_equal(ks[1][perm[100:200]], ks[1][perm[:100]])
+
+
+@pytest.mark.parametrize("window", [None, 5])
+def test_the_numpy_candle_path_matches_the_c_oracle(window):
+    """oracle/candle_np.py (the candle CPU path with BLAS matmuls, the timed
+    CPU baseline) against the C oracle on bf16-valued pools: decode rows,
+    prefill chunks and an empty row, GQA 4:1, f32 rounding apart."""
+    from oracle import candle_np
+    rng = np.random.default_rng(11 + (window or 0))
+    nb, bs, kvh, d, heads = 40, 16, 2, 32, 8
+    bits = lambda *s: (rng.standard_normal(s).astype(np.float32).view(np.uint32) >> 16
+                       ).astype(np.uint16)
+    kb, vb = bits(nb, bs, kvh, d), bits(nb, bs, kvh, d)
+    lens_q, lens_k = [1, 7, 0, 1, 20], [33, 60, 5, 1, 20]
+    perm = rng.permutation(nb)
+    tables, at = [], 0
+    for lk in lens_k:
+        n = -(-lk // bs)
+        tables.append(perm[at:at + n].tolist())
+        at += n
+    cu_q = np.concatenate([[0], np.cumsum(lens_q)]).astype(np.uint32)
+    cu_k = np.concatenate([[0], np.cumsum(lens_k)]).astype(np.uint32)
+    qb = bits(int(cu_q[-1]), heads, d)
+    got = candle_np.paged_attention(qb, kb, vb, cu_q, cu_k, tables, 0.3, window)
+    f = candle_np.bf16_bits_to_f32
+    want = oracle.paged_attention(f(qb), f(kb), f(vb), cu_q, cu_k, tables, 0.3, window)
+    assert got.shape == want.shape
+    assert np.abs(got - want).max() <= 1e-5
