@@ -452,20 +452,38 @@ __global__ __launch_bounds__(256) void paged_prefill_merge(AttnArgs a, uint32_t 
   if (row >= len_q * G) return;
   const uint64_t stride = (uint64_t)rows_per_item * (D + 2);
   const float* p0 = part + (uint64_t)base * n_split * stride + (uint64_t)row_in * (D + 2);
-  float M = kNegBig;
-  for (uint32_t sp = 0; sp < n_split; ++sp) {
-    const float2 ml = *(const float2*)(p0 + sp * stride);
-    if (ml.y > 0.f) M = fmaxf(M, ml.x);
-  }
-  float L = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
-  for (uint32_t sp = 0; sp < n_split; ++sp) {
-    const float* pr = p0 + sp * stride;
-    const float2 ml = *(const float2*)pr;
-    if (!(ml.y > 0.f)) continue;  // a share with no visible key
-    const float e = fast_exp2(ml.x - M);
-    L += ml.y * e;
-    const float4 x = *(const float4*)(pr + 2 + dq);
-    o[0] += x.x * e, o[1] += x.y * e, o[2] += x.z * e, o[3] += x.w * e;
+  // Eight splits per memory round trip: every (m, l) and o load of a batch
+  // is issued before any is used (loading o only after testing l serialised
+  // two round trips per split), then the batch joins the running (M, L, o).
+  constexpr uint32_t kB = 8;
+  float M = kNegBig, L = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
+  for (uint32_t s0 = 0; s0 < n_split; s0 += kB) {
+    float2 ml[kB];
+    float4 x[kB];
+#pragma unroll
+    for (uint32_t u = 0; u < kB; ++u) {
+      const bool in = s0 + u < n_split;
+      const float* pr = p0 + (uint64_t)(in ? s0 + u : s0) * stride;
+      ml[u] = *(const float2*)pr;
+      x[u] = *(const float4*)(pr + 2 + dq);
+      if (!in) ml[u].y = 0.f;
+    }
+    float Mn = M;
+#pragma unroll
+    for (uint32_t u = 0; u < kB; ++u)
+      if (ml[u].y > 0.f) Mn = fmaxf(Mn, ml[u].x);
+    const float f = fast_exp2(M - Mn);
+    L *= f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] *= f;
+#pragma unroll
+    for (uint32_t u = 0; u < kB; ++u) {
+      if (!(ml[u].y > 0.f)) continue;  // a share with no visible key (its o is stale)
+      const float e = fast_exp2(ml[u].x - Mn);
+      L += ml[u].y * e;
+      o[0] += x[u].x * e, o[1] += x[u].y * e, o[2] += x[u].z * e, o[3] += x[u].w * e;
+    }
+    M = Mn;
   }
   const uint32_t j = row / G, hl = row % G;
   T* orow = (T*)a.out + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * D + dq;
