@@ -365,27 +365,47 @@ __global__ __launch_bounds__(kGenThreads) void paged_attn_generic_merge(
   if (pr >= rows) return;
   const uint64_t base = (uint64_t)blockIdx.x * n_chunks;
   const uint64_t stride = (uint64_t)kGenRows * (D + 2);
-  float M = kNegBig;
-  for (int32_t c = c_first; c <= c_last; ++c) {
-    const float* pc = part + (base + c) * stride;
-    if (pc[2 * pr + 1] > 0.f) M = fmaxf(M, pc[2 * pr]);
-  }
-  float L = 0.f;
+  // Four chunks per memory round trip: every (m, l) and o load of a batch
+  // is issued before any is used, then the batch joins the running (M, L,
+  // o) (loading o only after testing l serialised two round trips per
+  // chunk).
   constexpr int kMaxDPer = DT ? (DT + 15) / 16 : 256 / 16;
+  constexpr int kB = 4;
+  float M = kNegBig, L = 0.f;
   float o[kMaxDPer];
 #pragma unroll
   for (int i = 0; i < kMaxDPer; ++i) o[i] = 0.f;
-  for (int32_t c = c_first; c <= c_last; ++c) {
-    const float* pc = part + (base + c) * stride;
-    const float l = pc[2 * pr + 1];
-    if (!(l > 0.f)) continue;  // a chunk no key of this row is visible in
-    const float e = __expf(pc[2 * pr] - M);
-    L += l * e;
+  for (int32_t c0 = c_first; c0 <= c_last; c0 += kB) {
+    float m[kB], l[kB], x[kB][kMaxDPer];
 #pragma unroll
-    for (int i = 0; i < kMaxDPer; ++i) {
-      const uint32_t d = pd + 16 * i;
-      if (d < D) o[i] += pc[2 * kGenRows + pr * D + d] * e;
+    for (int u = 0; u < kB; ++u) {
+      const bool in = c0 + u <= c_last;
+      const float* pc = part + (base + (in ? c0 + u : c0)) * stride;
+      m[u] = pc[2 * pr];
+      l[u] = in ? pc[2 * pr + 1] : 0.f;
+#pragma unroll
+      for (int i = 0; i < kMaxDPer; ++i) {
+        const uint32_t d = pd + 16 * i;
+        x[u][i] = d < D ? pc[2 * kGenRows + pr * D + d] : 0.f;
+      }
     }
+    float Mn = M;
+#pragma unroll
+    for (int u = 0; u < kB; ++u)
+      if (l[u] > 0.f) Mn = fmaxf(Mn, m[u]);
+    const float f = __expf(M - Mn);
+    L *= f;
+#pragma unroll
+    for (int i = 0; i < kMaxDPer; ++i) o[i] *= f;
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      if (!(l[u] > 0.f)) continue;  // a chunk no key of this row is visible in
+      const float e = __expf(m[u] - Mn);
+      L += l[u] * e;
+#pragma unroll
+      for (int i = 0; i < kMaxDPer; ++i) o[i] += x[u][i] * e;
+    }
+    M = Mn;
   }
   const uint32_t rr = row0 + pr, j = rr / G, hl = rr - j * G;
   T* orow = (T*)a.out + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * D;
