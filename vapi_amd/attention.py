@@ -268,7 +268,9 @@ def paged_attention_append_prepared(q: torch.Tensor, k: torch.Tensor, v: torch.T
     num_heads = q.shape[1]
     max_q = max(int(prepared.max_seqlen_q), 1)
     max_k = max(int(prepared.max_seqlen_k), 1)
-    if max_q > 1 and prepared.prefill_seqs is not None:
+    if max_q > 1 and prepared.prefill_seqs is not None and cache.pool.v:
+        # (A K-only pool goes to the library call below, which refuses it
+        # before writing anything.)
         # A step with prefill rows is not fused (the library runs the append
         # and then the attention); run that pair here so that the attention
         # gets the step's prefill list.
