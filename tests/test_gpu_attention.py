@@ -472,6 +472,9 @@ SPLIT_CASES = [
     (torch.bfloat16, 32, 8, 128, 16, [40, 1, 100], [3000, 2500, 2100], None, "NHD"),
     (torch.float16, 16, 4, 64, 32, [96, 1], [5000, 700], 1500, "HND"),
     (torch.bfloat16, 28, 4, 128, 16, [300], [2600], 700, "HND"),
+    # 5 query tiles x 4 kv heads: 13 splits, merged in a batch of eight and
+    # a partial batch of five.
+    (torch.bfloat16, 16, 4, 128, 16, [320], [4000], None, "HND"),
 ]
 
 

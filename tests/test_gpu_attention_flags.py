@@ -202,3 +202,49 @@ def test_a_prefill_only_call_ignores_the_prefill_list():
     want = oracle_out(q, c, 0, batch, scale)
     out = call_prepared(q, c, prep, scale, ATTN_NO_DECODE_ROWS, [])
     assert max_abs(out, want) <= 2e-2 * float(want.abs().max())
+
+
+def test_config2_mixed_step_matches_the_oracle():
+    """Config 2's pool and sequences as a chunked-prefill step: its first 63
+    sequences decoding, the 64th a 512-token chunk at positions 1536..2047
+    over its own blocks, through PreparedAttention (the prepared call with
+    the prefill list, the chunk's keys split over the GPU); every decode row
+    and 16-row samples of the chunk against the oracle."""
+    from vapi_amd import workload
+    from vapi_amd.cache import PagedKvCache
+    import oracle
+    from test_gpu_attention import host_f32
+    w = workload.config2_decode()
+    c = PagedKvCache(1, w.num_blocks, w.block_size, w.num_kv_heads, w.head_dim, torch.bfloat16,
+                     "HND")
+    workload.fill_normal(c._slab, workload.seed_for(2))
+    nd = 63
+    lens_q = [1] * nd + [512]
+    lens_k = [int(x) for x in w.lens[:nd]] + [2048]
+    tables = [t.tolist() for t in w.tables[:nd]] + [w.tables[nd].tolist()[:128]]
+    if len(tables[nd]) < 128:
+        used = set(x for t in tables for x in t)
+        tables[nd] = [x for x in range(w.num_blocks) if x not in used][:128]
+    batch = ForwardBatch(cu_seqlens_q=np.concatenate([[0], np.cumsum(lens_q)]).tolist(),
+                         cu_seqlens_k=np.concatenate([[0], np.cumsum(lens_k)]).tolist(),
+                         block_tables=tables, max_seqlen_q=512, max_seqlen_k=max(lens_k))
+    g = torch.Generator(device=DEV).manual_seed(63)
+    q = torch.randn(sum(lens_q), w.num_heads, w.head_dim, generator=g, device=DEV).to(
+        torch.bfloat16)
+    prep = PreparedAttention.from_batch(batch, DEV)
+    assert prep.n_prefill == 1 and prep.prefill_seqs.cpu().tolist() == [nd]
+    scale = w.head_dim ** -0.5
+    got = paged_attention_prepared(q, c, 0, prep, scale)
+    torch.cuda.synchronize()
+    kc = host_f32(c.reference_view(0, "k").contiguous())
+    vc = host_f32(c.reference_view(0, "v").contiguous())
+    dec = oracle.paged_attention(host_f32(q[:nd]), kc, vc, list(range(nd + 1)),
+                                 batch.cu_seqlens_k[:nd + 1], tables[:nd], scale, threads=8)
+    dec = torch.from_numpy(dec).to(torch.bfloat16).float()
+    assert max_abs(got[:nd], dec) <= 2e-2 * float(dec.abs().max())
+    for j0 in (0, 200, 496):
+        rows = q[nd + j0: nd + j0 + 16]
+        want = oracle.paged_attention(host_f32(rows), kc, vc, [0, 16], [0, 2048 - 512 + j0 + 16],
+                                      [tables[nd]], scale, threads=8)
+        want = torch.from_numpy(want).to(torch.bfloat16).float()
+        assert max_abs(got[nd + j0: nd + j0 + 16], want) <= 2e-2 * float(want.abs().max()), j0
