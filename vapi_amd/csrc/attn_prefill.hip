@@ -156,6 +156,12 @@ __device__ __forceinline__ void ds_read_tr16_x4(uint2 (&r)[8], const uint32_t (&
 }
 
 
+// Bytes of one (item, split) partial block: (m, l) f32 per row, then o / l
+// per row in a 16-bit type.
+__host__ __device__ constexpr uint64_t pf_part_bytes(uint32_t rows, uint32_t d) {
+  return (uint64_t)rows * (8 + 2 * d);
+}
+
 // With n_split > 1 the keys a workgroup would walk are cut into n_split
 // contiguous runs of steps, one workgroup each (a batch too small to fill
 // the GPU with query tiles alone); each writes its rows' (m, l, o) to
@@ -397,18 +403,24 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
   wait_vmcnt<0>();  // no load may land in LDS after the workgroup ends
 
   if constexpr (kSplit) {
-    // Partials of this split: row (m in scaled log2 units, l, o[D]),
-    // unnormalised; an empty share leaves l = 0.
-    float* pb = part + ((uint64_t)(rest * qtiles + qt) * n_split + split) * kPfRows * (D + 2);
+    // Partials of this split (pf_part_bytes per item and split): per row
+    // (m in scaled log2 units, l) as f32, then per row o / l in the pool's
+    // 16-bit type (half the bytes of f32 o; the merge weighs it by l). An
+    // empty share leaves l = 0 and its o unwritten.
+    char* pb = (char*)part + ((uint64_t)(rest * qtiles + qt) * n_split + split) *
+                                 pf_part_bytes(kPfRows, D);
 #pragma unroll
     for (int t = 0; t < kPfRT; ++t) {
       const float lt = wave_sum_g(l_run[t]);
-      float* pr = pb + (uint64_t)(wave * 16 * kPfRT + 16 * t + col) * (D + 2);
-      if (g == 0) *(float2*)pr = make_float2(m_run[t], lt);
+      const uint32_t row = wave * 16 * kPfRT + 16 * t + col;
+      if (g == 0) *(float2*)(pb + (uint64_t)row * 8) = make_float2(m_run[t], lt);
+      T* po = (T*)(pb + (uint64_t)kPfRows * 8) + (uint64_t)row * D;
+      const float sc = lt > 0.f ? 1.f / lt : 0.f;
 #pragma unroll
       for (int k = 0; k < DT; ++k)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pr[2 + 16 * k + 4 * g + i] = o[t][k][i];
+        *(uint2*)(po + 16 * k + 4 * g) =
+            make_uint2(pack2<T>(o[t][k][0] * sc, o[t][k][1] * sc),
+                       pack2<T>(o[t][k][2] * sc, o[t][k][3] * sc));
     }
     return;
   }
@@ -450,8 +462,10 @@ __global__ __launch_bounds__(256) void paged_prefill_merge(AttnArgs a, uint32_t 
   const uint32_t G = a.group;
   const uint32_t row = qt * rows_per_item + row_in;
   if (row >= len_q * G) return;
-  const uint64_t stride = (uint64_t)rows_per_item * (D + 2);
-  const float* p0 = part + (uint64_t)base * n_split * stride + (uint64_t)row_in * (D + 2);
+  const uint64_t stride = pf_part_bytes(rows_per_item, D);  // per split
+  const char* p0 = (const char*)part + (uint64_t)base * n_split * stride;
+  const uint64_t ml_off = (uint64_t)row_in * 8;
+  const uint64_t o_off = (uint64_t)rows_per_item * 8 + ((uint64_t)row_in * D + dq) * sizeof(T);
   // Eight splits per memory round trip: every (m, l) and o load of a batch
   // is issued before any is used (loading o only after testing l serialised
   // two round trips per split), then the batch joins the running (M, L, o).
@@ -459,13 +473,13 @@ __global__ __launch_bounds__(256) void paged_prefill_merge(AttnArgs a, uint32_t 
   float M = kNegBig, L = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
   for (uint32_t s0 = 0; s0 < n_split; s0 += kB) {
     float2 ml[kB];
-    float4 x[kB];
+    uint2 xb[kB];
 #pragma unroll
     for (uint32_t u = 0; u < kB; ++u) {
       const bool in = s0 + u < n_split;
-      const float* pr = p0 + (uint64_t)(in ? s0 + u : s0) * stride;
-      ml[u] = *(const float2*)pr;
-      x[u] = *(const float4*)(pr + 2 + dq);
+      const char* pr = p0 + (uint64_t)(in ? s0 + u : s0) * stride;
+      ml[u] = *(const float2*)(pr + ml_off);
+      xb[u] = *(const uint2*)(pr + o_off);
       if (!in) ml[u].y = 0.f;
     }
     float Mn = M;
@@ -480,8 +494,11 @@ __global__ __launch_bounds__(256) void paged_prefill_merge(AttnArgs a, uint32_t 
     for (uint32_t u = 0; u < kB; ++u) {
       if (!(ml[u].y > 0.f)) continue;  // a share with no visible key (its o is stale)
       const float e = fast_exp2(ml[u].x - Mn);
-      L += ml[u].y * e;
-      o[0] += x[u].x * e, o[1] += x[u].y * e, o[2] += x[u].z * e, o[3] += x[u].w * e;
+      const float w = ml[u].y * e;  // the partial's o is o / l
+      L += w;
+      const T* h = (const T*)&xb[u];
+      o[0] += to_f32(h[0]) * w, o[1] += to_f32(h[1]) * w;
+      o[2] += to_f32(h[2]) * w, o[3] += to_f32(h[3]) * w;
     }
     M = Mn;
   }
@@ -526,8 +543,8 @@ static uint32_t pf_splits(uint64_t base, uint32_t max_k) {
 }
 
 static uint64_t pf_split_bytes(uint64_t base, uint32_t n, uint32_t head_dim) {
-  constexpr uint64_t rows = 16 * VK_PF_RT * kPfWaves;
-  return n > 1 ? base * n * rows * (head_dim + 2) * sizeof(float) : 0;
+  constexpr uint32_t rows = 16 * VK_PF_RT * kPfWaves;
+  return n > 1 ? base * n * pf_part_bytes(rows, head_dim) : 0;
 }
 
 // At most this much workspace for the partials (fewer splits beyond).
