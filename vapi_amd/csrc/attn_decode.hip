@@ -145,6 +145,35 @@ __device__ __forceinline__ DecodePos locate(const AttnArgs& a, const uint32_t* _
   return p;
 }
 
+// The first step of the segment after `cur` in step order: (seq, kh + 1),
+// or kv head 0 of the next sequence that has decode steps. A wave's slice
+// is contiguous, so the step after a segment's last is always this one,
+// and a wave that moves on from a finished segment needs no search.
+__device__ __forceinline__ DecodePos next_segment(const AttnArgs& a,
+                                                  const uint32_t* __restrict__ cu_q,
+                                                  const uint32_t* __restrict__ cu_k,
+                                                  const uint32_t* P, const uint32_t* FZ,
+                                                  const DecodePos& cur) {
+  DecodePos p = cur;
+  if (cur.kh + 1 < a.kvh) {
+    p.kh = cur.kh + 1;
+  } else {
+    uint32_t s = cur.seq + 1;
+    while (s + 1 < a.batch && __builtin_amdgcn_readfirstlane(P[s + 1]) ==
+                                  __builtin_amdgcn_readfirstlane(P[s]))
+      ++s;  // sequences without decode steps
+    p.seq = s;
+    p.kh = 0;
+    p.q0 = cu_q[s];
+    p.len_k = (int32_t)(cu_k[s + 1] - cu_k[s]);
+    p.lo = a.wl >= 0 ? max(0, p.len_k - 1 - a.wl) : 0;
+    p.fuse = FZ ? FZ[s] : 0u;
+  }
+  p.key0 = p.lo & ~31;
+  p.seg_first = 1u;
+  return p;
+}
+
 template <typename T, int D>
 __device__ __forceinline__ void load_q(uint4* qs, const AttnArgs& a, const DecodePos& p,
                                        uint32_t lane, uint32_t col, uint32_t g) {
@@ -341,7 +370,7 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
       nxt.key0 += 32;
       nxt.seg_first = false;
     } else if (more) {
-      nxt = locate(a, cu_q, cu_k, P, FZ, t + 1);
+      nxt = next_segment(a, cu_q, cu_k, P, FZ, pos);
     } else {
       nxt.seq = 0;
       nxt.key0 = 0;
