@@ -921,8 +921,8 @@ def cpu_baseline(decode, budget_s=8.0):
 
 
 def cpu_baselines_more(decode, budget_s=4.0):
-    """BASELINE.md's other CPU legs, each on a bounded sample with the C
-    oracle, on one core and on every core this process may use: config-2
+    """The other CPU legs of the benchmark's configs, each on a bounded sample
+    with the C oracle, on one core and on every core this process may use: config-2
     decode on one core (the all-core figure is `cpu_baseline`), the config-1
     append scatter (write_rows), the config-3 chunked prefill (the last 64
     query rows of each sequence's chunk) and the config-4a block copy

@@ -655,7 +655,7 @@ int64_t vapi_spill_promote(vapi_spill_store* s, const vapi_kv_pool* pool, const 
       if (e != hipSuccess)
         VK_FAIL(VAPI_KV_EHIP, "vapi_spill_promote: %s", hipGetErrorString(e));
     }
-    // Resolve this round's chain entries in order, copy (or read from disk)
+    // Resolve this batch's chain entries in order, copy (or read from disk)
     // their blobs into the pinned slots on several threads, then account
     // in order as a get() per entry would: LRU touch and hit, or for an
     // unreadable disk entry forget it, count the error and the miss and end
