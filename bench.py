@@ -1084,6 +1084,12 @@ def main():
         extras["decode_small_batches"] = bench_small_batches(args.steps, args.warmup)
         extras["prefill_small_batches"] = bench_small_prefill(args.steps, args.warmup)
     extras["blocks_cfg4"] = bench_blocks(max(args.steps // 5, 3), 2, dec)
+    # The gather is a copy of scattered 4 KiB K/V tiles into a contiguous
+    # output: its fractions of 8 TB/s and of the random-16 KiB-run copy
+    # probe (the nearest measured pattern).
+    g, pr = extras["gather_cfg2"], extras["blocks_cfg4"]["probes"]
+    g["frac"] = g["gbs"] / HBM_PEAK_GBS
+    g["frac_of_runs_copy_probe"] = g["gbs"] / max(pr["copy_runs16k_gbs"], pr["copy_runs16k_nt_gbs"])
     if args.only == "blocks":
         return
     pd = probes_decode(dec)
