@@ -64,11 +64,12 @@ def timed(fn, steps, warmup):
     return start.elapsed_time(end) / steps, wall
 
 
-def timed_graph(fn, steps, warmup):
+def timed_graph(fn, steps, warmup, replays=7, detail=None):
     """Capture `steps` back-to-back calls of fn into one HIP graph (the way a
     serving loop replays its captured decode step), replay it untimed until
-    at least `warmup` calls have run, then time exactly one replay (`steps`
-    calls) between one pair of events. Returns ms per call."""
+    at least `warmup` calls have run, then time `replays` replays, each
+    between its own pair of events. Returns the median replay's ms per call;
+    `detail`, if given, receives every replay's us per call."""
     fn()
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
@@ -81,8 +82,18 @@ def timed_graph(fn, steps, warmup):
     torch.cuda.current_stream().wait_stream(side)
     for _ in range(max(-(-warmup // steps), 1)):
         graph.replay()
-    ms, _ = timed(graph.replay, 1, 0)
-    return ms / steps
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(replays)]
+    for a, b in evs:
+        a.record()
+        graph.replay()
+        b.record()
+    torch.cuda.synchronize()
+    per = sorted(a.elapsed_time(b) / steps for a, b in evs)
+    if detail is not None:
+        detail.extend(round(x * 1e3, 2) for x in per)
+    return per[len(per) // 2]
 
 
 # ---- config 2: decode (headline) ---------------------------------------------
@@ -137,8 +148,10 @@ def bench_decode(steps, warmup):
         f"{ms * 1e3:.1f} us/step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of 8 TB/s)")
     # The same call replayed from a HIP graph, as a serving loop that
     # captures its decode step runs it (GraphRunner, backend.rs:893-1216).
-    gms = timed_graph(d["step"], steps, warmup)
-    log(f"decode cfg2 in a graph: {gms * 1e3:.1f} us/step, "
+    graph_replays = []
+    gms = timed_graph(d["step"], steps, warmup, detail=graph_replays)
+    log(f"decode cfg2 in a graph: {gms * 1e3:.1f} us/step (median of {len(graph_replays)} "
+        f"replays of {steps} calls: {graph_replays}), "
         f"{d['alg_bytes'] / (gms * 1e-3) / 1e9:.0f} GB/s (layers rotating)")
     same = timed_graph(d["step_same_layer"], steps, warmup)
     log(f"decode cfg2 in a graph, one layer replayed: {same * 1e3:.1f} us/step, "
@@ -156,7 +169,8 @@ def bench_decode(steps, warmup):
     per = np.array([a.elapsed_time(b) * 1e3 for a, b in evs])
     spread = dict(median_us=float(np.median(per)), p10_us=float(np.percentile(per, 10)),
                   p90_us=float(np.percentile(per, 90)), calls=int(steps),
-                  graph_us=gms * 1e3, layers_rotated=DECODE_LAYERS,
+                  graph_us=gms * 1e3, graph_replays_us=graph_replays,
+                  layers_rotated=DECODE_LAYERS,
                   one_layer_replayed_graph_us=same * 1e3,
                   one_layer_replayed_graph_gbs=d["alg_bytes"] / (same * 1e-3) / 1e9)
     log(f"decode cfg2 per call: median {spread['median_us']:.1f} us "

@@ -284,9 +284,11 @@ int vapi_paged_attention_prepared(const vapi_kv_pool* pool, uint32_t layer, cons
  * VAPI_KV_ESPACE before anything is launched. Every call on one GPU shares
  * that GPU's array: calls that overlap on one GPU (different streams not
  * ordered against each other) race and must not be issued. The first call
- * on a device resolves the array's address and clears its XCD shares with a
- * small kernel on `stream`; later calls carry the shares over, as a kept
- * workspace does.
+ * on a device resolves the array's address; the first call not under HIP
+ * graph capture clears its XCD shares with a small kernel on `stream` (a
+ * captured call records no clear, so replays keep the shares); later calls
+ * carry the shares over, as a kept workspace does. The array is reserved in
+ * every process that loads the library, whether it calls this or not.
  */
 #define VAPI_ATTN_SCRATCH_BYTES (16u << 20)
 int vapi_paged_attention_noalloc(const vapi_kv_pool* pool, uint32_t layer, const void* q,

@@ -248,3 +248,64 @@ def test_config2_mixed_step_matches_the_oracle():
                                       [tables[nd]], scale, threads=8)
         want = torch.from_numpy(want).to(torch.bfloat16).float()
         assert max_abs(got[nd + j0: nd + j0 + 16], want) <= 2e-2 * float(want.abs().max()), j0
+
+
+def test_prefill_key_split_adds_no_error_beyond_the_unsplit_call():
+    """The key split keeps each split's partial (m, l, o / l) in f32, so the
+    split call's error against the oracle stays within 1.5x the unsplit
+    (deterministic, no split) call's on the same inputs."""
+    rng = np.random.default_rng(77)
+    c, q, batch = random_case(rng, torch.bfloat16, 32, 8, 128, 16, [512], [4096], "HND")
+    prep = PreparedAttention.from_batch(batch, DEV)
+    scale = 128 ** -0.5
+    b = 1
+    need = _lib.lib().vapi_paged_attention_workspace_size(c.pool, b, 32, 512, 4096)
+    ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=DEV)
+    split = call_ex(q, c, prep, scale, ATTN_NO_DECODE_ROWS, ws=ws)
+    unsplit = call_ex(q, c, prep, scale, ATTN_NO_DECODE_ROWS | ATTN_DETERMINISTIC, ws=ws)
+    torch.cuda.synchronize()
+    # oracle at f32, not rounded to bf16, so the two calls' own errors show
+    kc = c.reference_view(0, "k").contiguous().float().cpu().numpy()
+    vc = c.reference_view(0, "v").contiguous().float().cpu().numpy()
+    import oracle
+    ref = torch.from_numpy(oracle.paged_attention(q.float().cpu().numpy(), kc, vc,
+                                                  batch.cu_seqlens_q, batch.cu_seqlens_k,
+                                                  batch.block_tables, scale, threads=8))
+    e_split, e_unsplit = max_abs(split, ref), max_abs(unsplit, ref)
+    print(f"prefill 1 x 512 over 4096 keys, max-abs vs f32 oracle: split {e_split:.3e}, "
+          f"unsplit {e_unsplit:.3e}")
+    assert not torch.equal(split, unsplit)  # the split did run
+    assert e_split <= 1.5 * e_unsplit, (e_split, e_unsplit)
+
+
+def test_valu_context_past_max_seqlen_k_stays_inside_its_workspace():
+    """An f32 pool (the VALU kernel) whose device len_k exceeds the
+    max_seqlen_k the call was sized for: the key chunks stop at the launch's
+    last chunk (ceil(max_k / c) * c keys, 1,024 here for every chunk size c
+    the kernel picks), so neither kernel touches memory past the workspace,
+    and the row is the attention over those keys."""
+    rng = np.random.default_rng(5)
+    lens_k = [3000, 700]
+    c, q, batch = random_case(rng, torch.float32, 8, 2, 128, 16, [1, 1], lens_k, "HND")
+    prep = PreparedAttention.from_batch(batch, DEV)
+    lib = _lib.lib()
+    max_k = 1000  # smaller than sequence 0's 3,000 keys
+    need = lib.vapi_paged_attention_workspace_size(c.pool, 2, 8, 1, max_k)
+    guard = 1 << 16
+    ws = torch.full((need + guard,), 0xAB, dtype=torch.uint8, device=DEV)
+    ws[:need].zero_()
+    out = torch.full_like(q, float("nan"))
+    _lib.check(lib.vapi_paged_attention_ex(
+        c.pool, 0, q.data_ptr(), out.data_ptr(), prep.seqlens_q.data_ptr(),
+        prep.seqlens_k.data_ptr(), prep.block_table.data_ptr(), 2, prep.block_table.shape[1],
+        1, max_k, 8, 128 ** -0.5, -1, 0, 0, ws.data_ptr(), need, stream_handle()))
+    torch.cuda.synchronize()
+    assert bool((ws[need:] == 0xAB).all()), "the call wrote past its workspace"
+    trunc = ForwardBatch(cu_seqlens_q=[0, 1, 2], cu_seqlens_k=[0, 1024, 1024 + 700],
+                         block_tables=[batch.block_tables[0][:64], batch.block_tables[1]],
+                         max_seqlen_q=1, max_seqlen_k=1024)
+    want = oracle_out(q, c, 0, trunc, 128 ** -0.5)
+    assert max_abs(out[:1], want[:1]) <= 1e-5
+    # sequence 1 fits its 1,000-key bound: ordinary attention
+    full = oracle_out(q, c, 0, batch, 128 ** -0.5)
+    assert max_abs(out[1:], full[1:]) <= 1e-5

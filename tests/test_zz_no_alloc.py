@@ -83,3 +83,50 @@ def test_no_alloc_refuses_a_batch_past_its_scratch_and_writes_nothing():
     assert b"scratch" in _lib.lib().vapi_kv_last_error()
     torch.cuda.synchronize()
     assert bool(torch.isnan(out.float()).all())
+
+
+def first_call_under_capture():
+    """Run in a fresh process: the first noalloc call on the device is made
+    while a HIP graph is being captured. The share-clearing kernel must not
+    be recorded (it would reset the shares on every replay); each replay,
+    with eager work between them, must match the workspace entry point
+    within the bf16 tolerance."""
+    c, q, batch = case(4, *BIG)
+    prep = PreparedAttention.from_batch(batch, DEV)
+    out = torch.full_like(q, float("nan"))
+    a = args(q, c, prep, out)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            _lib.check(_lib.lib().vapi_paged_attention_noalloc(*a, 0, stream_handle()))
+    torch.cuda.current_stream().wait_stream(side)
+    want = with_workspace(q, c, prep, ATTN_DETERMINISTIC)
+    ref = oracle_out(q, c, 0, batch, q.shape[2] ** -0.5)
+    tol = 2e-2 * float(ref.abs().max())
+    for i in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert max_abs(out, ref) <= tol, ("replay", i, max_abs(out, ref))
+        assert max_abs(out, want) <= tol, ("replay", i)
+        with_workspace(q, c, prep, 0)  # eager work between replays
+    # An eager call after the capture clears the shares once and runs.
+    eager = no_alloc(q, c, prep, ATTN_DETERMINISTIC)
+    torch.cuda.synchronize()
+    assert torch.equal(eager, want)
+    print("first-call-under-capture ok", flush=True)
+
+
+def test_no_alloc_first_call_under_graph_capture():
+    import os
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    code = ("import sys; sys.path[:0] = [%r, %r]; import test_zz_no_alloc as t; "
+            "t.first_call_under_capture()" % (here, os.path.dirname(here)))
+    r = subprocess.run([sys.executable, "-c", code], cwd=here, capture_output=True, text=True,
+                       timeout=110)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+    assert "first-call-under-capture ok" in r.stdout

@@ -36,9 +36,6 @@ COMMON_FLAGS = [
     "-Wno-unused-function",
     f"-I{ROOT / 'include'}",
 ]
-# Extra hipcc flags for experiment builds (e.g. -DVK_DECODE_TRACE); the
-# product build sets none.
-COMMON_FLAGS += os.environ.get("VAPI_HIPCC_EXTRA", "").split()
 
 SOURCES = ["kv_ops.hip", "attention.hip", "attn_decode.hip", "attn_prefill.hip",
            "attn_generic.hip", "host.cpp", "spill.cpp"]

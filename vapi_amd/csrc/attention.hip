@@ -56,8 +56,14 @@ __global__ void scratch_clear_kernel(uint32_t* p, uint32_t n_words) {
   for (uint32_t i = threadIdx.x; i < n_words; i += blockDim.x) p[i] = 0u;
 }
 
-// The current device's scratch address; resolved (and its balance block
-// cleared on `stream`) by the first call on each device.
+// The current device's scratch address, resolved by the first call on each
+// device. Its balance block is cleared on `stream` by the first call that is
+// not being captured into a HIP graph: a clear recorded into a graph would
+// reset the shares on every replay. Until then the shares hold whatever the
+// array held; any shares give the same results (they only move where the
+// work is split, and unusable values count as uniform shares).
+static bool g_scratch_cleared[kMaxDevices];
+
 static int scratch_for_device(void** out, hipStream_t stream) {
   int dev = 0;
   VK_HIP(hipGetDevice(&dev));
@@ -71,10 +77,18 @@ static int scratch_for_device(void** out, hipStream_t stream) {
     if (e != hipSuccess || !ptr)
       VK_FAIL(VAPI_KV_EHIP, "vapi_paged_attention_noalloc: hipGetSymbolAddress(scratch): %s",
               hipGetErrorString(e));
-    hipLaunchKernelGGL(scratch_clear_kernel, dim3(1), dim3(256), 0, stream, (uint32_t*)ptr,
-                       (uint32_t)(kDecodeBalanceBytes / sizeof(uint32_t)));
-    VK_LAUNCHED("scratch_clear_kernel");
     g_scratch_ptr[dev] = ptr;
+  }
+  if (!g_scratch_cleared[dev]) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    VK_HIP(hipStreamIsCapturing(stream, &cap));
+    if (cap == hipStreamCaptureStatusNone) {
+      hipLaunchKernelGGL(scratch_clear_kernel, dim3(1), dim3(256), 0, stream,
+                         (uint32_t*)g_scratch_ptr[dev],
+                         (uint32_t)(kDecodeBalanceBytes / sizeof(uint32_t)));
+      VK_LAUNCHED("scratch_clear_kernel");
+      g_scratch_cleared[dev] = true;
+    }
   }
   *out = g_scratch_ptr[dev];
   return 0;
@@ -333,7 +347,6 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   a.ws_ml = nullptr;
   a.ws_o = nullptr;
   a.bal = nullptr;
-  a.trace = nullptr;
   a.k_new = fuse ? (const char*)fuse->k : nullptr;
   a.v_new = fuse ? (const char*)fuse->v : nullptr;
   a.slots = fuse ? fuse->slots : nullptr;

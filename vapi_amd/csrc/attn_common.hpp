@@ -49,7 +49,6 @@ struct AttnArgs {
   float* ws_ml;        // decode: partial (m, l) per slot and head
   float* ws_o;         // decode: partial outputs per slot and head
   uint32_t* bal;       // decode: XCD shares and per-wave timings, kept across launches
-  uint64_t* trace;  // decode timing probes (VK_DECODE_TRACE builds only)
   // Fused append (decode only; null otherwise): the step's new K/V rows
   // [n_new, kvh, D] and their slots.
   const char* k_new;

@@ -46,10 +46,7 @@ namespace vk {
 constexpr int kDecodeWavesPerWG = 4;
 constexpr int kDecodeWGsPerCU = 1;
 constexpr uint32_t kGroups = 8;          // XCDs; workgroup b runs on XCD b % 8
-#ifndef VK_MERGE_WAVES
-#define VK_MERGE_WAVES 4
-#endif
-constexpr uint32_t kMergeWaves = VK_MERGE_WAVES;  // merge: segments (waves) per workgroup
+constexpr uint32_t kMergeWaves = 4;  // merge: segments (waves) per workgroup
 constexpr uint32_t kMaxPlanSeqs = 4096;  // sequences per launch (host chunks beyond)
 
 // Balance block (u32 words, kept across launches at the start of the
@@ -327,10 +324,6 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
     }
     return;
   }
-#ifdef VK_DECODE_TRACE
-  const uint64_t tr0 = __builtin_amdgcn_s_memrealtime();
-  uint64_t tr_first = 0, tr_last = 0;
-#endif
 
   uint32_t t = t_begin;
   const uint32_t col = lane & 15, g = lane >> 4;
@@ -388,10 +381,6 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
       return key >= lo && key < len_k;
     });
     attend_pv<T, D>(vc, pf, o);
-#ifdef VK_DECODE_TRACE
-    tr_last = __builtin_amdgcn_s_memrealtime();
-    if (!tr_first) tr_first = tr_last;
-#endif
     if (!same_piece) {
       const uint32_t seg = pos.seq * a.kvh + pos.kh;
       if (lane == 0) {
@@ -413,25 +402,10 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
   };
   while (step(kA, vA, kB, vB) && step(kB, vB, kA, vA)) {
   }
-  const uint64_t tr1 = __builtin_amdgcn_s_memrealtime();
+  const uint32_t t_done = (uint32_t)__builtin_amdgcn_s_memrealtime();
   if (lane == 0) {
-    *(uint4*)stat = make_uint4(t_end - t_begin, t_entry, (uint32_t)tr1, 0u);
+    *(uint4*)stat = make_uint4(t_end - t_begin, t_entry, t_done, 0u);
   }
-#ifdef VK_DECODE_TRACE
-  // Per wave (8 words): start/end (100 MHz ticks), steps done << 32 | entry
-  // tick, HW_ID | XCC_ID << 32, the ends of the first and the last step's
-  // attention.
-  if (lane == 0) {
-    uint64_t* tr = a.trace + 8ull * gw;
-    tr[4] = tr_first;
-    tr[5] = tr_last;
-    tr[0] = tr0;
-    tr[1] = tr1;
-    tr[2] = ((uint64_t)(t_end - t_begin) << 32) | t_entry;
-    tr[3] = (uint64_t)__builtin_amdgcn_s_getreg((31 << 11) | 4) |
-            ((uint64_t)__builtin_amdgcn_s_getreg((3 << 11) | 20) << 32);
-  }
-#endif
 }
 
 // The next launch's shares from this launch's per-wave timings: each group
@@ -710,7 +684,7 @@ const size_t kDecodeBalanceBytes = kBalStats * sizeof(uint32_t);
 // everything else that a launch reads was written by that launch. A zeroed
 // workspace starts from uniform shares.
 struct DecodeWs {
-  size_t bal, ranges, ml, o, trace, total;
+  size_t bal, ranges, ml, o, total;
 };
 static DecodeWs decode_ws(uint32_t b, uint32_t kvh, uint32_t group, uint32_t head_dim,
                           uint32_t num_waves) {
@@ -720,11 +694,7 @@ static DecodeWs decode_ws(uint32_t b, uint32_t kvh, uint32_t group, uint32_t hea
   w.ranges = up256((kBalStats + kStatWords * (size_t)num_waves) * sizeof(uint32_t));
   w.ml = w.ranges + up256((size_t)b * kvh * 2 * sizeof(uint32_t));
   w.o = w.ml + up256(slots * group * 2 * sizeof(float));
-  w.trace = w.o + up256(slots * group * head_dim * sizeof(float));
-  w.total = w.trace;
-#ifdef VK_DECODE_TRACE
-  w.total += (size_t)num_waves * 8 * sizeof(uint64_t);
-#endif
+  w.total = w.o + up256(slots * group * head_dim * sizeof(float));
   return w;
 }
 
@@ -751,9 +721,6 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, bool bf16,
     c.seg_ranges = (uint32_t*)(ws + w.ranges);
     c.ws_ml = (float*)(ws + w.ml);
     c.ws_o = (float*)(ws + w.o);
-#ifdef VK_DECODE_TRACE
-    c.trace = (uint64_t*)(ws + w.trace);
-#endif
     // Fused append: the first chunk's merge launch also writes the new rows
     // (every chunk's stream reads a row's new key from the new rows).
     const bool fuse = a.k_new != nullptr;

@@ -46,11 +46,17 @@ __host__ __device__ __forceinline__ uint32_t gen_k_stride(uint32_t d) {
   return (d & 3) ? d + 1 : d + 4;
 }
 
-// Chunks a tile with visible keys [klo, khi] spans: [c_first, c_last].
+// Chunks a tile with visible keys [klo, khi] spans: [c_first, c_last],
+// within the launch's n_chunks. A len_k in device memory larger than the
+// max_seqlen_k the launch was sized for would otherwise name chunks past
+// the workspace; keys past the last launched chunk are treated as not
+// visible (the attention is truncated there), and c_last < c_first when
+// none of the tile's keys is covered.
 __device__ __forceinline__ void tile_chunks(int32_t klo, int32_t khi, uint32_t chunk,
-                                            int32_t& c_first, int32_t& c_last) {
+                                            uint32_t n_chunks, int32_t& c_first,
+                                            int32_t& c_last) {
   c_first = klo / (int32_t)chunk;
-  c_last = khi / (int32_t)chunk;
+  c_last = min(khi / (int32_t)chunk, (int32_t)n_chunks - 1);
 }
 
 // Four consecutive elements as f32 (16 bytes of f32, 8 of bf16 / f16).
@@ -106,7 +112,7 @@ __global__ __launch_bounds__(kGenThreads) void paged_attn_generic(AttnArgs a, ui
   key_range(offset + (int32_t)(row0 / G), len_k, a.wl, a.wr, klo, unused);
   key_range(offset + (int32_t)((row0 + rows - 1) / G), len_k, a.wl, a.wr, unused, khi);
   int32_t c_first, c_last;
-  tile_chunks(klo, khi, chunk_keys, c_first, c_last);
+  tile_chunks(klo, khi, chunk_keys, n_chunks, c_first, c_last);
   if (khi < klo || (int32_t)chunk < c_first || (int32_t)chunk > c_last) return;
   const bool split = c_last > c_first;
   klo = max(klo, (int32_t)(chunk * chunk_keys));
@@ -359,8 +365,8 @@ __global__ __launch_bounds__(kGenThreads) void paged_attn_generic_merge(
   int32_t klo, khi, unused, c_first, c_last;
   key_range(offset + (int32_t)(row0 / G), len_k, a.wl, a.wr, klo, unused);
   key_range(offset + (int32_t)((row0 + rows - 1) / G), len_k, a.wl, a.wr, unused, khi);
-  tile_chunks(klo, khi, chunk_keys, c_first, c_last);
-  if (khi < klo || c_last == c_first) return;
+  tile_chunks(klo, khi, chunk_keys, n_chunks, c_first, c_last);
+  if (khi < klo || c_last <= c_first) return;
   const uint32_t pr = tid >> 4, pd = tid & 15;
   if (pr >= rows) return;
   const uint64_t base = (uint64_t)blockIdx.x * n_chunks;

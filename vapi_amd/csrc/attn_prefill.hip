@@ -20,10 +20,7 @@
 
 namespace vk {
 
-#ifndef VK_PF_WAVES
-#define VK_PF_WAVES 8
-#endif
-constexpr int kPfWaves = VK_PF_WAVES;
+constexpr int kPfWaves = 8;
 constexpr int kPfThreads = 64 * kPfWaves;
 // Workgroup -> work item. The hardware deals workgroups round-robin to the
 // 8 XCDs (linear id % 8); each XCD here gets a contiguous range of work
@@ -157,9 +154,9 @@ __device__ __forceinline__ void ds_read_tr16_x4(uint2 (&r)[8], const uint32_t (&
 
 
 // Bytes of one (item, split) partial block: (m, l) f32 per row, then o / l
-// per row in a 16-bit type.
+// per row in f32 (the split adds no rounding before the merge).
 __host__ __device__ constexpr uint64_t pf_part_bytes(uint32_t rows, uint32_t d) {
-  return (uint64_t)rows * (8 + 2 * d);
+  return (uint64_t)rows * (8 + 4 * d);
 }
 
 // With n_split > 1 the keys a workgroup would walk are cut into n_split
@@ -285,21 +282,8 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
     ring_barrier();
   }
   // Step s reads buffer s % 3 and issues step s + 2 into (s + 2) % 3.
-#ifdef VK_PF_TRACE
-  // Phase timestamps (shader clock) of every wave of workgroup item 100,
-  // steps 16..47: [step][wave][phase].
-  uint32_t tr_step = 0;
-  const bool tr_on = item == 100 && lane == 0;
-  auto TR = [&](int ph) {
-    if (tr_on && tr_step >= 16 && tr_step < 48)
-      a.trace[((tr_step - 16) * 8 + wave) * 5 + ph] = __builtin_amdgcn_s_memtime();
-  };
-#else
-  auto TR = [](int) {};
-#endif
   auto step = [&](auto cur) __attribute__((always_inline)) {
     constexpr int B = decltype(cur)::value;
-    TR(0);
     uint16_t* const kbuf = B == 0 ? k0 : B == 1 ? k1 : k2;
     uint16_t* const vbuf = B == 0 ? v0 : B == 1 ? v1 : v2;
     uint16_t* const knext = B == 0 ? k2 : B == 1 ? k0 : k1;
@@ -334,7 +318,6 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
         }
       }
     }
-    TR(1);
     float mx[kPfRT];
     bool grow = false;
 #pragma unroll
@@ -350,7 +333,6 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
     uint4 pf[kPfRT];
 #pragma unroll
     for (int t = 0; t < kPfRT; ++t) pf[t] = exp_pack<T>(sc[t], m_run[t], l_run[t], a.scale_log2);
-    TR(2);
     // V^T fragments two d tiles at a time; a batch's MFMAs run while the
     // next batch's reads wait (measured: batches of two tiles 821-833
     // TFLOP/s, of four 803-814, of one 794-805 on config 3).
@@ -383,13 +365,8 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
     // Step s + 1's chunks (issued a step ago) are in LDS once this wave's
     // loads older than step s + 2's have landed; the barrier makes that
     // hold for every wave.
-    TR(3);
     wait_vmcnt<kLoadsPerStep>();
     ring_barrier();
-    TR(4);
-#ifdef VK_PF_TRACE
-    ++tr_step;
-#endif
     s0_ += 32;
   };
   while (true) {
@@ -404,9 +381,9 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
 
   if constexpr (kSplit) {
     // Partials of this split (pf_part_bytes per item and split): per row
-    // (m in scaled log2 units, l) as f32, then per row o / l in the pool's
-    // 16-bit type (half the bytes of f32 o; the merge weighs it by l). An
-    // empty share leaves l = 0 and its o unwritten.
+    // (m in scaled log2 units, l) as f32, then per row o / l as f32 (the
+    // merge weighs it by l). An empty share leaves l = 0 and its o
+    // unwritten.
     char* pb = (char*)part + ((uint64_t)(rest * qtiles + qt) * n_split + split) *
                                  pf_part_bytes(kPfRows, D);
 #pragma unroll
@@ -414,13 +391,12 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
       const float lt = wave_sum_g(l_run[t]);
       const uint32_t row = wave * 16 * kPfRT + 16 * t + col;
       if (g == 0) *(float2*)(pb + (uint64_t)row * 8) = make_float2(m_run[t], lt);
-      T* po = (T*)(pb + (uint64_t)kPfRows * 8) + (uint64_t)row * D;
+      float* po = (float*)(pb + (uint64_t)kPfRows * 8) + (uint64_t)row * D;
       const float sc = lt > 0.f ? 1.f / lt : 0.f;
 #pragma unroll
       for (int k = 0; k < DT; ++k)
-        *(uint2*)(po + 16 * k + 4 * g) =
-            make_uint2(pack2<T>(o[t][k][0] * sc, o[t][k][1] * sc),
-                       pack2<T>(o[t][k][2] * sc, o[t][k][3] * sc));
+        *(float4*)(po + 16 * k + 4 * g) = make_float4(o[t][k][0] * sc, o[t][k][1] * sc,
+                                                      o[t][k][2] * sc, o[t][k][3] * sc);
     }
     return;
   }
@@ -465,7 +441,7 @@ __global__ __launch_bounds__(256) void paged_prefill_merge(AttnArgs a, uint32_t 
   const uint64_t stride = pf_part_bytes(rows_per_item, D);  // per split
   const char* p0 = (const char*)part + (uint64_t)base * n_split * stride;
   const uint64_t ml_off = (uint64_t)row_in * 8;
-  const uint64_t o_off = (uint64_t)rows_per_item * 8 + ((uint64_t)row_in * D + dq) * sizeof(T);
+  const uint64_t o_off = (uint64_t)rows_per_item * 8 + ((uint64_t)row_in * D + dq) * sizeof(float);
   // Eight splits per memory round trip: every (m, l) and o load of a batch
   // is issued before any is used (loading o only after testing l serialised
   // two round trips per split), then the batch joins the running (M, L, o).
@@ -473,13 +449,13 @@ __global__ __launch_bounds__(256) void paged_prefill_merge(AttnArgs a, uint32_t 
   float M = kNegBig, L = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
   for (uint32_t s0 = 0; s0 < n_split; s0 += kB) {
     float2 ml[kB];
-    uint2 xb[kB];
+    float4 xb[kB];
 #pragma unroll
     for (uint32_t u = 0; u < kB; ++u) {
       const bool in = s0 + u < n_split;
       const char* pr = p0 + (uint64_t)(in ? s0 + u : s0) * stride;
       ml[u] = *(const float2*)(pr + ml_off);
-      xb[u] = *(const uint2*)(pr + o_off);
+      xb[u] = *(const float4*)(pr + o_off);
       if (!in) ml[u].y = 0.f;
     }
     float Mn = M;
@@ -496,9 +472,8 @@ __global__ __launch_bounds__(256) void paged_prefill_merge(AttnArgs a, uint32_t 
       const float e = fast_exp2(ml[u].x - Mn);
       const float w = ml[u].y * e;  // the partial's o is o / l
       L += w;
-      const T* h = (const T*)&xb[u];
-      o[0] += to_f32(h[0]) * w, o[1] += to_f32(h[1]) * w;
-      o[2] += to_f32(h[2]) * w, o[3] += to_f32(h[3]) * w;
+      o[0] += xb[u].x * w, o[1] += xb[u].y * w;
+      o[2] += xb[u].z * w, o[3] += xb[u].w * w;
     }
     M = Mn;
   }
@@ -508,25 +483,16 @@ __global__ __launch_bounds__(256) void paged_prefill_merge(AttnArgs a, uint32_t 
   *(uint2*)orow = make_uint2(pack2<T>(o[0] * inv, o[1] * inv), pack2<T>(o[2] * inv, o[3] * inv));
 }
 
-#ifndef VK_PF_RT
-#define VK_PF_RT 2
-#endif
-#ifndef VK_PF_OCC
-#define VK_PF_OCC 1
-#endif
-
-#ifdef VK_PF_TRACE
-__device__ uint64_t pf_trace_buf[32 * 8 * 5];
-}  // namespace vk
-extern "C" int vapi_pf_trace_copy(void* host) {
-  return hipMemcpyFromSymbol(host, HIP_SYMBOL(vk::pf_trace_buf), sizeof(vk::pf_trace_buf)) ==
-                 hipSuccess ? 0 : -3;
-}
-namespace vk {
-#endif
+// Row tiles (16 rows each) per wave, and workgroups per CU at head_dim 128.
+constexpr int kPfRowTiles = 2;
+constexpr int kPfOcc = 1;
+// head_dim 64 fits in 128 registers: two workgroups per CU (four waves per
+// SIMD) measured 1% faster than one on a config-3-shaped batch (676-678
+// against 669-673 TFLOP/s).
+constexpr int kPfOcc64 = 2;
 
 uint64_t prefill_grid(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t max_q) {
-  constexpr uint64_t rows = 16 * VK_PF_RT * kPfWaves;
+  constexpr uint64_t rows = 16 * kPfRowTiles * kPfWaves;
   return ((uint64_t)max_q * group + rows - 1) / rows * kvh * batch;
 }
 
@@ -543,7 +509,7 @@ static uint32_t pf_splits(uint64_t base, uint32_t max_k) {
 }
 
 static uint64_t pf_split_bytes(uint64_t base, uint32_t n, uint32_t head_dim) {
-  constexpr uint32_t rows = 16 * VK_PF_RT * kPfWaves;
+  constexpr uint32_t rows = 16 * kPfRowTiles * kPfWaves;
   return n > 1 ? base * n * pf_part_bytes(rows, head_dim) : 0;
 }
 
@@ -567,12 +533,7 @@ size_t prefill_split_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uint32_
 void launch_prefill(const AttnArgs& a_in, uint32_t max_q, uint32_t max_k, uint32_t head_dim,
                     bool bf16, void* split_ws, size_t split_ws_bytes, hipStream_t s) {
   AttnArgs a = a_in;
-#ifdef VK_PF_TRACE
-  void* tp = nullptr;
-  (void)hipGetSymbolAddress(&tp, HIP_SYMBOL(pf_trace_buf));
-  a.trace = (uint64_t*)tp;
-#endif
-  constexpr uint32_t rows = 16 * VK_PF_RT * kPfWaves;
+  constexpr uint32_t rows = 16 * kPfRowTiles * kPfWaves;
   const uint32_t qtiles = (uint32_t)(((uint64_t)max_q * a.group + rows - 1) / rows);
   const uint64_t base = (uint64_t)qtiles * a.kvh * a.pf_seqs_n;
   // As many splits as the workspace given holds (none without one); a
@@ -583,23 +544,17 @@ void launch_prefill(const AttnArgs& a_in, uint32_t max_q, uint32_t max_k, uint32
                                : 1;
   float* part = n_split > 1 ? (float*)split_ws : nullptr;
   const dim3 grid((uint32_t)(base * n_split)), block(kPfThreads);
-// head_dim 64 fits in 128 registers: two workgroups per CU (four waves per
-// SIMD) measured 1% faster than one on a config-3-shaped batch (676-678
-// against 669-673 TFLOP/s).
-#ifndef VK_PF_OCC64
-#define VK_PF_OCC64 2
-#endif
 #define VK_PF(T, DD)                                                                             \
   do {                                                                                           \
-    constexpr int occ = DD == 64 ? VK_PF_OCC64 : VK_PF_OCC;                                      \
+    constexpr int occ = DD == 64 ? kPfOcc64 : kPfOcc;                                      \
     if (n_split > 1) {                                                                           \
-      hipLaunchKernelGGL((paged_prefill_tiled<T, DD, VK_PF_RT, occ, true>), grid, block, 0, s, a, \
+      hipLaunchKernelGGL((paged_prefill_tiled<T, DD, kPfRowTiles, occ, true>), grid, block, 0, s, a, \
                          a.cu_q, a.cu_k, a.table, qtiles, n_split, part);                        \
       hipLaunchKernelGGL((paged_prefill_merge<T, DD>),                                           \
                          dim3((uint32_t)(base * (rows / (256 / (DD / 4))))), dim3(256), 0, s, a, \
                          qtiles, rows, n_split, part);                                           \
     } else {                                                                                     \
-      hipLaunchKernelGGL((paged_prefill_tiled<T, DD, VK_PF_RT, occ, false>), grid, block, 0, s,  \
+      hipLaunchKernelGGL((paged_prefill_tiled<T, DD, kPfRowTiles, occ, false>), grid, block, 0, s,  \
                          a, a.cu_q, a.cu_k, a.table, qtiles, 1u, nullptr);                       \
     }                                                                                            \
   } while (0)
