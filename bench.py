@@ -454,9 +454,20 @@ def bench_append(steps, warmup):
     def append():
         write_rows_indexed(cache, 0, k, v, idx)
 
-    # Host-launched calls: one Python + ctypes call per append (the host
-    # overhead is about the kernel's own duration at this size).
+    # Host-launched calls: one Python + ctypes call per append through the
+    # Python mirror (its argument checks included), and the bare C ABI call
+    # with every pointer prepared (what a compiled caller pays per call).
     ms_host, _ = timed(append, steps, warmup)
+    from vapi_amd._lib import check as _check, lib as _L
+    from vapi_amd.cache import stream_handle as _sh
+    fn, pool, sh = _L().vapi_kv_append_ex, cache.pool, _sh()
+    kp, vp, ip = k.data_ptr(), v.data_ptr(), idx.data_ptr()
+
+    def append_c():
+        fn(pool, 0, kp, vp, ip, w.n_tokens, 0, sh)
+
+    ms_host_c, _ = timed(append_c, max(steps, 50), warmup)
+    _check(fn(pool, 0, kp, vp, ip, w.n_tokens, 0, sh))
     # The same appends captured in one HIP graph and replayed, as a serving
     # step would issue its per-layer appends: per-append device time.
     ms = timed_graph(append, steps, warmup)
@@ -466,21 +477,24 @@ def bench_append(steps, warmup):
         f"({gbs:.0f} GB/s), {ms_host * 1e3:.1f} us/append host-launched")
     # Cold sources: the graph's appends rotate over 24 source sets (384 MB,
     # more than the 256 MB last-level cache), as a fresh layer's K/V rows
-    # would arrive, so the reads come from HBM.
+    # would arrive, so the reads come from HBM; with VAPI_APPEND_COLD_SOURCE
+    # (streaming loads) and without.
     n_sets = 24
     ks = torch.randn(n_sets, w.n_tokens, 8, 128, generator=g, device=DEV).to(torch.bfloat16)
     vs = torch.randn_like(ks)
     it = [0]
 
-    def append_cold():
+    def append_cold(flag):
         i = it[0] % n_sets
         it[0] += 1
-        write_rows_indexed(cache, 0, ks[i], vs[i], idx)
+        write_rows_indexed(cache, 0, ks[i], vs[i], idx, cold_source=flag)
 
-    ms_cold = timed_graph(append_cold, max(steps, n_sets), warmup)
+    ms_cold = timed_graph(lambda: append_cold(True), max(steps, n_sets), warmup)
+    ms_cold_plain = timed_graph(lambda: append_cold(False), max(steps, n_sets), warmup)
     gbs_cold = alg / (ms_cold * 1e-3) / 1e9
     log(f"append cfg1, sources rotated over {n_sets} sets: {ms_cold * 1e3:.2f} us/append "
-        f"({gbs_cold:.0f} GB/s)")
+        f"({gbs_cold:.0f} GB/s) with the cold-source flag, {ms_cold_plain * 1e3:.2f} us without; "
+        f"host-launched {ms_host_c * 1e3:.2f} us/append through the bare C ABI")
     del ks, vs
     # Ceiling for the cold leg: a trivial sequential copy of the same byte
     # count (the valid rows' K and V), its source rotated over 24 buffers the
@@ -520,9 +534,14 @@ def bench_append(steps, warmup):
                 cold_us=ms_cold * 1e3, cold_gbs=gbs_cold, cold_frac=gbs_cold / HBM_PEAK_GBS,
                 cold_frac_of_cold_copy_probe=gbs_cold / max(cold_probe["copy_seq_cold_gbs"],
                                                             cold_probe["copy_seq_cold_nt_gbs"]),
+                cold_flag="VAPI_APPEND_COLD_SOURCE (streaming source loads)",
+                cold_us_without_flag=ms_cold_plain * 1e3,
+                cold_gbs_without_flag=alg / (ms_cold_plain * 1e-3) / 1e9,
                 cold_probe=cold_probe,
                 us_host_launched=ms_host * 1e3,
                 gbs_host_launched=alg / (ms_host * 1e-3) / 1e9,
+                us_host_launched_c_abi=ms_host_c * 1e3,
+                gbs_host_launched_c_abi=alg / (ms_host_c * 1e-3) / 1e9,
                 layers4_one_launch_us=ms_l * 1e3, layers4_gbs=gbs_l)
 
 
@@ -867,6 +886,14 @@ def probes_copy(w, cache):
         ms = _probe_time(lambda: L.vapi_probe_copy(b.data_ptr(), a.data_ptr(), cbytes, nt, sh),
                          reps=10)
         out["copy_seq" + sfx + "_gbs"] = 2 * cbytes / (ms * 1e-3) / 1e9
+        # The same pairs as whole-block runs (917,504 B: every layer's K and V
+        # of a block adjacent, a block-major layout), over the pool's slab.
+        blob = run * 2 * w.num_layers
+        assert cache._slab.numel() * cache._slab.element_size() >= w.num_blocks * blob
+        bpr = torch.from_numpy(w.pairs.astype(np.uint32).reshape(-1).view(np.int32)).to(DEV)
+        ms = _probe_time(lambda: L.vapi_probe_copy_runs(cache._slab.data_ptr(), bpr.data_ptr(),
+                                                        w.pairs.shape[0], blob, nt, sh), reps=10)
+        out["copy_runs_block" + sfx + "_gbs"] = 2 * w.pairs.shape[0] * blob / (ms * 1e-3) / 1e9
     out["copy_bytes_each_way"] = cbytes
     del a, b
     log("probes (copy): " + ", ".join(f"{k} {v:.0f}" for k, v in out.items()
@@ -1145,7 +1172,15 @@ def main():
                                         "committed file, not measured in this run"),
                      "kernel": "paged_decode_stream + paged_decode_merge (one vapi_paged_attention call)"},
         "cpu_baseline": cpu,
+        # Config 1's append, three ways: replayed from a graph with its source
+        # rows warm (as a projection just wrote them), replayed with cold
+        # sources (rotated over 384 MB, read with the cold-source flag), and
+        # launched call by call from the host through the bare C ABI.
         "kv_append_gbs": round(extras["append_cfg1"]["gbs"], 1) if "append_cfg1" in extras else None,
+        "kv_append_cold_gbs": (round(extras["append_cfg1"]["cold_gbs"], 1)
+                               if "append_cfg1" in extras else None),
+        "kv_append_host_launched_gbs": (round(extras["append_cfg1"]["gbs_host_launched_c_abi"], 1)
+                                        if "append_cfg1" in extras else None),
         "extras": extras,
     }
     print(json.dumps(line), flush=True)

@@ -131,6 +131,20 @@ int vapi_kv_append(const vapi_kv_pool* pool, uint32_t layer, const void* k_src,
                    uint32_t n_tokens, vapi_stream_t stream);
 
 /*
+ * vapi_kv_append with flags. VAPI_APPEND_COLD_SOURCE: the source rows are
+ * not expected in the GPU's caches (rows read back from host memory or
+ * written long before, not just produced by a projection kernel), so they
+ * are read with streaming (non-temporal) loads that do not allocate in the
+ * last-level cache; a warm source is read slower that way. Same result
+ * either way. No counterpart flag in the reference (write_kv_to_cache,
+ * cache.rs:136-148, has one path).
+ */
+#define VAPI_APPEND_COLD_SOURCE 1u
+int vapi_kv_append_ex(const vapi_kv_pool* pool, uint32_t layer, const void* k_src,
+                      const void* v_src, const uint32_t* slot_mapping, uint32_t n_tokens,
+                      uint32_t flags, vapi_stream_t stream);
+
+/*
  * The same append over layers layer0 .. layer0 + n_layers - 1 in one launch
  * (one slot_mapping for all of them): layer l's rows are at k_src/v_src +
  * (l - layer0) * src_layer_stride bytes, each [n_tokens, num_kv_heads,

@@ -47,6 +47,9 @@ def test_bad_arguments_are_errors_not_crashes():
     assert L.vapi_kv_append(pool(), 1, 1, 1, 1, 1, None) == _lib.EINVAL
     assert L.vapi_kv_append(pool(), 0, None, 1, 1, 1, None) == _lib.EINVAL
     assert L.vapi_kv_append(pool(), 0, 1, 1, 1, 0, None) == _lib.OK  # nothing to do
+    assert L.vapi_kv_append_ex(pool(), 0, 1, 1, 1, 0, _lib.APPEND_COLD_SOURCE, None) == _lib.OK
+    assert L.vapi_kv_append_ex(pool(), 0, 1, 1, 1, 1, 0x2, None) == _lib.EINVAL
+    assert b"flags" in L.vapi_kv_last_error()
     assert L.vapi_kv_gather(pool(), 0, 1, 2, 33, 1, 1, None) == _lib.EINVAL
     assert b"exceeds" in L.vapi_kv_last_error()
     args = [1, 1, 1, 1, 1, 2, 4, 1, 100, 5, 0.1, -1, 0, None, 0, None]

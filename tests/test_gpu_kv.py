@@ -108,6 +108,34 @@ def test_append_matches_the_oracle_bit_exactly(layout, dtype, kvh, d):
 
 
 @pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("dtype,kvh,d", [(torch.bfloat16, 8, 128), (torch.float16, 2, 64),
+                                         (torch.float32, 3, 5)])
+def test_a_cold_source_append_writes_the_same_bytes(layout, dtype, kvh, d):
+    """VAPI_APPEND_COLD_SOURCE (streaming loads of the source rows) against
+    the oracle's scatter, padded and past-the-pool slots included."""
+    from vapi_amd.cache import write_rows_indexed
+    rng = np.random.default_rng(13)
+    bs, nb, n = 16, 64, 333
+    c = PagedKvCache(1, nb, bs, kvh, d, dtype, layout)
+    c._slab.copy_(torch.randn(c._slab.shape, device=DEV).to(dtype))
+    slots = rng.permutation(nb * bs)[:n].astype(np.uint32)
+    slots[rng.choice(n, 17, replace=False)] = _lib.SLOT_SKIP
+    slots[5] = nb * bs + 1
+    k = torch.randn(n, kvh, d, device=DEV).to(dtype)
+    v = torch.randn(n, kvh, d, device=DEV).to(dtype)
+    dropped = slots.copy()
+    dropped[5] = _lib.SLOT_SKIP
+    want_k, want_v = as_np(ref_pool(c, 0, "k")), as_np(ref_pool(c, 0, "v"))
+    oracle.write_rows(want_k, as_np(k), dropped)
+    oracle.write_rows(want_v, as_np(v), dropped)
+    write_rows_indexed(c, 0, k, v, torch.from_numpy(slots.view(np.int32)).to(DEV),
+                       cold_source=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(as_np(ref_pool(c, 0, "k")), want_k)
+    np.testing.assert_array_equal(as_np(ref_pool(c, 0, "v")), want_v)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
 @pytest.mark.parametrize("dtype,kvh,d", [(torch.bfloat16, 8, 128), (torch.float32, 3, 5)])
 def test_a_multi_layer_append_is_one_append_per_layer(layout, dtype, kvh, d):
     """vapi_kv_append_layers over layers 1..3 of a 4-layer pool, the rows of

@@ -18,11 +18,12 @@ SLOT_SKIP = 0xFFFFFFFF
 OK, EINVAL, EUNSUP, EHIP, ESPACE = 0, -1, -2, -3, -4
 ATTN_DETERMINISTIC, ATTN_NO_DECODE_ROWS = 0x1, 0x2
 ATTN_SCRATCH_BYTES = 16 << 20  # VAPI_ATTN_SCRATCH_BYTES
+APPEND_COLD_SOURCE = 0x1  # VAPI_APPEND_COLD_SOURCE
 
 # Every symbol include/vapi_kv.h declares.
 EXPORTS = (
     "vapi_kv_last_error", "vapi_kv_version", "vapi_kv_block_bytes",
-    "vapi_kv_layer_bytes", "vapi_kv_append", "vapi_kv_gather",
+    "vapi_kv_layer_bytes", "vapi_kv_append", "vapi_kv_append_ex", "vapi_kv_gather",
     "vapi_paged_attention_workspace_size", "vapi_paged_attention",
     "vapi_paged_attention_append", "vapi_kv_append_layers",
     "vapi_kv_copy_blocks", "vapi_kv_export_blocks", "vapi_kv_import_blocks",
@@ -96,6 +97,7 @@ def lib():
     L.vapi_kv_layer_bytes.argtypes = [_poolp]
     L.vapi_kv_layer_bytes.restype = _sz
     L.vapi_kv_append.argtypes = [_poolp, _u32, _vp, _vp, _vp, _u32, _vp]
+    L.vapi_kv_append_ex.argtypes = [_poolp, _u32, _vp, _vp, _vp, _u32, _u32, _vp]
     L.vapi_kv_gather.argtypes = [_poolp, _u32, _vp, _u32, _u32, _vp, _vp, _vp]
     L.vapi_paged_attention_workspace_size.argtypes = [_poolp, _u32, _u32, _u32, _u32]
     L.vapi_paged_attention_workspace_size.restype = _sz

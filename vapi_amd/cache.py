@@ -17,7 +17,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import Pool, check, lib
+from ._lib import APPEND_COLD_SOURCE, Pool, check, lib
 
 _DTYPES = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}
 _LAYOUTS = {"HND": _lib.LAYOUT_HND, "NHD": _lib.LAYOUT_NHD}
@@ -283,11 +283,12 @@ def scatter_index(slot_mapping, device) -> torch.Tensor:
 
 
 def write_rows_indexed(cache, layer: int, k: torch.Tensor, v: torch.Tensor | None,
-                       idx: torch.Tensor, stream=None) -> None:
+                       idx: torch.Tensor, stream=None, cold_source: bool = False) -> None:
     """Append with a prebuilt device slot index (cache.rs:178-215): one
     launch for K and V, or for K alone when v is None (the reference's
     write_rows_indexed, cache.rs:176-185). Out-of-range slots are dropped
-    on the device."""
+    on the device. cold_source: the rows are not in the GPU's caches (read
+    with streaming loads, VAPI_APPEND_COLD_SOURCE); same result."""
     cache, layer = _per_layer(cache, layer)
     if idx.dim() != 1 or idx.shape[0] != k.shape[0]:
         raise ValueError(f"scatter index {tuple(idx.shape)} does not match rows "
@@ -300,8 +301,10 @@ def write_rows_indexed(cache, layer: int, k: torch.Tensor, v: torch.Tensor | Non
                                    idx.data_ptr(), k.shape[0], stream_handle(stream)))
         return
     v = v.contiguous()
-    check(lib().vapi_kv_append(cache.pool, layer, k.data_ptr(), v.data_ptr(),
-                               idx.data_ptr(), k.shape[0], stream_handle(stream)))
+    check(lib().vapi_kv_append_ex(cache.pool, layer, k.data_ptr(), v.data_ptr(),
+                                  idx.data_ptr(), k.shape[0],
+                                  APPEND_COLD_SOURCE if cold_source else 0,
+                                  stream_handle(stream)))
 
 
 def write_v_rows_indexed(cache, layer: int, v: torch.Tensor, idx: torch.Tensor,

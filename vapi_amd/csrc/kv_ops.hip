@@ -97,7 +97,7 @@ struct AppendArgs {
   uint64_t src_layer_b, dst_layer_b;  // layer strides (grid y = layer)
 };
 
-template <int C, int ITEMS, bool kStream, bool kKV>
+template <int C, int ITEMS, bool kStream, bool kKV, bool kLoadNT = false>
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   using V = typename Chunk<C>::T;
   // Layer blockIdx.y of a multi-layer append (0 for one layer).
@@ -124,7 +124,8 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
       // does not depend on the slot), so one memory round trip precedes the
       // store.
       const uint64_t src_off = ((uint64_t)t * a.kvh.d + h) * a.row_bytes + (uint64_t)u * C;
-      val[j] = *(const V*)((kv ? a.v_src : a.k_src) + src_off);
+      const V* sp = (const V*)((kv ? a.v_src : a.k_src) + src_off);
+      val[j] = kLoadNT ? load_stream(sp) : *sp;
       const uint32_t slot = a.slots[t];
       if (slot < a.num_slots) {  // VAPI_KV_SLOT_SKIP and out-of-range drop
         const uint32_t blk = a.bs.div(slot);
@@ -152,7 +153,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
 // them. A multi-layer append already has layers times that grid and keeps
 // one chunk per thread (4 layers: 21.2 us against 29.5 us with two).
 template <int C>
-static void launch_append(const AppendArgs& a, uint32_t layers, hipStream_t s) {
+static void launch_append(const AppendArgs& a, uint32_t layers, uint32_t flags, hipStream_t s) {
   if (!a.has_v) {
     const uint32_t grid = (a.total + 255) / 256;
     hipLaunchKernelGGL((kv_append_kernel<C, 1, false, false>), dim3(grid, layers), dim3(256),
@@ -160,7 +161,18 @@ static void launch_append(const AppendArgs& a, uint32_t layers, hipStream_t s) {
   } else if (layers == 1) {
     constexpr int ITEMS = 2;
     const uint32_t grid = (a.total + 256 * ITEMS - 1) / (256 * ITEMS);
-    hipLaunchKernelGGL((kv_append_kernel<C, ITEMS, true, true>), dim3(grid), dim3(256), 0, s, a);
+    // A cold source (VAPI_APPEND_COLD_SOURCE) is read with streaming loads:
+    // config 1 with its sources rotated over 384 MB, graph replays, two
+    // boxes: 7.1-7.5 against 7.9-8.1 us; with a warm source they cost
+    // 5.2-7.2 against 4.5-4.6 us. Ordinary stores with the streaming loads
+    // measured the same cold and slower warm; 1 or 4 chunks per thread, and
+    // lanes walking four tokens of one tile instead of four heads of one
+    // token, slower.
+    if (flags & VAPI_APPEND_COLD_SOURCE)
+      hipLaunchKernelGGL((kv_append_kernel<C, ITEMS, true, true, true>), dim3(grid), dim3(256), 0,
+                         s, a);
+    else
+      hipLaunchKernelGGL((kv_append_kernel<C, ITEMS, true, true>), dim3(grid), dim3(256), 0, s, a);
   } else {
     const uint32_t grid = (a.total + 255) / 256;
     hipLaunchKernelGGL((kv_append_kernel<C, 1, false, true>), dim3(grid, layers), dim3(256),
@@ -373,8 +385,10 @@ size_t vapi_kv_layer_bytes(const vapi_kv_pool* p) {
 static int append_impl(const char* who, const vapi_kv_pool* pool, uint32_t layer0,
                        uint32_t n_layers, const void* k_src, const void* v_src,
                        uint64_t src_layer_stride, const uint32_t* slot_mapping,
-                       uint32_t n_tokens, vapi_stream_t stream) {
+                       uint32_t n_tokens, uint32_t flags, vapi_stream_t stream) {
   if (int rc = check_pool(pool, who)) return rc;
+  if (flags & ~VAPI_APPEND_COLD_SOURCE)
+    VK_FAIL(VAPI_KV_EINVAL, "%s: unknown flags %#x", who, flags);
   if (n_layers == 0 || layer0 >= pool->num_layers || n_layers > pool->num_layers - layer0)
     VK_FAIL(VAPI_KV_EINVAL, "%s: layers %u..%u of %u", who, layer0, layer0 + n_layers,
             pool->num_layers);
@@ -419,7 +433,7 @@ static int append_impl(const char* who, const vapi_kv_pool* pool, uint32_t layer
   a.tok_b = g.tok * elt;
   a.src_layer_b = n_layers > 1 ? src_layer_stride : 0;
   a.dst_layer_b = n_layers > 1 ? pool->layer_stride_bytes : 0;
-#define L_APPEND(C) launch_append<C>(a, n_layers, hs(stream))
+#define L_APPEND(C) launch_append<C>(a, n_layers, flags, hs(stream))
   VK_DISPATCH_CHUNK(c, L_APPEND)
 #undef L_APPEND
   VK_LAUNCHED("kv_append");
@@ -430,7 +444,14 @@ int vapi_kv_append(const vapi_kv_pool* pool, uint32_t layer, const void* k_src,
                    const void* v_src, const uint32_t* slot_mapping,
                    uint32_t n_tokens, vapi_stream_t stream) {
   return append_impl("vapi_kv_append", pool, layer, 1, k_src, v_src, 0, slot_mapping,
-                     n_tokens, stream);
+                     n_tokens, 0, stream);
+}
+
+int vapi_kv_append_ex(const vapi_kv_pool* pool, uint32_t layer, const void* k_src,
+                      const void* v_src, const uint32_t* slot_mapping, uint32_t n_tokens,
+                      uint32_t flags, vapi_stream_t stream) {
+  return append_impl("vapi_kv_append_ex", pool, layer, 1, k_src, v_src, 0, slot_mapping,
+                     n_tokens, flags, stream);
 }
 
 int vapi_kv_append_layers(const vapi_kv_pool* pool, uint32_t layer0, uint32_t n_layers,
@@ -438,7 +459,7 @@ int vapi_kv_append_layers(const vapi_kv_pool* pool, uint32_t layer0, uint32_t n_
                           const uint32_t* slot_mapping, uint32_t n_tokens,
                           vapi_stream_t stream) {
   return append_impl("vapi_kv_append_layers", pool, layer0, n_layers, k_src, v_src,
-                     src_layer_stride, slot_mapping, n_tokens, stream);
+                     src_layer_stride, slot_mapping, n_tokens, 0, stream);
 }
 
 int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,

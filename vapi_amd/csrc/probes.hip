@@ -97,16 +97,18 @@ __global__ __launch_bounds__(kThreads) void probe_copy_kernel(uint4* __restrict_
   }
 }
 
-// One workgroup per run: run_bytes / 4096 chunks of 16 B per thread.
+// One workgroup per 16 KiB piece of a run (runs of `pieces` pieces):
+// 16 KiB / 4096 chunks of 16 B per thread.
 template <int ITEMS, bool NT>
 __global__ __launch_bounds__(kThreads) void probe_runs_kernel(char* __restrict__ base,
                                                               const uint32_t* __restrict__ pairs,
-                                                              uint32_t n_runs) {
-  const uint32_t r = blockIdx.x;
+                                                              uint32_t n_runs, uint32_t pieces) {
+  const uint32_t r = blockIdx.x / pieces, pc = blockIdx.x % pieces;
   if (r >= n_runs) return;
-  constexpr uint64_t kRun = ITEMS * kThreads * 16ull;
-  const uint4* s = (const uint4*)(base + (uint64_t)pairs[2 * r] * kRun);
-  uint4* d = (uint4*)(base + (uint64_t)pairs[2 * r + 1] * kRun);
+  constexpr uint64_t kPiece = ITEMS * kThreads * 16ull;
+  const uint64_t run = kPiece * pieces;
+  const uint4* s = (const uint4*)(base + (uint64_t)pairs[2 * r] * run + pc * kPiece);
+  uint4* d = (uint4*)(base + (uint64_t)pairs[2 * r + 1] * run + pc * kPiece);
   uint4 v[ITEMS];
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) v[i] = ld<NT>(s + i * kThreads + threadIdx.x);
@@ -172,17 +174,20 @@ int vapi_probe_copy(void* dst, const void* src, uint64_t bytes, uint32_t streami
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
-// Copies n_runs runs of run_bytes (16384) from base + pairs[2i] * run_bytes
-// to base + pairs[2i + 1] * run_bytes (pairs: device u32[n_runs][2]).
+// Copies n_runs runs of run_bytes (a multiple of 16384) from base +
+// pairs[2i] * run_bytes to base + pairs[2i + 1] * run_bytes (pairs: device
+// u32[n_runs][2]), one workgroup per 16 KiB.
 int vapi_probe_copy_runs(void* base, const uint32_t* pairs, uint32_t n_runs, uint32_t run_bytes,
                          uint32_t streaming, hipStream_t stream) {
-  if (run_bytes != 16384) return -1;
+  if (run_bytes == 0 || run_bytes % 16384) return -1;
+  const uint32_t pieces = run_bytes / 16384;
+  if ((uint64_t)n_runs * pieces >= (1ull << 31)) return -1;
   if (streaming)
-    hipLaunchKernelGGL((probe_runs_kernel<4, true>), dim3(n_runs), dim3(kThreads), 0, stream,
-                       (char*)base, pairs, n_runs);
+    hipLaunchKernelGGL((probe_runs_kernel<4, true>), dim3(n_runs * pieces), dim3(kThreads), 0,
+                       stream, (char*)base, pairs, n_runs, pieces);
   else
-    hipLaunchKernelGGL((probe_runs_kernel<4, false>), dim3(n_runs), dim3(kThreads), 0, stream,
-                       (char*)base, pairs, n_runs);
+    hipLaunchKernelGGL((probe_runs_kernel<4, false>), dim3(n_runs * pieces), dim3(kThreads), 0,
+                       stream, (char*)base, pairs, n_runs, pieces);
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
