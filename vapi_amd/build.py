@@ -51,18 +51,19 @@ EXTRA_FLAGS = {"attn_decode.hip": ["-fno-honor-nans", "-Rpass-analysis=kernel-re
 # publishes its partials after an explicit vmcnt(0); a register spill would
 # add scratch traffic to those counts (and slow the stream), so a build
 # whose attention kernels use scratch is refused.
-NO_SCRATCH = {"attn_prefill.hip": "paged_prefill_tiled", "attn_decode.hip": "paged_decode_stream"}
+NO_SCRATCH = {"attn_prefill.hip": ("paged_prefill_tiled", "paged_mixed_stream"),
+              "attn_decode.hip": ("paged_decode_stream",)}
 
 
 def _check_no_scratch(src: Path, remarks: str) -> None:
-    kernel = NO_SCRATCH.get(src.name)
-    if not kernel:
+    kernels = NO_SCRATCH.get(src.name)
+    if not kernels:
         return
     current = None
     for line in remarks.splitlines():
         if "Function Name:" in line:
             current = line.split("Function Name:")[1].split()[0]
-        elif "ScratchSize" in line and current and kernel in current:
+        elif "ScratchSize" in line and current and any(k in current for k in kernels):
             size = int(line.split("ScratchSize [bytes/lane]:")[1].split()[0])
             if size != 0:
                 raise RuntimeError(f"{current} uses {size} bytes of scratch per lane; its "

@@ -380,14 +380,26 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   if (mfma_ok(pool, num_heads)) {
     const bool bf16 = pool->dtype == VAPI_KV_BF16;
     a.num_waves = decode_num_waves();
+    const size_t off = std::max<size_t>((need + 255) & ~(size_t)255, 256);
+    const bool room = workspace && workspace_bytes > off;
+    // Decode rows and prefill rows in one step: both kernels in one launch.
+    const bool mixed = !skip_decode && !fuse && max_seqlen_q > 1 && pf_n > 0 &&
+                       batch <= decode_max_plan_seqs() &&
+                       mixed_prefill_items(pf_n, g.kvh, num_heads / g.kvh, max_seqlen_q) <
+                           (1ull << 30);
+    if (mixed) {
+      a.num_waves = decode_num_waves();
+      launch_mixed(a, workspace, max_seqlen_q, max_seqlen_k, g.d, bf16,
+                   room ? (char*)workspace + off : nullptr, room ? workspace_bytes - off : 0, s);
+      VK_LAUNCHED("paged_attention");
+      return 0;
+    }
     if (skip_decode) a.pf_min_q = 1;
     else launch_decode(a, workspace, g.d, bf16, s);
     if (max_seqlen_q > 1 && pf_n > 0) {
       // The workspace past the decode's part serves the prefill's key split
       // (never its first 256 bytes, which carry the decode's XCD shares
       // from call to call).
-      const size_t off = std::max<size_t>((need + 255) & ~(size_t)255, 256);
-      const bool room = workspace && workspace_bytes > off;
       launch_prefill(a, max_seqlen_q, max_seqlen_k, g.d, bf16,
                      room ? (char*)workspace + off : nullptr, room ? workspace_bytes - off : 0, s);
     }

@@ -427,6 +427,17 @@ uint64_t prefill_grid(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t max
 // small to fill the GPU splits its keys over more workgroups.
 void launch_prefill(const AttnArgs& a, uint32_t max_q, uint32_t max_k, uint32_t head_dim,
                     bool bf16, void* split_ws, size_t split_ws_bytes, hipStream_t s);
+// A step with decode rows and prefill rows (at most kMaxPlanSeqs sequences,
+// no fused append) in one launch of both kernels' workgroups side by side,
+// then the decode's merge and, when the prefill split its keys, the
+// prefill's merge. `workspace` is the decode's; split_ws the prefill's part.
+void launch_mixed(const AttnArgs& a, void* workspace, uint32_t max_q, uint32_t max_k,
+                  uint32_t head_dim, bool bf16, void* split_ws, size_t split_ws_bytes,
+                  hipStream_t s);
+// Prefill workgroups (before any key split) of a mixed launch.
+uint64_t mixed_prefill_items(uint32_t n_seqs, uint32_t kvh, uint32_t group, uint32_t max_q);
+// Sequences one decode launch plans for (larger batches are cut into launches).
+uint32_t decode_max_plan_seqs();
 // Workspace the prefill's key split wants for this shape (0: no split).
 size_t prefill_split_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t head_dim,
                            uint32_t max_q, uint32_t max_k);

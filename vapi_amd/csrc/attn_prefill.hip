@@ -17,6 +17,7 @@
 #include <type_traits>
 
 #include "attn_common.hpp"
+#include "attn_decode.hpp"
 
 namespace vk {
 
@@ -74,11 +75,12 @@ __device__ __forceinline__ uint32_t pf_chunk(uint32_t r, uint32_t p) {
   return (r * CPR + (p ^ pf_swz<D>(r))) * 8;
 }
 
-// Issues the step at s0 into buffer b: each thread moves one 16-byte chunk
-// of K and one of V (D = 128), or one of K or V (D = 64: waves 0-3 K,
-// waves 4-7 V). LDS slot t of a tensor holds the chunk its swizzled
+// Issues the step at s0 into buffer b with W waves (8, or 4 in the mixed
+// launch): each thread moves 8 / W 16-byte chunks of K and as many of V
+// (D = 128), or with 8 waves one of K or V (D = 64: waves 0-3 K, waves 4-7
+// V), with 4 waves one of each. LDS slot t of a tensor holds the chunk its swizzled
 // position names; a wave's 64 slots are contiguous, as the load writes them.
-template <typename T, int D>
+template <typename T, int D, int W>
 __device__ __forceinline__ void pf_dma(uint16_t* kdst, uint16_t* vdst, const uint32_t* __restrict__ tab,
                                        const T* kb, const T* vb, const AttnArgs& a, int32_t s0,
                                        int32_t last, uint32_t tid, uint32_t wave) {
@@ -104,11 +106,17 @@ __device__ __forceinline__ void pf_dma(uint16_t* kdst, uint16_t* vdst, const uin
                                      (LdsVoid*)(buf + wslot0 * 8), 16, 0, 0);
   };
   if constexpr (D == 128) {
-    one(kb, kdst, tid, 64 * wave);
-    one(vb, vdst, tid, 64 * wave);
-  } else {
+#pragma unroll
+    for (int j = 0; j < 8 / W; ++j) {
+      one(kb, kdst, tid + 64 * W * j, 64 * wave + 64 * W * j);
+      one(vb, vdst, tid + 64 * W * j, 64 * wave + 64 * W * j);
+    }
+  } else if constexpr (W == 8) {
     if (wave < 4) one(kb, kdst, tid, 64 * wave);
     else one(vb, vdst, tid - 256, 64 * (wave - 4));
+  } else {
+    one(kb, kdst, tid, 64 * wave);
+    one(vb, vdst, tid, 64 * wave);
   }
 }
 
@@ -163,19 +171,21 @@ __host__ __device__ constexpr uint64_t pf_part_bytes(uint32_t rows, uint32_t d) 
 // contiguous runs of steps, one workgroup each (a batch too small to fill
 // the GPU with query tiles alone); each writes its rows' (m, l, o) to
 // `part` and paged_prefill_merge combines them.
-template <typename T, int D, int RT, int OCC, bool kSplit>
-__global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
-    AttnArgs a, const uint32_t* __restrict__ cu_q, const uint32_t* __restrict__ cu_k,
+// Workgroup `bid` of `n_items` (W waves) of a prefill launch.
+template <typename T, int D, int RT, int W, bool kSplit>
+__device__ __forceinline__ void prefill_body(
+    const AttnArgs& a, const uint32_t* __restrict__ cu_q, const uint32_t* __restrict__ cu_k,
     const uint32_t* __restrict__ table, uint32_t qtiles, uint32_t n_split_arg,
-    float* __restrict__ part) {
+    float* __restrict__ part, uint32_t bid, uint32_t n_items) {
   // The unsplit launch compiles without the split's arithmetic.
   const uint32_t n_split = kSplit ? n_split_arg : 1u;
-  static_assert(kPfWaves == 8, "the step's K and V are 8 waves' loads");
+  static_assert(W == 8 || W == 4, "a step's K and V are loaded by 8 or 4 waves");
   constexpr int KC = D / 32;
   constexpr int DT = D / 16;  // 16-column d tiles
   constexpr int kPfRT = RT;
-  constexpr uint32_t kPfRows = 16 * RT * kPfWaves;
-  constexpr int kLoadsPerStep = D == 128 ? 2 : 1;
+  constexpr uint32_t kPfRows = 16 * RT * W;
+  // Direct loads per thread per step (the ring's vmcnt waits count them).
+  constexpr int kLoadsPerStep = W == 8 ? (D == 128 ? 2 : 1) : (D == 128 ? 4 : 2);
   // The ring's three buffers per tensor are separate LDS objects, each
   // named by a compile-time index where it is used: the compiler's wait
   // insertion then knows that a direct load into one buffer cannot alias
@@ -183,8 +193,7 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
   // every LDS read.
   __shared__ __attribute__((aligned(16))) uint16_t k0[32 * D], k1[32 * D], k2[32 * D];
   __shared__ __attribute__((aligned(16))) uint16_t v0[32 * D], v1[32 * D], v2[32 * D];
-  const uint32_t n_items = gridDim.x;
-  const uint32_t item = xcd_remap(blockIdx.x, n_items);
+  const uint32_t item = xcd_remap(bid, n_items);
   // Item order: query tile fastest, then key split, kv head, sequence (the
   // q-tiles of one split read the same K/V and run on one XCD).
   const uint32_t qt = item % qtiles, rest_s = item / qtiles;
@@ -276,8 +285,8 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
   int32_t s0_ = klo & ~31;
   const int32_t s_last = khi & ~31;
   if (!kSplit || s0_ <= khi) {  // (uniform) an empty key split issues no loads
-    pf_dma<T, D>(k0, v0, tab, kb, vb, a, s0_, last, tid, wave);
-    pf_dma<T, D>(k1, v1, tab, kb, vb, a, min(s0_ + 32, s_last), last, tid, wave);
+    pf_dma<T, D, W>(k0, v0, tab, kb, vb, a, s0_, last, tid, wave);
+    pf_dma<T, D, W>(k1, v1, tab, kb, vb, a, min(s0_ + 32, s_last), last, tid, wave);
     wait_vmcnt<kLoadsPerStep>();
     ring_barrier();
   }
@@ -289,7 +298,7 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
     uint16_t* const knext = B == 0 ? k2 : B == 1 ? k0 : k1;
     uint16_t* const vnext = B == 0 ? v2 : B == 1 ? v0 : v1;
     const int32_t s0 = __builtin_amdgcn_readfirstlane(s0_);
-    pf_dma<T, D>(knext, vnext, tab, kb, vb, a, min(s0 + 64, s_last), last, tid, wave);
+    pf_dma<T, D, W>(knext, vnext, tab, kb, vb, a, min(s0 + 64, s_last), last, tid, wave);
     // Steps inside [full_lo, full_hi] need no mask (a uniform branch).
     const bool masked = !(s0 >= full_lo && s0 + 31 <= full_hi);
     KTile<D> kt;
@@ -416,18 +425,27 @@ __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
   }
 }
 
+template <typename T, int D, int RT, int OCC, bool kSplit>
+__global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
+    AttnArgs a, const uint32_t* __restrict__ cu_q, const uint32_t* __restrict__ cu_k,
+    const uint32_t* __restrict__ table, uint32_t qtiles, uint32_t n_split_arg,
+    float* __restrict__ part) {
+  prefill_body<T, D, RT, kPfWaves, kSplit>(a, cu_q, cu_k, table, qtiles, n_split_arg, part,
+                                           blockIdx.x, gridDim.x);
+}
+
 // Combines the key splits' partials of a prefill launch: thread (row, four
 // consecutive d) over the splits, in split order.
 template <typename T, int D>
-__global__ __launch_bounds__(256) void paged_prefill_merge(AttnArgs a, uint32_t qtiles,
-                                                           uint32_t rows_per_item,
-                                                           uint32_t n_split,
-                                                           const float* __restrict__ part) {
+__device__ __forceinline__ void prefill_merge_body(const AttnArgs& a, uint32_t qtiles,
+                                                   uint32_t rows_per_item, uint32_t n_split,
+                                                   const float* __restrict__ part,
+                                                   uint32_t bid) {
   constexpr uint32_t kTpr = D / 4;           // threads per row
   constexpr uint32_t kRpw = 256 / kTpr;      // rows per workgroup
   const uint32_t blocks_per_item = rows_per_item / kRpw;
-  const uint32_t base = blockIdx.x / blocks_per_item;
-  const uint32_t row_in = (blockIdx.x % blocks_per_item) * kRpw + threadIdx.x / kTpr;
+  const uint32_t base = bid / blocks_per_item;
+  const uint32_t row_in = (bid % blocks_per_item) * kRpw + threadIdx.x / kTpr;
   const uint32_t dq = (threadIdx.x % kTpr) * 4;
   const uint32_t qt = base % qtiles, rest = base / qtiles;
   const uint32_t kh = rest % a.kvh;
@@ -483,6 +501,14 @@ __global__ __launch_bounds__(256) void paged_prefill_merge(AttnArgs a, uint32_t 
   *(uint2*)orow = make_uint2(pack2<T>(o[0] * inv, o[1] * inv), pack2<T>(o[2] * inv, o[3] * inv));
 }
 
+template <typename T, int D>
+__global__ __launch_bounds__(256) void paged_prefill_merge(AttnArgs a, uint32_t qtiles,
+                                                           uint32_t rows_per_item,
+                                                           uint32_t n_split,
+                                                           const float* __restrict__ part) {
+  prefill_merge_body<T, D>(a, qtiles, rows_per_item, n_split, part, blockIdx.x);
+}
+
 // Row tiles (16 rows each) per wave, and workgroups per CU at head_dim 128.
 constexpr int kPfRowTiles = 2;
 constexpr int kPfOcc = 1;
@@ -508,8 +534,8 @@ static uint32_t pf_splits(uint64_t base, uint32_t max_k) {
   return (uint32_t)std::min<uint64_t>(n, 64);
 }
 
-static uint64_t pf_split_bytes(uint64_t base, uint32_t n, uint32_t head_dim) {
-  constexpr uint32_t rows = 16 * kPfRowTiles * kPfWaves;
+static uint64_t pf_split_bytes(uint64_t base, uint32_t n, uint32_t head_dim,
+                               uint32_t rows = 16 * kPfRowTiles * kPfWaves) {
   return n > 1 ? base * n * pf_part_bytes(rows, head_dim) : 0;
 }
 
@@ -517,10 +543,112 @@ static uint64_t pf_split_bytes(uint64_t base, uint32_t n, uint32_t head_dim) {
 constexpr uint64_t kPfSplitMaxBytes = 256ull << 20;
 
 static uint32_t pf_splits_within(uint64_t base, uint32_t max_k, uint32_t head_dim,
-                                 uint64_t bytes) {
+                                 uint64_t bytes, uint32_t rows = 16 * kPfRowTiles * kPfWaves) {
   uint32_t n = pf_splits(base, max_k);
-  while (n > 1 && pf_split_bytes(base, n, head_dim) > std::min(bytes, kPfSplitMaxBytes)) --n;
+  while (n > 1 && pf_split_bytes(base, n, head_dim, rows) > std::min(bytes, kPfSplitMaxBytes))
+    --n;
   return n;
+}
+
+// ---- a mixed step in one launch ---------------------------------------------
+//
+// A step with decode rows and prefill chunks: workgroups 0 .. nwg - 1 are
+// the decode's persistent stream (one per CU, workgroup b on XCD b % 8, as
+// in paged_decode_stream), the rest run the prefill with 4 waves each (128
+// rows). Each kind uses at most 256 registers per lane and 64 KiB of LDS,
+// so a CU holds a decode workgroup and a prefill workgroup side by side:
+// the HBM-bound decode wave and the MFMA-bound prefill wave of each SIMD
+// overlap instead of running one launch after the other.
+constexpr int kMixRowTiles = 2;
+constexpr int kMixPfWaves = 4;
+constexpr uint32_t kMixRows = 16 * kMixRowTiles * kMixPfWaves;
+
+template <typename T, int D, bool kSplit>
+__global__ __launch_bounds__(256, 2) void paged_mixed_stream(AttnArgs a, uint32_t nwg,
+                                                             uint32_t qtiles, uint32_t n_split,
+                                                             float* __restrict__ part) {
+  static_assert(64 * kDecodeWavesPerWG == 256 && 64 * kMixPfWaves == 256, "256 threads");
+  extern __shared__ uint32_t P[];
+  if (blockIdx.x < nwg)
+    decode_stream_body<T, D, false>(a, a.cu_q, a.cu_k, a.table, P, blockIdx.x, nwg);
+  else {
+    prefill_body<T, D, kMixRowTiles, kMixPfWaves, kSplit>(a, a.cu_q, a.cu_k, a.table, qtiles,
+                                                          n_split, part, blockIdx.x - nwg,
+                                                          gridDim.x - nwg);
+  }
+}
+
+// The mixed step's merges in one launch: the decode's (workgroups 0 ..
+// merge_wgs - 1) and the prefill key split's (the rest).
+template <typename T, int D, int WPS>
+__global__ __launch_bounds__(256) void paged_mixed_merge(AttnArgs a, uint32_t nwg,
+                                                         uint32_t merge_wgs, uint32_t qtiles,
+                                                         uint32_t n_split,
+                                                         const float* __restrict__ part) {
+  if (blockIdx.x < merge_wgs)
+    decode_merge_body<T, D, false, WPS>(a, nwg, merge_wgs, blockIdx.x, merge_wgs);
+  else
+    prefill_merge_body<T, D>(a, qtiles, kMixRows, n_split, part, blockIdx.x - merge_wgs);
+}
+
+uint64_t mixed_prefill_items(uint32_t n_seqs, uint32_t kvh, uint32_t group, uint32_t max_q) {
+  return ((uint64_t)max_q * group + kMixRows - 1) / kMixRows * kvh * n_seqs;
+}
+
+void launch_mixed(const AttnArgs& a_in, void* workspace, uint32_t max_q, uint32_t max_k,
+                  uint32_t head_dim, bool bf16, void* split_ws, size_t split_ws_bytes,
+                  hipStream_t s) {
+  AttnArgs c = a_in;
+  decode_bind(c, workspace, head_dim);
+  const uint32_t nwg = c.num_waves / kDecodeWavesPerWG;
+  const uint32_t qtiles = (uint32_t)(((uint64_t)max_q * c.group + kMixRows - 1) / kMixRows);
+  const uint64_t base = (uint64_t)qtiles * c.kvh * c.pf_seqs_n;
+  // The prefill workgroups run beside the decode's, one per CU: as many key
+  // splits as keep them within one round of the GPU's CUs (a second round
+  // starts late and ends late: config 2's pool with 63 decode rows and a
+  // 512-token chunk, 128 items, took 145 us per step with 2 splits, 151
+  // with 1, 167 with 3 or 4).
+  uint32_t n_split = 1;
+  if (split_ws && !c.deterministic && base > 0 && base < nwg) {
+    n_split = std::min<uint32_t>((uint32_t)(nwg / base), std::max<uint32_t>(1u, max_k / 256));
+    n_split = std::min<uint32_t>(n_split, 64);
+    while (n_split > 1 && pf_split_bytes(base, n_split, head_dim, kMixRows) >
+                              std::min<uint64_t>(split_ws_bytes, kPfSplitMaxBytes))
+      --n_split;
+  }
+  float* part = n_split > 1 ? (float*)split_ws : nullptr;
+  const dim3 grid((uint32_t)(nwg + base * n_split)), block(256);
+  const size_t lds = (c.batch + 1) * sizeof(uint32_t);
+  bool wide = false;
+  const uint32_t merge_wgs = decode_merge_wgs(c.batch, c.kvh, &wide);
+#define VK_MIX(T, DD)                                                                         \
+  do {                                                                                        \
+    if (n_split > 1)                                                                          \
+      hipLaunchKernelGGL((paged_mixed_stream<T, DD, true>), grid, block, lds, s, c, nwg,      \
+                         qtiles, n_split, part);                                              \
+    else                                                                                      \
+      hipLaunchKernelGGL((paged_mixed_stream<T, DD, false>), grid, block, lds, s, c, nwg,     \
+                         qtiles, 1u, nullptr);                                                \
+    if (n_split == 1) {                                                                       \
+      launch_decode_merge(c, nwg, DD, bf16, s);                                               \
+    } else {                                                                                  \
+      const uint32_t pf_wgs = (uint32_t)(base * (kMixRows / (256 / (DD / 4))));               \
+      if (wide)                                                                               \
+        hipLaunchKernelGGL((paged_mixed_merge<T, DD, kMergeWaves>), dim3(merge_wgs + pf_wgs), \
+                           dim3(256), 0, s, c, nwg, merge_wgs, qtiles, n_split, part);        \
+      else                                                                                    \
+        hipLaunchKernelGGL((paged_mixed_merge<T, DD, 1>), dim3(merge_wgs + pf_wgs), dim3(256), \
+                           0, s, c, nwg, merge_wgs, qtiles, n_split, part);                   \
+    }                                                                                         \
+  } while (0)
+  if (bf16) {
+    if (head_dim == 128) VK_MIX(bf16_t, 128);
+    else VK_MIX(bf16_t, 64);
+  } else {
+    if (head_dim == 128) VK_MIX(f16_t, 128);
+    else VK_MIX(f16_t, 64);
+  }
+#undef VK_MIX
 }
 
 size_t prefill_split_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t head_dim,
