@@ -303,26 +303,33 @@ def bench_mixed_step(d, steps, warmup):
 
 
 def bench_valu(steps, warmup):
-    """The VALU attention kernel that f32 pools and head dims other than 64 /
-    128 run on: config 0 (Qwen3-0.6B-shaped f32 decode, the reference's CPU
-    parity case) and config 2's batch over an f32 pool (1.5 GB of K/V)."""
+    """f32 pools: config 0 (Qwen3-0.6B-shaped f32 decode, the reference's CPU
+    parity case) and config 2's batch over an f32 pool (1.5 GB of K/V), both
+    on the f32-MFMA decode stream; and the VALU kernel that head dims without
+    an MFMA kernel run on, on config 2's batch with head_dim 80 (f32)."""
     out = {}
-    for name, w, heads, kvh in (("cfg0_f32", workload.config0_decode_small(), 16, 8),
-                                ("cfg2_shape_f32", workload.config2_decode(), 32, 8)):
-        cache = PagedKvCache(1, w.num_blocks, w.block_size, kvh, w.head_dim, torch.float32, "HND")
+    for name, w, heads, kvh, d in (("cfg0_f32", workload.config0_decode_small(), 16, 8, None),
+                                   ("cfg2_shape_f32", workload.config2_decode(), 32, 8, None),
+                                   ("cfg2_shape_f32_d80_valu", workload.config2_decode(), 32, 8,
+                                    80)):
+        d = d or w.head_dim
+        cache = PagedKvCache(1, w.num_blocks, w.block_size, kvh, d, torch.float32, "HND")
         workload.fill_normal(cache._slab, workload.seed_for(0))
-        q = torch.randn(w.batch, heads, w.head_dim, device=DEV)
+        q = torch.randn(w.batch, heads, d, device=DEV)
         batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
                              block_tables=[t.tolist() for t in w.tables], max_seqlen_q=1,
                              max_seqlen_k=int(w.lens.max()))
         prep = PreparedAttention.from_batch(batch, DEV)
         o = torch.empty_like(q)
-        ms, _ = timed(lambda: paged_attention_prepared(q, cache, 0, prep, w.head_dim ** -0.5,
-                                                       out=o), max(steps // 5, 3), 2)
-        kv = int(w.lens.sum()) * 2 * kvh * w.head_dim * 4
-        out[name] = dict(us=ms * 1e3, kv_bytes=kv, gbs=kv / (ms * 1e-3) / 1e9)
-        log(f"VALU attention {name}: {ms * 1e3:.1f} us, {kv / 1e6:.1f} MB of K/V, "
-            f"{out[name]['gbs']:.0f} GB/s")
+        call = lambda: paged_attention_prepared(q, cache, 0, prep, d ** -0.5, out=o)  # noqa: E731
+        ms, _ = timed(call, max(steps // 2, 5), 3)
+        gms = timed_graph(call, max(steps // 2, 5), 3)
+        kv = int(w.lens.sum()) * 2 * kvh * d * 4
+        out[name] = dict(us=ms * 1e3, graph_us=gms * 1e3, kv_bytes=kv,
+                         gbs=kv / (ms * 1e-3) / 1e9, graph_gbs=kv / (gms * 1e-3) / 1e9,
+                         path="VALU kernel" if name.endswith("valu") else "f32 MFMA decode stream")
+        log(f"f32 attention {name}: {ms * 1e3:.1f} us ({gms * 1e3:.1f} us in a graph), "
+            f"{kv / 1e6:.1f} MB of K/V, {out[name]['gbs']:.0f} GB/s, {out[name]['path']}")
         del cache
     return out
 
@@ -1120,7 +1127,7 @@ def main():
         # calls (849 -> 959 -> 983 TFLOP/s over three runs of 13 calls on one
         # box), so it warms up for 30 calls, as a serving loop's steady state.
         extras["prefill_cfg3"] = bench_prefill(max(args.steps, 10), 30)
-        extras["valu_attention"] = bench_valu(args.steps, args.warmup)
+        extras["f32_attention"] = bench_valu(args.steps, args.warmup)
         extras["head_dim_64"] = bench_head_dim_64(args.steps, args.warmup)
         extras["decode_small_batches"] = bench_small_batches(args.steps, args.warmup)
         extras["prefill_small_batches"] = bench_small_prefill(args.steps, args.warmup)

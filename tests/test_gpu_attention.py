@@ -307,6 +307,54 @@ def test_config2_decode_full_size_matches_the_oracle():
         assert max_abs(got, want) <= bound
 
 
+F32_DECODE_CASES = [
+    # heads, kvh, d, bs, lens_k, window, layout: every row a decode row, so
+    # the f32 pool runs the decode stream on f32 MFMAs
+    (16, 8, 128, 16, [1, 17, 600, 1500, 4000], None, "HND"),
+    (32, 8, 128, 16, [5, 33, 800, 2047, 64], 100, "NHD"),
+    (8, 2, 64, 32, [1, 31, 640, 3000], None, "HND"),
+    (64, 4, 128, 16, [48, 700, 1201], None, "HND"),
+    (8, 8, 128, 64, [65, 1000, 129, 2], 40, "NHD"),
+    (12, 4, 64, 16, [300] * 40, None, "HND"),
+]
+
+
+@pytest.mark.parametrize("case", F32_DECODE_CASES, ids=lambda c: f"h{c[0]}-kv{c[1]}-d{c[2]}-bs{c[3]}-w{c[5]}-{c[6]}")
+def test_f32_decode_on_mfma_matches_within_1e_5(case):
+    """f32 pools, pure decode batches (v_mfma_f32_16x16x4_f32 stream):
+    max-abs <= 1e-5 against the f32 oracle (the reference's CPU bar), for
+    GQA 1..16, head_dim 64 and 128, blocks of 16..64, windows, both layouts,
+    and the negated scale on the first case."""
+    heads, kvh, d, bs, lens_k, window, layout = case
+    rng = np.random.default_rng(zlib.crc32(str(case).encode()))
+    c, q, batch = random_case(rng, torch.float32, heads, kvh, d, bs, [1] * len(lens_k), lens_k,
+                              layout)
+    scales = [d ** -0.5] + ([-(d ** -0.5)] if case is F32_DECODE_CASES[0] else [])
+    for scale in scales:
+        want = oracle_out(q, c, 0, batch, scale, window)
+        got = paged_attention(q, c, 0, batch, scale, window)
+        assert max_abs(got, want) <= 1e-5, (scale, max_abs(got, want))
+
+
+def test_config2_shape_f32_decode_full_size_matches_within_1e_5():
+    """Config 2's batch (64 sequences, contexts up to 8k, 32k blocks) over an
+    f32 pool: every row within 1e-5 of the f32 oracle, on repeated calls."""
+    w = workload.config2_decode()
+    c = PagedKvCache(1, w.num_blocks, w.block_size, 8, 128, torch.float32)
+    workload.fill_normal(c._slab, workload.seed_for(2))
+    g = torch.Generator(device=DEV).manual_seed(9)
+    q = torch.randn(w.batch, 32, 128, generator=g, device=DEV)
+    batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
+                         block_tables=[t.tolist() for t in w.tables], max_seqlen_q=1,
+                         max_seqlen_k=int(w.lens.max()))
+    scale = 128 ** -0.5
+    want = oracle_out(q, c, 0, batch, scale)
+    prep = PreparedAttention.from_batch(batch, DEV)
+    for _ in range(3):
+        got = paged_attention_prepared(q, c, 0, prep, scale)
+        assert max_abs(got, want) <= 1e-5
+
+
 def test_config3_prefill_rows_match_the_oracle():
     """BASELINE config 3 (32 x 512-token chunks over 4,096 keys, shared
     prefixes): the whole batch runs in one call; rows at the start, middle and

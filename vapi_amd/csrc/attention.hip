@@ -3,8 +3,9 @@
 //  * the persistent MFMA decode stream (attn_decode.hip) for decode rows,
 //  * the MFMA prefill kernel (attn_prefill.hip) for prefill rows,
 // when the pool is bf16/f16 with head_dim 64 or 128, a power-of-two
-// block_size >= 16 and at most 16 query heads per kv head; every other shape
-// (f32 pools included) runs the VALU kernel (attn_generic.hip).
+// block_size >= 16 and at most 16 query heads per kv head; an f32 pool of
+// that shape runs the decode stream on f32 MFMAs when every row is a decode
+// row; every other shape runs the VALU kernel (attn_generic.hip).
 // Replaces paged_attention_cuda/_windowed/_prepared (vapi
 // crates/vapi-backend-candle/src/attention.rs:170-288).
 #include <mutex>
@@ -12,6 +13,18 @@
 #include "attn_common.hpp"
 
 namespace vk {
+
+// An f32 pool's pure-decode call (every row len_q == 1) runs the decode
+// stream on v_mfma_f32_16x16x4_f32; any prefill row sends the call to the
+// VALU kernel.
+static bool f32_decode_ok(const vapi_kv_pool* p, uint32_t num_heads, uint32_t max_seqlen_q) {
+  if (p->dtype != VAPI_KV_F32 || max_seqlen_q != 1) return false;
+  if (p->head_dim != 64 && p->head_dim != 128) return false;
+  if (p->block_size < 16 || (p->block_size & (p->block_size - 1))) return false;
+  if (num_heads == 0 || num_heads % p->num_kv_heads) return false;
+  const uint32_t G = num_heads / p->num_kv_heads;
+  return G >= 1 && G <= 16;
+}
 
 static bool mfma_ok(const vapi_kv_pool* p, uint32_t num_heads) {
   if (p->dtype != VAPI_KV_BF16 && p->dtype != VAPI_KV_F16) return false;
@@ -116,6 +129,9 @@ static size_t required_workspace(const vapi_kv_pool* pool, uint32_t batch, uint3
       num_heads == 0)
     return 0;
   const uint32_t group = num_heads / pool->num_kv_heads;
+  if (f32_decode_ok(pool, num_heads, max_seqlen_q))
+    return decode_workspace_bytes(batch, pool->num_kv_heads, group, pool->head_dim,
+                                  decode_num_waves());
   if (!mfma_ok(pool, num_heads))
     return generic_workspace_bytes(batch, pool->num_kv_heads, group, pool->head_dim,
                                    std::max(max_seqlen_q, 1u), max_seqlen_k);
@@ -306,7 +322,8 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
     VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: block table width 0");
   if (flags & ~(uint32_t)(VAPI_ATTN_DETERMINISTIC | VAPI_ATTN_NO_DECODE_ROWS))
     VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: unknown flags 0x%x", flags);
-  if (num_heads > 65535 || (batch > 65535 && !mfma_ok(pool, num_heads)))
+  if (num_heads > 65535 ||
+      (batch > 65535 && !mfma_ok(pool, num_heads) && !f32_decode_ok(pool, num_heads, max_seqlen_q)))
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: batch %u / heads %u too large",
             batch, num_heads);
   // A batch the caller says has no decode rows (and which is not a fused
@@ -395,7 +412,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
       return 0;
     }
     if (skip_decode) a.pf_min_q = 1;
-    else launch_decode(a, workspace, g.d, bf16, s);
+    else launch_decode(a, workspace, g.d, pool->dtype, s);
     if (max_seqlen_q > 1 && pf_n > 0) {
       // The workspace past the decode's part serves the prefill's key split
       // (never its first 256 bytes, which carry the decode's XCD shares
@@ -403,6 +420,9 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
       launch_prefill(a, max_seqlen_q, max_seqlen_k, g.d, bf16,
                      room ? (char*)workspace + off : nullptr, room ? workspace_bytes - off : 0, s);
     }
+  } else if (f32_decode_ok(pool, num_heads, max_seqlen_q)) {
+    a.num_waves = decode_num_waves();
+    launch_decode(a, workspace, g.d, pool->dtype, s);
   } else {
     if (g.d > 256)
       VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: head_dim %u > 256", g.d);

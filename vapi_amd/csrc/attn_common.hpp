@@ -411,13 +411,119 @@ __device__ __forceinline__ void attend_step(const KVStep<D>& st, const uint4 (&q
   attend_pv<T, D>(st.v, pf, o);
 }
 
+// ---- f32 pools: v_mfma_f32_16x16x4_f32 --------------------------------------
+//
+// The same operand scheme at K = 4 per MFMA, one 16-key tile (a half step)
+// at a time. S^T = K Q^T: lane (key r, g) loads K[r][16c + 4g .. +3] as one
+// float4 per c, element j feeding MFMA (c, j), whose k-slot g is d = 16c +
+// 4g + j; lane (col, g) supplies Q[col] at the same d. The result is the
+// 16-bit path's score layout: lane (col, g) holds keys 4g .. 4g + 3 of the
+// tile for query column col. O^T += V^T P^T: MFMA (i) takes key 4g + i in
+// k-slot g, so its B operand is the lane's own score p[i]; its A operand is
+// V[4g + i][d] with output row m <-> d = 64h + 4m + j for d tile t = 4h + j,
+// from one float4 V[4g + i][64h + 4m .. +3] per (i, h). Lane (col, g) then
+// holds output d = 64h + 16g + 4i + j in o[4h + j][i]. P stays f32.
+template <int D>
+struct KHalfF32 {
+  float4 k[D / 16];
+};
+template <int D>
+struct VHalfF32 {
+  float4 v[4][D / 64];
+};
+template <int D>
+struct KTileF32 {
+  KHalfF32<D> h[2];
+};
+template <int D>
+struct VTileF32 {
+  VHalfF32<D> h[2];
+};
+
+__device__ __forceinline__ floatx4 mfma16x16x4f32(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// K and V of the 16-key tile at s0 + 16 tt (keys past `last` re-read it).
+template <int D>
+__device__ __forceinline__ void load_half_f32(KHalfF32<D>& kt, VHalfF32<D>& vt,
+                                              const uint32_t* __restrict__ tab, const float* kb,
+                                              const float* vb, const AttnArgs& a, int32_t s0,
+                                              int tt, int32_t last, uint32_t col, uint32_t g) {
+  const int32_t ts = min(s0 + 16 * tt, last & ~15);
+  const int32_t lim = last - ts;
+  const char* kp = tile_base(tab, kb, a, ts) +
+                   ((uint32_t)min((int32_t)col, lim) * a.tok_e + 4 * g) * sizeof(float);
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) kt.k[c] = load_stream((const float4*)(kp + 64u * c));
+  const char* vp = tile_base(tab, vb, a, ts);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const char* row =
+        vp + ((uint32_t)min((int32_t)(4 * g + i), lim) * a.tok_e + 4 * col) * sizeof(float);
+#pragma unroll
+    for (int h = 0; h < D / 64; ++h) vt.v[i][h] = load_stream((const float4*)(row + 256u * h));
+  }
+}
+
+__device__ __forceinline__ float f4(const float4& x, int j) {
+  return j == 0 ? x.x : j == 1 ? x.y : j == 2 ? x.z : x.w;
+}
+
+// Online softmax over one 16-key tile for 16 query columns: S^T, lazy
+// rescale, P = exp2(s c - m) in f32, O^T += V^T P^T. visible(i): key 4g + i
+// of the tile.
+template <int D, typename Mask>
+__device__ __forceinline__ void attend_half_f32(const KHalfF32<D>& kt, const VHalfF32<D>& vt,
+                                                const float4 (&qf)[D / 16],
+                                                floatx4 (&o)[D / 16], float& m_run,
+                                                float& l_run, float scale_log2, Mask visible) {
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = mfma16x16x4f32(f4(kt.k[c], j), f4(qf[c], j), acc);
+  float s[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s[i] = visible(i) ? acc[i] : -INFINITY;
+  const float mx = max_nc(max_nc(s[0], s[1]), max_nc(s[2], s[3])) * scale_log2;
+  rescale_rows<D>(mx, o, m_run, l_run);
+  float p[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = fast_exp2(__builtin_fmaf(s[i], scale_log2, -m_run));
+  l_run += (p[0] + p[1]) + (p[2] + p[3]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int h = 0; h < D / 64; ++h)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[4 * h + j] = mfma16x16x4f32(f4(vt.v[i][h], j), p[i], o[4 * h + j]);
+}
+
+// Row `col`'s outputs of o (the f32 layout above), scaled, as float4 runs
+// d = 64h + 16g + 4i .. +3, to `row` (f32 output or partial).
+template <int D>
+__device__ __forceinline__ void store_row_f32(float* row, const floatx4 (&o)[D / 16],
+                                              float scale, uint32_t g) {
+#pragma unroll
+  for (int h = 0; h < D / 64; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *(float4*)(row + 64 * h + 16 * g + 4 * i) =
+          make_float4(o[4 * h][i] * scale, o[4 * h + 1][i] * scale, o[4 * h + 2][i] * scale,
+                      o[4 * h + 3][i] * scale);
+}
+
 // ---- launchers (one per translation unit) ----------------------------------
 
 
-// Decode rows (len_q == 1) of the batch; bf16/f16, head_dim 64 or 128.
+// Decode rows (len_q == 1) of the batch; bf16/f16/f32, head_dim 64 or 128
+// (f32: no fused append).
 size_t decode_workspace_bytes(uint32_t batch, uint32_t kvh, uint32_t group,
                               uint32_t head_dim, uint32_t num_waves);
-void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, bool bf16, hipStream_t s);
+void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t dtype,
+                   hipStream_t s);
 // Prefill rows (len_q > 1); same dtypes and head dims.
 // Workgroups of the prefill launch (query tiles x kv heads x sequences); a
 // launch needs it below 2^32.

@@ -91,8 +91,9 @@ void launch_decode_merge(const AttnArgs& c, uint32_t nwg, uint32_t head_dim, boo
 #undef VK_MRG
 }
 
-void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, bool bf16,
+void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t dtype,
                    hipStream_t s) {
+  const bool bf16 = dtype == VAPI_KV_BF16;
   const uint32_t W = a.num_waves;
   const uint32_t nwg = W / kDecodeWavesPerWG;
   const uint32_t total = a.batch;
@@ -134,7 +135,10 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, bool bf16,
     else               \
       VK_DEC(T, DD, false); \
   } while (0)
-    if (bf16) {
+    if (dtype == VAPI_KV_F32) {  // no fused append on f32 pools
+      if (head_dim == 128) VK_DEC(float, 128, false);
+      else VK_DEC(float, 64, false);
+    } else if (bf16) {
       if (head_dim == 128) VK_DEC2(bf16_t, 128);
       else VK_DEC2(bf16_t, 64);
     } else {

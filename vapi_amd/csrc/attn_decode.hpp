@@ -39,6 +39,7 @@
 // exactly once.
 #pragma once
 #include <cstdlib>
+#include <type_traits>
 
 #include "attn_common.hpp"
 
@@ -181,11 +182,23 @@ __device__ __forceinline__ void load_q(uint4* qs, const AttnArgs& a, const Decod
   // results are computed and never stored.
   const uint32_t h = col < a.group ? col : 0;
   const T* qrow = (const T*)a.q + ((uint64_t)p.q0 * a.num_heads + p.kh * a.group + h) * D;
+  if constexpr (sizeof(T) == 4) {
+    // f32: D / 16 float4 per lane, Q[h][16c + 4g .. +3] (the f32 MFMA's k
+    // order); a negative scale flips the sign bit of every element.
+    const uint32_t sg = a.q_sign ? 0x80000000u : 0u;
 #pragma unroll
-  for (int c = 0; c < D / 32; ++c) {
-    uint4 x = *(const uint4*)(qrow + 32 * c + 8 * g);
-    x.x ^= a.q_sign, x.y ^= a.q_sign, x.z ^= a.q_sign, x.w ^= a.q_sign;
-    qs[c * 64 + lane] = x;
+    for (int c = 0; c < D / 16; ++c) {
+      uint4 x = *(const uint4*)(qrow + 16 * c + 4 * g);
+      x.x ^= sg, x.y ^= sg, x.z ^= sg, x.w ^= sg;
+      qs[c * 64 + lane] = x;
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c) {
+      uint4 x = *(const uint4*)(qrow + 32 * c + 8 * g);
+      x.x ^= a.q_sign, x.y ^= a.q_sign, x.z ^= a.q_sign, x.w ^= a.q_sign;
+      qs[c * 64 + lane] = x;
+    }
   }
 }
 
@@ -226,6 +239,16 @@ __device__ __forceinline__ void flush_piece(const AttnArgs& a, const DecodePos& 
   // they would pin registers the K/V buffers need.
   asm volatile("" : "+v"(col), "+v"(g));
   if (col >= G) return;  // lanes of padding columns hold no head
+  if constexpr (sizeof(T) == 4) {
+    if (whole) {
+      float* orow = (float*)a.out + ((uint64_t)p.q0 * a.num_heads + p.kh * G + col) * D;
+      store_row_f32<D>(orow, o, l_tot > 0.f ? 1.f / l_tot : 0.f, g);
+    } else {
+      store_row_f32<D>(a.ws_o + ((uint64_t)slot * G + col) * D, o, 1.f, g);
+      if (g == 0) *(float2*)(a.ws_ml + ((uint64_t)slot * G + col) * 2) = make_float2(m_run, l_tot);
+    }
+    return;
+  }
   if (whole) {
     T* orow = (T*)a.out + ((uint64_t)p.q0 * a.num_heads + p.kh * G + col) * D;
     store_row<T, D>(orow, o, l_tot > 0.f ? 1.f / l_tot : 0.f, g);
@@ -333,7 +356,8 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
   DecodePos pos = locate(a, cu_q, cu_k, P, FZ, t);
   // The Q^T operand of the current segment lives in LDS (read back every
   // step) to keep the K/V buffers in registers.
-  __shared__ uint4 q_lds[kDecodeWavesPerWG][D / 32 * 64];
+  constexpr bool kF32 = sizeof(T) == 4;
+  __shared__ uint4 q_lds[kDecodeWavesPerWG][D / 32 * 64 * sizeof(T) / 2];
   uint4* qs = q_lds[wave];
   load_q<T, D>(qs, a, pos, lane, col, g);
   bool piece_first = pos.seg_first;
@@ -342,15 +366,33 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
 #pragma unroll
   for (int k = 0; k < DPL; ++k) o[k] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  KTile<D> kA, kB;
-  VTile<D> vA, vB;
-  load_step_k<T, D>(kA, a, table, pos, col, g);
-  load_step_v<T, D>(vA, a, table, pos, col, g);
+  // 16-bit pools: two 32-key steps in registers (the next one loading while
+  // the current one is computed). f32 pools: one 32-key step as two 16-key
+  // halves, each reloaded with the next step's half once it is computed.
+  using KBuf = std::conditional_t<kF32, KTileF32<D>, KTile<D>>;
+  using VBuf = std::conditional_t<kF32, VTileF32<D>, VTile<D>>;
+  KBuf kA, kB;
+  VBuf vA, vB;
+  const float* kbf = (const float*)a.k;
+  const float* vbf = (const float*)a.v;
+  auto load_halves = [&](KTileF32<D>& kt, VTileF32<D>& vt, const DecodePos& p, int tt)
+      __attribute__((always_inline)) {
+    load_half_f32<D>(kt.h[tt], vt.h[tt], table + (uint64_t)p.seq * a.max_blocks,
+                     kbf + p.kh * a.head_e, vbf + p.kh * a.head_e, a, p.key0, tt, p.len_k - 1,
+                     col, g);
+  };
+  if constexpr (kF32) {
+    load_halves(kA, vA, pos, 0);
+    load_halves(kA, vA, pos, 1);
+  } else {
+    load_step_k<T, D>(kA, a, table, pos, col, g);
+    load_step_v<T, D>(vA, a, table, pos, col, g);
+  }
 
   // One step: find the next step, issue its K and V, attend over the current
   // one, flush when the piece ends (segment or slice boundary). Returns
   // false when the slice is done.
-  auto step = [&](KTile<D>& kc, VTile<D>& vc, KTile<D>& kn, VTile<D>& vn) -> bool {
+  auto step = [&](KBuf& kc, VBuf& vc, KBuf& kn, VBuf& vn) -> bool {
     const bool more = t + 1 < t_end;
     const bool seg_ends = pos.key0 + 32 >= pos.len_k;
     const bool same_piece = more && !seg_ends;
@@ -373,17 +415,37 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
       nxt.len_k = 1;
       nxt.fuse = 0;
     }
-    load_step_k<T, D>(kn, a, table, nxt, col, g);
-    load_step_v<T, D>(vn, a, table, nxt, col, g);
     const int32_t lo = pos.lo, len_k = pos.len_k, key0 = pos.key0;
-    uint4 qf[D / 32];
+    if constexpr (kF32) {
+      // kn, vn are kc, vc: each half is refilled with the next step's once
+      // it has been computed (16 KiB in flight per wave, as 16-bit steps).
+      float4 qf[D / 16];
 #pragma unroll
-    for (int c = 0; c < D / 32; ++c) qf[c] = qs[c * 64 + lane];
-    const uint4 pf = attend_qk<T, D>(kc, qf, o, m_run, l_run, a.scale_log2, g, [&](int tt, int i) {
-      const int32_t key = key0 + 16 * tt + 4 * (int32_t)g + i;
-      return key >= lo && key < len_k;
-    });
-    attend_pv<T, D>(vc, pf, o);
+      for (int c = 0; c < D / 16; ++c) {
+        const uint4 x = qs[c * 64 + lane];
+        qf[c] = make_float4(__uint_as_float(x.x), __uint_as_float(x.y), __uint_as_float(x.z),
+                            __uint_as_float(x.w));
+      }
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        attend_half_f32<D>(kc.h[tt], vc.h[tt], qf, o, m_run, l_run, a.scale_log2, [&](int i) {
+          const int32_t key = key0 + 16 * tt + 4 * (int32_t)g + i;
+          return key >= lo && key < len_k;
+        });
+        load_halves(kn, vn, nxt, tt);
+      }
+    } else {
+      load_step_k<T, D>(kn, a, table, nxt, col, g);
+      load_step_v<T, D>(vn, a, table, nxt, col, g);
+      uint4 qf[D / 32];
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c) qf[c] = qs[c * 64 + lane];
+      const uint4 pf = attend_qk<T, D>(kc, qf, o, m_run, l_run, a.scale_log2, g, [&](int tt, int i) {
+        const int32_t key = key0 + 16 * tt + 4 * (int32_t)g + i;
+        return key >= lo && key < len_k;
+      });
+      attend_pv<T, D>(vc, pf, o);
+    }
     if (!same_piece) {
       const uint32_t seg = pos.seq * a.kvh + pos.kh;
       if (lane == 0) {
@@ -403,7 +465,12 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
     ++t;
     return true;
   };
-  while (step(kA, vA, kB, vB) && step(kB, vB, kA, vA)) {
+  if constexpr (kF32) {
+    while (step(kA, vA, kA, vA)) {
+    }
+  } else {
+    while (step(kA, vA, kB, vB) && step(kB, vB, kA, vA)) {
+    }
   }
   const uint32_t t_done = (uint32_t)__builtin_amdgcn_s_memrealtime();
   if (lane == 0) {
@@ -510,9 +577,17 @@ __device__ __forceinline__ void store_outputs(T* dst, uint32_t n, const float (&
   float v[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) v[j] = L[j] > 0.f ? O[j] / L[j] : 0.f;
-  if (n == 8 && ((uintptr_t)dst & 15) == 0) {
+  if constexpr (sizeof(T) == 4) {
+    if (n == 8 && ((uintptr_t)dst & 15) == 0) {
+      ((float4*)dst)[0] = make_float4(v[0], v[1], v[2], v[3]);
+      ((float4*)dst)[1] = make_float4(v[4], v[5], v[6], v[7]);
+      return;
+    }
+  } else if (n == 8 && ((uintptr_t)dst & 15) == 0) {
     *(uint4*)dst = pack8<T>(v);
-  } else {
+    return;
+  }
+  {
     for (uint32_t j = 0; j < n; ++j) dst[j] = from_f32<T>(v[j]);
   }
 }
@@ -529,9 +604,11 @@ __device__ __forceinline__ void decode_merge_body(const AttnArgs& a, uint32_t nw
                                                   uint32_t merge_wgs, uint32_t bid,
                                                   uint32_t nbid) {
   static_assert(WPS == 1 || WPS == kMergeWaves, "a wave or a workgroup per segment");
-  if (kFuse && bid >= merge_wgs) {
-    copy_new_rows<T, D>(a, bid - merge_wgs, nbid - merge_wgs);
-    return;
+  if constexpr (kFuse) {
+    if (bid >= merge_wgs) {
+      copy_new_rows<T, D>(a, bid - merge_wgs, nbid - merge_wgs);
+      return;
+    }
   }
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);

@@ -126,10 +126,10 @@ template <typename V>
 __device__ __forceinline__ void store_stream(V* p, V v) {
   if constexpr (sizeof(V) == 16) {
     typedef uint32_t v4 __attribute__((ext_vector_type(4)));
-    __builtin_nontemporal_store(v4{v.x, v.y, v.z, v.w}, (v4*)p);
+    __builtin_nontemporal_store(__builtin_bit_cast(v4, v), (v4*)p);
   } else if constexpr (sizeof(V) == 8) {
     typedef uint32_t v2 __attribute__((ext_vector_type(2)));
-    __builtin_nontemporal_store(v2{v.x, v.y}, (v2*)p);
+    __builtin_nontemporal_store(__builtin_bit_cast(v2, v), (v2*)p);
   } else {
     __builtin_nontemporal_store(v, p);
   }
@@ -140,18 +140,15 @@ __device__ __forceinline__ void store_stream(V* p, V v) {
 // loads 6.18 -> 6.93 TB/s, random 4 KiB tiles 6.04 -> 6.80 TB/s.
 template <typename V>
 __device__ __forceinline__ V load_stream(const V* p) {
+  // The loaded words are bit-cast, not converted, into V (uint4, float4 ...).
   if constexpr (sizeof(V) == 16) {
     typedef uint32_t v4 __attribute__((ext_vector_type(4)));
     const v4 r = __builtin_nontemporal_load((const v4*)p);
-    V v;
-    v.x = r.x, v.y = r.y, v.z = r.z, v.w = r.w;
-    return v;
+    return __builtin_bit_cast(V, r);
   } else if constexpr (sizeof(V) == 8) {
     typedef uint32_t v2 __attribute__((ext_vector_type(2)));
     const v2 r = __builtin_nontemporal_load((const v2*)p);
-    V v;
-    v.x = r.x, v.y = r.y;
-    return v;
+    return __builtin_bit_cast(V, r);
   } else {
     return __builtin_nontemporal_load(p);
   }
