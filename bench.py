@@ -249,9 +249,13 @@ def bench_fused_step(d, steps, warmup):
 
     ms_two, _ = timed(two, steps, warmup)
     ms_fused, _ = timed(fused, steps, warmup)
+    # The same two sequences replayed from HIP graphs (no host launch cost).
+    g_two = timed_graph(two, steps, warmup)
+    g_fused = timed_graph(fused, steps, warmup)
     log(f"decode cfg2 + append of {w.batch} tokens: two calls {ms_two * 1e3:.1f} us, "
-        f"fused {ms_fused * 1e3:.1f} us")
-    return {"two_calls_us": round(ms_two * 1e3, 2), "fused_us": round(ms_fused * 1e3, 2)}
+        f"fused {ms_fused * 1e3:.1f} us; in graphs {g_two * 1e3:.1f} / {g_fused * 1e3:.1f} us")
+    return {"two_calls_us": round(ms_two * 1e3, 2), "fused_us": round(ms_fused * 1e3, 2),
+            "two_calls_graph_us": round(g_two * 1e3, 2), "fused_graph_us": round(g_fused * 1e3, 2)}
 
 
 # ---- the VALU kernel (f32 pools, other head dims) ---------------------------------
@@ -1080,7 +1084,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["decode", "append", "prefill", "copy", "blocks", "valu"],
+    ap.add_argument("--only", choices=["decode", "append", "prefill", "copy", "blocks", "valu",
+                                       "mixed"],
                     default=None)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate", action="store_true",
@@ -1112,6 +1117,9 @@ def main():
         return
     if args.only == "valu":
         bench_valu(args.steps, args.warmup)
+        return
+    if args.only == "mixed":
+        bench_mixed_step(setup_decode(), args.steps, args.warmup)
         return
     dec = bench_decode(args.steps, args.warmup)
     if args.only == "decode":
