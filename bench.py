@@ -1196,6 +1196,16 @@ def main():
                                if "append_cfg1" in extras else None),
         "kv_append_host_launched_gbs": (round(extras["append_cfg1"]["gbs_host_launched_c_abi"], 1)
                                         if "append_cfg1" in extras else None),
+        # Tokens per second per layer (one GPU): config 2's 64 decode tokens
+        # per call, config 1's 3,891 appended tokens per call, config 3's
+        # 16,384 prefill query tokens per call.
+        "tokens_per_s": {
+            "decode_cfg2": round(64 / (dec["graph_ms"] * 1e-3)),
+            "append_cfg1": (round(3891 / (extras["append_cfg1"]["us"] * 1e-6))
+                            if "append_cfg1" in extras else None),
+            "prefill_cfg3": (round(32 * 512 / (extras["prefill_cfg3"]["ms"] * 1e-3))
+                             if "prefill_cfg3" in extras else None),
+        },
         "extras": extras,
     }
     print(json.dumps(line), flush=True)
