@@ -144,22 +144,28 @@ __device__ __forceinline__ uint32_t lds_addr(const uint16_t* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)p;
 }
 
-// Four ds_read_b64_tr_b16 (two V^T fragments, reads 4h .. 4h + 3) as one
-// inline-assembly block that also waits for them: the compiler does not
-// see these LDS reads, so it neither waits for the direct loads in flight
-// into the other ring buffers before them nor could it track their results.
-__device__ __forceinline__ void ds_read_tr16_x4(uint2 (&r)[8], const uint32_t (&addr)[8], int h) {
+// Four ds_read_b64_tr_b16 issued without waiting (results valid only after
+// a later lgkm wait that names the same registers).
+__device__ __forceinline__ void ds_read_tr16_issue4(uint2 (&r)[4], const uint32_t (&addr)[4]) {
   __asm__ volatile(
       "ds_read_b64_tr_b16 %0, %4\n\t"
       "ds_read_b64_tr_b16 %1, %5\n\t"
       "ds_read_b64_tr_b16 %2, %6\n\t"
-      "ds_read_b64_tr_b16 %3, %7\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(r[4 * h]), "=&v"(r[4 * h + 1]), "=&v"(r[4 * h + 2]), "=&v"(r[4 * h + 3])
-      : "v"(addr[4 * h]), "v"(addr[4 * h + 1]), "v"(addr[4 * h + 2]), "v"(addr[4 * h + 3])
+      "ds_read_b64_tr_b16 %3, %7"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+      : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3])
       : "memory");
 }
-
+// Waits until at most N LDS/scalar-memory operations are in flight; the
+// registers of the batch that completes are named so that no use of them
+// moves above the wait.
+template <int N>
+__device__ __forceinline__ void lgkm_wait(uint2 (&r)[4]) {
+  __asm__ volatile("s_waitcnt lgkmcnt(%4)"
+                   : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3])
+                   : "n"(N)
+                   : "memory");
+}
 
 // Bytes of one (item, split) partial block: (m, l) f32 per row, then o / l
 // per row in f32 (the split adds no rounding before the merge).
@@ -301,14 +307,28 @@ __device__ __forceinline__ void prefill_body(
     pf_dma<T, D, W>(knext, vnext, tab, kb, vb, a, min(s0 + 64, s_last), last, tid, wave);
     // Steps inside [full_lo, full_hi] need no mask (a uniform branch).
     const bool masked = !(s0 >= full_lo && s0 + 31 <= full_hi);
-    KTile<D> kt;
+    // V^T fragments in batches of two d tiles (four transposing reads): batch
+    // b + 1 is issued before batch b's MFMAs, and batch 0 right after the
+    // score MFMAs, so its reads land during the softmax.
+    const uint32_t vbase = lds_addr(vbuf);
+    constexpr int NB = DT / 2;
+    uint2 r[NB][4];
+    auto issue = [&](int b) __attribute__((always_inline)) {
+      uint32_t ad[4];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+      for (int k = 0; k < 2; ++k)
 #pragma unroll
-      for (int c = 0; c < KC; ++c) kt.k[tt][c] = *(const uint4*)(kbuf + k_off[tt][c]);
+        for (int h = 0; h < 2; ++h) ad[2 * k + h] = vbase + 2 * v_off[2 * b + k][h];
+      ds_read_tr16_issue4(r[b], ad);
+    };
     float sc[kPfRT][8];
     {
       floatx4 acc[kPfRT][2];
+      KTile<D> kt;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int c = 0; c < KC; ++c) kt.k[tt][c] = *(const uint4*)(kbuf + k_off[tt][c]);
 #pragma unroll
       for (int t = 0; t < kPfRT; ++t) qk_scores<T, D>(kt, qf[t], acc[t]);
 #pragma unroll
@@ -327,6 +347,7 @@ __device__ __forceinline__ void prefill_body(
         }
       }
     }
+    issue(0);
     float mx[kPfRT];
     bool grow = false;
 #pragma unroll
@@ -342,33 +363,26 @@ __device__ __forceinline__ void prefill_body(
     uint4 pf[kPfRT];
 #pragma unroll
     for (int t = 0; t < kPfRT; ++t) pf[t] = exp_pack<T>(sc[t], m_run[t], l_run[t], a.scale_log2);
-    // V^T fragments two d tiles at a time; a batch's MFMAs run while the
-    // next batch's reads wait (measured: batches of two tiles 821-833
-    // TFLOP/s, of four 803-814, of one 794-805 on config 3).
-    const uint32_t vbase = lds_addr(vbuf);
+    // Measured on config 3 (runs alternated on one box): reads waited for
+    // batch by batch 969-970 TFLOP/s, batch b + 1 issued before batch b's
+    // MFMAs 996-999, and batch 0 issued before the softmax 1,017-1,018
+    // against 1,012 (two batches before it: 964-968; the K fragments read
+    // the same way, four and four: 941-943 against 981-984).
 #pragma unroll
-    for (int k0 = 0; k0 < DT; k0 += 4) {
-      uint32_t ad[8];
-      uint2 r[8];
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) ad[2 * k + h] = vbase + 2 * v_off[k0 + k][h];
-      ds_read_tr16_x4(r, ad, 0);
+    for (int b = 0; b < NB; ++b) {
+      if (b + 1 < NB) {
+        issue(b + 1);
+        lgkm_wait<4>(r[b]);
+      } else {
+        lgkm_wait<0>(r[b]);
+      }
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
-        const uint4 vf = make_uint4(r[2 * k].x, r[2 * k].y, r[2 * k + 1].x, r[2 * k + 1].y);
+        const uint4 vf = make_uint4(r[b][2 * k].x, r[b][2 * k].y, r[b][2 * k + 1].x,
+                                    r[b][2 * k + 1].y);
 #pragma unroll
         for (int t = 0; t < kPfRT; ++t)
-          o[t][k0 + k] = mfma16x16x32<T>(vf, pf[t], o[t][k0 + k]);
-      }
-      ds_read_tr16_x4(r, ad, 1);
-#pragma unroll
-      for (int k = 2; k < 4; ++k) {
-        const uint4 vf = make_uint4(r[2 * k].x, r[2 * k].y, r[2 * k + 1].x, r[2 * k + 1].y);
-#pragma unroll
-        for (int t = 0; t < kPfRT; ++t)
-          o[t][k0 + k] = mfma16x16x32<T>(vf, pf[t], o[t][k0 + k]);
+          o[t][2 * b + k] = mfma16x16x32<T>(vf, pf[t], o[t][2 * b + k]);
       }
     }
     // Step s + 1's chunks (issued a step ago) are in LDS once this wave's
