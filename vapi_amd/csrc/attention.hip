@@ -400,8 +400,10 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
     const size_t off = std::max<size_t>((need + 255) & ~(size_t)255, 256);
     const bool room = workspace && workspace_bytes > off;
     // Decode rows and prefill rows in one step: both kernels in one launch.
+    // (At most 4,000 sequences: the launch's dynamic LDS, 4 bytes per
+    // sequence, then still lets a decode and a prefill workgroup share a CU.)
     const bool mixed = !skip_decode && !fuse && max_seqlen_q > 1 && pf_n > 0 &&
-                       batch <= decode_max_plan_seqs() &&
+                       batch <= std::min(decode_max_plan_seqs(), 4000u) &&
                        mixed_prefill_items(pf_n, g.kvh, num_heads / g.kvh, max_seqlen_q) <
                            (1ull << 30);
     if (mixed) {
