@@ -407,7 +407,6 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
                        mixed_prefill_items(pf_n, g.kvh, num_heads / g.kvh, max_seqlen_q) <
                            (1ull << 30);
     if (mixed) {
-      a.num_waves = decode_num_waves();
       launch_mixed(a, workspace, max_seqlen_q, max_seqlen_k, g.d, bf16,
                    room ? (char*)workspace + off : nullptr, room ? workspace_bytes - off : 0, s);
       VK_LAUNCHED("paged_attention");
