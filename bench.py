@@ -451,6 +451,36 @@ def bench_head_dim_64(steps, warmup):
     return res
 
 
+def bench_wide_group(steps, warmup):
+    """Config 2's batch with 64 query heads over 2 kv heads (32 query heads
+    per kv head: the decode runs each group as two virtual kv heads of 16,
+    each reading the group's K/V) on a bf16 pool: K/V bytes are a quarter of
+    config 2's."""
+    w = workload.config2_decode()
+    cache = PagedKvCache(DECODE_LAYERS, w.num_blocks, w.block_size, 2, 128, torch.bfloat16,
+                         "HND")
+    workload.fill_normal(cache._slab, workload.seed_for(2))
+    q = torch.randn(w.batch, 64, 128, device=DEV).to(torch.bfloat16)
+    batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
+                         block_tables=[t.tolist() for t in w.tables], max_seqlen_q=1,
+                         max_seqlen_k=int(w.lens.max()))
+    prep = PreparedAttention.from_batch(batch, DEV)
+    out = torch.empty_like(q)
+    turn = [0]
+
+    def call():
+        paged_attention_prepared(q, cache, turn[0] % DECODE_LAYERS, prep, 128 ** -0.5, out=out)
+        turn[0] += 1
+
+    gms = timed_graph(call, steps, warmup)
+    kv = int(w.lens.sum()) * 2 * 2 * 128 * 2
+    log(f"decode cfg2 batch, 64 q / 2 kv heads (G = 32): {gms * 1e3:.1f} us, "
+        f"{kv / (gms * 1e-3) / 1e9:.0f} GB/s of unique K/V (each group's K/V read twice)")
+    del cache, q, out
+    return dict(us=gms * 1e3, kv_bytes=kv, gbs_unique_kv=kv / (gms * 1e-3) / 1e9,
+                gbs_read=2 * kv / (gms * 1e-3) / 1e9)
+
+
 # ---- config 1: append --------------------------------------------------------------
 
 def bench_append(steps, warmup):
@@ -1137,6 +1167,7 @@ def main():
         extras["prefill_cfg3"] = bench_prefill(max(args.steps, 10), 30)
         extras["f32_attention"] = bench_valu(args.steps, args.warmup)
         extras["head_dim_64"] = bench_head_dim_64(args.steps, args.warmup)
+        extras["wide_group_g32"] = bench_wide_group(args.steps, args.warmup)
         extras["decode_small_batches"] = bench_small_batches(args.steps, args.warmup)
         extras["prefill_small_batches"] = bench_small_prefill(args.steps, args.warmup)
     extras["blocks_cfg4"] = bench_blocks(max(args.steps // 5, 3), 2, dec)

@@ -314,15 +314,38 @@ def test_the_build_refuses_a_prefill_kernel_that_spills():
 
 
 def test_the_valu_workspace_follows_its_key_chunks():
-    """f32 pools run the VALU kernel: keys split into chunks of 512, halved
-    down to 64 while the launch has fewer than 512 workgroups; a call whose
-    keys fit one chunk needs no workspace."""
+    """Head dims without an MFMA kernel (80 here) run the VALU kernel: keys
+    split into chunks of 512, halved down to 64 while the launch has fewer
+    than 512 workgroups; a call whose keys fit one chunk needs no
+    workspace."""
     L = _lib.lib()
-    f32 = pool(dtype=_lib.F32, num_kv_heads=8, head_dim=128)
+    f32 = pool(dtype=_lib.F32, num_kv_heads=8, head_dim=80)
     # 64 rows x 8 kv heads = 512 row tiles: 512-key chunks, one chunk.
     assert L.vapi_paged_attention_workspace_size(f32, 64, 32, 1, 512) == 0
     # Two sequences: 16 tiles, so 64-key chunks (8 of them for 512 keys).
     need = L.vapi_paged_attention_workspace_size(f32, 2, 32, 1, 512)
     tiles, chunks = 2 * 8, 8
-    assert need == 256 + tiles * chunks * 16 * (128 + 2) * 4
+    assert need == 256 + tiles * chunks * 16 * (80 + 2) * 4
     assert L.vapi_paged_attention_workspace_size(f32, 2, 32, 1, 64) == 0
+
+
+def test_f32_decode_and_wide_groups_size_the_decode_workspace():
+    """An f32 pool's decode-only call sizes the decode stream's workspace
+    (balance block, ranges, f32 partials), as a bf16 pool's does; so does a
+    group of 32 query heads per kv head (two virtual kv heads of 16), whose
+    partials are as large as 32 heads' and whose segments twice as many."""
+    L = _lib.lib()
+    f32 = pool(dtype=_lib.F32, num_kv_heads=8, head_dim=128)
+    bf16 = pool(dtype=_lib.BF16, num_kv_heads=8, head_dim=128)
+    a = L.vapi_paged_attention_workspace_size(f32, 64, 32, 1, 4096)
+    b = L.vapi_paged_attention_workspace_size(bf16, 64, 32, 1, 4096)
+    assert a == b and a > 0
+    one = pool(dtype=_lib.BF16, num_kv_heads=1, head_dim=128)
+    two = pool(dtype=_lib.BF16, num_kv_heads=2, head_dim=128)
+    # G = 32 on one kv head is decoded as two kv heads of 16: the same
+    # workspace as 32 heads over two kv heads.
+    assert (L.vapi_paged_attention_workspace_size(one, 64, 32, 1, 4096) ==
+            L.vapi_paged_attention_workspace_size(two, 64, 32, 1, 4096))
+    # G = 17 has no split: the VALU kernel, which needs no decode workspace
+    # for short contexts.
+    assert L.vapi_paged_attention_workspace_size(one, 64, 17, 1, 64) == 0

@@ -179,9 +179,17 @@ CASES = [
     (torch.bfloat16, 32, 8, 128, 64, [1, 20, 1], [1000, 200, 65], None, "HND"),
     (torch.float16, 16, 4, 64, 128, [1, 33, 1], [700, 300, 129], 50, "NHD"),
     (torch.bfloat16, 8, 8, 128, 256, [1, 1, 17], [2000, 257, 600], None, "HND"),
-    # 16-bit pools the MFMA paths do not take, on the generic kernel: more
-    # than 16 query heads per kv head, head_dim 256, block_size 8.
+    # More than 16 query heads per kv head: the decode splits each group
+    # into 2 or 4 virtual kv heads of at most 16 (G = 32, 24, 48, 64); the
+    # prefill rows take them as they are. G = 17 has no such split and runs
+    # the generic kernel.
     (torch.bfloat16, 32, 1, 128, 16, [1, 9, 1], [300, 40, 77], None, "HND"),
+    (torch.float16, 48, 2, 64, 16, [1, 1, 20, 1], [700, 2000, 200, 33], 100, "NHD"),
+    (torch.bfloat16, 48, 1, 128, 32, [1, 1, 1], [4000, 1, 650], None, "HND"),
+    (torch.bfloat16, 64, 1, 128, 16, [1, 5, 1], [1500, 900, 64], 300, "HND"),
+    (torch.bfloat16, 17, 1, 128, 16, [1, 4, 1], [500, 60, 1000], None, "HND"),
+    # 16-bit pools the MFMA paths do not take, on the generic kernel:
+    # head_dim 256, block_size 8.
     (torch.float16, 8, 4, 256, 16, [1, 6], [500, 70], 30, "NHD"),
     (torch.bfloat16, 16, 8, 128, 8, [1, 12], [210, 50], None, "HND"),
     # The VALU kernel's split contexts (more than 512 visible keys: chunks
@@ -316,6 +324,9 @@ F32_DECODE_CASES = [
     (64, 4, 128, 16, [48, 700, 1201], None, "HND"),
     (8, 8, 128, 64, [65, 1000, 129, 2], 40, "NHD"),
     (12, 4, 64, 16, [300] * 40, None, "HND"),
+    # G = 32 and 64 (two and four virtual kv heads of 16 query heads)
+    (32, 1, 128, 16, [1, 700, 2500], None, "HND"),
+    (64, 1, 64, 16, [90, 3000], 50, "NHD"),
 ]
 
 

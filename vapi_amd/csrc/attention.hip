@@ -3,7 +3,8 @@
 //  * the persistent MFMA decode stream (attn_decode.hip) for decode rows,
 //  * the MFMA prefill kernel (attn_prefill.hip) for prefill rows,
 // when the pool is bf16/f16 with head_dim 64 or 128, a power-of-two
-// block_size >= 16 and at most 16 query heads per kv head; an f32 pool of
+// block_size >= 16 and at most 16 query heads per kv head (up to 64 when a
+// split into 2 or 4 equal groups of at most 16 exists); an f32 pool of
 // that shape runs the decode stream on f32 MFMAs when every row is a decode
 // row; every other shape runs the VALU kernel (attn_generic.hip).
 // Replaces paged_attention_cuda/_windowed/_prepared (vapi
@@ -14,6 +15,16 @@
 
 namespace vk {
 
+// The decode's MFMA tile has 16 query-head columns: a group of G > 16
+// query heads per kv head runs as 2^s virtual kv heads of G / 2^s heads
+// each (each reading its pool head's K/V). The shift s, or -1 when G has
+// no such split (G > 64, or not a multiple of 2^s).
+static int decode_group_shift(uint32_t G) {
+  for (int s = 0; s <= 2; ++s)
+    if ((G >> s) <= 16 && (G & ((1u << s) - 1)) == 0 && (G >> s) >= 1) return s;
+  return -1;
+}
+
 // An f32 pool's pure-decode call (every row len_q == 1) runs the decode
 // stream on v_mfma_f32_16x16x4_f32; any prefill row sends the call to the
 // VALU kernel.
@@ -22,16 +33,23 @@ static bool f32_decode_ok(const vapi_kv_pool* p, uint32_t num_heads, uint32_t ma
   if (p->head_dim != 64 && p->head_dim != 128) return false;
   if (p->block_size < 16 || (p->block_size & (p->block_size - 1))) return false;
   if (num_heads == 0 || num_heads % p->num_kv_heads) return false;
-  const uint32_t G = num_heads / p->num_kv_heads;
-  return G >= 1 && G <= 16;
+  return decode_group_shift(num_heads / p->num_kv_heads) >= 0;
 }
 
 static bool mfma_ok(const vapi_kv_pool* p, uint32_t num_heads) {
   if (p->dtype != VAPI_KV_BF16 && p->dtype != VAPI_KV_F16) return false;
   if (p->head_dim != 64 && p->head_dim != 128) return false;
   if (p->block_size < 16 || (p->block_size & (p->block_size - 1))) return false;
+  if (num_heads == 0 || num_heads % p->num_kv_heads) return false;
+  return decode_group_shift(num_heads / p->num_kv_heads) >= 0;
+}
+
+// The decode's view of the kv heads (virtual ones when G > 16).
+static size_t decode_ws_for(const vapi_kv_pool* p, uint32_t batch, uint32_t num_heads) {
   const uint32_t G = num_heads / p->num_kv_heads;
-  return G >= 1 && G <= 16;
+  const int sh = decode_group_shift(G);
+  return decode_workspace_bytes(batch, p->num_kv_heads << sh, G >> sh, p->head_dim,
+                                decode_num_waves());
 }
 
 // The sequences with prefill rows, named by the host (vapi_paged_attention_prepared).
@@ -129,15 +147,11 @@ static size_t required_workspace(const vapi_kv_pool* pool, uint32_t batch, uint3
       num_heads == 0)
     return 0;
   const uint32_t group = num_heads / pool->num_kv_heads;
-  if (f32_decode_ok(pool, num_heads, max_seqlen_q))
-    return decode_workspace_bytes(batch, pool->num_kv_heads, group, pool->head_dim,
-                                  decode_num_waves());
+  if (f32_decode_ok(pool, num_heads, max_seqlen_q)) return decode_ws_for(pool, batch, num_heads);
   if (!mfma_ok(pool, num_heads))
     return generic_workspace_bytes(batch, pool->num_kv_heads, group, pool->head_dim,
                                    std::max(max_seqlen_q, 1u), max_seqlen_k);
-  return skip_decode ? 0
-                     : decode_workspace_bytes(batch, pool->num_kv_heads, group, pool->head_dim,
-                                              decode_num_waves());
+  return skip_decode ? 0 : decode_ws_for(pool, batch, num_heads);
 }
 
 extern "C" {
@@ -250,7 +264,8 @@ int vapi_paged_attention_append_ex(const vapi_kv_pool* pool, uint32_t layer, con
   if (int rc = check_pool(pool, "vapi_paged_attention_append")) return rc;
   if (!pool->v) VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention_append: a K-only pool has no V to attend over");
   const bool fused = n_tokens > 0 && batch > 0 && max_seqlen_q == 1 && num_heads > 0 &&
-                     num_heads % pool->num_kv_heads == 0 && mfma_ok(pool, num_heads);
+                     num_heads % pool->num_kv_heads == 0 && mfma_ok(pool, num_heads) &&
+                     num_heads / pool->num_kv_heads <= 16;
   if (!fused) {
     if (int rc = vapi_kv_append(pool, layer, k_src, v_src, slot_mapping, n_tokens, stream))
       return rc;
@@ -392,7 +407,17 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   a.pf_min_q = 2;
   a.pf_seqs = listed ? pf->seqs : nullptr;
   a.pf_seqs_n = pf_n;
+  a.kv_shift = 0;
   const hipStream_t s = hs(stream);
+  // The decode kernels' arguments: with G > 16 query heads per kv head, the
+  // virtual kv heads of at most 16 query heads each.
+  const int gsh = decode_group_shift(a.group);
+  AttnArgs dec = a;
+  if (gsh > 0) {
+    dec.kvh = a.kvh << gsh;
+    dec.group = a.group >> gsh;
+    dec.kv_shift = (uint32_t)gsh;
+  }
 
   if (mfma_ok(pool, num_heads)) {
     const bool bf16 = pool->dtype == VAPI_KV_BF16;
@@ -402,7 +427,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
     // Decode rows and prefill rows in one step: both kernels in one launch.
     // (At most 4,000 sequences: the launch's dynamic LDS, 4 bytes per
     // sequence, then still lets a decode and a prefill workgroup share a CU.)
-    const bool mixed = !skip_decode && !fuse && max_seqlen_q > 1 && pf_n > 0 &&
+    const bool mixed = !skip_decode && !fuse && gsh == 0 && max_seqlen_q > 1 && pf_n > 0 &&
                        batch <= std::min(decode_max_plan_seqs(), 4000u) &&
                        mixed_prefill_items(pf_n, g.kvh, num_heads / g.kvh, max_seqlen_q) <
                            (1ull << 30);
@@ -412,8 +437,12 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
       VK_LAUNCHED("paged_attention");
       return 0;
     }
-    if (skip_decode) a.pf_min_q = 1;
-    else launch_decode(a, workspace, g.d, pool->dtype, s);
+    if (skip_decode) {
+      a.pf_min_q = 1;
+    } else {
+      dec.num_waves = a.num_waves;
+      launch_decode(dec, workspace, g.d, pool->dtype, s);
+    }
     if (max_seqlen_q > 1 && pf_n > 0) {
       // The workspace past the decode's part serves the prefill's key split
       // (never its first 256 bytes, which carry the decode's XCD shares
@@ -422,8 +451,8 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
                      room ? (char*)workspace + off : nullptr, room ? workspace_bytes - off : 0, s);
     }
   } else if (f32_decode_ok(pool, num_heads, max_seqlen_q)) {
-    a.num_waves = decode_num_waves();
-    launch_decode(a, workspace, g.d, pool->dtype, s);
+    dec.num_waves = decode_num_waves();
+    launch_decode(dec, workspace, g.d, pool->dtype, s);
   } else {
     if (g.d > 256)
       VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: head_dim %u > 256", g.d);

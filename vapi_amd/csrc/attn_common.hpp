@@ -70,6 +70,10 @@ struct AttnArgs {
   // batch - 1); the host names the sequences with prefill rows.
   const uint32_t* pf_seqs;
   uint32_t pf_seqs_n;
+  // decode: more than 16 query heads per kv head run as 2^kv_shift virtual
+  // kv heads of G / 2^kv_shift query heads each (kvh and group then count
+  // the virtual ones); virtual head v reads the K/V of pool head v >> kv_shift.
+  uint32_t kv_shift;
 };
 
 __device__ __forceinline__ void key_range(int32_t p, int32_t len_k, int32_t wl,

@@ -207,7 +207,7 @@ __device__ __forceinline__ void load_step_k(KTile<D>& st, const AttnArgs& a,
                                             const uint32_t* __restrict__ table,
                                             const DecodePos& p, uint32_t col, uint32_t g) {
   const uint32_t* __restrict__ tab = table + (uint64_t)p.seq * a.max_blocks;
-  const T* kb = (const T*)a.k + p.kh * a.head_e;
+  const T* kb = (const T*)a.k + (p.kh >> a.kv_shift) * a.head_e;
   const char* knew =
       p.fuse ? a.k_new + ((uint64_t)p.q0 * a.kvh + p.kh) * D * sizeof(T) : nullptr;
   load_k<T, D>(st, tab, kb, a, p.key0, p.len_k - 1, col, g, knew);
@@ -218,7 +218,7 @@ __device__ __forceinline__ void load_step_v(VTile<D>& st, const AttnArgs& a,
                                             const uint32_t* __restrict__ table,
                                             const DecodePos& p, uint32_t col, uint32_t g) {
   const uint32_t* __restrict__ tab = table + (uint64_t)p.seq * a.max_blocks;
-  const T* vb = (const T*)a.v + p.kh * a.head_e;
+  const T* vb = (const T*)a.v + (p.kh >> a.kv_shift) * a.head_e;
   const char* vnew =
       p.fuse ? a.v_new + ((uint64_t)p.q0 * a.kvh + p.kh) * D * sizeof(T) : nullptr;
   load_v<T, D>(st, tab, vb, a, p.key0, p.len_k - 1, col, g, vnew);
@@ -378,7 +378,8 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
   auto load_halves = [&](KTileF32<D>& kt, VTileF32<D>& vt, const DecodePos& p, int tt)
       __attribute__((always_inline)) {
     load_half_f32<D>(kt.h[tt], vt.h[tt], table + (uint64_t)p.seq * a.max_blocks,
-                     kbf + p.kh * a.head_e, vbf + p.kh * a.head_e, a, p.key0, tt, p.len_k - 1,
+                     kbf + (p.kh >> a.kv_shift) * a.head_e, vbf + (p.kh >> a.kv_shift) * a.head_e,
+                     a, p.key0, tt, p.len_k - 1,
                      col, g);
   };
   if constexpr (kF32) {
