@@ -177,7 +177,8 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
  * paged_attention_cpu (attention.rs:90-163) as the numerical contract.
  *
  * q:   device [cu_seqlens_q[batch], num_heads, head_dim], pool dtype.
- * out: device, same shape and dtype as q.
+ * out: device, same shape and dtype as q. q and out must be 16-byte aligned
+ *   (the kernels move 16-byte chunks of their rows); VAPI_KV_EINVAL otherwise.
  * cu_seqlens_q, cu_seqlens_k: device u32[batch+1]; len_k includes the cached
  *   prefix and len_q <= len_k. Query j of a sequence sits at absolute
  *   position p = len_k - len_q + j (bottom-right aligned).

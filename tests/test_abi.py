@@ -52,13 +52,13 @@ def test_bad_arguments_are_errors_not_crashes():
     assert b"flags" in L.vapi_kv_last_error()
     assert L.vapi_kv_gather(pool(), 0, 1, 2, 33, 1, 1, None) == _lib.EINVAL
     assert b"exceeds" in L.vapi_kv_last_error()
-    args = [1, 1, 1, 1, 1, 2, 4, 1, 100, 5, 0.1, -1, 0, None, 0, None]
+    args = [16, 16, 16, 16, 16, 2, 4, 1, 100, 5, 0.1, -1, 0, None, 0, None]
     assert L.vapi_paged_attention(pool(), 0, *args) == _lib.EINVAL
     assert b"multiple" in L.vapi_kv_last_error()
     # Workspace too small for a split-K decode.
     need = L.vapi_paged_attention_workspace_size(pool(), 2, 8, 1, 5000)
     assert need > 0
-    args = [1, 1, 1, 1, 1, 2, 320, 1, 5000, 8, 0.1, -1, 0, None, 0, None]
+    args = [16, 16, 16, 16, 16, 2, 320, 1, 5000, 8, 0.1, -1, 0, None, 0, None]
     assert L.vapi_paged_attention(pool(), 0, *args) == _lib.ESPACE
     assert L.vapi_kv_copy_blocks(pool(num_layers=2, layer_stride_bytes=16), 1, 1, None) == _lib.EINVAL
     assert L.vapi_kv_swap_out(pool(), 1, 1, 1, 1, 10, None) == _lib.ESPACE
@@ -70,11 +70,11 @@ def test_bad_arguments_are_errors_not_crashes():
     assert b"stride" in L.vapi_kv_last_error()
     assert L.vapi_kv_append_layers(two, 1, 1, 1, 1, 0, 1, 0, None) == _lib.OK
     # Fused append + attention: the append's and the attention's errors.
-    args = [1, 1, 1, 1, 1, 1, 2, 4, 1, 100, 8, 0.1, -1, 0, None, 0, None]
+    args = [16, 16, 16, 16, 16, 1, 2, 4, 1, 100, 8, 0.1, -1, 0, None, 0, None]
     assert L.vapi_paged_attention_append(pool(dtype=9), 0, 1, 1, 1, *args) == _lib.EINVAL
     assert L.vapi_paged_attention_append(pool(), 0, None, 1, 1, *args) == _lib.EINVAL
     assert b"null source" in L.vapi_kv_last_error()
-    args = [1, 1, 1, 1, 1, 1, 2, 320, 1, 5000, 8, 0.1, -1, 0, None, 0, None]
+    args = [16, 16, 16, 16, 16, 1, 2, 320, 1, 5000, 8, 0.1, -1, 0, None, 0, None]
     assert L.vapi_paged_attention_append(pool(), 0, 1, 1, 1, *args) == _lib.ESPACE
 
 
@@ -90,12 +90,16 @@ def test_misaligned_pools_and_unknown_flags_are_refused():
     assert L.vapi_kv_copy_blocks(two, 1, 1, None) == _lib.EINVAL
     assert b"multiple of 16" in L.vapi_kv_last_error()
     assert L.vapi_kv_export_blocks(two, 1, 1, 1, None) == _lib.EINVAL
-    args = [1, 1, 1, 1, 1, 2, 4, 1, 100, 8, 0.1, -1, 0]
+    args = [16, 16, 16, 16, 16, 2, 4, 1, 100, 8, 0.1, -1, 0]
     assert L.vapi_paged_attention_ex(pool(), 0, *args, 0x80, None, 0, None) == _lib.EINVAL
     assert b"flags" in L.vapi_kv_last_error()
+    # q and out rows are moved in 16-byte chunks.
+    for bad in ([24] + args[1:], args[:1] + [8] + args[2:]):
+        assert L.vapi_paged_attention_ex(pool(), 0, *bad, 0, None, 0, None) == _lib.EINVAL
+        assert b"16-byte aligned" in L.vapi_kv_last_error()
     # The flags call keeps vapi_paged_attention's own checks.
     need = L.vapi_paged_attention_workspace_size(pool(), 2, 8, 1, 5000)
-    args = [1, 1, 1, 1, 1, 2, 320, 1, 5000, 8, 0.1, -1, 0]
+    args = [16, 16, 16, 16, 16, 2, 320, 1, 5000, 8, 0.1, -1, 0]
     assert L.vapi_paged_attention_ex(pool(), 0, *args, _lib.ATTN_DETERMINISTIC, None, 0,
                                      None) == _lib.ESPACE
     assert need > 0
@@ -108,7 +112,7 @@ def test_the_prepared_call_checks_its_prefill_list_and_sizes_its_split():
     512-token chunk splits that chunk; counted over all 64 sequences it would
     not)."""
     L = _lib.lib()
-    args = [1, 1, 1, 1, 1, 2, 4, 512, 2048, 32, 0.1, -1, 0, 0]
+    args = [16, 16, 16, 16, 16, 2, 4, 512, 2048, 32, 0.1, -1, 0, 0]
     assert L.vapi_paged_attention_prepared(pool(), 0, *args, 1, 3, None, 0,
                                            None) == _lib.EINVAL
     assert b"prefill sequences" in L.vapi_kv_last_error()
@@ -133,12 +137,12 @@ def test_launches_too_large_for_one_grid_are_refused():
     refused before anything is launched, not truncated."""
     L = _lib.lib()
     # MFMA prefill: 65,535 sequences x 2^24 query rows x 4 heads per group.
-    args = [1, 1, 1, 1, 1, 65535, 1, 1 << 24, 1 << 24, 8, 0.1, -1, 0]
+    args = [16, 16, 16, 16, 16, 65535, 1, 1 << 24, 1 << 24, 8, 0.1, -1, 0]
     assert L.vapi_paged_attention_ex(pool(), 0, *args, _lib.ATTN_NO_DECODE_ROWS, None, 0,
                                      None) == _lib.EUNSUP
     assert b"too large" in L.vapi_kv_last_error()
     # VALU path (f32 pool): row tiles x kv heads x sequences x key chunks.
-    args = [1, 1, 1, 1, 1, 60000, 1, 1 << 20, 1 << 20, 8, 0.1, -1, 0]
+    args = [16, 16, 16, 16, 16, 60000, 1, 1 << 20, 1 << 20, 8, 0.1, -1, 0]
     assert L.vapi_paged_attention_ex(pool(dtype=_lib.F32), 0, *args, 0, 1, 1 << 62,
                                      None) == _lib.EUNSUP
     assert b"too large" in L.vapi_kv_last_error()

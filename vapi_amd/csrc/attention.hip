@@ -331,6 +331,8 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   if (batch == 0 || max_seqlen_q == 0) return 0;
   if (!q || !out || !cu_seqlens_q || !cu_seqlens_k || !block_table)
     VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: null device pointer");
+  if (((uintptr_t)q | (uintptr_t)out) & 15)
+    VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: q and out must be 16-byte aligned");
   if (pool->num_blocks == 0 && max_seqlen_k > 0)
     VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: keys to attend over in an empty pool");
   if (max_blocks == 0)
