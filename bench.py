@@ -481,6 +481,46 @@ def bench_wide_group(steps, warmup):
                 gbs_read=2 * kv / (gms * 1e-3) / 1e9)
 
 
+def bench_head_dim_256(steps, warmup):
+    """Config 2's batch (32 query / 8 kv heads) with head_dim 256 on a bf16
+    pool: the decode stream at twice config 2's K/V bytes per key."""
+    w = workload.config2_decode()
+    layers = 2
+    cache = PagedKvCache(layers, w.num_blocks, w.block_size, 8, 256, torch.bfloat16, "HND")
+    workload.fill_normal(cache._slab, workload.seed_for(2))
+    q = torch.randn(w.batch, 32, 256, device=DEV).to(torch.bfloat16)
+    batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
+                         block_tables=[t.tolist() for t in w.tables], max_seqlen_q=1,
+                         max_seqlen_k=int(w.lens.max()))
+    prep = PreparedAttention.from_batch(batch, DEV)
+    out = torch.empty_like(q)
+    turn = [0]
+
+    def call():
+        paged_attention_prepared(q, cache, turn[0] % layers, prep, 256 ** -0.5, out=out)
+        turn[0] += 1
+
+    gms = timed_graph(call, steps, warmup)
+    kv = int(w.lens.sum()) * 8 * 256 * 2 * 2
+    # The same rows declared with max_seqlen_q = 2 run the VALU kernel (the
+    # path every head_dim-256 call took before the decode stream took them).
+    batch2 = ForwardBatch(cu_seqlens_q=batch.cu_seqlens_q, cu_seqlens_k=batch.cu_seqlens_k,
+                          block_tables=batch.block_tables, max_seqlen_q=2,
+                          max_seqlen_k=batch.max_seqlen_k)
+    prep2 = PreparedAttention.from_batch(batch2, DEV)
+
+    def call_valu():
+        paged_attention_prepared(q, cache, turn[0] % layers, prep2, 256 ** -0.5, out=out)
+        turn[0] += 1
+
+    vms = timed_graph(call_valu, max(steps // 5, 3), 2, replays=3)
+    log(f"decode cfg2 batch, head_dim 256: {gms * 1e3:.1f} us, "
+        f"{kv / (gms * 1e-3) / 1e9:.0f} GB/s of K/V (VALU kernel: {vms * 1e3:.1f} us)")
+    del cache, q, out
+    return dict(us=gms * 1e3, kv_bytes=kv, gbs=kv / (gms * 1e-3) / 1e9,
+                frac_of_8tbs=kv / (gms * 1e-3) / 8e12, valu_us=vms * 1e3)
+
+
 # ---- config 1: append --------------------------------------------------------------
 
 def bench_append(steps, warmup):
@@ -1115,7 +1155,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", choices=["decode", "append", "prefill", "copy", "blocks", "valu",
-                                       "mixed"],
+                                       "mixed", "shapes"],
                     default=None)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate", action="store_true",
@@ -1148,6 +1188,11 @@ def main():
     if args.only == "valu":
         bench_valu(args.steps, args.warmup)
         return
+    if args.only == "shapes":
+        bench_head_dim_64(args.steps, args.warmup)
+        bench_wide_group(args.steps, args.warmup)
+        bench_head_dim_256(args.steps, args.warmup)
+        return
     if args.only == "mixed":
         bench_mixed_step(setup_decode(), args.steps, args.warmup)
         return
@@ -1168,6 +1213,7 @@ def main():
         extras["f32_attention"] = bench_valu(args.steps, args.warmup)
         extras["head_dim_64"] = bench_head_dim_64(args.steps, args.warmup)
         extras["wide_group_g32"] = bench_wide_group(args.steps, args.warmup)
+        extras["head_dim_256"] = bench_head_dim_256(args.steps, args.warmup)
         extras["decode_small_batches"] = bench_small_batches(args.steps, args.warmup)
         extras["prefill_small_batches"] = bench_small_prefill(args.steps, args.warmup)
     extras["blocks_cfg4"] = bench_blocks(max(args.steps // 5, 3), 2, dec)

@@ -208,8 +208,11 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
  *   MiB) to split its keys over more workgroups. That part is optional: a
  *   workspace holding only the decode's part (or none, for a call with
  *   VAPI_ATTN_NO_DECODE_ROWS) runs the prefill unsplit, and a
- *   VAPI_ATTN_DETERMINISTIC call never splits. On the VALU path
- *   (f32 pools, other head dims) it holds the split-context partials and
+ *   VAPI_ATTN_DETERMINISTIC call never splits. A decode-only call
+ *   (max_seqlen_q == 1) on an f32 pool with head_dim 64 or 128, or on a
+ *   bf16/f16 pool with head_dim 256, runs the decode stream and needs the
+ *   decode's part only. On the VALU path (the other calls on those pools,
+ *   other head dims) it holds the split-context partials and
  *   grows with the batch, max_seqlen_q and max_seqlen_k (0 while
  *   max_seqlen_k <= 64; small batches split their keys into chunks of 64
  *   to 512 keys to fill the GPU).

@@ -191,6 +191,12 @@ CASES = [
     # 16-bit pools the MFMA paths do not take, on the generic kernel:
     # head_dim 256, block_size 8.
     (torch.float16, 8, 4, 256, 16, [1, 6], [500, 70], 30, "NHD"),
+    # head_dim 256 decode-only batches on the MFMA decode stream (G = 4, 1,
+    # 8 and 32 as two virtual kv heads; windows; both layouts).
+    (torch.bfloat16, 32, 8, 256, 16, [1, 1, 1, 1, 1], [1, 17, 600, 1500, 4000], None, "HND"),
+    (torch.float16, 8, 8, 256, 32, [1, 1, 1], [65, 2100, 31], 40, "NHD"),
+    (torch.bfloat16, 16, 2, 256, 64, [1, 0, 1], [3000, 9, 129], None, "NHD"),
+    (torch.bfloat16, 64, 2, 256, 16, [1, 1], [900, 2500], 300, "HND"),
     (torch.bfloat16, 16, 8, 128, 8, [1, 12], [210, 50], None, "HND"),
     # The VALU kernel's split contexts (more than 512 visible keys: chunks
     # combined by its merge), odd head dims on its scalar dot path.
