@@ -482,8 +482,9 @@ def bench_wide_group(steps, warmup):
 
 
 def bench_head_dim_256(steps, warmup):
-    """Config 2's batch (32 query / 8 kv heads) with head_dim 256 on a bf16
-    pool: the decode stream at twice config 2's K/V bytes per key."""
+    """Configs 2 and 3 with head_dim 256 (32 q / 8 kv heads of 256) on bf16
+    pools: the decode stream at twice config 2's K/V bytes per key, and the
+    prefill (one 16-row tile per wave) at twice config 3's FLOPs."""
     w = workload.config2_decode()
     layers = 2
     cache = PagedKvCache(layers, w.num_blocks, w.block_size, 8, 256, torch.bfloat16, "HND")
@@ -502,23 +503,27 @@ def bench_head_dim_256(steps, warmup):
 
     gms = timed_graph(call, steps, warmup)
     kv = int(w.lens.sum()) * 8 * 256 * 2 * 2
-    # The same rows declared with max_seqlen_q = 2 run the VALU kernel (the
-    # path every head_dim-256 call took before the decode stream took them).
-    batch2 = ForwardBatch(cu_seqlens_q=batch.cu_seqlens_q, cu_seqlens_k=batch.cu_seqlens_k,
-                          block_tables=batch.block_tables, max_seqlen_q=2,
-                          max_seqlen_k=batch.max_seqlen_k)
-    prep2 = PreparedAttention.from_batch(batch2, DEV)
-
-    def call_valu():
-        paged_attention_prepared(q, cache, turn[0] % layers, prep2, 256 ** -0.5, out=out)
-        turn[0] += 1
-
-    vms = timed_graph(call_valu, max(steps // 5, 3), 2, replays=3)
-    log(f"decode cfg2 batch, head_dim 256: {gms * 1e3:.1f} us, "
-        f"{kv / (gms * 1e-3) / 1e9:.0f} GB/s of K/V (VALU kernel: {vms * 1e3:.1f} us)")
+    res = {"decode_cfg2_d256": dict(us=gms * 1e3, kv_bytes=kv, gbs=kv / (gms * 1e-3) / 1e9,
+                                    frac_of_8tbs=kv / (gms * 1e-3) / 8e12)}
     del cache, q, out
-    return dict(us=gms * 1e3, kv_bytes=kv, gbs=kv / (gms * 1e-3) / 1e9,
-                frac_of_8tbs=kv / (gms * 1e-3) / 8e12, valu_us=vms * 1e3)
+    p = workload.config3_prefill()
+    cache = PagedKvCache(1, p.num_blocks, p.block_size, 8, 256, torch.bfloat16, "HND")
+    workload.fill_normal(cache._slab, workload.seed_for(3))
+    q = torch.randn(p.batch * p.len_q, 32, 256, device=DEV).to(torch.bfloat16)
+    batch = ForwardBatch(cu_seqlens_q=p.cu_q().tolist(), cu_seqlens_k=p.cu_k().tolist(),
+                         block_tables=[t.tolist() for t in p.tables], max_seqlen_q=p.len_q,
+                         max_seqlen_k=p.len_k)
+    prep = PreparedAttention.from_batch(batch, DEV)
+    out = torch.empty_like(q)
+    ms, _ = timed(lambda: paged_attention_prepared(q, cache, 0, prep, 256 ** -0.5, out=out),
+                  max(steps, 10), 30)
+    flops = p.flops() * 2  # head_dim 256
+    res["prefill_cfg3_d256"] = dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12)
+    log("head_dim 256: decode cfg2 {:.1f} us ({:.0f} GB/s), prefill cfg3 {:.3f} ms ({:.0f} "
+        "TFLOP/s)".format(res["decode_cfg2_d256"]["us"], res["decode_cfg2_d256"]["gbs"], ms,
+                          res["prefill_cfg3_d256"]["tflops"]))
+    del cache, q, out
+    return res
 
 
 # ---- config 1: append --------------------------------------------------------------

@@ -202,17 +202,17 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
  *   or ordered streams).
  * max_seqlen_q/k must bound every sequence's len_q/len_k (as in
  *   flash-attention); max_seqlen_q sizes the prefill grid. On the MFMA path
- *   (bf16/f16, head_dim 64 or 128) the decode's part depends on the batch,
+ *   (bf16/f16, head_dim 64, 128 or 256) the decode's part depends on the batch,
  *   the heads and the GPU's CU count, not on the lengths; a prefill batch
  *   with fewer query tiles than the GPU has CUs asks for more (up to 256
  *   MiB) to split its keys over more workgroups. That part is optional: a
  *   workspace holding only the decode's part (or none, for a call with
  *   VAPI_ATTN_NO_DECODE_ROWS) runs the prefill unsplit, and a
  *   VAPI_ATTN_DETERMINISTIC call never splits. A decode-only call
- *   (max_seqlen_q == 1) on an f32 pool with head_dim 64 or 128, or on a
- *   bf16/f16 pool with head_dim 256, runs the decode stream and needs the
- *   decode's part only. On the VALU path (the other calls on those pools,
- *   other head dims) it holds the split-context partials and
+ *   (max_seqlen_q == 1) on an f32 pool with head_dim 64 or 128 runs the
+ *   decode stream and needs the decode's part only. On the VALU path (f32
+ *   calls with prefill rows, other head dims) it holds the split-context
+ *   partials and
  *   grows with the batch, max_seqlen_q and max_seqlen_k (0 while
  *   max_seqlen_k <= 64; small batches split their keys into chunks of 64
  *   to 512 keys to fill the GPU).
@@ -325,7 +325,7 @@ int vapi_paged_attention_noalloc(const vapi_kv_pool* pool, uint32_t layer, const
  * write, then the attention: models/qwen.rs:371-391, models/llama.rs:157-165).
  *
  * When every row is a decode row (max_seqlen_q == 1) on the MFMA path
- * (bf16/f16, head_dim 64 or 128), it takes one launch fewer: the attention
+ * (bf16/f16, head_dim 64, 128 or 256), it takes one launch fewer: the attention
  * reads the new key of row s (position len_k - 1) straight from token
  * cu_seqlens_q[s] of k_src/v_src, provided slot_mapping sends that token to
  * the slot the row's block table gives position len_k - 1 (checked per row

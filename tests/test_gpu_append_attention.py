@@ -90,6 +90,8 @@ STEPS = [
     (torch.float16, 16, 8, 128, 32, [1, 1, 1], [1100, 40, 513], 100, "HND"),
     (torch.bfloat16, 8, 8, 64, 16, [1, 1], [900, 100], None, "NHD"),
     (torch.bfloat16, 64, 4, 64, 32, [1, 1, 1], [70, 64, 2], 9, "NHD"),
+    (torch.bfloat16, 16, 4, 256, 16, [1, 1, 1], [900, 31, 2], None, "HND"),
+    (torch.float16, 8, 2, 256, 32, [1, 1], [64, 1300], 50, "NHD"),
     # Prefill rows in the batch: the two calls run inside.
     (torch.bfloat16, 32, 8, 128, 16, [1, 37, 1], [700, 37, 33], None, "HND"),
     (torch.float32, 16, 8, 128, 16, [1, 1], [64, 512], None, "HND"),

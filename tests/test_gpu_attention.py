@@ -188,22 +188,25 @@ CASES = [
     (torch.bfloat16, 48, 1, 128, 32, [1, 1, 1], [4000, 1, 650], None, "HND"),
     (torch.bfloat16, 64, 1, 128, 16, [1, 5, 1], [1500, 900, 64], 300, "HND"),
     (torch.bfloat16, 17, 1, 128, 16, [1, 4, 1], [500, 60, 1000], None, "HND"),
-    # 16-bit pools the MFMA paths do not take, on the generic kernel:
-    # head_dim 256, block_size 8.
+    # head_dim 256 on the MFMA kernels (one 16-row tile per prefill wave):
+    # decode-only batches (G = 4, 1, 8, and 32 as two virtual kv heads) and
+    # batches with prefill rows (decode and prefill launched separately).
     (torch.float16, 8, 4, 256, 16, [1, 6], [500, 70], 30, "NHD"),
-    # head_dim 256 decode-only batches on the MFMA decode stream (G = 4, 1,
-    # 8 and 32 as two virtual kv heads; windows; both layouts).
     (torch.bfloat16, 32, 8, 256, 16, [1, 1, 1, 1, 1], [1, 17, 600, 1500, 4000], None, "HND"),
     (torch.float16, 8, 8, 256, 32, [1, 1, 1], [65, 2100, 31], 40, "NHD"),
     (torch.bfloat16, 16, 2, 256, 64, [1, 0, 1], [3000, 9, 129], None, "NHD"),
     (torch.bfloat16, 64, 2, 256, 16, [1, 1], [900, 2500], 300, "HND"),
+    (torch.bfloat16, 32, 8, 256, 16, [64, 1, 200, 17], [1000, 300, 200, 900], None, "HND"),
+    (torch.float16, 64, 2, 256, 32, [33, 1, 5], [700, 1200, 5], 100, "NHD"),
+    # A 16-bit pool the MFMA paths do not take, on the generic kernel:
+    # block_size 8.
     (torch.bfloat16, 16, 8, 128, 8, [1, 12], [210, 50], None, "HND"),
     # The VALU kernel's split contexts (more than 512 visible keys: chunks
     # combined by its merge), odd head dims on its scalar dot path.
     (torch.float32, 12, 4, 80, 16, [1, 20, 1], [3000, 1500, 700], None, "HND"),
     (torch.float32, 4, 2, 3, 4, [1, 5], [1100, 600], 100, "NHD"),
     (torch.float32, 8, 8, 128, 16, [1, 37], [2100, 1100], 700, "HND"),
-    (torch.bfloat16, 16, 4, 256, 16, [1, 9], [2000, 800], None, "HND"),
+    (torch.float32, 16, 4, 256, 16, [1, 9], [2000, 800], None, "HND"),
     # More head dims the VALU kernel compiles as constants (96, 32), and a
     # block size that is not a power of two.
     (torch.bfloat16, 16, 4, 96, 16, [1, 7], [900, 130], None, "HND"),
@@ -540,6 +543,8 @@ SPLIT_CASES = [
     # 5 query tiles x 4 kv heads: 13 splits, merged in a batch of eight and
     # a partial batch of five.
     (torch.bfloat16, 16, 4, 128, 16, [320], [4000], None, "HND"),
+    (torch.bfloat16, 16, 4, 256, 16, [100, 1], [3000, 2000], None, "HND"),
+    (torch.float16, 8, 8, 256, 32, [48], [2500], 900, "NHD"),
 ]
 
 

@@ -2,11 +2,11 @@
 // and chunked-prefill rows (len_q > 1), dispatched to
 //  * the persistent MFMA decode stream (attn_decode.hip) for decode rows,
 //  * the MFMA prefill kernel (attn_prefill.hip) for prefill rows,
-// when the pool is bf16/f16 with head_dim 64 or 128, a power-of-two
+// when the pool is bf16/f16 with head_dim 64, 128 or 256, a power-of-two
 // block_size >= 16 and at most 16 query heads per kv head (up to 64 when a
 // split into 2 or 4 equal groups of at most 16 exists); an f32 pool of
-// that shape, and a 16-bit pool with head_dim 256, run the decode stream
-// when every row is a decode row; every other shape runs the VALU kernel
+// that shape (head_dim 64 or 128) runs the decode stream on f32 MFMAs when
+// every row is a decode row; every other shape runs the VALU kernel
 // (attn_generic.hip).
 // Replaces paged_attention_cuda/_windowed/_prepared (vapi
 // crates/vapi-backend-candle/src/attention.rs:170-288).
@@ -26,18 +26,12 @@ static int decode_group_shift(uint32_t G) {
   return -1;
 }
 
-// Pure-decode calls (every row len_q == 1) that only the decode stream
-// takes: an f32 pool with head_dim 64 or 128 (on v_mfma_f32_16x16x4_f32)
-// and a 16-bit pool with head_dim 256 (the prefill kernel's LDS ring has no
-// room for 256-wide rows); any prefill row sends such a call to the VALU
-// kernel.
-static bool decode_only_ok(const vapi_kv_pool* p, uint32_t num_heads, uint32_t max_seqlen_q) {
-  if (max_seqlen_q != 1) return false;
-  if (p->dtype == VAPI_KV_F32) {
-    if (p->head_dim != 64 && p->head_dim != 128) return false;
-  } else if (p->head_dim != 256) {
-    return false;
-  }
+// An f32 pool's pure-decode call (every row len_q == 1) runs the decode
+// stream on v_mfma_f32_16x16x4_f32; any prefill row sends the call to the
+// VALU kernel.
+static bool f32_decode_ok(const vapi_kv_pool* p, uint32_t num_heads, uint32_t max_seqlen_q) {
+  if (p->dtype != VAPI_KV_F32 || max_seqlen_q != 1) return false;
+  if (p->head_dim != 64 && p->head_dim != 128) return false;
   if (p->block_size < 16 || (p->block_size & (p->block_size - 1))) return false;
   if (num_heads == 0 || num_heads % p->num_kv_heads) return false;
   return decode_group_shift(num_heads / p->num_kv_heads) >= 0;
@@ -45,7 +39,7 @@ static bool decode_only_ok(const vapi_kv_pool* p, uint32_t num_heads, uint32_t m
 
 static bool mfma_ok(const vapi_kv_pool* p, uint32_t num_heads) {
   if (p->dtype != VAPI_KV_BF16 && p->dtype != VAPI_KV_F16) return false;
-  if (p->head_dim != 64 && p->head_dim != 128) return false;
+  if (p->head_dim != 64 && p->head_dim != 128 && p->head_dim != 256) return false;
   if (p->block_size < 16 || (p->block_size & (p->block_size - 1))) return false;
   if (num_heads == 0 || num_heads % p->num_kv_heads) return false;
   return decode_group_shift(num_heads / p->num_kv_heads) >= 0;
@@ -154,7 +148,7 @@ static size_t required_workspace(const vapi_kv_pool* pool, uint32_t batch, uint3
       num_heads == 0)
     return 0;
   const uint32_t group = num_heads / pool->num_kv_heads;
-  if (decode_only_ok(pool, num_heads, max_seqlen_q)) return decode_ws_for(pool, batch, num_heads);
+  if (f32_decode_ok(pool, num_heads, max_seqlen_q)) return decode_ws_for(pool, batch, num_heads);
   if (!mfma_ok(pool, num_heads))
     return generic_workspace_bytes(batch, pool->num_kv_heads, group, pool->head_dim,
                                    std::max(max_seqlen_q, 1u), max_seqlen_k);
@@ -347,7 +341,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   if (flags & ~(uint32_t)(VAPI_ATTN_DETERMINISTIC | VAPI_ATTN_NO_DECODE_ROWS))
     VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: unknown flags 0x%x", flags);
   if (num_heads > 65535 ||
-      (batch > 65535 && !mfma_ok(pool, num_heads) && !decode_only_ok(pool, num_heads, max_seqlen_q)))
+      (batch > 65535 && !mfma_ok(pool, num_heads) && !f32_decode_ok(pool, num_heads, max_seqlen_q)))
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: batch %u / heads %u too large",
             batch, num_heads);
   // A batch the caller says has no decode rows (and which is not a fused
@@ -365,7 +359,8 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   if (mfma_ok(pool, num_heads) && max_seqlen_q > 1 && pf_n > 65535)
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: %u prefill sequences > 65535", pf_n);
   if (mfma_ok(pool, num_heads) && max_seqlen_q > 1 &&
-      prefill_grid(pf_n, pool->num_kv_heads, num_heads / pool->num_kv_heads, max_seqlen_q) >
+      prefill_grid(pf_n, pool->num_kv_heads, num_heads / pool->num_kv_heads, max_seqlen_q,
+                   pool->head_dim) >
           0xFFFFFFFFull)
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: prefill batch too large for one launch");
   const size_t need =
@@ -435,8 +430,10 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
     const bool room = workspace && workspace_bytes > off;
     // Decode rows and prefill rows in one step: both kernels in one launch.
     // (At most 4,000 sequences: the launch's dynamic LDS, 4 bytes per
-    // sequence, then still lets a decode and a prefill workgroup share a CU.)
-    const bool mixed = !skip_decode && !fuse && gsh == 0 && max_seqlen_q > 1 && pf_n > 0 &&
+    // sequence, then still lets a decode and a prefill workgroup share a CU.
+    // At head_dim 256 neither kernel fits half a CU's registers.)
+    const bool mixed = !skip_decode && !fuse && gsh == 0 && g.d != 256 && max_seqlen_q > 1 &&
+                       pf_n > 0 &&
                        batch <= std::min(decode_max_plan_seqs(), 4000u) &&
                        mixed_prefill_items(pf_n, g.kvh, num_heads / g.kvh, max_seqlen_q) <
                            (1ull << 30);
@@ -459,7 +456,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
       launch_prefill(a, max_seqlen_q, max_seqlen_k, g.d, bf16,
                      room ? (char*)workspace + off : nullptr, room ? workspace_bytes - off : 0, s);
     }
-  } else if (decode_only_ok(pool, num_heads, max_seqlen_q)) {
+  } else if (f32_decode_ok(pool, num_heads, max_seqlen_q)) {
     dec.num_waves = decode_num_waves();
     launch_decode(dec, workspace, g.d, pool->dtype, s);
   } else {

@@ -522,16 +522,17 @@ __device__ __forceinline__ void store_row_f32(float* row, const floatx4 (&o)[D /
 // ---- launchers (one per translation unit) ----------------------------------
 
 
-// Decode rows (len_q == 1) of the batch; bf16/f16/f32, head_dim 64 or 128
-// (f32: no fused append).
+// Decode rows (len_q == 1) of the batch; bf16/f16 with head_dim 64, 128 or
+// 256, f32 with head_dim 64 or 128 (f32: no fused append).
 size_t decode_workspace_bytes(uint32_t batch, uint32_t kvh, uint32_t group,
                               uint32_t head_dim, uint32_t num_waves);
 void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t dtype,
                    hipStream_t s);
-// Prefill rows (len_q > 1); same dtypes and head dims.
+// Prefill rows (len_q > 1); bf16/f16, head_dim 64, 128 or 256.
 // Workgroups of the prefill launch (query tiles x kv heads x sequences); a
 // launch needs it below 2^32.
-uint64_t prefill_grid(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t max_q);
+uint64_t prefill_grid(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t max_q,
+                      uint32_t head_dim);
 // The prefill launch over a.pf_seqs_n sequences (those a.pf_seqs names, or
 // all a.batch); with a workspace (`split_ws`, `split_ws_bytes`) a batch too
 // small to fill the GPU splits its keys over more workgroups.

@@ -138,14 +138,13 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t dtyp
     if (dtype == VAPI_KV_F32) {  // no fused append on f32 pools
       if (head_dim == 128) VK_DEC(float, 128, false);
       else VK_DEC(float, 64, false);
-    } else if (head_dim == 256) {  // decode-only calls, no fused append
-      if (bf16) VK_DEC(bf16_t, 256, false);
-      else VK_DEC(f16_t, 256, false);
     } else if (bf16) {
-      if (head_dim == 128) VK_DEC2(bf16_t, 128);
+      if (head_dim == 256) VK_DEC2(bf16_t, 256);
+      else if (head_dim == 128) VK_DEC2(bf16_t, 128);
       else VK_DEC2(bf16_t, 64);
     } else {
-      if (head_dim == 128) VK_DEC2(f16_t, 128);
+      if (head_dim == 256) VK_DEC2(f16_t, 256);
+      else if (head_dim == 128) VK_DEC2(f16_t, 128);
       else VK_DEC2(f16_t, 64);
     }
 #undef VK_DEC2

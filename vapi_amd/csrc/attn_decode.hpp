@@ -641,7 +641,7 @@ __device__ __forceinline__ void decode_merge_body(const AttnArgs& a, uint32_t nw
   const uint32_t h0 = e_lane / D, h1 = (e_lane + E - 1) / D;
   T* orow = (T*)a.out + ((uint64_t)q0 * a.num_heads + kh * G) * D;
   // Up to R ranges per round trip; E is a multiple of 4 for G*D >= 256
-  // (D is 64 or 128), so outputs move as float4.
+  // (D is 64, 128 or 256), so outputs move as float4.
   constexpr int R = WPS == 1 ? 8 : 16;
   __shared__ float cmb[WPS > 1 ? WPS : 1][3][WPS > 1 ? 64 * 8 : 1];
   for (uint32_t j0 = 0; j0 < E; j0 += 8) {

@@ -1,8 +1,9 @@
-// Chunked-prefill paged attention on MFMA (bf16/f16, head_dim 64 or 128).
+// Chunked-prefill paged attention on MFMA (bf16/f16, head_dim 64, 128, 256).
 //
 // Rows are the (query token, head) pairs of one kv head, r = j*G + h_local,
 // so the G query heads of a group share every K/V byte. A workgroup owns 256
-// rows (8 waves x 2 tiles of 16; one workgroup per CU, two waves per SIMD)
+// rows (8 waves x 2 tiles of 16; one workgroup per CU, two waves per SIMD;
+// at head_dim 256, 128 rows of one tile per wave)
 // and walks the keys they can see in 32-key steps. Each step's K and V rows
 // are copied from HBM straight into LDS by direct loads (global_load_lds:
 // no staging registers, no LDS store instructions) into a ring of three
@@ -57,10 +58,12 @@ using LdsVoid = __attribute__((address_space(3))) void;
 // use 8 distinct chunk pairs (XOR with r alone puts rows 2m and 2m + 1 on
 // the same pair). Measured 0.5-1% faster than XOR with r; the bank-conflict
 // counter reads the same either way (2 cycles per transposing read).
+// D = 256 (32 chunks, 512-byte rows): the same rotation, XORed into the
+// low four bits of the chunk index (chunks p and p ^ 16 share banks).
 // D = 64: r mod 8.
 template <int D>
 __device__ __forceinline__ uint32_t pf_swz(uint32_t r) {
-  if constexpr (D == 128) {
+  if constexpr (D >= 128) {
     const uint32_t x = r & 15;
     return ((x << 1) | (x >> 3)) & 15;
   } else {
@@ -76,9 +79,9 @@ __device__ __forceinline__ uint32_t pf_chunk(uint32_t r, uint32_t p) {
 }
 
 // Issues the step at s0 into buffer b with W waves (8, or 4 in the mixed
-// launch): each thread moves 8 / W 16-byte chunks of K and as many of V
-// (D = 128), or with 8 waves one of K or V (D = 64: waves 0-3 K, waves 4-7
-// V), with 4 waves one of each. LDS slot t of a tensor holds the chunk its swizzled
+// launch): each thread moves D / (16 W) 16-byte chunks of K and as many of
+// V (D = 128, 256), or with 8 waves one of K or V (D = 64: waves 0-3 K,
+// waves 4-7 V), with 4 waves one of each. LDS slot t of a tensor holds the chunk its swizzled
 // position names; a wave's 64 slots are contiguous, as the load writes them.
 template <typename T, int D, int W>
 __device__ __forceinline__ void pf_dma(uint16_t* kdst, uint16_t* vdst, const uint32_t* __restrict__ tab,
@@ -105,9 +108,9 @@ __device__ __forceinline__ void pf_dma(uint16_t* kdst, uint16_t* vdst, const uin
     __builtin_amdgcn_global_load_lds((const void*)(base + kk * a.tok_e + 8 * p),
                                      (LdsVoid*)(buf + wslot0 * 8), 16, 0, 0);
   };
-  if constexpr (D == 128) {
+  if constexpr (D >= 128) {
 #pragma unroll
-    for (int j = 0; j < 8 / W; ++j) {
+    for (int j = 0; j < D / (16 * W); ++j) {
       one(kb, kdst, tid + 64 * W * j, 64 * wave + 64 * W * j);
       one(vb, vdst, tid + 64 * W * j, 64 * wave + 64 * W * j);
     }
@@ -191,7 +194,7 @@ __device__ __forceinline__ void prefill_body(
   constexpr int kPfRT = RT;
   constexpr uint32_t kPfRows = 16 * RT * W;
   // Direct loads per thread per step (the ring's vmcnt waits count them).
-  constexpr int kLoadsPerStep = W == 8 ? (D == 128 ? 2 : 1) : (D == 128 ? 4 : 2);
+  constexpr int kLoadsPerStep = D >= 128 ? 2 * D / (16 * W) : (W == 8 ? 1 : 2);
   // The ring's three buffers per tensor are separate LDS objects, each
   // named by a compile-time index where it is used: the compiler's wait
   // insertion then knows that a direct load into one buffer cannot alias
@@ -524,15 +527,26 @@ __global__ __launch_bounds__(256) void paged_prefill_merge(AttnArgs a, uint32_t 
 }
 
 // Row tiles (16 rows each) per wave, and workgroups per CU at head_dim 128.
+// At head_dim 256 a wave holds one row tile (its O and Q^T fragments, 64 +
+// 32 registers, beside a 64-register K tile: two tiles would not fit the
+// 256 registers of a wave at two waves per SIMD), and the ring's six
+// buffers take 96 KiB of LDS.
 constexpr int kPfRowTiles = 2;
+constexpr int kPfRowTiles256 = 1;
 constexpr int kPfOcc = 1;
 // head_dim 64 fits in 128 registers: two workgroups per CU (four waves per
 // SIMD) measured 1% faster than one on a config-3-shaped batch (676-678
 // against 669-673 TFLOP/s).
 constexpr int kPfOcc64 = 2;
 
-uint64_t prefill_grid(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t max_q) {
-  constexpr uint64_t rows = 16 * kPfRowTiles * kPfWaves;
+// Query rows of one prefill workgroup.
+static uint32_t pf_rows(uint32_t head_dim) {
+  return 16 * (head_dim == 256 ? kPfRowTiles256 : kPfRowTiles) * kPfWaves;
+}
+
+uint64_t prefill_grid(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t max_q,
+                      uint32_t head_dim) {
+  const uint64_t rows = pf_rows(head_dim);
   return ((uint64_t)max_q * group + rows - 1) / rows * kvh * batch;
 }
 
@@ -668,43 +682,48 @@ void launch_mixed(const AttnArgs& a_in, void* workspace, uint32_t max_q, uint32_
 size_t prefill_split_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t head_dim,
                            uint32_t max_q, uint32_t max_k) {
   if (max_q <= 1) return 0;
-  const uint64_t base = prefill_grid(batch, kvh, group, max_q);
-  return (size_t)pf_split_bytes(base, pf_splits_within(base, max_k, head_dim, ~0ull), head_dim);
+  const uint32_t rows = pf_rows(head_dim);
+  const uint64_t base = prefill_grid(batch, kvh, group, max_q, head_dim);
+  return (size_t)pf_split_bytes(base, pf_splits_within(base, max_k, head_dim, ~0ull, rows),
+                                head_dim, rows);
 }
 
 void launch_prefill(const AttnArgs& a_in, uint32_t max_q, uint32_t max_k, uint32_t head_dim,
                     bool bf16, void* split_ws, size_t split_ws_bytes, hipStream_t s) {
   AttnArgs a = a_in;
-  constexpr uint32_t rows = 16 * kPfRowTiles * kPfWaves;
+  const uint32_t rows = pf_rows(head_dim);
   const uint32_t qtiles = (uint32_t)(((uint64_t)max_q * a.group + rows - 1) / rows);
   const uint64_t base = (uint64_t)qtiles * a.kvh * a.pf_seqs_n;
   // As many splits as the workspace given holds (none without one); a
   // deterministic call does not split, so its output does not depend on
   // the workspace it is given.
   const uint32_t n_split = split_ws && !a.deterministic
-                               ? pf_splits_within(base, max_k, head_dim, split_ws_bytes)
+                               ? pf_splits_within(base, max_k, head_dim, split_ws_bytes, rows)
                                : 1;
   float* part = n_split > 1 ? (float*)split_ws : nullptr;
   const dim3 grid((uint32_t)(base * n_split)), block(kPfThreads);
 #define VK_PF(T, DD)                                                                             \
   do {                                                                                           \
     constexpr int occ = DD == 64 ? kPfOcc64 : kPfOcc;                                      \
+    constexpr int rt = DD == 256 ? kPfRowTiles256 : kPfRowTiles;                                 \
     if (n_split > 1) {                                                                           \
-      hipLaunchKernelGGL((paged_prefill_tiled<T, DD, kPfRowTiles, occ, true>), grid, block, 0, s, a, \
+      hipLaunchKernelGGL((paged_prefill_tiled<T, DD, rt, occ, true>), grid, block, 0, s, a, \
                          a.cu_q, a.cu_k, a.table, qtiles, n_split, part);                        \
       hipLaunchKernelGGL((paged_prefill_merge<T, DD>),                                           \
                          dim3((uint32_t)(base * (rows / (256 / (DD / 4))))), dim3(256), 0, s, a, \
                          qtiles, rows, n_split, part);                                           \
     } else {                                                                                     \
-      hipLaunchKernelGGL((paged_prefill_tiled<T, DD, kPfRowTiles, occ, false>), grid, block, 0, s,  \
+      hipLaunchKernelGGL((paged_prefill_tiled<T, DD, rt, occ, false>), grid, block, 0, s,  \
                          a, a.cu_q, a.cu_k, a.table, qtiles, 1u, nullptr);                       \
     }                                                                                            \
   } while (0)
   if (bf16) {
-    if (head_dim == 128) VK_PF(bf16_t, 128);
+    if (head_dim == 256) VK_PF(bf16_t, 256);
+    else if (head_dim == 128) VK_PF(bf16_t, 128);
     else VK_PF(bf16_t, 64);
   } else {
-    if (head_dim == 128) VK_PF(f16_t, 128);
+    if (head_dim == 256) VK_PF(f16_t, 256);
+    else if (head_dim == 128) VK_PF(f16_t, 128);
     else VK_PF(f16_t, 64);
   }
 #undef VK_PF
