@@ -335,6 +335,21 @@ def bench_valu(steps, warmup):
         log(f"f32 attention {name}: {ms * 1e3:.1f} us ({gms * 1e3:.1f} us in a graph), "
             f"{kv / 1e6:.1f} MB of K/V, {out[name]['gbs']:.0f} GB/s, {out[name]['path']}")
         del cache
+    # Config 3 (32 x 512-token chunks over 4,096 keys) on an f32 pool.
+    p = workload.config3_prefill()
+    cache = PagedKvCache(1, p.num_blocks, p.block_size, 8, 128, torch.float32, "HND")
+    workload.fill_normal(cache._slab, workload.seed_for(3))
+    q = torch.randn(p.batch * p.len_q, 32, 128, device=DEV)
+    batch = ForwardBatch(cu_seqlens_q=p.cu_q().tolist(), cu_seqlens_k=p.cu_k().tolist(),
+                         block_tables=[t.tolist() for t in p.tables], max_seqlen_q=p.len_q,
+                         max_seqlen_k=p.len_k)
+    prep = PreparedAttention.from_batch(batch, DEV)
+    o = torch.empty_like(q)
+    ms, _ = timed(lambda: paged_attention_prepared(q, cache, 0, prep, 128 ** -0.5, out=o), 3, 2)
+    flops = p.flops()
+    out["cfg3_f32"] = dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12)
+    log(f"f32 attention cfg3_f32: {ms:.2f} ms, {out['cfg3_f32']['tflops']:.1f} TFLOP/s")
+    del cache, q, o
     return out
 
 

@@ -141,10 +141,15 @@ def test_launches_too_large_for_one_grid_are_refused():
     assert L.vapi_paged_attention_ex(pool(), 0, *args, _lib.ATTN_NO_DECODE_ROWS, None, 0,
                                      None) == _lib.EUNSUP
     assert b"too large" in L.vapi_kv_last_error()
-    # VALU path (f32 pool): row tiles x kv heads x sequences x key chunks.
+    # VALU path (head_dim 80): row tiles x kv heads x sequences x key chunks.
     args = [16, 16, 16, 16, 16, 60000, 1, 1 << 20, 1 << 20, 8, 0.1, -1, 0]
-    assert L.vapi_paged_attention_ex(pool(dtype=_lib.F32), 0, *args, 0, 1, 1 << 62,
-                                     None) == _lib.EUNSUP
+    assert L.vapi_paged_attention_ex(pool(dtype=_lib.F32, head_dim=80), 0, *args, 0, 1,
+                                     1 << 62, None) == _lib.EUNSUP
+    assert b"too large" in L.vapi_kv_last_error()
+    # f32 MFMA prefill: 32-row tiles x kv heads x sequences waves.
+    args = [16, 16, 16, 16, 16, 65535, 1, 1 << 24, 1 << 24, 2, 0.1, -1, 0]
+    assert L.vapi_paged_attention_ex(pool(dtype=_lib.F32), 0, *args, _lib.ATTN_NO_DECODE_ROWS,
+                                     None, 0, None) == _lib.EUNSUP
     assert b"too large" in L.vapi_kv_last_error()
 
 
@@ -334,7 +339,7 @@ def test_the_valu_workspace_follows_its_key_chunks():
 
 
 def test_f32_decode_and_wide_groups_size_the_decode_workspace():
-    """An f32 pool's decode-only call sizes the decode stream's workspace
+    """An f32 pool's call sizes the decode stream's workspace
     (balance block, ranges, f32 partials), as a bf16 pool's does; so does a
     group of 32 query heads per kv head (two virtual kv heads of 16), whose
     partials are as large as 32 heads' and whose segments twice as many."""
@@ -344,6 +349,8 @@ def test_f32_decode_and_wide_groups_size_the_decode_workspace():
     a = L.vapi_paged_attention_workspace_size(f32, 64, 32, 1, 4096)
     b = L.vapi_paged_attention_workspace_size(bf16, 64, 32, 1, 4096)
     assert a == b and a > 0
+    # f32 prefill rows run without a key split: the decode's part only.
+    assert L.vapi_paged_attention_workspace_size(f32, 64, 32, 512, 4096) == a
     one = pool(dtype=_lib.BF16, num_kv_heads=1, head_dim=128)
     two = pool(dtype=_lib.BF16, num_kv_heads=2, head_dim=128)
     # G = 32 on one kv head is decoded as two kv heads of 16: the same

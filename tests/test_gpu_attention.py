@@ -375,6 +375,58 @@ def test_config2_shape_f32_decode_full_size_matches_within_1e_5():
         assert max_abs(got, want) <= 1e-5
 
 
+F32_PREFILL_CASES = [
+    # heads, kvh, d, bs, lens_q, lens_k, window, layout: f32 pools with
+    # prefill rows (decode rows on the f32 decode stream, prefill rows on
+    # paged_prefill_f32)
+    (32, 8, 128, 16, [64, 1, 200, 17], [1000, 300, 200, 900], None, "HND"),
+    (16, 8, 128, 32, [1, 37, 1, 3], [700, 37, 33, 2100], 100, "NHD"),
+    (8, 2, 64, 16, [100, 1], [900, 100], None, "HND"),
+    (64, 4, 64, 64, [2, 1, 45], [70, 64, 3000], 9, "NHD"),
+    (12, 4, 128, 16, [0, 5, 1, 0, 130], [5, 100, 40, 7, 1200], None, "HND"),
+    (32, 1, 128, 16, [1, 9, 1], [300, 40, 77], None, "HND"),
+]
+
+
+@pytest.mark.parametrize("case", F32_PREFILL_CASES, ids=lambda c: f"h{c[0]}-kv{c[1]}-d{c[2]}-bs{c[3]}-q{max(c[4])}-w{c[6]}-{c[7]}")
+def test_f32_prefill_on_mfma_matches_within_1e_5(case):
+    """f32 pools with prefill rows (GQA 1-32, head_dim 64 and 128, blocks of
+    16-64, windows, both layouts, sequences without rows): max-abs <= 1e-5
+    against the f32 oracle."""
+    heads, kvh, d, bs, lens_q, lens_k, window, layout = case
+    rng = np.random.default_rng(zlib.crc32(str(case).encode()))
+    c, q, batch = random_case(rng, torch.float32, heads, kvh, d, bs, lens_q, lens_k, layout)
+    scale = d ** -0.5
+    want = oracle_out(q, c, 0, batch, scale, window)
+    got = paged_attention(q, c, 0, batch, scale, window)
+    assert max_abs(got, want) <= 1e-5, max_abs(got, want)
+
+
+def test_config3_f32_prefill_rows_match_within_1e_5():
+    """Config 3's batch over an f32 pool (paged_prefill_f32): rows at the
+    start, middle and end of four sequences within 1e-5 of the f32 oracle."""
+    w = workload.config3_prefill()
+    c = PagedKvCache(1, w.num_blocks, w.block_size, 8, 128, torch.float32)
+    workload.fill_normal(c._slab, workload.seed_for(3))
+    g = torch.Generator(device=DEV).manual_seed(8)
+    q = torch.randn(w.batch * w.len_q, 32, 128, generator=g, device=DEV)
+    batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
+                         block_tables=[t.tolist() for t in w.tables], max_seqlen_q=w.len_q,
+                         max_seqlen_k=w.len_k)
+    scale = 128 ** -0.5
+    got = paged_attention(q, c, 0, batch, scale)
+    kc = host_f32(c.reference_view(0, "k").contiguous())
+    vc = host_f32(c.reference_view(0, "v").contiguous())
+    for s in (0, 9, 18, 31):
+        for j0 in (0, 250, w.len_q - 16):
+            rows_q = q[s * w.len_q + j0: s * w.len_q + j0 + 16]
+            lk = w.len_k - w.len_q + j0 + 16
+            want = oracle.paged_attention(host_f32(rows_q), kc, vc, [0, 16], [0, lk],
+                                          [w.tables[s].tolist()], scale, threads=8)
+            gr = got[s * w.len_q + j0: s * w.len_q + j0 + 16]
+            assert max_abs(gr, torch.from_numpy(want)) <= 1e-5, (s, j0)
+
+
 def test_config3_prefill_rows_match_the_oracle():
     """BASELINE config 3 (32 x 512-token chunks over 4,096 keys, shared
     prefixes): the whole batch runs in one call; rows at the start, middle and

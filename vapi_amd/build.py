@@ -38,13 +38,15 @@ COMMON_FLAGS = [
 ]
 
 SOURCES = ["kv_ops.hip", "attention.hip", "attn_decode.hip", "attn_prefill.hip",
-           "attn_generic.hip", "host.cpp", "spill.cpp"]
+           "attn_prefill_f32.hip", "attn_generic.hip", "host.cpp", "spill.cpp"]
 
 # The MFMA attention kernels never produce NaN from finite K/V/Q (masked
 # scores are -inf, running maxima start finite), so fmaxf on MFMA results
 # needs no operand quieting: -fno-honor-nans drops one instruction per score.
 EXTRA_FLAGS = {"attn_decode.hip": ["-fno-honor-nans", "-Rpass-analysis=kernel-resource-usage"],
-               "attn_prefill.hip": ["-fno-honor-nans", "-Rpass-analysis=kernel-resource-usage"]}
+               "attn_prefill.hip": ["-fno-honor-nans", "-Rpass-analysis=kernel-resource-usage"],
+               "attn_prefill_f32.hip": ["-fno-honor-nans",
+                                        "-Rpass-analysis=kernel-resource-usage"]}
 
 # The prefill kernel's step barrier counts its own vector-memory operations
 # (the direct loads into LDS) with an explicit vmcnt wait, and the decode
@@ -52,7 +54,8 @@ EXTRA_FLAGS = {"attn_decode.hip": ["-fno-honor-nans", "-Rpass-analysis=kernel-re
 # add scratch traffic to those counts (and slow the stream), so a build
 # whose attention kernels use scratch is refused.
 NO_SCRATCH = {"attn_prefill.hip": ("paged_prefill_tiled", "paged_mixed_stream"),
-              "attn_decode.hip": ("paged_decode_stream",)}
+              "attn_decode.hip": ("paged_decode_stream",),
+              "attn_prefill_f32.hip": ("paged_prefill_f32",)}
 
 
 def _check_no_scratch(src: Path, remarks: str) -> None:

@@ -5,9 +5,9 @@
 // when the pool is bf16/f16 with head_dim 64, 128 or 256, a power-of-two
 // block_size >= 16 and at most 16 query heads per kv head (up to 64 when a
 // split into 2 or 4 equal groups of at most 16 exists); an f32 pool of
-// that shape (head_dim 64 or 128) runs the decode stream on f32 MFMAs when
-// every row is a decode row; every other shape runs the VALU kernel
-// (attn_generic.hip).
+// that shape (head_dim 64 or 128) runs the decode stream and an f32 prefill
+// kernel (attn_prefill_f32.hip) on f32 MFMAs; every other shape runs the
+// VALU kernel (attn_generic.hip).
 // Replaces paged_attention_cuda/_windowed/_prepared (vapi
 // crates/vapi-backend-candle/src/attention.rs:170-288).
 #include <mutex>
@@ -26,11 +26,10 @@ static int decode_group_shift(uint32_t G) {
   return -1;
 }
 
-// An f32 pool's pure-decode call (every row len_q == 1) runs the decode
-// stream on v_mfma_f32_16x16x4_f32; any prefill row sends the call to the
-// VALU kernel.
-static bool f32_decode_ok(const vapi_kv_pool* p, uint32_t num_heads, uint32_t max_seqlen_q) {
-  if (p->dtype != VAPI_KV_F32 || max_seqlen_q != 1) return false;
+// An f32 pool whose calls run on v_mfma_f32_16x16x4_f32: decode rows on the
+// decode stream, prefill rows on paged_prefill_f32.
+static bool f32_mfma_ok(const vapi_kv_pool* p, uint32_t num_heads) {
+  if (p->dtype != VAPI_KV_F32) return false;
   if (p->head_dim != 64 && p->head_dim != 128) return false;
   if (p->block_size < 16 || (p->block_size & (p->block_size - 1))) return false;
   if (num_heads == 0 || num_heads % p->num_kv_heads) return false;
@@ -148,8 +147,7 @@ static size_t required_workspace(const vapi_kv_pool* pool, uint32_t batch, uint3
       num_heads == 0)
     return 0;
   const uint32_t group = num_heads / pool->num_kv_heads;
-  if (f32_decode_ok(pool, num_heads, max_seqlen_q)) return decode_ws_for(pool, batch, num_heads);
-  if (!mfma_ok(pool, num_heads))
+  if (!mfma_ok(pool, num_heads) && !f32_mfma_ok(pool, num_heads))
     return generic_workspace_bytes(batch, pool->num_kv_heads, group, pool->head_dim,
                                    std::max(max_seqlen_q, 1u), max_seqlen_k);
   return skip_decode ? 0 : decode_ws_for(pool, batch, num_heads);
@@ -341,7 +339,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   if (flags & ~(uint32_t)(VAPI_ATTN_DETERMINISTIC | VAPI_ATTN_NO_DECODE_ROWS))
     VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: unknown flags 0x%x", flags);
   if (num_heads > 65535 ||
-      (batch > 65535 && !mfma_ok(pool, num_heads) && !f32_decode_ok(pool, num_heads, max_seqlen_q)))
+      (batch > 65535 && !mfma_ok(pool, num_heads) && !f32_mfma_ok(pool, num_heads)))
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: batch %u / heads %u too large",
             batch, num_heads);
   // A batch the caller says has no decode rows (and which is not a fused
@@ -349,7 +347,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   // len_q == 1 included, so the result does not depend on the hint. It needs
   // no workspace.
   const bool skip_decode = (flags & VAPI_ATTN_NO_DECODE_ROWS) && !fuse && max_seqlen_q > 1 &&
-                           mfma_ok(pool, num_heads);
+                           (mfma_ok(pool, num_heads) || f32_mfma_ok(pool, num_heads));
   // The sequences the prefill grid covers: those the host named (a mixed
   // step's few prefill chunks among many decode rows), else all of them. A
   // prefill-only call covers every row and ignores the list.
@@ -362,6 +360,10 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
       prefill_grid(pf_n, pool->num_kv_heads, num_heads / pool->num_kv_heads, max_seqlen_q,
                    pool->head_dim) >
           0xFFFFFFFFull)
+    VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: prefill batch too large for one launch");
+  if (f32_mfma_ok(pool, num_heads) && max_seqlen_q > 1 &&
+      prefill_f32_items(pf_n, pool->num_kv_heads, num_heads / pool->num_kv_heads,
+                        max_seqlen_q) > 0xFFFFFFFFull)
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: prefill batch too large for one launch");
   const size_t need =
       required_workspace(pool, batch, num_heads, max_seqlen_q, max_seqlen_k, skip_decode);
@@ -456,9 +458,14 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
       launch_prefill(a, max_seqlen_q, max_seqlen_k, g.d, bf16,
                      room ? (char*)workspace + off : nullptr, room ? workspace_bytes - off : 0, s);
     }
-  } else if (f32_decode_ok(pool, num_heads, max_seqlen_q)) {
-    dec.num_waves = decode_num_waves();
-    launch_decode(dec, workspace, g.d, pool->dtype, s);
+  } else if (f32_mfma_ok(pool, num_heads)) {
+    if (skip_decode) {
+      a.pf_min_q = 1;
+    } else {
+      dec.num_waves = decode_num_waves();
+      launch_decode(dec, workspace, g.d, pool->dtype, s);
+    }
+    if (max_seqlen_q > 1 && pf_n > 0) launch_prefill_f32(a, max_seqlen_q, g.d, s);
   } else {
     if (g.d > 256)
       VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: head_dim %u > 256", g.d);

@@ -82,6 +82,17 @@ __device__ __forceinline__ void key_range(int32_t p, int32_t len_k, int32_t wl,
   hi = wr >= 0 ? min(len_k - 1, p + wr) : len_k - 1;
 }
 
+// Workgroup -> work item. The hardware deals workgroups round-robin to the
+// 8 XCDs (linear id % 8); each XCD here gets a contiguous range of work
+// items, so the q-tiles of one (sequence, kv head), which read the same K/V,
+// run at the same time under one L2.
+__device__ __forceinline__ uint32_t xcd_remap(uint32_t lin, uint32_t n) {
+  constexpr uint32_t kXcds = 8;
+  const uint32_t x = lin % kXcds, i = lin / kXcds;
+  const uint32_t per = n / kXcds, extra = n % kXcds;  // XCD x gets per + (x < extra)
+  return x * per + min(x, extra) + i;
+}
+
 // ---------------------------------------------------------------------------
 // MFMA helpers
 // ---------------------------------------------------------------------------
@@ -449,7 +460,9 @@ __device__ __forceinline__ floatx4 mfma16x16x4f32(float a, float b, floatx4 c) {
 }
 
 // K and V of the 16-key tile at s0 + 16 tt (keys past `last` re-read it).
-template <int D>
+// kStream: streaming loads (the decode reads each byte once); the prefill's
+// waves share a kv head's K/V through L2 and load them the ordinary way.
+template <int D, bool kStream = true>
 __device__ __forceinline__ void load_half_f32(KHalfF32<D>& kt, VHalfF32<D>& vt,
                                               const uint32_t* __restrict__ tab, const float* kb,
                                               const float* vb, const AttnArgs& a, int32_t s0,
@@ -459,14 +472,17 @@ __device__ __forceinline__ void load_half_f32(KHalfF32<D>& kt, VHalfF32<D>& vt,
   const char* kp = tile_base(tab, kb, a, ts) +
                    ((uint32_t)min((int32_t)col, lim) * a.tok_e + 4 * g) * sizeof(float);
 #pragma unroll
-  for (int c = 0; c < D / 16; ++c) kt.k[c] = load_stream((const float4*)(kp + 64u * c));
+  for (int c = 0; c < D / 16; ++c)
+    kt.k[c] = kStream ? load_stream((const float4*)(kp + 64u * c)) : *(const float4*)(kp + 64u * c);
   const char* vp = tile_base(tab, vb, a, ts);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const char* row =
         vp + ((uint32_t)min((int32_t)(4 * g + i), lim) * a.tok_e + 4 * col) * sizeof(float);
 #pragma unroll
-    for (int h = 0; h < D / 64; ++h) vt.v[i][h] = load_stream((const float4*)(row + 256u * h));
+    for (int h = 0; h < D / 64; ++h)
+      vt.v[i][h] = kStream ? load_stream((const float4*)(row + 256u * h))
+                           : *(const float4*)(row + 256u * h);
   }
 }
 
@@ -552,6 +568,10 @@ uint32_t decode_max_plan_seqs();
 // Workspace the prefill's key split wants for this shape (0: no split).
 size_t prefill_split_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t head_dim,
                            uint32_t max_q, uint32_t max_k);
+// Prefill rows of an f32 pool (head_dim 64 or 128) on f32 MFMAs, over
+// a.pf_seqs_n sequences; waves of the launch (a launch needs it below 2^32).
+uint64_t prefill_f32_items(uint32_t n_seqs, uint32_t kvh, uint32_t group, uint32_t max_q);
+void launch_prefill_f32(const AttnArgs& a, uint32_t max_q, uint32_t head_dim, hipStream_t s);
 // Any row, any dtype, head_dim <= 256 (VALU); split contexts combine their
 // partials through `workspace` (generic_workspace_bytes).
 void launch_generic(const AttnArgs& a, uint32_t max_q, uint32_t max_k, uint32_t head_dim,

@@ -24,17 +24,6 @@ namespace vk {
 
 constexpr int kPfWaves = 8;
 constexpr int kPfThreads = 64 * kPfWaves;
-// Workgroup -> work item. The hardware deals workgroups round-robin to the
-// 8 XCDs (linear id % 8); each XCD here gets a contiguous range of work
-// items, so the q-tiles of one (sequence, kv head), which read the same K/V,
-// run at the same time under one L2.
-__device__ __forceinline__ uint32_t xcd_remap(uint32_t lin, uint32_t n) {
-  constexpr uint32_t kXcds = 8;
-  const uint32_t x = lin % kXcds, i = lin / kXcds;
-  const uint32_t per = n / kXcds, extra = n % kXcds;  // XCD x gets per + (x < extra)
-  return x * per + min(x, extra) + i;
-}
-
 // ---- K and V staged by direct global-to-LDS loads --------------------------
 //
 // Rows keep the pool's order (key rows of D elements); each row's 16-byte
