@@ -525,7 +525,8 @@ constexpr int kPfRowTiles256 = 1;
 constexpr int kPfOcc = 1;
 // head_dim 64 fits in 128 registers: two workgroups per CU (four waves per
 // SIMD) measured 1% faster than one on a config-3-shaped batch (676-678
-// against 669-673 TFLOP/s).
+// against 669-673 TFLOP/s), and four row tiles per wave at one workgroup
+// per CU no faster (817-819 against 823-824).
 constexpr int kPfOcc64 = 2;
 
 // Query rows of one prefill workgroup.
