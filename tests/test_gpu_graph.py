@@ -103,15 +103,24 @@ def test_a_captured_decode_step_replays_like_the_eager_step(fused):
                 2e-2 * float(want[layer].abs().max())
 
 
-def test_a_captured_chunked_prefill_step_replays_like_the_eager_step():
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float32, 128),
+                                     (torch.bfloat16, 256)], ids=["bf16-d128", "f32-d128", "bf16-d256"])
+def test_a_captured_chunked_prefill_step_replays_like_the_eager_step(dtype, d):
     """A step of 20 decode rows and one 96-token prefill chunk per layer
     (append, then the prepared attention with the step's prefill list, the
     chunk's keys split over the GPU through the workspace), captured and
     replayed with eager work in between: every replay equals the oracle
-    within bf16 tolerance and leaves the pool as the eager step left it."""
+    within the dtype's tolerance (f32: 1e-5) and leaves the pool as the
+    eager step left it. The f32 pool runs the f32 decode stream and
+    paged_prefill_f32; head_dim 256 the decode and prefill as two launches."""
+    def close(got, want):
+        if dtype == torch.float32:
+            return float((got - want).abs().max()) <= 1e-5
+        return float((got - want).abs().max()) <= 2e-2 * float(want.abs().max())
+
     rng = np.random.default_rng(34)
-    L, nb, bs, hq, kvh, d = 2, 2048, 16, 32, 8, 128
-    cache = PagedKvCache(L, nb, bs, kvh, d, torch.bfloat16)
+    L, nb, bs, hq, kvh = 2, 2048, 16, 32, 8
+    cache = PagedKvCache(L, nb, bs, kvh, d, dtype)
     lens = np.concatenate([rng.integers(40, 1500, size=20), [900]])
     lens_q = [1] * 20 + [96]
     perm = rng.permutation(nb)
@@ -123,15 +132,15 @@ def test_a_captured_chunked_prefill_step_replays_like_the_eager_step():
     ctx = [t[p // bs] * bs + p % bs for t, n, lq in zip(tables, lens, lens_q)
            for p in range(n - lq)]
     for layer in range(L):
-        k = torch.randn(len(ctx), kvh, d, device=DEV).to(torch.bfloat16)
+        k = torch.randn(len(ctx), kvh, d, device=DEV).to(dtype)
         write_kv_to_cache(cache, layer, k, k.flip(0), ctx)
     new_slots = [t[p // bs] * bs + p % bs for t, n, lq in zip(tables, lens, lens_q)
                  for p in range(n - lq, n)]
     idx = scatter_index(new_slots, DEV)
     nt = len(new_slots)
-    k_new = [torch.randn(nt, kvh, d, device=DEV).to(torch.bfloat16) for _ in range(L)]
-    v_new = [torch.randn(nt, kvh, d, device=DEV).to(torch.bfloat16) for _ in range(L)]
-    q = [torch.randn(nt, hq, d, device=DEV).to(torch.bfloat16) for _ in range(L)]
+    k_new = [torch.randn(nt, kvh, d, device=DEV).to(dtype) for _ in range(L)]
+    v_new = [torch.randn(nt, kvh, d, device=DEV).to(dtype) for _ in range(L)]
+    q = [torch.randn(nt, hq, d, device=DEV).to(dtype) for _ in range(L)]
     batch = ForwardBatch(cu_seqlens_q=np.concatenate([[0], np.cumsum(lens_q)]).tolist(),
                          cu_seqlens_k=np.concatenate([[0], np.cumsum(lens)]).tolist(),
                          block_tables=tables, max_seqlen_q=96, max_seqlen_k=int(lens.max()))
@@ -154,9 +163,8 @@ def test_a_captured_chunked_prefill_step_replays_like_the_eager_step():
         vc = cache.reference_view(layer, "v").contiguous().float().cpu().numpy()
         w = oracle.paged_attention(q[layer].float().cpu().numpy(), kc, vc, batch.cu_seqlens_q,
                                    batch.cu_seqlens_k, tables, scale, threads=8)
-        want.append(torch.from_numpy(w).to(torch.bfloat16).float())
-        assert float((out[layer].float().cpu() - want[layer]).abs().max()) <= \
-            2e-2 * float(want[layer].abs().max())
+        want.append(torch.from_numpy(w).to(dtype).float())
+        assert close(out[layer].float().cpu(), want[layer])
 
     graph = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream()
@@ -176,4 +184,4 @@ def test_a_captured_chunked_prefill_step_replays_like_the_eager_step():
         for layer in range(L):
             got = out[layer].float().cpu()
             assert not torch.isnan(got).any(), f"replay {rep} layer {layer}: rows not written"
-            assert float((got - want[layer]).abs().max()) <= 2e-2 * float(want[layer].abs().max())
+            assert close(got, want[layer]), f"replay {rep} layer {layer}"
