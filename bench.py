@@ -1175,7 +1175,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", choices=["decode", "append", "prefill", "copy", "blocks", "valu",
-                                       "mixed", "shapes"],
+                                       "mixed", "shapes", "small"],
                     default=None)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate", action="store_true",
@@ -1207,6 +1207,10 @@ def main():
         return
     if args.only == "valu":
         bench_valu(args.steps, args.warmup)
+        return
+    if args.only == "small":
+        bench_small_batches(args.steps, args.warmup)
+        bench_small_prefill(args.steps, args.warmup)
         return
     if args.only == "shapes":
         bench_head_dim_64(args.steps, args.warmup)
