@@ -196,7 +196,7 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // K and V of one 32-key step (two 16-key tiles) in MFMA operand order.
 //  KTile::k[tt][c]: this lane's key row (tile tt, key col) at d = 32c + 8g .. +8.
 //  VTile::v[j]: the V row of key slot j (tile j/4, key 4g + j%4) at
-//  d = DPL*col .. +DPL.
+//  d = v_d(col, 0 .. DPL - 1) (DPL*col .. +DPL below head_dim 256).
 template <int D>
 struct KTile {
   uint4 k[2][D / 32];
@@ -256,6 +256,17 @@ __device__ __forceinline__ void load_k(KTile<D>& st, const uint32_t* __restrict_
   }
 }
 
+// The d index of V value k (0..D/16-1) that lane column m holds: DPL
+// consecutive values from DPL m, or at head_dim 256 two runs of 8, d = 8 m +
+// k and 128 + 8 m + k - 8 (so that every V load reads whole rows).
+template <int D>
+__host__ __device__ constexpr uint32_t v_d(uint32_t m, int k) {
+  return D == 256 ? (uint32_t)(k >> 3) * 128 + 8 * m + (uint32_t)(k & 7)
+                  : (uint32_t)(D / 16) * m + (uint32_t)k;
+}
+template <int D>
+__host__ __device__ constexpr uint32_t v_col0(uint32_t m) { return v_d<D>(m, 0); }
+
 template <typename T, int D>
 __device__ __forceinline__ void load_v(VTile<D>& st, const uint32_t* __restrict__ tab,
                                        const T* vb, const AttnArgs& a, int32_t s0, int32_t last,
@@ -269,10 +280,20 @@ __device__ __forceinline__ void load_v(VTile<D>& st, const uint32_t* __restrict_
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t vr =
-          ((uint32_t)min((int32_t)(4 * g + i), lim) * a.tok_e + DPL * col) * sizeof(T);
+          ((uint32_t)min((int32_t)(4 * g + i), lim) * a.tok_e + v_col0<D>(col)) * sizeof(T);
       const char* src = vt + vr;
-      if (vnew != nullptr && (int32_t)(4 * g + i) >= lim) src = vnew + DPL * col * sizeof(T);
-      st.v[4 * tt + i] = load_vrow<DPL>(src);
+      if (vnew != nullptr && (int32_t)(4 * g + i) >= lim) src = vnew + v_col0<D>(col) * sizeof(T);
+      if constexpr (D == 256) {
+        // Two 16-byte runs, d = 8 col .. +7 and 128 + 8 col .. +7: each load
+        // instruction then reads whole 256-byte rows across the 16 lanes.
+        const uint4 x0 = load_stream((const uint4*)src);
+        const uint4 x1 = load_stream((const uint4*)(src + 128 * sizeof(T)));
+        VRow<DPL>& w = st.v[4 * tt + i];
+        w.w[0] = x0.x, w.w[1] = x0.y, w.w[2] = x0.z, w.w[3] = x0.w;
+        w.w[4] = x1.x, w.w[5] = x1.y, w.w[6] = x1.z, w.w[7] = x1.w;
+      } else {
+        st.v[4 * tt + i] = load_vrow<DPL>(src);
+      }
     }
   }
 }
@@ -384,9 +405,10 @@ __device__ __forceinline__ uint4 attend_qk(const KTile<D>& kt, const uint4 (&qf)
 }
 
 // Second half: O^T += V^T P^T. The V fragments are the A operand (MFMA k's
-// row m <-> d = DPL*m + k) and P^T is the B operand exactly as the score
-// layout left it, so the result lands as lane (g, col) holding query row col
-// at d = DPL*(4g + i) + k (i = 0..3, k = 0..DPL-1): every lane's accumulators
+// row m <-> d = v_d(m, k), DPL*m + k below head_dim 256) and P^T is the B
+// operand exactly as the score layout left it, so the result lands as lane
+// (g, col) holding query row col at d = v_d(4g + i, k) (i = 0..3, k =
+// 0..DPL-1): every lane's accumulators
 // belong to its own row, and rescaling needs no cross-lane traffic.
 template <typename T, int D>
 __device__ __forceinline__ void attend_pv(const VTile<D>& vt, uint4 pf, floatx4 (&o)[D / 16]) {
@@ -395,8 +417,8 @@ __device__ __forceinline__ void attend_pv(const VTile<D>& vt, uint4 pf, floatx4 
   for (int k = 0; k < DPL; ++k) o[k] = mfma16x16x32<T>(vcol<DPL>(vt.v, k), pf, o[k]);
 }
 
-// Store row `col`'s DPL-wide runs d = DPL*(4g + i) .. +DPL of o, scaled, to
-// `row` (16-bit output).
+// Store row `col`'s outputs d = v_d(4g + i, k) of o, scaled, to `row`
+// (16-bit output; DPL-wide runs, or two runs of 8 at head_dim 256).
 template <typename T, int D>
 __device__ __forceinline__ void store_row(T* row, const floatx4 (&o)[D / 16], float scale,
                                           uint32_t g) {
@@ -407,6 +429,13 @@ __device__ __forceinline__ void store_row(T* row, const floatx4 (&o)[D / 16], fl
 #pragma unroll
     for (int k = 0; k < DPL / 2; ++k)
       w[k] = pack2<T>(o[2 * k][i] * scale, o[2 * k + 1][i] * scale);
+    if constexpr (D == 256) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        *(uint4*)(row + v_d<D>(4 * g + i, 8 * h)) =
+            make_uint4(w[4 * h], w[4 * h + 1], w[4 * h + 2], w[4 * h + 3]);
+      continue;
+    }
     T* dst = row + DPL * (4 * g + i);
     if constexpr (DPL == 4) {
       *(uint2*)dst = make_uint2(w[0], w[1]);

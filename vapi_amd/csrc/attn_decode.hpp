@@ -258,7 +258,7 @@ __device__ __forceinline__ void flush_piece(const AttnArgs& a, const DecodePos& 
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int k = 0; k < DPL; k += 4)
-        *(float4*)(po + DPL * (4 * g + i) + k) =
+        *(float4*)(po + v_d<D>(4 * g + i, k)) =
             make_float4(o[k][i], o[k + 1][i], o[k + 2][i], o[k + 3][i]);
     if (g == 0) *(float2*)(a.ws_ml + ((uint64_t)slot * G + col) * 2) = make_float2(m_run, l_tot);
   }
