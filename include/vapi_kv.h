@@ -77,6 +77,17 @@ typedef enum {
  * 89-96), one (1, width) row per token, num_kv_heads 1 and head_dim width.
  * Appends and gathers then move K only; attention rejects the pool.
  *
+ * block_stride_bytes: 0 packs a layer buffer's blocks densely (block b at
+ * b * block_size * num_kv_heads * head_dim elements, as above). Nonzero
+ * places block b of every layer buffer at b * block_stride_bytes from that
+ * buffer's base instead: a block-major pool, where one allocation holds,
+ * per block, every layer's K and V block side by side (layer_stride_bytes
+ * then the distance between two layers' blocks within it, at least one
+ * block's bytes, and block_stride_bytes at least (num_layers - 1) *
+ * layer_stride_bytes plus one block's bytes; both multiples of 16). A
+ * copy-on-write pair and an exported blob are then one contiguous run;
+ * every call accepts either form.
+ *
  * next chains further pools of the same cache (same num_blocks and
  * block_size; any geometry, dtype, layout, with or without V), in layer
  * order: a cache whose layers differ (PagedKvCache::with_layouts,
@@ -97,6 +108,7 @@ typedef struct vapi_kv_pool {
   uint32_t dtype;  /* vapi_kv_dtype */
   uint32_t layout; /* vapi_kv_layout */
   const struct vapi_kv_pool* next; /* the next pool of the same cache, or NULL */
+  uint64_t block_stride_bytes;       /* 0: dense blocks; else the block stride */
 } vapi_kv_pool;
 
 /* Thread-local message for the last failing call on this thread ("" if none). */

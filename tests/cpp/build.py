@@ -6,6 +6,7 @@ Usage: python tests/cpp/build.py
 """
 from __future__ import annotations
 
+import hashlib
 import subprocess
 import sys
 from pathlib import Path
@@ -13,10 +14,28 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 ROOT = HERE.parents[1]
 OUT = HERE / "_build" / "backend_tests"
+STAMP = HERE / "_build" / "backend_tests.sources"
+# What the binary is compiled from: a binary built against another version
+# of the C header passes descriptors of another layout to the library.
+SOURCES = [ROOT / "include" / "vapi_kv.h", ROOT / "include" / "vapi_kv.hpp",
+           HERE / "backend_tests.cpp"]
+
+
+def sources_digest() -> str:
+    h = hashlib.sha256()
+    for p in SOURCES:
+        h.update(p.read_bytes())
+    return h.hexdigest()
+
+
+def is_current() -> bool:
+    """The binary exists and was built from the sources as they are now."""
+    return OUT.exists() and STAMP.exists() and STAMP.read_text().strip() == sources_digest()
 
 
 def build() -> Path:
     OUT.parent.mkdir(exist_ok=True)
+    digest = sources_digest()
     tmp = OUT.with_suffix(".tmp")
     cmd = ["/opt/rocm/bin/hipcc", "-std=c++17", "-O1", "-Wall", "-Wextra", "-Werror",
            f"-I{ROOT / 'include'}", str(HERE / "backend_tests.cpp"), "-o", str(tmp),
@@ -26,6 +45,7 @@ def build() -> Path:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError("build of backend_tests failed")
     tmp.replace(OUT)
+    STAMP.write_text(digest + "\n")
     return OUT
 
 

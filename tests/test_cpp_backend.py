@@ -13,11 +13,14 @@ BIN = HERE / "cpp" / "_build" / "backend_tests"
 
 
 def _binary(build_if_missing: bool) -> Path:
-    if not BIN.exists():
+    sys.path.insert(0, str(HERE / "cpp"))
+    import build as cpp_build  # tests/cpp/build.py
+    if not cpp_build.is_current():
+        # A binary built against another version of the C header would hand
+        # the library descriptors of another layout: never run one.
         if not build_if_missing:
-            pytest.fail(f"{BIN} is not built (python tests/cpp/build.py)")
-        sys.path.insert(0, str(HERE / "cpp"))
-        import build as cpp_build  # tests/cpp/build.py
+            pytest.fail(f"{BIN} is missing or older than its sources "
+                        "(python tests/cpp/build.py)")
         cpp_build.build()
     return BIN
 

@@ -145,8 +145,13 @@ def test_the_sliding_window_closed_form_on_the_device():
 # ---- random mixed batches over every kernel path --------------------------------
 
 def random_case(rng, dtype, heads, kvh, d, bs, lens_q, lens_k, layout, nb=None):
+    """A random batch over a fresh pool; layout "HND-bm"/"NHD-bm" is a
+    two-layer block-major pool (layer 0 attended; blocks 4 blocks apart)."""
     nb = nb or sum(-(-l // bs) for l in lens_k) + 3
-    c = PagedKvCache(1, nb, bs, kvh, d, dtype, layout)
+    if layout.endswith("-bm"):
+        c = PagedKvCache(2, nb, bs, kvh, d, dtype, layout[:-3], block_major=True)
+    else:
+        c = PagedKvCache(1, nb, bs, kvh, d, dtype, layout)
     workload.fill_normal(c._slab, int(rng.integers(1 << 30)))
     perm = rng.permutation(nb)
     tables, at = [], 0
@@ -198,6 +203,13 @@ CASES = [
     (torch.bfloat16, 64, 2, 256, 16, [1, 1], [900, 2500], 300, "HND"),
     (torch.bfloat16, 32, 8, 256, 16, [64, 1, 200, 17], [1000, 300, 200, 900], None, "HND"),
     (torch.float16, 64, 2, 256, 32, [33, 1, 5], [700, 1200, 5], 100, "NHD"),
+    # Block-major pools (blocks strided by every layer's K and V block):
+    # MFMA decode + prefill, the mixed launch, f32 and head_dim 256.
+    (torch.bfloat16, 32, 8, 128, 16, [1, 37, 1, 64], [700, 37, 33, 300], None, "HND-bm"),
+    (torch.float16, 16, 4, 64, 32, [1, 1, 20, 1], [900, 65, 300, 2], 50, "NHD-bm"),
+    (torch.float32, 16, 8, 128, 16, [1, 9, 1], [64, 512, 200], None, "HND-bm"),
+    (torch.bfloat16, 16, 4, 256, 16, [1, 30, 1], [1000, 300, 17], None, "HND-bm"),
+    (torch.float32, 12, 4, 80, 16, [1, 20], [1500, 700], None, "NHD-bm"),
     # A 16-bit pool the MFMA paths do not take, on the generic kernel:
     # block_size 8.
     (torch.bfloat16, 16, 8, 128, 8, [1, 12], [210, 50], None, "HND"),

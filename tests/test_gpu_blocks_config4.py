@@ -36,12 +36,13 @@ def say(msg):
     print(f"[config4] {msg}", flush=True)
 
 
-@pytest.fixture(scope="module")
-def cfg4():
+@pytest.fixture(scope="module", params=[False, True], ids=["layer-major", "block-major"])
+def cfg4(request):
     w = workload.config4_block_ops()
-    say(f"pool: {w.num_layers} layers x {w.num_blocks} blocks, bf16")
+    say(f"pool: {w.num_layers} layers x {w.num_blocks} blocks, bf16, "
+        f"block_major={request.param}")
     c = PagedKvCache(w.num_layers, w.num_blocks, w.block_size, w.num_kv_heads, w.head_dim,
-                     torch.bfloat16, "HND")
+                     torch.bfloat16, "HND", block_major=request.param)
     workload.fill_normal(c._slab, workload.seed_for(4))
     torch.cuda.synchronize()
     yield w, c

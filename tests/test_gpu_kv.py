@@ -13,14 +13,25 @@ import torch
 import oracle
 from vapi_amd import _lib
 from vapi_amd.backend import KvBlockBackend
-from vapi_amd.cache import PagedKvCache, gather_kv, write_kv_to_cache
+from vapi_amd.cache import PagedKvCache as _PagedKvCache, gather_kv, write_kv_to_cache
 from vapi_amd import workload
 
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
 BS = 4
-LAYOUTS = ["HND", "NHD"]
+# "-bm": a block-major pool (every layer's K and V block of a block side by
+# side), the same kernels over a block stride.
+LAYOUTS = ["HND", "NHD", "HND-bm", "NHD-bm"]
+
+
+def PagedKvCache(*args, **kw):
+    """The cache, with a "-bm" layout suffix meaning block_major=True."""
+    args = list(args)
+    if len(args) >= 7 and args[6].endswith("-bm"):
+        args[6] = args[6][:-3]
+        kw["block_major"] = True
+    return _PagedKvCache(*args, **kw)
 
 
 def rows(n, base, heads=2, width=3, dtype=torch.float32):
@@ -654,7 +665,7 @@ def test_attention_over_a_layer_of_a_mixed_cache_matches_the_oracle():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("layout", ["HND", "NHD"])
 def test_a_bf16_mixed_cache_runs_the_mfma_kernels_per_layer(layout):
     """bf16 K/V layers of different geometry (head_dim 64 and 128, 2 and 4
     kv heads) beside rows layers: each layer's attention (decode and

@@ -61,6 +61,7 @@ class Pool(ctypes.Structure):
         ("dtype", ctypes.c_uint32),
         ("layout", ctypes.c_uint32),
         ("next", ctypes.c_void_p),
+        ("block_stride_bytes", ctypes.c_uint64),
     ]
 
 

@@ -43,11 +43,18 @@ class PagedKvCache:
     "NHD": [num_blocks, block_size, num_kv_heads, head_dim], the reference's
     own layout (cache.rs:7-11). Both are addressed by the same flat slot
     block*block_size + offset (cache.rs:113-117).
+
+    block_major: one allocation [num_blocks, 2, num_layers, block] holding,
+    per block, every layer's K block then every layer's V block, so that a
+    copy-on-write pair is one contiguous run; each layer buffer is then a
+    strided view (block stride 2 * num_layers blocks). The default keeps each
+    layer's K and V buffers contiguous, as the reference's per-layer tensors.
     """
 
     def __init__(self, num_layers: int, num_blocks: int, block_size: int,
                  num_kv_heads: int, head_dim: int, dtype: torch.dtype = torch.bfloat16,
-                 layout: str = "HND", device: str | torch.device = "cuda"):
+                 layout: str = "HND", device: str | torch.device = "cuda",
+                 block_major: bool = False):
         if layout not in _LAYOUTS:
             raise ValueError(f"layout must be HND or NHD, not {layout!r}")
         self.num_layers = num_layers
@@ -57,16 +64,34 @@ class PagedKvCache:
         self.head_dim = head_dim
         self.dtype = dtype
         self.layout = layout
+        self.block_major = block_major
         self.device = torch.device(device)
-        layer_elems = num_blocks * block_size * num_kv_heads * head_dim
+        block_elems = block_size * num_kv_heads * head_dim
+        layer_elems = num_blocks * block_elems
         elt = torch.tensor([], dtype=dtype).element_size()
+        shape = ((num_blocks, num_kv_heads, block_size, head_dim) if layout == "HND"
+                 else (num_blocks, block_size, num_kv_heads, head_dim))
+        if block_major:
+            if (block_elems * elt) % 16:
+                raise ValueError("a block-major pool needs blocks of a multiple of 16 bytes")
+            self._slab = torch.zeros((num_blocks, 2, num_layers, block_elems), dtype=dtype,
+                                     device=self.device)
+            self.k = [self._slab[:, 0, i].view(shape) for i in range(num_layers)]
+            self.v = [self._slab[:, 1, i].view(shape) for i in range(num_layers)]
+            base = self._slab.data_ptr()
+            self.pool = Pool(
+                k=base if num_layers else None,
+                v=base + num_layers * block_elems * elt if num_layers else None,
+                layer_stride_bytes=block_elems * elt,
+                num_layers=num_layers, num_blocks=num_blocks, block_size=block_size,
+                num_kv_heads=num_kv_heads, head_dim=head_dim, dtype=dtype_code(dtype),
+                layout=_LAYOUTS[layout], block_stride_bytes=2 * num_layers * block_elems * elt)
+            return
         # Pad each layer to a multiple of 256 bytes so every layer is aligned.
         pad_elems = (-(layer_elems * elt) % 256) // elt
         self._stride_elems = layer_elems + pad_elems
         self._slab = torch.zeros((2, num_layers, self._stride_elems), dtype=dtype,
                                  device=self.device)
-        shape = ((num_blocks, num_kv_heads, block_size, head_dim) if layout == "HND"
-                 else (num_blocks, block_size, num_kv_heads, head_dim))
         self.k = [self._slab[0, i, :layer_elems].view(shape) for i in range(num_layers)]
         self.v = [self._slab[1, i, :layer_elems].view(shape) for i in range(num_layers)]
         self.pool = Pool(
@@ -202,7 +227,7 @@ def _k_only(cache, which: str = "k"):
     return Pool(k=base, v=None, layer_stride_bytes=p.layer_stride_bytes,
                 num_layers=p.num_layers, num_blocks=p.num_blocks, block_size=p.block_size,
                 num_kv_heads=p.num_kv_heads, head_dim=p.head_dim, dtype=p.dtype,
-                layout=p.layout)
+                layout=p.layout, block_stride_bytes=p.block_stride_bytes)
 
 
 def _slots_host(slot_mapping) -> np.ndarray:

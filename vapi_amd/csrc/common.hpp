@@ -59,7 +59,8 @@ constexpr uint32_t kMaxPoolChain = 4096;  // chained pools beyond the first
 // Element strides of one layer buffer, for either layout.
 struct Geom {
   uint32_t num_blocks, block_size, kvh, d;
-  uint64_t blk;   // elements per block
+  uint64_t blk;   // stride between blocks (elements)
+  uint64_t blk_elems;  // elements of one block of one layer buffer
   uint64_t head;  // stride between kv heads
   uint64_t tok;   // stride between token offsets within a block
 };
@@ -70,7 +71,8 @@ inline Geom make_geom(const vapi_kv_pool* p) {
   g.block_size = p->block_size;
   g.kvh = p->num_kv_heads;
   g.d = p->head_dim;
-  g.blk = (uint64_t)p->block_size * p->num_kv_heads * p->head_dim;
+  g.blk_elems = (uint64_t)p->block_size * p->num_kv_heads * p->head_dim;
+  g.blk = p->block_stride_bytes ? p->block_stride_bytes / dtype_size(p->dtype) : g.blk_elems;
   if (p->layout == VAPI_KV_LAYOUT_HND) {
     g.head = (uint64_t)p->block_size * p->head_dim;
     g.tok = p->head_dim;

@@ -50,6 +50,7 @@ int vapi_cache_new(uint32_t num_layers, uint32_t num_blocks,
   p.dtype = dtype;
   p.layout = layout;
   p.next = nullptr;
+  p.block_stride_bytes = 0;
   const size_t layer_bytes = vapi_kv_layer_bytes(&p);
   // Align each layer buffer to 256 bytes.
   p.layer_stride_bytes = (layer_bytes + 255) & ~(size_t)255;

@@ -40,12 +40,26 @@ int check_pool(const vapi_kv_pool* p, const char* who) {
   if ((uint64_t)p->num_blocks * p->block_size >= 0xFFFFFFFFull)
     VK_FAIL(VAPI_KV_EINVAL, "%s: %u blocks of %u slots overflow u32 slots", who,
             p->num_blocks, p->block_size);
-  uint64_t layer_bytes = (uint64_t)p->num_blocks * p->block_size *
-                         p->num_kv_heads * p->head_dim * dtype_size(p->dtype);
-  if (p->num_layers > 1 && p->layer_stride_bytes < layer_bytes)
-    VK_FAIL(VAPI_KV_EINVAL, "%s: layer stride %llu < layer size %llu", who,
-            (unsigned long long)p->layer_stride_bytes,
-            (unsigned long long)layer_bytes);
+  const uint64_t block_bytes =
+      (uint64_t)p->block_size * p->num_kv_heads * p->head_dim * dtype_size(p->dtype);
+  if (p->block_stride_bytes == 0) {
+    const uint64_t layer_bytes = (uint64_t)p->num_blocks * block_bytes;
+    if (p->num_layers > 1 && p->layer_stride_bytes < layer_bytes)
+      VK_FAIL(VAPI_KV_EINVAL, "%s: layer stride %llu < layer size %llu", who,
+              (unsigned long long)p->layer_stride_bytes,
+              (unsigned long long)layer_bytes);
+  } else {
+    // Block-major: a block's layers side by side, blocks apart by the stride.
+    if (p->block_stride_bytes & 15)
+      VK_FAIL(VAPI_KV_EINVAL, "%s: block stride %llu is not a multiple of 16 bytes", who,
+              (unsigned long long)p->block_stride_bytes);
+    if (p->num_layers > 1 && p->layer_stride_bytes < block_bytes)
+      VK_FAIL(VAPI_KV_EINVAL, "%s: layer stride %llu < block size %llu", who,
+              (unsigned long long)p->layer_stride_bytes, (unsigned long long)block_bytes);
+    if (p->block_stride_bytes < (p->num_layers - 1) * p->layer_stride_bytes + block_bytes)
+      VK_FAIL(VAPI_KV_EINVAL, "%s: block stride %llu < the %u layers' extent in a block", who,
+              (unsigned long long)p->block_stride_bytes, p->num_layers);
+  }
   if (p->num_blocks > 0 && !p->k) VK_FAIL(VAPI_KV_EINVAL, "%s: null K base pointer", who);
   // Every kernel moves 16-byte chunks of rows that start at these bases
   // (the attention kernels load 16 bytes per lane, also into LDS).
@@ -252,15 +266,15 @@ struct CopyArgs {
 // random 16 KiB runs reaches and 85% of a sequential copy of the same
 // bytes; the order the runs are walked in, a persistent grid-stride
 // variant and two runs per workgroup measured no better.
-template <int C, int ITEMS>
-__global__ __launch_bounds__(256) void kv_copy_kernel(CopyArgs a) {
+template <int C, int ITEMS, int NT>
+__global__ __launch_bounds__(NT) void kv_copy_kernel(CopyArgs a) {
   using V = typename Chunk<C>::T;
-  const uint32_t base = blockIdx.x * (256u * ITEMS) + threadIdx.x;
+  const uint32_t base = blockIdx.x * (NT * ITEMS) + threadIdx.x;
   V val[ITEMS];
   char* dst[ITEMS];
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j) {
-    const uint32_t i = base + j * 256u;
+    const uint32_t i = base + j * (uint32_t)NT;
     dst[j] = nullptr;
     if (i < a.total) {
       const uint32_t r = a.upb.div(i);
@@ -504,7 +518,10 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
   a.blk_b = g.blk * elt;
   a.head_b = g.head * elt;
   a.tok_b = g.tok * elt;
-  constexpr int ITEMS = 4;
+  // One chunk per thread: 8,192 keys 13.8-13.9 against 15.0-15.5 us with
+  // four (two with 128 threads 14.7-14.9, one or two with 64 threads
+  // 14.2-14.3; one box, runs alternated).
+  constexpr int ITEMS = 1;
   const uint32_t grid = (a.total + 256 * ITEMS - 1) / (256 * ITEMS);
 #define L_GATHER(C)                                                        \
   hipLaunchKernelGGL((kv_gather_kernel<C, ITEMS>), dim3(grid), dim3(256), 0, \
@@ -520,7 +537,7 @@ static int copy_pool(const vapi_kv_pool* pool, const uint32_t* pairs, uint32_t n
                      hipStream_t stream) {
   const Geom g = make_geom(pool);
   const uint32_t elt = dtype_size(pool->dtype);
-  const uint64_t blk_b = g.blk * elt;
+  const uint64_t blk_b = g.blk_elems * elt;  // one layer's block
   const int c = chunk_bytes_for(blk_b);
   const uint64_t upb = blk_b / c;
   const uint32_t nbuf = pool->v ? 2 : 1;
@@ -533,19 +550,23 @@ static int copy_pool(const vapi_kv_pool* pool, const uint32_t* pairs, uint32_t n
   a.k = (char*)pool->k;
   a.v = (char*)pool->v;
   a.layer_b = pool->layer_stride_bytes;
-  a.blk_b = blk_b;
+  a.blk_b = g.blk * elt;  // block stride
   a.upb = FastDiv((uint32_t)upb);
   a.two_l = FastDiv(nbuf * pool->num_layers);  // segment s >= num_layers is V
   a.num_layers = pool->num_layers;
   a.num_blocks = pool->num_blocks;
-  constexpr int ITEMS = 4;
+  // One chunk per thread in workgroups of 64: a block-major pool's pairs
+  // (917,504-byte runs at config 4's shape) copy at 6.42 against 5.24 TB/s
+  // with four chunks per thread in workgroups of 256; config 4's 16 KiB
+  // runs of a layer-major pool copy the same either way (5.0-5.1 TB/s).
+  constexpr int ITEMS = 1, NT = 64;
   for (uint32_t p0 = 0; p0 < n_pairs; p0 += pairs_per_launch) {
     const uint32_t np = std::min(pairs_per_launch, n_pairs - p0);
     a.pairs = pairs + 2ull * p0;
     a.total = (uint32_t)(np * per_pair);
-    const uint32_t grid = (a.total + 256 * ITEMS - 1) / (256 * ITEMS);
-#define L_COPY(C)                                                        \
-  hipLaunchKernelGGL((kv_copy_kernel<C, ITEMS>), dim3(grid), dim3(256), 0, \
+    const uint32_t grid = (a.total + NT * ITEMS - 1) / (NT * ITEMS);
+#define L_COPY(C)                                                            \
+  hipLaunchKernelGGL((kv_copy_kernel<C, ITEMS, NT>), dim3(grid), dim3(NT), 0, \
                      stream, a)
     VK_DISPATCH_CHUNK(c, L_COPY)
 #undef L_COPY
@@ -594,7 +615,7 @@ static int blob_pool(const vapi_kv_pool* pool, const uint32_t* ids, uint32_t n, 
   a.two_l = FastDiv(nbuf * pool->num_layers);
   a.num_layers = pool->num_layers;
   a.row_bytes = row_bytes;
-  a.seg_bytes = (uint32_t)(g.blk * elt);
+  a.seg_bytes = (uint32_t)(g.blk_elems * elt);
   a.num_blocks = pool->num_blocks;
   constexpr int ITEMS = 4;
   for (uint32_t b0 = 0; b0 < n; b0 += blocks_per_launch) {
