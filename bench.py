@@ -466,6 +466,35 @@ def bench_head_dim_64(steps, warmup):
     return res
 
 
+def bench_decode_block_major(steps, warmup):
+    """Config 2's decode over a block-major pool of 4 layers (block stride
+    8 blocks: each 4 KiB (block, head) tile of a layer sits apart from the
+    next block's by every layer's K and V), rotating layers as the headline."""
+    w = workload.config2_decode()
+    cache = PagedKvCache(DECODE_LAYERS, w.num_blocks, w.block_size, w.num_kv_heads, w.head_dim,
+                         torch.bfloat16, "HND", block_major=True)
+    workload.fill_normal(cache._slab, workload.seed_for(2))
+    q = torch.randn(w.batch, w.num_heads, w.head_dim, device=DEV).to(torch.bfloat16)
+    batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
+                         block_tables=[t.tolist() for t in w.tables], max_seqlen_q=1,
+                         max_seqlen_k=int(w.lens.max()))
+    prep = PreparedAttention.from_batch(batch, DEV)
+    out = torch.empty_like(q)
+    turn = [0]
+
+    def call():
+        paged_attention_prepared(q, cache, turn[0] % DECODE_LAYERS, prep, 128 ** -0.5, out=out)
+        turn[0] += 1
+
+    gms = timed_graph(call, steps, warmup)
+    kv = int(w.lens.sum()) * 2 * 8 * 128 * 2
+    log(f"decode cfg2 over a block-major pool: {gms * 1e3:.1f} us, "
+        f"{kv / (gms * 1e-3) / 1e9:.0f} GB/s of K/V")
+    del cache, q, out
+    torch.cuda.empty_cache()
+    return dict(us=gms * 1e3, gbs=kv / (gms * 1e-3) / 1e9)
+
+
 def bench_wide_group(steps, warmup):
     """Config 2's batch with 64 query heads over 2 kv heads (32 query heads
     per kv head: the decode runs each group as two virtual kv heads of 16,
@@ -709,6 +738,7 @@ def bench_blocks(steps, warmup, decode):
     dst = torch.from_numpy(w.pairs[:, 1].astype(np.int64)).to(DEV)
     copy_ok = all(torch.equal(t[src], t[dst]) for t in cache.k + cache.v)
     copy_probes = probes_copy(w, cache)
+    bm = bench_copy_block_major(w, pairs_dev, steps, warmup)
 
     # Swap: 4,096 blocks out to pinned host and back into other blocks.
     n = len(w.swap_ids)
@@ -833,6 +863,7 @@ def bench_blocks(steps, warmup, decode):
                copy_frac_of_seq_copy_probe=copy_gbs / max(copy_probes["copy_seq_gbs"],
                                                           copy_probes["copy_seq_nt_gbs"]),
                probes=copy_probes, copy_bit_exact=bool(copy_ok),
+               copy_block_major=bm,
                swap_out_gbs=gb / (out_ms * 1e-3), swap_in_gbs=gb / (in_ms * 1e-3),
                swap_round_trip_bit_exact=bool(swap_ok),
                swap_out_overlapped_gbs=gb / (overlap_out_ms * 1e-3),
@@ -861,6 +892,30 @@ def bench_copy(steps, warmup):
                                                           stream_handle())), steps, warmup)
     alg = n * be.block_bytes() * 2
     log(f"copy cfg4a: {alg / 1e9:.2f} GB moved, {ms:.3f} ms, {alg / (ms * 1e-3) / 1e9:.0f} GB/s")
+
+
+def bench_copy_block_major(w, pairs_dev, steps, warmup):
+    """Config 4a's pairs on a block-major pool (block_major=True: per block,
+    every layer's K and V side by side), where a pair is one 917,504-byte
+    run: the same vapi_kv_copy_blocks call."""
+    from vapi_amd._lib import check, lib
+    from vapi_amd.cache import stream_handle
+    cache = PagedKvCache(w.num_layers, w.num_blocks, w.block_size, w.num_kv_heads,
+                         w.head_dim, torch.bfloat16, "HND", block_major=True)
+    workload.fill_normal(cache._slab, workload.seed_for(4))
+    n = w.pairs.shape[0]
+    ms, _ = timed(lambda: check(lib().vapi_kv_copy_blocks(cache.pool, pairs_dev.data_ptr(), n,
+                                                          stream_handle())), steps, warmup)
+    alg = n * KvBlockBackend(cache).block_bytes() * 2
+    gbs = alg / (ms * 1e-3) / 1e9
+    src = torch.from_numpy(w.pairs[:, 0].astype(np.int64)).to(DEV)
+    dst = torch.from_numpy(w.pairs[:, 1].astype(np.int64)).to(DEV)
+    ok = all(torch.equal(t[src], t[dst]) for t in cache.k + cache.v)
+    log(f"copy cfg4a, block-major pool: {alg / 1e9:.2f} GB moved, {ms:.3f} ms, {gbs:.0f} GB/s"
+        f" ({gbs / HBM_PEAK_GBS:.1%} of 8 TB/s), bit-exact {ok}")
+    del cache
+    torch.cuda.empty_cache()
+    return dict(ms=ms, gbs=gbs, frac=gbs / HBM_PEAK_GBS, bit_exact=ok)
 
 
 def _copy_on(stream, dst, src):
@@ -1216,6 +1271,7 @@ def main():
         bench_head_dim_64(args.steps, args.warmup)
         bench_wide_group(args.steps, args.warmup)
         bench_head_dim_256(args.steps, args.warmup)
+        bench_decode_block_major(args.steps, args.warmup)
         return
     if args.only == "mixed":
         bench_mixed_step(setup_decode(), args.steps, args.warmup)
@@ -1238,6 +1294,7 @@ def main():
         extras["head_dim_64"] = bench_head_dim_64(args.steps, args.warmup)
         extras["wide_group_g32"] = bench_wide_group(args.steps, args.warmup)
         extras["head_dim_256"] = bench_head_dim_256(args.steps, args.warmup)
+        extras["decode_cfg2_block_major"] = bench_decode_block_major(args.steps, args.warmup)
         extras["decode_small_batches"] = bench_small_batches(args.steps, args.warmup)
         extras["prefill_small_batches"] = bench_small_prefill(args.steps, args.warmup)
     extras["blocks_cfg4"] = bench_blocks(max(args.steps // 5, 3), 2, dec)
@@ -1297,6 +1354,13 @@ def main():
                                if "append_cfg1" in extras else None),
         "kv_append_host_launched_gbs": (round(extras["append_cfg1"]["gbs_host_launched_c_abi"], 1)
                                         if "append_cfg1" in extras else None),
+        # Config 4a's copy-on-write: the layer-major pool (each layer's K and
+        # V buffers contiguous, as the reference's tensors) and a block-major
+        # one (a pair is one contiguous run).
+        "kv_copy_gbs": (round(extras["blocks_cfg4"]["copy_gbs"], 1)
+                        if "blocks_cfg4" in extras else None),
+        "kv_copy_block_major_gbs": (round(extras["blocks_cfg4"]["copy_block_major"]["gbs"], 1)
+                                    if "blocks_cfg4" in extras else None),
         # Tokens per second per layer (one GPU): config 2's 64 decode tokens
         # per call, config 1's 3,891 appended tokens per call, config 3's
         # 16,384 prefill query tokens per call.

@@ -297,6 +297,28 @@ __global__ __launch_bounds__(NT) void kv_copy_kernel(CopyArgs a) {
     if (dst[j]) store_stream((V*)dst[j], val[j]);
 }
 
+// A block-major pool whose blocks hold every layer's K and V contiguously
+// (layer stride = one layer's block, V right after the K layers, block
+// stride = all of them): a pair is one run of run_units 16-byte chunks.
+// Workgroup w copies 64 chunks of run w / wgs_per_run.
+struct CopyRunsArgs {
+  char* base;
+  const uint32_t* pairs;
+  uint64_t run_b;       // block stride = run bytes
+  uint32_t run_units;   // 16-byte chunks per run
+  FastDiv wgs_per_run;
+  uint32_t num_blocks;
+};
+
+__global__ __launch_bounds__(64) void kv_copy_runs_kernel(CopyRunsArgs a) {
+  const uint32_t p = a.wgs_per_run.div(blockIdx.x);
+  const uint32_t u = (blockIdx.x - p * a.wgs_per_run.d) * 64u + threadIdx.x;
+  const uint32_t src_blk = a.pairs[2 * p], dst_blk = a.pairs[2 * p + 1];
+  if (u >= a.run_units || src_blk >= a.num_blocks || dst_blk >= a.num_blocks) return;
+  const uint4 x = load_stream((const uint4*)(a.base + src_blk * a.run_b) + u);
+  store_stream((uint4*)(a.base + dst_blk * a.run_b) + u, x);
+}
+
 // ---- export / import (reference blob order) ----------------------------------
 
 // Blob of block i: the K block of every layer of the cache in order, then
@@ -546,11 +568,35 @@ static int copy_pool(const vapi_kv_pool* pool, const uint32_t* pairs, uint32_t n
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_kv_copy_blocks: block too large");
   const uint32_t pairs_per_launch =
       (uint32_t)std::min<uint64_t>(n_pairs, ((1ull << 31) - 1) / per_pair);
+  const uint64_t stride_b = g.blk * elt;
+  const uint64_t run_b = (uint64_t)nbuf * pool->num_layers * blk_b;
+  if (pool->block_stride_bytes == run_b && (pool->num_layers == 1 ||
+                                            pool->layer_stride_bytes == blk_b) &&
+      (!pool->v || (const char*)pool->v == (const char*)pool->k + pool->num_layers * blk_b) &&
+      run_b % 16 == 0 && run_b / 16 < (1ull << 31)) {
+    // Each pair is one contiguous run (config 4 at block-major: 6.2 TB/s
+    // against 5.1 TB/s for its 56 runs of 16 KiB in a layer-major pool).
+    CopyRunsArgs r;
+    r.base = (char*)pool->k;
+    r.run_b = run_b;
+    r.run_units = (uint32_t)(run_b / 16);
+    const uint32_t wpr = (r.run_units + 63) / 64;
+    r.wgs_per_run = FastDiv(wpr);
+    r.num_blocks = pool->num_blocks;
+    const uint32_t per_launch = (uint32_t)std::min<uint64_t>(n_pairs, 0xFFFFFFFFull / wpr);
+    for (uint32_t p0 = 0; p0 < n_pairs; p0 += per_launch) {
+      const uint32_t np = std::min(per_launch, n_pairs - p0);
+      r.pairs = pairs + 2ull * p0;
+      hipLaunchKernelGGL(kv_copy_runs_kernel, dim3(np * wpr), dim3(64), 0, stream, r);
+      VK_LAUNCHED("kv_copy_blocks");
+    }
+    return 0;
+  }
   CopyArgs a;
   a.k = (char*)pool->k;
   a.v = (char*)pool->v;
   a.layer_b = pool->layer_stride_bytes;
-  a.blk_b = g.blk * elt;  // block stride
+  a.blk_b = stride_b;  // block stride
   a.upb = FastDiv((uint32_t)upb);
   a.two_l = FastDiv(nbuf * pool->num_layers);  // segment s >= num_layers is V
   a.num_layers = pool->num_layers;
