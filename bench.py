@@ -1230,7 +1230,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", choices=["decode", "append", "prefill", "copy", "blocks", "valu",
-                                       "mixed", "shapes", "small"],
+                                       "mixed", "shapes", "small", "copy_bm"],
                     default=None)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate", action="store_true",
@@ -1256,6 +1256,11 @@ def main():
         return
     if args.only == "copy":
         bench_copy(args.steps, args.warmup)
+        return
+    if args.only == "copy_bm":
+        w = workload.config4_block_ops()
+        pairs_dev = torch.from_numpy(w.pairs.astype(np.int32).reshape(-1)).to(DEV)
+        bench_copy_block_major(w, pairs_dev, args.steps, args.warmup)
         return
     if args.only == "prefill":
         bench_prefill(args.steps, args.warmup)
