@@ -105,6 +105,25 @@ def test_misaligned_pools_and_unknown_flags_are_refused():
     assert need > 0
 
 
+def test_block_major_descriptors_are_checked():
+    """block_stride_bytes: a multiple of 16, room for every layer's block
+    within a block, layers at least one block apart; refused before any
+    launch otherwise. A zero-pair copy on a valid one does nothing."""
+    L = _lib.lib()
+    blk = 16 * 2 * 64 * 2  # block_size x kv_heads x head_dim x bf16
+    ok = pool(num_layers=3, layer_stride_bytes=blk, block_stride_bytes=6 * blk)
+    assert L.vapi_kv_copy_blocks(ok, 1, 0, None) == _lib.OK
+    assert L.vapi_kv_append(ok, 0, 1, 1, 1, 0, None) == _lib.OK
+    bad = [dict(block_stride_bytes=6 * blk + 8),           # not a multiple of 16
+           dict(block_stride_bytes=2 * blk),               # 3 layers do not fit
+           dict(layer_stride_bytes=blk // 2, block_stride_bytes=6 * blk)]  # layers overlap
+    for kw in bad:
+        args = dict(num_layers=3, layer_stride_bytes=blk)
+        args.update(kw)
+        assert L.vapi_kv_copy_blocks(pool(**args), 1, 1, None) == _lib.EINVAL, kw
+        assert b"stride" in L.vapi_kv_last_error()
+
+
 def test_the_prepared_call_checks_its_prefill_list_and_sizes_its_split():
     """vapi_paged_attention_prepared refuses a list longer than the batch or
     a null list, before anything is launched; its workspace size covers the
