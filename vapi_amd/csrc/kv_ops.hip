@@ -583,7 +583,8 @@ static int copy_pool(const vapi_kv_pool* pool, const uint32_t* pairs, uint32_t n
     const uint32_t wpr = (r.run_units + 63) / 64;
     r.wgs_per_run = FastDiv(wpr);
     r.num_blocks = pool->num_blocks;
-    const uint32_t per_launch = (uint32_t)std::min<uint64_t>(n_pairs, 0xFFFFFFFFull / wpr);
+    // FastDiv is exact below 2^31: at most that many workgroups per launch.
+    const uint32_t per_launch = (uint32_t)std::min<uint64_t>(n_pairs, 0x7FFFFFFFull / wpr);
     for (uint32_t p0 = 0; p0 < n_pairs; p0 += per_launch) {
       const uint32_t np = std::min(per_launch, n_pairs - p0);
       r.pairs = pairs + 2ull * p0;
