@@ -243,7 +243,7 @@ def test_random_mixed_batches_match_the_oracle(case):
 
 def drawn_case(seed):
     """A batch drawn from a seed: dtype, GQA group (1-32), head_dim, block
-    size, layout, window, and 1-6 sequences mixing decode rows with prefill
+    size, layout (block-major for every fourth seed), window, and 1-6 sequences mixing decode rows with prefill
     chunks of up to 150 tokens over up to 2,500 keys."""
     rng = np.random.default_rng(1000 + seed)
     dtype = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(3))]
@@ -256,6 +256,8 @@ def drawn_case(seed):
     bs = int(rng.choice([16, 32, 64]))
     layout = "HND" if rng.random() < 0.7 else "NHD"
     window = None if rng.random() < 0.6 else int(rng.integers(1, 600))
+    if seed % 4 == 3:
+        layout += "-bm"  # a block-major pool
     n = int(rng.integers(1, 7))
     lens_k = [int(x) for x in rng.integers(1, 2500, n)]
     lens_q = [1 if rng.random() < 0.5 else int(rng.integers(0, min(lk, 150) + 1)) for lk in lens_k]
