@@ -1230,7 +1230,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", choices=["decode", "append", "prefill", "copy", "blocks", "valu",
-                                       "mixed", "shapes", "small", "copy_bm"],
+                                       "mixed", "shapes", "small", "copy_bm", "gather"],
                     default=None)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate", action="store_true",
@@ -1256,6 +1256,9 @@ def main():
         return
     if args.only == "copy":
         bench_copy(args.steps, args.warmup)
+        return
+    if args.only == "gather":
+        bench_gather(setup_decode(), args.steps, args.warmup)
         return
     if args.only == "copy_bm":
         w = workload.config4_block_ops()
