@@ -266,21 +266,26 @@ enum class MemoryLayout : uint32_t { HND = VAPI_KV_LAYOUT_HND, NHD = VAPI_KV_LAY
  * the same layout run together in one device allocation, described by one
  * vapi_kv_pool; the pools are chained in layer order, so the block calls
  * (export/import/copy) walk every layer in the reference's order. Move-only:
- * the pool descriptors point at each other.
+ * the pool descriptors point at each other. block_major: each run's
+ * allocation holds, per block, every layer's K block then every layer's V
+ * block (vapi_kv_pool.block_stride_bytes), so a copy-on-write pair is one
+ * contiguous run; blocks must then be a multiple of 16 bytes.
  */
 class PagedKvCache {
  public:
   static Result<PagedKvCache> create(size_t num_layers, size_t num_blocks, size_t block_size,
                                      size_t num_kv_heads, size_t head_dim, DType dtype,
-                                     MemoryLayout layout = MemoryLayout::HND) {
+                                     MemoryLayout layout = MemoryLayout::HND,
+                                     bool block_major = false) {
     return with_layouts(std::vector<LayerLayout>(num_layers,
                                                  LayerLayout::Kv(num_kv_heads, head_dim)),
-                        num_blocks, block_size, dtype, layout);
+                        num_blocks, block_size, dtype, layout, block_major);
   }
 
   static Result<PagedKvCache> with_layouts(const std::vector<LayerLayout>& layouts,
                                            size_t num_blocks, size_t block_size, DType dtype,
-                                           MemoryLayout layout = MemoryLayout::HND) {
+                                           MemoryLayout layout = MemoryLayout::HND,
+                                           bool block_major = false) {
     PagedKvCache c;
     c.layouts_ = layouts;
     c.num_blocks_ = num_blocks;
@@ -300,19 +305,32 @@ class PagedKvCache {
       const LayerLayout& ll = layouts[runs[p].first];
       const bool rows = ll.kind == LayerLayout::Kind::Rows;
       const size_t heads = rows ? 1 : ll.num_kv_heads, d = rows ? ll.width : ll.head_dim;
-      const size_t tensor = num_blocks * block_size * heads * d * dtype_size(dtype);
+      const size_t block = block_size * heads * d * dtype_size(dtype);
+      const size_t tensor = num_blocks * block;
       const size_t stride = (tensor + 255) / 256 * 256;  // 16-byte alignment and more
       const size_t per_layer = stride * (rows ? 1 : 2);
-      auto buf = detail::device_alloc(per_layer * runs[p].second);
+      if (block_major && block % 16)
+        return Error{"a block-major cache needs blocks of a multiple of 16 bytes"};
+      // Layer-major: per layer a K then a V buffer. Block-major: per block,
+      // the run's K blocks then its V blocks.
+      const size_t run_blocks = runs[p].second * (rows ? 1 : 2);
+      const size_t bytes = block_major ? num_blocks * block * run_blocks
+                                       : per_layer * runs[p].second;
+      auto buf = detail::device_alloc(bytes);
       if (buf.is_err()) return buf.error();
       char* base = (char*)buf.value().get();
-      if (per_layer * runs[p].second)
-        VAPI_TRY(detail::hip(hipMemset(base, 0, per_layer * runs[p].second), "hipMemset"));
+      if (bytes) VAPI_TRY(detail::hip(hipMemset(base, 0, bytes), "hipMemset"));
       vapi_kv_pool& pool = c.pools_[p];
       std::memset(&pool, 0, sizeof pool);
       pool.k = base;
-      pool.v = rows ? nullptr : base + stride;
-      pool.layer_stride_bytes = per_layer;
+      if (block_major) {
+        pool.v = rows ? nullptr : base + runs[p].second * block;
+        pool.layer_stride_bytes = block;
+        pool.block_stride_bytes = block * run_blocks;
+      } else {
+        pool.v = rows ? nullptr : base + stride;
+        pool.layer_stride_bytes = per_layer;
+      }
       pool.num_layers = (uint32_t)runs[p].second;
       pool.num_blocks = (uint32_t)num_blocks;
       pool.block_size = (uint32_t)block_size;

@@ -524,8 +524,9 @@ TEST(a_bidirectional_window_is_not_causal, true) {
 
 // ---- the backend's block methods (backend.rs:695-797) --------------------------
 
-Result<HipBackend> filled_backend(size_t layers, size_t blocks) {
-  auto c = PagedKvCache::create(layers, blocks, 16, 4, 128, DType::BF16);
+Result<HipBackend> filled_backend(size_t layers, size_t blocks, bool block_major = false) {
+  auto c = PagedKvCache::create(layers, blocks, 16, 4, 128, DType::BF16, MemoryLayout::HND,
+                                block_major);
   if (c.is_err()) return c.error();
   for (size_t l = 0; l < layers; ++l) {
     std::vector<float> kv(blocks * 16 * 4 * 128);
@@ -572,6 +573,21 @@ TEST(copy_blocks_copies_every_layer_k_and_v, true) {
   EXPECT(OK(be.export_block(1)) == b2);
   EXPECT(OK(be.export_block(5)) == b5);  // untouched
   EXPECT(be.copy_blocks({{0, 6}}).is_err());
+}
+
+TEST(a_block_major_cache_moves_blocks_like_a_layer_major_one, true) {
+  // The same contents in both allocations: every block exports the same
+  // blob, and a copy (one run per pair in the block-major one) and an
+  // import leave them equal.
+  auto lm = OK(filled_backend(3, 6));
+  auto bm = OK(filled_backend(3, 6, true));
+  for (BlockId b = 0; b < 6; ++b) EXPECT(OK(bm.export_block(b)) == OK(lm.export_block(b)));
+  OK_VOID(lm.copy_blocks({{0, 4}, {2, 1}}));
+  OK_VOID(bm.copy_blocks({{0, 4}, {2, 1}}));
+  const auto b3 = OK(lm.export_block(3));
+  OK_VOID(lm.import_block(5, b3.data(), b3.size()));
+  OK_VOID(bm.import_block(5, b3.data(), b3.size()));
+  for (BlockId b = 0; b < 6; ++b) EXPECT(OK(bm.export_block(b)) == OK(lm.export_block(b)));
 }
 
 // ---- Scheduler::fork's copy pairs (crates/vapi-engine/tests/scheduler.rs:524-637) ----
