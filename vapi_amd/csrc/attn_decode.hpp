@@ -56,6 +56,7 @@ constexpr uint32_t kMaxPlanSeqs = 4096;  // sequences per launch (host chunks be
 // workspace): shares f32[8] at 0, per-wave (steps, entry tick, end tick, 0)
 // from kBalStats.
 constexpr uint32_t kBalStats = 64;
+constexpr uint32_t kMinStepsPerWave = 8;  // launches that move the shares
 constexpr uint32_t kStatWords = 4;
 
 // Steps of sequence s (0 for rows that are not decode rows).
@@ -526,6 +527,12 @@ __device__ __forceinline__ void update_shares(const AttnArgs& a, uint32_t nwg, u
                __shfl(cnt, (int)(y * kDecodeWavesPerWG)) * (float)first;
   }
   if (lane != 0) return;
+  // A launch of fewer than kMinStepsPerWave steps per wave is bound by its
+  // fixed costs, and its timings say little about the XCDs' rates: the
+  // shares stay as they are.
+  float s_tot = 0.f;
+  for (uint32_t y = 0; y < kGroups; ++y) s_tot += steps[y];
+  if (s_tot < (float)(kMinStepsPerWave * W)) return;
   float w[kGroups], rate[kGroups], w_tot = 0.f, r_tot = 0.f;
   load_shares(a, nwg, w);
   for (uint32_t y = 0; y < kGroups; ++y) {
@@ -596,7 +603,7 @@ __device__ __forceinline__ void store_outputs(T* dst, uint32_t n, const float (&
 // WPS waves per segment: 1 (four segments per workgroup) when segments are
 // many and each has a few pieces; 4 (one segment per workgroup) when they
 // are few, so that each has many pieces: wave v then combines pieces r0 +
-// v, r0 + v + 4, ..., 16 per round trip, and the four waves' results are
+// v, r0 + v + 4, ..., 8 per round trip, and the four waves' results are
 // combined through LDS.
 // Workgroup `bid` of `nbid` (kMergeWaves waves); workgroups from merge_wgs
 // on copy the fused append's new rows.
@@ -641,8 +648,10 @@ __device__ __forceinline__ void decode_merge_body(const AttnArgs& a, uint32_t nw
   const uint32_t h0 = e_lane / D, h1 = (e_lane + E - 1) / D;
   T* orow = (T*)a.out + ((uint64_t)q0 * a.num_heads + kh * G) * D;
   // Up to R ranges per round trip; E is a multiple of 4 for G*D >= 256
-  // (D is 64, 128 or 256), so outputs move as float4.
-  constexpr int R = WPS == 1 ? 8 : 16;
+  // (D is 64, 128 or 256), so outputs move as float4. (With a workgroup per
+  // segment, 8 ranges per wave measured 0.6-2.4 us faster per call than 16
+  // at B = 1-16, and 4 slower at B = 1.)
+  constexpr int R = 8;
   __shared__ float cmb[WPS > 1 ? WPS : 1][3][WPS > 1 ? 64 * 8 : 1];
   for (uint32_t j0 = 0; j0 < E; j0 += 8) {
     const uint32_t n = min(8u, E - j0);
