@@ -28,7 +28,7 @@ SKIP = _lib.SLOT_SKIP
 
 def clone(c: PagedKvCache) -> PagedKvCache:
     d = PagedKvCache(c.num_layers, c.num_blocks, c.block_size, c.num_kv_heads, c.head_dim,
-                     c.dtype, c.layout)
+                     c.dtype, c.layout, block_major=c.block_major)
     d._slab.copy_(c._slab)
     return d
 
@@ -92,6 +92,7 @@ STEPS = [
     (torch.bfloat16, 64, 4, 64, 32, [1, 1, 1], [70, 64, 2], 9, "NHD"),
     (torch.bfloat16, 16, 4, 256, 16, [1, 1, 1], [900, 31, 2], None, "HND"),
     (torch.float16, 8, 2, 256, 32, [1, 1], [64, 1300], 50, "NHD"),
+    (torch.bfloat16, 32, 8, 128, 16, [1, 1, 1], [900, 31, 2], None, "HND-bm"),
     # Prefill rows in the batch: the two calls run inside.
     (torch.bfloat16, 32, 8, 128, 16, [1, 37, 1], [700, 37, 33], None, "HND"),
     (torch.float32, 16, 8, 128, 16, [1, 1], [64, 512], None, "HND"),
