@@ -11,8 +11,16 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
   decode_stream_body<T, D, kFuse>(a, cu_q, cu_k, table, P, blockIdx.x, gridDim.x);
 }
 
+// Waves per segment of a merge with a workgroup per segment: 8 for at most
+// kFewSegs segments (each then has many pieces), else 4. Per call, one box:
+// B = 1 x 8,192 keys 22.2 against 24.8 us with 4 (x 32,768: 38.1 against
+// 41.3); B = 4 x 4,096 (32 segments) 23.8 against 22.7; 16 waves slower
+// everywhere (34.3 us at B = 1 x 8,192).
+constexpr uint32_t kFewSegs = 16;
+constexpr uint32_t merge_threads(int wps) { return 64u * (wps > (int)kMergeWaves ? wps : kMergeWaves); }
+
 template <typename T, int D, bool kFuse, int WPS>
-__global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_merge(AttnArgs a, uint32_t nwg,
+__global__ __launch_bounds__(merge_threads(WPS)) void paged_decode_merge(AttnArgs a, uint32_t nwg,
                                                                       uint32_t merge_wgs) {
   decode_merge_body<T, D, kFuse, WPS>(a, nwg, merge_wgs, blockIdx.x, gridDim.x);
 }
@@ -74,9 +82,12 @@ void launch_decode_merge(const AttnArgs& c, uint32_t nwg, uint32_t head_dim, boo
   const uint32_t merge_wgs = decode_merge_wgs(c.batch, c.kvh, &wide);
 #define VK_MRG(T, DD)                                                                        \
   do {                                                                                       \
-    if (wide)                                                                                \
+    if (wide && c.batch * c.kvh <= kFewSegs)                                                 \
+      hipLaunchKernelGGL((paged_decode_merge<T, DD, false, 8>), dim3(merge_wgs),             \
+                         dim3(merge_threads(8)), 0, s, c, nwg, merge_wgs);                   \
+    else if (wide)                                                                           \
       hipLaunchKernelGGL((paged_decode_merge<T, DD, false, kMergeWaves>), dim3(merge_wgs),   \
-                         dim3(64 * kMergeWaves), 0, s, c, nwg, merge_wgs);                   \
+                         dim3(merge_threads(kMergeWaves)), 0, s, c, nwg, merge_wgs);         \
     else                                                                                     \
       hipLaunchKernelGGL((paged_decode_merge<T, DD, false, 1>), dim3(merge_wgs),             \
                          dim3(64 * kMergeWaves), 0, s, c, nwg, merge_wgs);                   \
@@ -121,9 +132,12 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t dtyp
   do {                                                                                          \
     hipLaunchKernelGGL((paged_decode_stream<T, DD, F>), dim3(nwg), dim3(64 * kDecodeWavesPerWG), \
                        lds, s, c, c.cu_q, c.cu_k, c.table);                                    \
-    if (wide)                                                                                   \
+    if (wide && nb * c.kvh <= kFewSegs)                                                        \
+      hipLaunchKernelGGL((paged_decode_merge<T, DD, F, 8>), dim3(merge_wgs + copy_wgs),         \
+                         dim3(merge_threads(8)), 0, s, c, nwg, merge_wgs);                      \
+    else if (wide)                                                                              \
       hipLaunchKernelGGL((paged_decode_merge<T, DD, F, kMergeWaves>), dim3(merge_wgs + copy_wgs), \
-                         dim3(64 * kMergeWaves), 0, s, c, nwg, merge_wgs);                      \
+                         dim3(merge_threads(kMergeWaves)), 0, s, c, nwg, merge_wgs);            \
     else                                                                                        \
       hipLaunchKernelGGL((paged_decode_merge<T, DD, F, 1>), dim3(merge_wgs + copy_wgs),         \
                          dim3(64 * kMergeWaves), 0, s, c, nwg, merge_wgs);                      \

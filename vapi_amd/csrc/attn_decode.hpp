@@ -560,6 +560,7 @@ __device__ __forceinline__ void copy_new_rows(const AttnArgs& a, uint32_t wg, ui
   constexpr uint32_t kThreads = 64 * kMergeWaves;
   const uint32_t rows = a.n_new * a.kvh;             // per tensor
   const uint64_t total = 2ull * rows * kChunks;
+  if (threadIdx.x >= kThreads) return;  // workgroups of more waves (a wide merge's)
   for (uint64_t i = (uint64_t)wg * kThreads + threadIdx.x; i < total; i += (uint64_t)n_wg * kThreads) {
     const uint32_t c = (uint32_t)(i % kChunks);
     const uint64_t r2 = i / kChunks;
@@ -611,7 +612,7 @@ template <typename T, int D, bool kFuse, int WPS>
 __device__ __forceinline__ void decode_merge_body(const AttnArgs& a, uint32_t nwg,
                                                   uint32_t merge_wgs, uint32_t bid,
                                                   uint32_t nbid) {
-  static_assert(WPS == 1 || WPS == kMergeWaves, "a wave or a workgroup per segment");
+  static_assert(WPS == 1 || WPS >= (int)kMergeWaves, "a wave or a workgroup per segment");
   if constexpr (kFuse) {
     if (bid >= merge_wgs) {
       copy_new_rows<T, D>(a, bid - merge_wgs, nbid - merge_wgs);
@@ -621,7 +622,7 @@ __device__ __forceinline__ void decode_merge_body(const AttnArgs& a, uint32_t nw
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t nseg = a.batch * a.kvh;
-  constexpr uint32_t kSegsPerWG = kMergeWaves / WPS;
+  constexpr uint32_t kSegsPerWG = WPS >= (int)kMergeWaves ? 1 : kMergeWaves / WPS;
   const uint32_t segi = bid * kSegsPerWG + wave / WPS;
   const uint32_t v = wave % WPS;
   if (segi == nseg) {
