@@ -349,7 +349,7 @@ F32_DECODE_CASES = [
     (8, 2, 64, 32, [1, 31, 640, 3000], None, "HND"),
     (64, 4, 128, 16, [48, 700, 1201], None, "HND"),
     (8, 8, 128, 64, [65, 1000, 129, 2], 40, "NHD"),
-    (12, 4, 64, 16, [300] * 40, None, "HND"),
+    (12, 4, 64, 16, [300] * 39 + [600], None, "HND"),
     # G = 32 and 64 (two and four virtual kv heads of 16 query heads)
     (32, 1, 128, 16, [1, 700, 2500], None, "HND"),
     (64, 1, 64, 16, [90, 3000], 50, "NHD"),
