@@ -27,15 +27,19 @@ static int decode_group_shift(uint32_t G) {
 }
 
 // An f32 pool whose calls run on v_mfma_f32_16x16x4_f32: decode rows on the
-// decode stream, prefill rows on paged_prefill_f32. A pure-decode call over
-// at most kSmallKeys keys (config 0's shape) runs the VALU kernel instead:
-// one launch with no split, 14.1 against 16.4 us for config 0 replayed
-// from a graph.
+// decode stream, prefill rows on paged_prefill_f32. A small pure-decode call
+// (at most 512 keys per sequence and 8,192 over the batch, config 0's shape)
+// runs the VALU kernel instead, in one launch with no merge. Replayed from
+// a graph, 16 q / 8 kv heads: config 0 (8 x <= 512 keys) 14.1 against
+// 16.4 us; 16 x 128 10.8 against 14.5; 64 x 256 27.3 against 26.3 and
+// 32 x 512 29.2 against 25.8, where the decode stream takes over.
 constexpr uint32_t kSmallKeys = 512;
+constexpr uint64_t kSmallBatchKeys = 8192;
 static bool f32_mfma_ok(const vapi_kv_pool* p, uint32_t num_heads, uint32_t max_q,
-                        uint32_t max_k) {
+                        uint32_t max_k, uint32_t batch) {
   if (p->dtype != VAPI_KV_F32) return false;
-  if (max_q <= 1 && max_k <= kSmallKeys) return false;
+  if (max_q <= 1 && max_k <= kSmallKeys && (uint64_t)batch * max_k <= kSmallBatchKeys)
+    return false;
   if (p->head_dim != 64 && p->head_dim != 128) return false;
   if (p->block_size < 16 || (p->block_size & (p->block_size - 1))) return false;
   if (num_heads == 0 || num_heads % p->num_kv_heads) return false;
@@ -153,7 +157,7 @@ static size_t required_workspace(const vapi_kv_pool* pool, uint32_t batch, uint3
       num_heads == 0)
     return 0;
   const uint32_t group = num_heads / pool->num_kv_heads;
-  if (!mfma_ok(pool, num_heads) && !f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k))
+  if (!mfma_ok(pool, num_heads) && !f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch))
     return generic_workspace_bytes(batch, pool->num_kv_heads, group, pool->head_dim,
                                    std::max(max_seqlen_q, 1u), max_seqlen_k);
   return skip_decode ? 0 : decode_ws_for(pool, batch, num_heads);
@@ -345,7 +349,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   if (flags & ~(uint32_t)(VAPI_ATTN_DETERMINISTIC | VAPI_ATTN_NO_DECODE_ROWS))
     VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: unknown flags 0x%x", flags);
   if (num_heads > 65535 ||
-      (batch > 65535 && !mfma_ok(pool, num_heads) && !f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k)))
+      (batch > 65535 && !mfma_ok(pool, num_heads) && !f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch)))
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: batch %u / heads %u too large",
             batch, num_heads);
   // A batch the caller says has no decode rows (and which is not a fused
@@ -354,7 +358,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   // no workspace.
   const bool skip_decode = (flags & VAPI_ATTN_NO_DECODE_ROWS) && !fuse && max_seqlen_q > 1 &&
                            (mfma_ok(pool, num_heads) ||
-                            f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k));
+                            f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch));
   // The sequences the prefill grid covers: those the host named (a mixed
   // step's few prefill chunks among many decode rows), else all of them. A
   // prefill-only call covers every row and ignores the list.
@@ -368,7 +372,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
                    pool->head_dim) >
           0xFFFFFFFFull)
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: prefill batch too large for one launch");
-  if (f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k) && max_seqlen_q > 1 &&
+  if (f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch) && max_seqlen_q > 1 &&
       prefill_f32_items(pf_n, pool->num_kv_heads, num_heads / pool->num_kv_heads,
                         max_seqlen_q) > 0xFFFFFFFFull)
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: prefill batch too large for one launch");
@@ -465,7 +469,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
       launch_prefill(a, max_seqlen_q, max_seqlen_k, g.d, bf16,
                      room ? (char*)workspace + off : nullptr, room ? workspace_bytes - off : 0, s);
     }
-  } else if (f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k)) {
+  } else if (f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch)) {
     if (skip_decode) {
       a.pf_min_q = 1;
     } else {
