@@ -614,6 +614,10 @@ SPLIT_CASES = [
     (torch.bfloat16, 16, 4, 128, 16, [320], [4000], None, "HND"),
     (torch.bfloat16, 16, 4, 256, 16, [100, 1], [3000, 2000], None, "HND"),
     (torch.float16, 8, 8, 256, 32, [48], [2500], 900, "NHD"),
+    # f32 pools: paged_prefill_f32's split (waves, not workgroups) and its merge.
+    (torch.float32, 32, 8, 128, 16, [128], [8192], None, "HND"),
+    (torch.float32, 16, 4, 64, 32, [100, 1], [3000, 2000], 500, "NHD"),
+    (torch.float32, 32, 8, 128, 16, [512], [4096], None, "HND-bm"),
 ]
 
 
@@ -634,7 +638,8 @@ def test_small_prefill_batches_split_their_keys_and_match_the_oracle(case):
     assert full > decode_only  # the split asks for room
     wl = -1 if window is None else window - 1
     want = oracle_out(q, c, 0, batch, d ** -0.5, window)
-    tol = (2e-2 if dtype == torch.bfloat16 else 1e-2) * float(want.abs().max())
+    tol = (1e-5 if dtype == torch.float32 else
+           (2e-2 if dtype == torch.bfloat16 else 1e-2) * float(want.abs().max()))
     prep = PreparedAttention.from_batch(batch, DEV, cache=c, num_heads=heads)
     got = torch.full_like(q, float("nan"))
     _lib.check(lib.vapi_paged_attention(

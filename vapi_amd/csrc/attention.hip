@@ -163,6 +163,23 @@ static size_t required_workspace(const vapi_kv_pool* pool, uint32_t batch, uint3
   return skip_decode ? 0 : decode_ws_for(pool, batch, num_heads);
 }
 
+// The optional part of the workspace: the prefill key split's partials for
+// n_prefill sequences with prefill rows (a batch of `batch`).
+static size_t split_bytes(const vapi_kv_pool* pool, uint32_t batch, uint32_t num_heads,
+                          uint32_t max_seqlen_q, uint32_t max_seqlen_k, uint32_t n_prefill) {
+  if (!pool || pool->num_kv_heads == 0 || num_heads % pool->num_kv_heads || batch == 0 ||
+      num_heads == 0)
+    return 0;
+  const uint32_t kvh = pool->num_kv_heads, group = num_heads / kvh;
+  if (mfma_ok(pool, num_heads))
+    return prefill_split_bytes(n_prefill, kvh, group, pool->head_dim, max_seqlen_q,
+                               max_seqlen_k);
+  if (f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch))
+    return prefill_f32_split_bytes(n_prefill, kvh, group, pool->head_dim, max_seqlen_q,
+                                   max_seqlen_k);
+  return 0;
+}
+
 extern "C" {
 
 size_t vapi_paged_attention_workspace_size(const vapi_kv_pool* pool,
@@ -171,13 +188,9 @@ size_t vapi_paged_attention_workspace_size(const vapi_kv_pool* pool,
                                            uint32_t max_seqlen_k) {
   const size_t need =
       required_workspace(pool, batch, num_heads, max_seqlen_q, max_seqlen_k, false);
-  if (!pool || pool->num_kv_heads == 0 || num_heads % pool->num_kv_heads || batch == 0 ||
-      num_heads == 0 || !mfma_ok(pool, num_heads))
-    return need;
   // Past the decode's part: what a small prefill batch's key split uses
   // (optional: a smaller workspace only means fewer splits).
-  return need + prefill_split_bytes(batch, pool->num_kv_heads, num_heads / pool->num_kv_heads,
-                                    pool->head_dim, max_seqlen_q, max_seqlen_k);
+  return need + split_bytes(pool, batch, num_heads, max_seqlen_q, max_seqlen_k, batch);
 }
 
 size_t vapi_paged_attention_prepared_workspace_size(const vapi_kv_pool* pool, uint32_t batch,
@@ -186,12 +199,8 @@ size_t vapi_paged_attention_prepared_workspace_size(const vapi_kv_pool* pool, ui
                                                     uint32_t max_seqlen_k) {
   const size_t need =
       required_workspace(pool, batch, num_heads, max_seqlen_q, max_seqlen_k, false);
-  if (!pool || pool->num_kv_heads == 0 || num_heads % pool->num_kv_heads || batch == 0 ||
-      num_heads == 0 || !mfma_ok(pool, num_heads))
-    return need;
-  return need + prefill_split_bytes(std::min(n_prefill, batch), pool->num_kv_heads,
-                                    num_heads / pool->num_kv_heads, pool->head_dim,
-                                    max_seqlen_q, max_seqlen_k);
+  return need + split_bytes(pool, batch, num_heads, max_seqlen_q, max_seqlen_k,
+                            std::min(n_prefill, batch));
 }
 
 int vapi_paged_attention_prepared(const vapi_kv_pool* pool, uint32_t layer, const void* q,
@@ -476,7 +485,15 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
       dec.num_waves = decode_num_waves();
       launch_decode(dec, workspace, g.d, pool->dtype, s);
     }
-    if (max_seqlen_q > 1 && pf_n > 0) launch_prefill_f32(a, max_seqlen_q, g.d, s);
+    if (max_seqlen_q > 1 && pf_n > 0) {
+      // The workspace past the decode's part (never its first 256 bytes,
+      // the XCD shares) serves the key split, as for 16-bit pools.
+      const size_t off = std::max<size_t>((need + 255) & ~(size_t)255, 256);
+      const bool room = workspace && workspace_bytes > off;
+      launch_prefill_f32(a, max_seqlen_q, max_seqlen_k, g.d,
+                         room ? (char*)workspace + off : nullptr,
+                         room ? workspace_bytes - off : 0, s);
+    }
   } else {
     if (g.d > 256)
       VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: head_dim %u > 256", g.d);

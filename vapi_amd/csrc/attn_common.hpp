@@ -564,6 +564,13 @@ __device__ __forceinline__ void store_row_f32(float* row, const floatx4 (&o)[D /
                       o[4 * h + 3][i] * scale);
 }
 
+// Bytes of one (item, split) partial block of a prefill key split: (m, l)
+// f32 per row, then o / l per row in f32 (the split adds no rounding before
+// the merge).
+__host__ __device__ constexpr uint64_t pf_part_bytes(uint32_t rows, uint32_t d) {
+  return (uint64_t)rows * (8 + 4 * d);
+}
+
 // ---- launchers (one per translation unit) ----------------------------------
 
 
@@ -600,7 +607,16 @@ size_t prefill_split_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uint32_
 // Prefill rows of an f32 pool (head_dim 64 or 128) on f32 MFMAs, over
 // a.pf_seqs_n sequences; waves of the launch (a launch needs it below 2^32).
 uint64_t prefill_f32_items(uint32_t n_seqs, uint32_t kvh, uint32_t group, uint32_t max_q);
-void launch_prefill_f32(const AttnArgs& a, uint32_t max_q, uint32_t head_dim, hipStream_t s);
+// With a workspace (`split_ws`), a batch of fewer waves than the GPU holds
+// splits its keys; the merge runs as a second launch.
+void launch_prefill_f32(const AttnArgs& a, uint32_t max_q, uint32_t max_k, uint32_t head_dim,
+                        void* split_ws, size_t split_ws_bytes, hipStream_t s);
+// Workspace the f32 prefill's key split wants for this shape (0: no split).
+size_t prefill_f32_split_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t head_dim,
+                               uint32_t max_q, uint32_t max_k);
+void launch_prefill_merge_f32(const AttnArgs& a, uint32_t qtiles, uint32_t rows_per_item,
+                              uint32_t n_split, const float* part, uint64_t base,
+                              uint32_t head_dim, hipStream_t s);
 // Any row, any dtype, head_dim <= 256 (VALU); split contexts combine their
 // partials through `workspace` (generic_workspace_bytes).
 void launch_generic(const AttnArgs& a, uint32_t max_q, uint32_t max_k, uint32_t head_dim,

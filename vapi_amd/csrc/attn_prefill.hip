@@ -159,11 +159,6 @@ __device__ __forceinline__ void lgkm_wait(uint2 (&r)[4]) {
                    : "memory");
 }
 
-// Bytes of one (item, split) partial block: (m, l) f32 per row, then o / l
-// per row in f32 (the split adds no rounding before the merge).
-__host__ __device__ constexpr uint64_t pf_part_bytes(uint32_t rows, uint32_t d) {
-  return (uint64_t)rows * (8 + 4 * d);
-}
 
 // With n_split > 1 the keys a workgroup would walk are cut into n_split
 // contiguous runs of steps, one workgroup each (a batch too small to fill
@@ -504,7 +499,10 @@ __device__ __forceinline__ void prefill_merge_body(const AttnArgs& a, uint32_t q
   const uint32_t j = row / G, hl = row % G;
   T* orow = (T*)a.out + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * D + dq;
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  *(uint2*)orow = make_uint2(pack2<T>(o[0] * inv, o[1] * inv), pack2<T>(o[2] * inv, o[3] * inv));
+  if constexpr (sizeof(T) == 4)
+    *(float4*)orow = make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
+  else
+    *(uint2*)orow = make_uint2(pack2<T>(o[0] * inv, o[1] * inv), pack2<T>(o[2] * inv, o[3] * inv));
 }
 
 template <typename T, int D>
@@ -667,6 +665,21 @@ void launch_mixed(const AttnArgs& a_in, void* workspace, uint32_t max_q, uint32_
     else VK_MIX(f16_t, 64);
   }
 #undef VK_MIX
+}
+
+// The merge of paged_prefill_f32's key split: `base` items of rows_per_item
+// rows, n_split partials each.
+void launch_prefill_merge_f32(const AttnArgs& a, uint32_t qtiles, uint32_t rows_per_item,
+                              uint32_t n_split, const float* part, uint64_t base,
+                              uint32_t head_dim, hipStream_t s) {
+  if (head_dim == 128)
+    hipLaunchKernelGGL((paged_prefill_merge<float, 128>),
+                       dim3((uint32_t)(base * (rows_per_item / (256 / 32)))), dim3(256), 0, s, a,
+                       qtiles, rows_per_item, n_split, part);
+  else
+    hipLaunchKernelGGL((paged_prefill_merge<float, 64>),
+                       dim3((uint32_t)(base * (rows_per_item / (256 / 16)))), dim3(256), 0, s, a,
+                       qtiles, rows_per_item, n_split, part);
 }
 
 size_t prefill_split_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t head_dim,

@@ -25,15 +25,22 @@ namespace vk {
 
 constexpr int kPf32Waves = 4;
 
-template <int D, int RT>
+// kSplit: the keys a wave would walk are cut into n_split contiguous runs
+// of steps, one wave each (a batch too small to fill the GPU with query
+// tiles alone); each writes its rows' (m, l, o / l) to `part`
+// (pf_part_bytes of 16 * RT rows per (item, split)) for the merge.
+template <int D, int RT, bool kSplit>
 __global__ __launch_bounds__(64 * kPf32Waves, 1) void paged_prefill_f32(
-    AttnArgs a, uint32_t qtiles, uint32_t n_items) {
+    AttnArgs a, uint32_t qtiles, uint32_t n_items, uint32_t n_split_arg,
+    float* __restrict__ part) {
+  const uint32_t n_split = kSplit ? n_split_arg : 1u;
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t item = xcd_remap(blockIdx.x, gridDim.x) * kPf32Waves + wave;
   if (item >= n_items) return;
-  // Item order: query tile fastest, then kv head, then sequence.
-  const uint32_t qt = item % qtiles, rest = item / qtiles;
+  // Item order: query tile fastest, then key split, kv head, sequence.
+  const uint32_t qt = item % qtiles, rest_s = item / qtiles;
+  const uint32_t split = rest_s % n_split, rest = rest_s / n_split;
   const uint32_t kh = rest % a.kvh;
   const uint32_t seq = a.pf_seqs ? a.pf_seqs[rest / a.kvh] : rest / a.kvh;
   if (seq >= a.batch) return;
@@ -76,6 +83,14 @@ __global__ __launch_bounds__(64 * kPf32Waves, 1) void paged_prefill_f32(
   int32_t klo, khi, unused;
   key_range(offset + (int32_t)(row0 / G), len_k, a.wl, a.wr, klo, unused);
   key_range(offset + (int32_t)(r_last / G), len_k, a.wl, a.wr, unused, khi);
+  if (kSplit) {
+    // This split's share of the wave's 32-key steps (empty: khi < klo).
+    const int32_t first = klo & ~31;
+    const uint32_t steps = khi >= klo ? (uint32_t)(((khi & ~31) - first) / 32 + 1) : 0u;
+    const uint32_t a0 = split * steps / n_split, a1 = (split + 1) * steps / n_split;
+    klo = max(klo, first + 32 * (int32_t)a0);
+    khi = min(khi, first + 32 * (int32_t)a1 - 1);
+  }
 
   float m_run[RT], l_run[RT];
   floatx4 o[RT][D / 16];
@@ -119,6 +134,19 @@ __global__ __launch_bounds__(64 * kPf32Waves, 1) void paged_prefill_f32(
     }
   }
 
+  if constexpr (kSplit) {
+    char* pb = (char*)part + ((uint64_t)(rest * qtiles + qt) * n_split + split) *
+                                 pf_part_bytes(16 * RT, D);
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      const float lt = wave_sum_g(l_run[t]);
+      const uint32_t row = 16 * t + col;
+      if (g == 0) *(float2*)(pb + (uint64_t)row * 8) = make_float2(m_run[t], lt);
+      float* po = (float*)(pb + (uint64_t)16 * RT * 8) + (uint64_t)row * D;
+      store_row_f32<D>(po, o[t], lt > 0.f ? 1.f / lt : 0.f, g);
+    }
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
     const float lt = wave_sum_g(l_run[t]);
@@ -131,23 +159,59 @@ __global__ __launch_bounds__(64 * kPf32Waves, 1) void paged_prefill_f32(
 }
 
 constexpr int kPf32RowTiles = 2;
+constexpr uint32_t kPf32Rows = 16 * kPf32RowTiles;
 
 uint64_t prefill_f32_items(uint32_t n_seqs, uint32_t kvh, uint32_t group, uint32_t max_q) {
-  constexpr uint64_t rows = 16 * kPf32RowTiles;
-  return ((uint64_t)max_q * group + rows - 1) / rows * kvh * n_seqs;
+  return ((uint64_t)max_q * group + kPf32Rows - 1) / kPf32Rows * kvh * n_seqs;
 }
 
-void launch_prefill_f32(const AttnArgs& a, uint32_t max_q, uint32_t head_dim, hipStream_t s) {
-  constexpr uint32_t rows = 16 * kPf32RowTiles;
-  const uint32_t qtiles = (uint32_t)(((uint64_t)max_q * a.group + rows - 1) / rows);
-  const uint64_t items = (uint64_t)qtiles * a.kvh * a.pf_seqs_n;
+// Key splits for `base` waves over at most max_k keys: enough for about one
+// wave per SIMD of a 256-CU GPU (one wave each is the kernel's occupancy),
+// each split keeping at least 8 steps of 32 keys, at most 64; fewer when
+// the workspace given holds fewer partials (at most 256 MiB of them).
+static uint32_t pf32_splits(uint64_t base, uint32_t max_k, uint32_t head_dim, uint64_t bytes) {
+  constexpr uint64_t kTarget = 1024;
+  if (base == 0 || base >= kTarget) return 1;
+  uint64_t n = std::min<uint64_t>((kTarget + base - 1) / base, std::max<uint32_t>(1u, max_k / 256));
+  n = std::min<uint64_t>(n, 64);
+  const uint64_t cap = std::min<uint64_t>(bytes, 256ull << 20);
+  while (n > 1 && base * n * pf_part_bytes(kPf32Rows, head_dim) > cap) --n;
+  return (uint32_t)n;
+}
+
+size_t prefill_f32_split_bytes(uint32_t batch, uint32_t kvh, uint32_t group, uint32_t head_dim,
+                               uint32_t max_q, uint32_t max_k) {
+  if (max_q <= 1) return 0;
+  const uint64_t base = prefill_f32_items(batch, kvh, group, max_q);
+  const uint32_t n = pf32_splits(base, max_k, head_dim, ~0ull);
+  return n > 1 ? (size_t)(base * n * pf_part_bytes(kPf32Rows, head_dim)) : 0;
+}
+
+void launch_prefill_f32(const AttnArgs& a, uint32_t max_q, uint32_t max_k, uint32_t head_dim,
+                        void* split_ws, size_t split_ws_bytes, hipStream_t s) {
+  const uint32_t qtiles = (uint32_t)(((uint64_t)max_q * a.group + kPf32Rows - 1) / kPf32Rows);
+  const uint64_t base = (uint64_t)qtiles * a.kvh * a.pf_seqs_n;
+  // No split without a workspace, nor for a deterministic call (its output
+  // must not depend on the workspace it is given).
+  const uint32_t n_split =
+      split_ws && !a.deterministic ? pf32_splits(base, max_k, head_dim, split_ws_bytes) : 1;
+  const uint64_t items = base * n_split;
   const uint32_t wgs = (uint32_t)((items + kPf32Waves - 1) / kPf32Waves);
-  if (head_dim == 128)
-    hipLaunchKernelGGL((paged_prefill_f32<128, kPf32RowTiles>), dim3(wgs), dim3(64 * kPf32Waves),
-                       0, s, a, qtiles, (uint32_t)items);
-  else
-    hipLaunchKernelGGL((paged_prefill_f32<64, kPf32RowTiles>), dim3(wgs), dim3(64 * kPf32Waves),
-                       0, s, a, qtiles, (uint32_t)items);
+  float* part = n_split > 1 ? (float*)split_ws : nullptr;
+#define VK_PF32(DD)                                                                             \
+  do {                                                                                          \
+    if (n_split > 1) {                                                                          \
+      hipLaunchKernelGGL((paged_prefill_f32<DD, kPf32RowTiles, true>), dim3(wgs),               \
+                         dim3(64 * kPf32Waves), 0, s, a, qtiles, (uint32_t)items, n_split, part); \
+      launch_prefill_merge_f32(a, qtiles, kPf32Rows, n_split, part, base, DD, s);               \
+    } else {                                                                                    \
+      hipLaunchKernelGGL((paged_prefill_f32<DD, kPf32RowTiles, false>), dim3(wgs),              \
+                         dim3(64 * kPf32Waves), 0, s, a, qtiles, (uint32_t)items, 1u, nullptr); \
+    }                                                                                           \
+  } while (0)
+  if (head_dim == 128) VK_PF32(128);
+  else VK_PF32(64);
+#undef VK_PF32
 }
 
 }  // namespace vk
