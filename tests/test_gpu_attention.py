@@ -210,6 +210,16 @@ CASES = [
     (torch.float32, 16, 8, 128, 16, [1, 9, 1], [64, 512, 200], None, "HND-bm"),
     (torch.bfloat16, 16, 4, 256, 16, [1, 30, 1], [1000, 300, 17], None, "HND-bm"),
     (torch.float32, 12, 4, 80, 16, [1, 20], [1500, 700], None, "NHD-bm"),
+    # Other head dims (multiples of 8 up to 256) in decode-only batches: the
+    # decode stream at the next of 64, 128, 256, zeros past head_dim.
+    (torch.bfloat16, 32, 8, 80, 16, [1, 1, 1, 1, 1], [1, 17, 600, 1500, 4000], None, "HND"),
+    (torch.float16, 16, 4, 96, 32, [1, 1, 1], [65, 2100, 31], 40, "NHD"),
+    (torch.bfloat16, 8, 8, 48, 16, [1, 1], [900, 129], None, "HND"),
+    (torch.bfloat16, 6, 2, 16, 16, [1, 1], [50, 700], 6, "HND"),
+    (torch.bfloat16, 64, 2, 160, 16, [1, 1], [900, 2500], 300, "HND"),
+    (torch.bfloat16, 12, 4, 112, 64, [1, 0, 1], [3000, 9, 129], None, "NHD-bm"),
+    (torch.float16, 6, 2, 192, 16, [1, 1, 1], [500, 70, 2000], 30, "HND"),
+    (torch.bfloat16, 24, 8, 80, 16, [1] * 3, [1000, 20, 300], None, "HND"),
     # A 16-bit pool the MFMA paths do not take, on the generic kernel:
     # block_size 8.
     (torch.bfloat16, 16, 8, 128, 8, [1, 12], [210, 50], None, "HND"),

@@ -6,8 +6,10 @@
 // block_size >= 16 and at most 16 query heads per kv head (up to 64 when a
 // split into 2 or 4 equal groups of at most 16 exists); an f32 pool of
 // that shape (head_dim 64 or 128) runs the decode stream and an f32 prefill
-// kernel (attn_prefill_f32.hip) on f32 MFMAs; every other shape runs the
-// VALU kernel (attn_generic.hip).
+// kernel (attn_prefill_f32.hip) on f32 MFMAs; a 16-bit decode-only call at a
+// head_dim that is another multiple of 8 up to 256 runs the decode stream
+// padded to the next of 64, 128, 256; every other shape runs the VALU kernel
+// (attn_generic.hip).
 // Replaces paged_attention_cuda/_windowed/_prepared (vapi
 // crates/vapi-backend-candle/src/attention.rs:170-288).
 #include <mutex>
@@ -54,11 +56,29 @@ static bool mfma_ok(const vapi_kv_pool* p, uint32_t num_heads) {
   return decode_group_shift(num_heads / p->num_kv_heads) >= 0;
 }
 
+// The decode kernel's D for a pool's head_dim: itself for 64, 128 and 256,
+// else the next of them (elements past head_dim are zeros).
+static uint32_t decode_dim(uint32_t hd) { return hd <= 64 ? 64 : hd <= 128 ? 128 : 256; }
+
+// A 16-bit pure-decode call whose head_dim is not 64, 128 or 256 (a multiple
+// of 8 below 256: Phi-2's 80, Phi-3's 96, ...) runs the decode stream at
+// decode_dim; calls with prefill rows, and other head dims, stay on the VALU
+// kernel.
+static bool pad_decode_ok(const vapi_kv_pool* p, uint32_t num_heads, uint32_t max_seqlen_q) {
+  if (p->dtype != VAPI_KV_BF16 && p->dtype != VAPI_KV_F16) return false;
+  if (max_seqlen_q > 1) return false;
+  const uint32_t hd = p->head_dim;
+  if (hd == 0 || hd % 8 || hd > 256 || hd == 64 || hd == 128 || hd == 256) return false;
+  if (p->block_size < 16 || (p->block_size & (p->block_size - 1))) return false;
+  if (num_heads == 0 || num_heads % p->num_kv_heads) return false;
+  return decode_group_shift(num_heads / p->num_kv_heads) >= 0;
+}
+
 // The decode's view of the kv heads (virtual ones when G > 16).
 static size_t decode_ws_for(const vapi_kv_pool* p, uint32_t batch, uint32_t num_heads) {
   const uint32_t G = num_heads / p->num_kv_heads;
   const int sh = decode_group_shift(G);
-  return decode_workspace_bytes(batch, p->num_kv_heads << sh, G >> sh, p->head_dim,
+  return decode_workspace_bytes(batch, p->num_kv_heads << sh, G >> sh, decode_dim(p->head_dim),
                                 decode_num_waves());
 }
 
@@ -157,7 +177,9 @@ static size_t required_workspace(const vapi_kv_pool* pool, uint32_t batch, uint3
       num_heads == 0)
     return 0;
   const uint32_t group = num_heads / pool->num_kv_heads;
-  if (!mfma_ok(pool, num_heads) && !f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch))
+  if (!mfma_ok(pool, num_heads) &&
+      !f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch) &&
+      !pad_decode_ok(pool, num_heads, max_seqlen_q))
     return generic_workspace_bytes(batch, pool->num_kv_heads, group, pool->head_dim,
                                    std::max(max_seqlen_q, 1u), max_seqlen_k);
   return skip_decode ? 0 : decode_ws_for(pool, batch, num_heads);
@@ -358,7 +380,9 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   if (flags & ~(uint32_t)(VAPI_ATTN_DETERMINISTIC | VAPI_ATTN_NO_DECODE_ROWS))
     VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: unknown flags 0x%x", flags);
   if (num_heads > 65535 ||
-      (batch > 65535 && !mfma_ok(pool, num_heads) && !f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch)))
+      (batch > 65535 && !mfma_ok(pool, num_heads) &&
+       !f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch) &&
+       !pad_decode_ok(pool, num_heads, max_seqlen_q)))
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: batch %u / heads %u too large",
             batch, num_heads);
   // A batch the caller says has no decode rows (and which is not a fused
@@ -434,6 +458,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   a.pf_seqs = listed ? pf->seqs : nullptr;
   a.pf_seqs_n = pf_n;
   a.kv_shift = 0;
+  a.hd = g.d;
   const hipStream_t s = hs(stream);
   // The decode kernels' arguments: with G > 16 query heads per kv head, the
   // virtual kv heads of at most 16 query heads each.
@@ -478,6 +503,9 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
       launch_prefill(a, max_seqlen_q, max_seqlen_k, g.d, bf16,
                      room ? (char*)workspace + off : nullptr, room ? workspace_bytes - off : 0, s);
     }
+  } else if (pad_decode_ok(pool, num_heads, max_seqlen_q)) {
+    dec.num_waves = decode_num_waves();
+    launch_decode(dec, workspace, decode_dim(g.d), pool->dtype, s);
   } else if (f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch)) {
     if (skip_decode) {
       a.pf_min_q = 1;

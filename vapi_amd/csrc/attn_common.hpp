@@ -74,6 +74,10 @@ struct AttnArgs {
   // kv heads of G / 2^kv_shift query heads each (kvh and group then count
   // the virtual ones); virtual head v reads the K/V of pool head v >> kv_shift.
   uint32_t kv_shift;
+  // The pool's head_dim. The decode also runs head dims that are not a
+  // kernel's D (a multiple of 8 up to 256) at the next of 64, 128 or 256:
+  // elements d >= hd are loaded as zeros and not stored.
+  uint32_t hd;
 };
 
 __device__ __forceinline__ void key_range(int32_t p, int32_t len_k, int32_t wl,
@@ -239,7 +243,7 @@ __device__ __forceinline__ const char* tile_base(const uint32_t* __restrict__ ta
 // K and V tiles of the 32-key step at s0 (keys past `last` re-read it). With
 // `knew` / `vnew` (the row's new key, D contiguous elements) key `last` is
 // read from there instead of the pool: a per-lane address select, no branch.
-template <typename T, int D>
+template <typename T, int D, bool kPad = false>
 __device__ __forceinline__ void load_k(KTile<D>& st, const uint32_t* __restrict__ tab,
                                        const T* kb, const AttnArgs& a, int32_t s0, int32_t last,
                                        uint32_t col, uint32_t g, const char* knew = nullptr) {
@@ -252,7 +256,13 @@ __device__ __forceinline__ void load_k(KTile<D>& st, const uint32_t* __restrict_
     const char* src = kt + kr;
     if (knew != nullptr && (int32_t)col >= last - ts) src = knew + 8 * g * sizeof(T);
 #pragma unroll
-    for (int c = 0; c < KC; ++c) st.k[tt][c] = load_stream((const uint4*)(src + 64u * c));
+    for (int c = 0; c < KC; ++c) {
+      if constexpr (kPad)
+        st.k[tt][c] = 32 * c + 8 * g < a.hd ? load_stream((const uint4*)(src + 64u * c))
+                                             : make_uint4(0u, 0u, 0u, 0u);
+      else
+        st.k[tt][c] = load_stream((const uint4*)(src + 64u * c));
+    }
   }
 }
 
@@ -267,7 +277,7 @@ __host__ __device__ constexpr uint32_t v_d(uint32_t m, int k) {
 template <int D>
 __host__ __device__ constexpr uint32_t v_col0(uint32_t m) { return v_d<D>(m, 0); }
 
-template <typename T, int D>
+template <typename T, int D, bool kPad = false>
 __device__ __forceinline__ void load_v(VTile<D>& st, const uint32_t* __restrict__ tab,
                                        const T* vb, const AttnArgs& a, int32_t s0, int32_t last,
                                        uint32_t col, uint32_t g, const char* vnew = nullptr) {
@@ -286,11 +296,20 @@ __device__ __forceinline__ void load_v(VTile<D>& st, const uint32_t* __restrict_
       if constexpr (D == 256) {
         // Two 16-byte runs, d = 8 col .. +7 and 128 + 8 col .. +7: each load
         // instruction then reads whole 256-byte rows across the 16 lanes.
-        const uint4 x0 = load_stream((const uint4*)src);
-        const uint4 x1 = load_stream((const uint4*)(src + 128 * sizeof(T)));
+        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+        const uint4 x0 = !kPad || v_d<D>(col, 0) < a.hd ? load_stream((const uint4*)src) : z;
+        const uint4 x1 = !kPad || v_d<D>(col, 8) < a.hd
+                             ? load_stream((const uint4*)(src + 128 * sizeof(T))) : z;
         VRow<DPL>& w = st.v[4 * tt + i];
         w.w[0] = x0.x, w.w[1] = x0.y, w.w[2] = x0.z, w.w[3] = x0.w;
         w.w[4] = x1.x, w.w[5] = x1.y, w.w[6] = x1.z, w.w[7] = x1.w;
+      } else if constexpr (kPad) {
+        if (v_col0<D>(col) < a.hd) {
+          st.v[4 * tt + i] = load_vrow<DPL>(src);
+        } else {
+#pragma unroll
+          for (int w = 0; w < DPL / 2; ++w) st.v[4 * tt + i].w[w] = 0u;
+        }
       } else {
         st.v[4 * tt + i] = load_vrow<DPL>(src);
       }
@@ -419,9 +438,9 @@ __device__ __forceinline__ void attend_pv(const VTile<D>& vt, uint4 pf, floatx4 
 
 // Store row `col`'s outputs d = v_d(4g + i, k) of o, scaled, to `row`
 // (16-bit output; DPL-wide runs, or two runs of 8 at head_dim 256).
-template <typename T, int D>
+template <typename T, int D, bool kPad = false>
 __device__ __forceinline__ void store_row(T* row, const floatx4 (&o)[D / 16], float scale,
-                                          uint32_t g) {
+                                          uint32_t g, uint32_t hd = D) {
   constexpr int DPL = D / 16;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -432,10 +451,12 @@ __device__ __forceinline__ void store_row(T* row, const floatx4 (&o)[D / 16], fl
     if constexpr (D == 256) {
 #pragma unroll
       for (int h = 0; h < 2; ++h)
-        *(uint4*)(row + v_d<D>(4 * g + i, 8 * h)) =
-            make_uint4(w[4 * h], w[4 * h + 1], w[4 * h + 2], w[4 * h + 3]);
+        if (!kPad || v_d<D>(4 * g + i, 8 * h) < hd)
+          *(uint4*)(row + v_d<D>(4 * g + i, 8 * h)) =
+              make_uint4(w[4 * h], w[4 * h + 1], w[4 * h + 2], w[4 * h + 3]);
       continue;
     }
+    if (kPad && DPL * (4 * g + i) >= hd) continue;  // padding columns
     T* dst = row + DPL * (4 * g + i);
     if constexpr (DPL == 4) {
       *(uint2*)dst = make_uint2(w[0], w[1]);

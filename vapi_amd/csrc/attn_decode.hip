@@ -3,12 +3,12 @@
 
 namespace vk {
 
-template <typename T, int D, bool kFuse>
+template <typename T, int D, bool kFuse, bool kPad = false>
 __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged_decode_stream(
     AttnArgs a, const uint32_t* __restrict__ cu_q, const uint32_t* __restrict__ cu_k,
     const uint32_t* __restrict__ table) {
   extern __shared__ uint32_t P[];
-  decode_stream_body<T, D, kFuse>(a, cu_q, cu_k, table, P, blockIdx.x, gridDim.x);
+  decode_stream_body<T, D, kFuse, kPad>(a, cu_q, cu_k, table, P, blockIdx.x, gridDim.x);
 }
 
 // Waves per segment of a merge with a workgroup per segment: 8 for at most
@@ -19,10 +19,10 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
 constexpr uint32_t kFewSegs = 16;
 constexpr uint32_t merge_threads(int wps) { return 64u * (wps > (int)kMergeWaves ? wps : kMergeWaves); }
 
-template <typename T, int D, bool kFuse, int WPS>
+template <typename T, int D, bool kFuse, int WPS, bool kPad = false>
 __global__ __launch_bounds__(merge_threads(WPS)) void paged_decode_merge(AttnArgs a, uint32_t nwg,
                                                                       uint32_t merge_wgs) {
-  decode_merge_body<T, D, kFuse, WPS>(a, nwg, merge_wgs, blockIdx.x, gridDim.x);
+  decode_merge_body<T, D, kFuse, WPS, kPad>(a, nwg, merge_wgs, blockIdx.x, gridDim.x);
 }
 
 uint32_t decode_num_waves() {
@@ -128,20 +128,22 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t dtyp
       copy_wgs = (uint32_t)std::min<uint64_t>((chunks + 64 * kMergeWaves - 1) / (64 * kMergeWaves), 1024);
     }
     const size_t lds = (nb + 1 + (fuse ? nb : 0)) * sizeof(uint32_t);
-#define VK_DEC(T, DD, F)                                                                        \
+#define VK_DECP(T, DD, F, PAD)                                                                  \
   do {                                                                                          \
-    hipLaunchKernelGGL((paged_decode_stream<T, DD, F>), dim3(nwg), dim3(64 * kDecodeWavesPerWG), \
-                       lds, s, c, c.cu_q, c.cu_k, c.table);                                    \
+    hipLaunchKernelGGL((paged_decode_stream<T, DD, F, PAD>), dim3(nwg),                         \
+                       dim3(64 * kDecodeWavesPerWG), lds, s, c, c.cu_q, c.cu_k, c.table);      \
     if (wide && nb * c.kvh <= kFewSegs)                                                        \
-      hipLaunchKernelGGL((paged_decode_merge<T, DD, F, 8>), dim3(merge_wgs + copy_wgs),         \
+      hipLaunchKernelGGL((paged_decode_merge<T, DD, F, 8, PAD>), dim3(merge_wgs + copy_wgs),    \
                          dim3(merge_threads(8)), 0, s, c, nwg, merge_wgs);                      \
     else if (wide)                                                                              \
-      hipLaunchKernelGGL((paged_decode_merge<T, DD, F, kMergeWaves>), dim3(merge_wgs + copy_wgs), \
-                         dim3(merge_threads(kMergeWaves)), 0, s, c, nwg, merge_wgs);            \
+      hipLaunchKernelGGL((paged_decode_merge<T, DD, F, kMergeWaves, PAD>),                      \
+                         dim3(merge_wgs + copy_wgs), dim3(merge_threads(kMergeWaves)), 0, s, c, \
+                         nwg, merge_wgs);                                                       \
     else                                                                                        \
-      hipLaunchKernelGGL((paged_decode_merge<T, DD, F, 1>), dim3(merge_wgs + copy_wgs),         \
+      hipLaunchKernelGGL((paged_decode_merge<T, DD, F, 1, PAD>), dim3(merge_wgs + copy_wgs),    \
                          dim3(64 * kMergeWaves), 0, s, c, nwg, merge_wgs);                      \
   } while (0)
+#define VK_DEC(T, DD, F) VK_DECP(T, DD, F, false)
 #define VK_DEC2(T, DD) \
   do {                 \
     if (fuse)          \
@@ -149,7 +151,18 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t dtyp
     else               \
       VK_DEC(T, DD, false); \
   } while (0)
-    if (dtype == VAPI_KV_F32) {  // no fused append on f32 pools
+    if (a.hd != head_dim) {  // a head dim run at the next D (16-bit, no fused append)
+      if (head_dim == 256) {
+        if (bf16) VK_DECP(bf16_t, 256, false, true);
+        else VK_DECP(f16_t, 256, false, true);
+      } else if (head_dim == 128) {
+        if (bf16) VK_DECP(bf16_t, 128, false, true);
+        else VK_DECP(f16_t, 128, false, true);
+      } else {
+        if (bf16) VK_DECP(bf16_t, 64, false, true);
+        else VK_DECP(f16_t, 64, false, true);
+      }
+    } else if (dtype == VAPI_KV_F32) {  // no fused append on f32 pools
       if (head_dim == 128) VK_DEC(float, 128, false);
       else VK_DEC(float, 64, false);
     } else if (bf16) {
@@ -163,6 +176,7 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t dtyp
     }
 #undef VK_DEC2
 #undef VK_DEC
+#undef VK_DECP
   }
 }
 

@@ -175,14 +175,17 @@ __device__ __forceinline__ DecodePos next_segment(const AttnArgs& a,
   return p;
 }
 
-template <typename T, int D>
+// kPad: the pool's head_dim a.hd is below D (its rows are a.hd apart);
+// elements d >= a.hd are zeros.
+template <typename T, int D, bool kPad = false>
 __device__ __forceinline__ void load_q(uint4* qs, const AttnArgs& a, const DecodePos& p,
                                        uint32_t lane, uint32_t col, uint32_t g) {
   asm volatile("" : "+v"(lane), "+v"(col), "+v"(g));  // see flush_piece
   // MFMA columns past the group carry a copy of the group's first head: their
   // results are computed and never stored.
   const uint32_t h = col < a.group ? col : 0;
-  const T* qrow = (const T*)a.q + ((uint64_t)p.q0 * a.num_heads + p.kh * a.group + h) * D;
+  const uint32_t hd = kPad ? a.hd : (uint32_t)D;
+  const T* qrow = (const T*)a.q + ((uint64_t)p.q0 * a.num_heads + p.kh * a.group + h) * hd;
   if constexpr (sizeof(T) == 4) {
     // f32: D / 16 float4 per lane, Q[h][16c + 4g .. +3] (the f32 MFMA's k
     // order); a negative scale flips the sign bit of every element.
@@ -196,14 +199,15 @@ __device__ __forceinline__ void load_q(uint4* qs, const AttnArgs& a, const Decod
   } else {
 #pragma unroll
     for (int c = 0; c < D / 32; ++c) {
-      uint4 x = *(const uint4*)(qrow + 32 * c + 8 * g);
+      uint4 x = !kPad || 32 * c + 8 * g < hd ? *(const uint4*)(qrow + 32 * c + 8 * g)
+                                             : make_uint4(0u, 0u, 0u, 0u);
       x.x ^= a.q_sign, x.y ^= a.q_sign, x.z ^= a.q_sign, x.w ^= a.q_sign;
       qs[c * 64 + lane] = x;
     }
   }
 }
 
-template <typename T, int D>
+template <typename T, int D, bool kPad = false>
 __device__ __forceinline__ void load_step_k(KTile<D>& st, const AttnArgs& a,
                                             const uint32_t* __restrict__ table,
                                             const DecodePos& p, uint32_t col, uint32_t g) {
@@ -211,10 +215,10 @@ __device__ __forceinline__ void load_step_k(KTile<D>& st, const AttnArgs& a,
   const T* kb = (const T*)a.k + (p.kh >> a.kv_shift) * a.head_e;
   const char* knew =
       p.fuse ? a.k_new + ((uint64_t)p.q0 * a.kvh + p.kh) * D * sizeof(T) : nullptr;
-  load_k<T, D>(st, tab, kb, a, p.key0, p.len_k - 1, col, g, knew);
+  load_k<T, D, kPad>(st, tab, kb, a, p.key0, p.len_k - 1, col, g, knew);
 }
 
-template <typename T, int D>
+template <typename T, int D, bool kPad = false>
 __device__ __forceinline__ void load_step_v(VTile<D>& st, const AttnArgs& a,
                                             const uint32_t* __restrict__ table,
                                             const DecodePos& p, uint32_t col, uint32_t g) {
@@ -222,13 +226,13 @@ __device__ __forceinline__ void load_step_v(VTile<D>& st, const AttnArgs& a,
   const T* vb = (const T*)a.v + (p.kh >> a.kv_shift) * a.head_e;
   const char* vnew =
       p.fuse ? a.v_new + ((uint64_t)p.q0 * a.kvh + p.kh) * D * sizeof(T) : nullptr;
-  load_v<T, D>(st, tab, vb, a, p.key0, p.len_k - 1, col, g, vnew);
+  load_v<T, D, kPad>(st, tab, vb, a, p.key0, p.len_k - 1, col, g, vnew);
 }
 
 
 // Write a finished piece of segment (p.seq, p.kh): the final output if the
 // piece is the whole segment, else a partial in slot `slot`.
-template <typename T, int D>
+template <typename T, int D, bool kPad = false>
 __device__ __forceinline__ void flush_piece(const AttnArgs& a, const DecodePos& p, bool whole,
                                             uint32_t slot, const floatx4 (&o)[D / 16],
                                             float m_run, float l_run, uint32_t col, uint32_t g) {
@@ -251,8 +255,9 @@ __device__ __forceinline__ void flush_piece(const AttnArgs& a, const DecodePos& 
     return;
   }
   if (whole) {
-    T* orow = (T*)a.out + ((uint64_t)p.q0 * a.num_heads + p.kh * G + col) * D;
-    store_row<T, D>(orow, o, l_tot > 0.f ? 1.f / l_tot : 0.f, g);
+    const uint32_t hd = kPad ? a.hd : (uint32_t)D;
+    T* orow = (T*)a.out + ((uint64_t)p.q0 * a.num_heads + p.kh * G + col) * hd;
+    store_row<T, D, kPad>(orow, o, l_tot > 0.f ? 1.f / l_tot : 0.f, g, hd);
   } else {
     float* po = a.ws_o + ((uint64_t)slot * G + col) * D;
 #pragma unroll
@@ -268,7 +273,7 @@ __device__ __forceinline__ void flush_piece(const AttnArgs& a, const DecodePos& 
 // The persistent stream of workgroup `bid` of `nwg` (4 waves). P: the
 // launch's dynamic LDS, step prefix sums (batch + 1), then with kFuse the
 // per-sequence fused-append flags FZ (batch).
-template <typename T, int D, bool kFuse>
+template <typename T, int D, bool kFuse, bool kPad = false>
 __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
                                                    const uint32_t* __restrict__ cu_q,
                                                    const uint32_t* __restrict__ cu_k,
@@ -360,7 +365,7 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
   constexpr bool kF32 = sizeof(T) == 4;
   __shared__ uint4 q_lds[kDecodeWavesPerWG][D / 32 * 64 * sizeof(T) / 2];
   uint4* qs = q_lds[wave];
-  load_q<T, D>(qs, a, pos, lane, col, g);
+  load_q<T, D, kPad>(qs, a, pos, lane, col, g);
   bool piece_first = pos.seg_first;
   float m_run = kNegBig, l_run = 0.f;
   floatx4 o[DPL];
@@ -387,8 +392,8 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
     load_halves(kA, vA, pos, 0);
     load_halves(kA, vA, pos, 1);
   } else {
-    load_step_k<T, D>(kA, a, table, pos, col, g);
-    load_step_v<T, D>(vA, a, table, pos, col, g);
+    load_step_k<T, D, kPad>(kA, a, table, pos, col, g);
+    load_step_v<T, D, kPad>(vA, a, table, pos, col, g);
   }
 
   // One step: find the next step, issue its K and V, attend over the current
@@ -437,8 +442,8 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
         load_halves(kn, vn, nxt, tt);
       }
     } else {
-      load_step_k<T, D>(kn, a, table, nxt, col, g);
-      load_step_v<T, D>(vn, a, table, nxt, col, g);
+      load_step_k<T, D, kPad>(kn, a, table, nxt, col, g);
+      load_step_v<T, D, kPad>(vn, a, table, nxt, col, g);
       uint4 qf[D / 32];
 #pragma unroll
       for (int c = 0; c < D / 32; ++c) qf[c] = qs[c * 64 + lane];
@@ -454,13 +459,13 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
         if (piece_first) a.seg_ranges[2 * seg] = r;
         if (seg_ends) a.seg_ranges[2 * seg + 1] = r;
       }
-      flush_piece<T, D>(a, pos, piece_first && seg_ends, r + seg, o, m_run, l_run, col, g);
+      flush_piece<T, D, kPad>(a, pos, piece_first && seg_ends, r + seg, o, m_run, l_run, col, g);
       if (!more) return false;
       m_run = kNegBig;
       l_run = 0.f;
 #pragma unroll
       for (int k = 0; k < DPL; ++k) o[k] = floatx4{0.f, 0.f, 0.f, 0.f};
-      load_q<T, D>(qs, a, nxt, lane, col, g);
+      load_q<T, D, kPad>(qs, a, nxt, lane, col, g);
       piece_first = nxt.seg_first;
     }
     pos = nxt;
@@ -608,7 +613,7 @@ __device__ __forceinline__ void store_outputs(T* dst, uint32_t n, const float (&
 // combined through LDS.
 // Workgroup `bid` of `nbid` (kMergeWaves waves); workgroups from merge_wgs
 // on copy the fused append's new rows.
-template <typename T, int D, bool kFuse, int WPS>
+template <typename T, int D, bool kFuse, int WPS, bool kPad = false>
 __device__ __forceinline__ void decode_merge_body(const AttnArgs& a, uint32_t nwg,
                                                   uint32_t merge_wgs, uint32_t bid,
                                                   uint32_t nbid) {
@@ -647,7 +652,23 @@ __device__ __forceinline__ void decode_merge_body(const AttnArgs& a, uint32_t nw
   const uint32_t E = G * D / 64;
   const uint32_t e_lane = lane * E;
   const uint32_t h0 = e_lane / D, h1 = (e_lane + E - 1) / D;
-  T* orow = (T*)a.out + ((uint64_t)q0 * a.num_heads + kh * G) * D;
+  // kPad: output rows are a.hd apart and elements d >= a.hd (padding) are
+  // not stored; the n outputs from index e of the [G][D] partials are
+  // stored one by one (they may span two heads).
+  const uint32_t hd = kPad ? a.hd : (uint32_t)D;
+  T* orow = (T*)a.out + ((uint64_t)q0 * a.num_heads + kh * G) * hd;
+  auto store = [&](uint32_t e, uint32_t n, const float (&O)[8], const float (&L)[8]) {
+    if constexpr (kPad) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t ej = e + j, d = ej % D;
+        if (j < (int)n && d < hd)
+          orow[(ej / D) * hd + d] = from_f32<T>(L[j] > 0.f ? O[j] / L[j] : 0.f);
+      }
+    } else {
+      store_outputs<T>(orow + e, n, O, L);
+    }
+  };
   // Up to R ranges per round trip; E is a multiple of 4 for G*D >= 256
   // (D is 64, 128 or 256), so outputs move as float4. (With a workgroup per
   // segment, 8 ranges per wave measured 0.6-2.4 us faster per call than 16
@@ -742,11 +763,11 @@ __device__ __forceinline__ void decode_merge_body(const AttnArgs& a, uint32_t nw
           }
           L[j] = Lj, O[j] = Oj;
         }
-        store_outputs<T>(orow + e_lane + j0, n, O, L);
+        store(e_lane + j0, n, O, L);
       }
       __syncthreads();  // cmb is reused by the next eight outputs
     } else {
-      store_outputs<T>(orow + e_lane + j0, n, O, L);
+      store(e_lane + j0, n, O, L);
     }
   }
 }
