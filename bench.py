@@ -310,13 +310,12 @@ def bench_valu(steps, warmup):
     """f32 pools: config 0 (Qwen3-0.6B-shaped f32 decode, the reference's CPU
     parity case: at most 512 keys, so the VALU kernel in one launch), config
     2's batch over an f32 pool (1.5 GB of K/V, the f32-MFMA decode stream),
-    the VALU kernel on config 2's batch with head_dim 80, and config 3 on an
-    f32 pool (the f32-MFMA prefill)."""
+    the same batch at head_dim 80 (the stream padded to 128), and config 3
+    on an f32 pool (the f32-MFMA prefill)."""
     out = {}
     for name, w, heads, kvh, d in (("cfg0_f32", workload.config0_decode_small(), 16, 8, None),
                                    ("cfg2_shape_f32", workload.config2_decode(), 32, 8, None),
-                                   ("cfg2_shape_f32_d80_valu", workload.config2_decode(), 32, 8,
-                                    80)):
+                                   ("cfg2_shape_f32_d80", workload.config2_decode(), 32, 8, 80)):
         d = d or w.head_dim
         cache = PagedKvCache(1, w.num_blocks, w.block_size, kvh, d, torch.float32, "HND")
         workload.fill_normal(cache._slab, workload.seed_for(0))
@@ -332,8 +331,9 @@ def bench_valu(steps, warmup):
         kv = int(w.lens.sum()) * 2 * kvh * d * 4
         out[name] = dict(us=ms * 1e3, graph_us=gms * 1e3, kv_bytes=kv,
                          gbs=kv / (ms * 1e-3) / 1e9, graph_gbs=kv / (gms * 1e-3) / 1e9,
-                         path=("VALU kernel" if name.endswith("valu") or name == "cfg0_f32"
-                               else "f32 MFMA decode stream"))
+                         path=("VALU kernel" if name == "cfg0_f32"
+                               else "f32 MFMA decode stream (head_dim 80: padded to 128)"
+                               if name.endswith("d80") else "f32 MFMA decode stream"))
         log(f"f32 attention {name}: {ms * 1e3:.1f} us ({gms * 1e3:.1f} us in a graph), "
             f"{kv / 1e6:.1f} MB of K/V, {out[name]['gbs']:.0f} GB/s, {out[name]['path']}")
         del cache

@@ -342,18 +342,18 @@ def test_the_build_refuses_a_prefill_kernel_that_spills():
 
 
 def test_the_valu_workspace_follows_its_key_chunks():
-    """Head dims without an MFMA kernel (80 here) run the VALU kernel: keys
-    split into chunks of 512, halved down to 64 while the launch has fewer
-    than 512 workgroups; a call whose keys fit one chunk needs no
-    workspace."""
+    """Head dims without an MFMA kernel (82 here: not a multiple of 4) run the
+    VALU kernel: keys split into chunks of 512, halved down to 64 while the
+    launch has fewer than 512 workgroups; a call whose keys fit one chunk
+    needs no workspace."""
     L = _lib.lib()
-    f32 = pool(dtype=_lib.F32, num_kv_heads=8, head_dim=80)
+    f32 = pool(dtype=_lib.F32, num_kv_heads=8, head_dim=82)
     # 64 rows x 8 kv heads = 512 row tiles: 512-key chunks, one chunk.
     assert L.vapi_paged_attention_workspace_size(f32, 64, 32, 1, 512) == 0
     # Two sequences: 16 tiles, so 64-key chunks (8 of them for 512 keys).
     need = L.vapi_paged_attention_workspace_size(f32, 2, 32, 1, 512)
     tiles, chunks = 2 * 8, 8
-    assert need == 256 + tiles * chunks * 16 * (80 + 2) * 4
+    assert need == 256 + tiles * chunks * 16 * (82 + 2) * 4
     assert L.vapi_paged_attention_workspace_size(f32, 2, 32, 1, 64) == 0
 
 

@@ -220,6 +220,9 @@ CASES = [
     (torch.bfloat16, 12, 4, 112, 64, [1, 0, 1], [3000, 9, 129], None, "NHD-bm"),
     (torch.float16, 6, 2, 192, 16, [1, 1, 1], [500, 70, 2000], 30, "HND"),
     (torch.bfloat16, 24, 8, 80, 16, [1] * 3, [1000, 20, 300], None, "HND"),
+    (torch.float32, 32, 8, 80, 16, [1, 1, 1, 1], [1, 600, 1500, 4000], None, "HND"),
+    (torch.float32, 16, 4, 96, 32, [1, 1, 1], [65, 2100, 31], 40, "NHD"),
+    (torch.float32, 8, 8, 40, 16, [1, 1], [900, 1290], None, "HND-bm"),
     # A 16-bit pool the MFMA paths do not take, on the generic kernel:
     # block_size 8.
     (torch.bfloat16, 16, 8, 128, 8, [1, 12], [210, 50], None, "HND"),

@@ -290,14 +290,14 @@ def test_prefill_key_split_adds_no_error_beyond_the_unsplit_call():
 
 
 def test_valu_context_past_max_seqlen_k_stays_inside_its_workspace():
-    """An f32 pool with head_dim 80 (the VALU kernel) whose device len_k exceeds the
+    """An f32 pool with head_dim 82 (not a multiple of 4: the VALU kernel) whose device len_k exceeds the
     max_seqlen_k the call was sized for: the key chunks stop at the launch's
     last chunk (ceil(max_k / c) * c keys, 1,024 here for every chunk size c
     the kernel picks), so neither kernel touches memory past the workspace,
     and the row is the attention over those keys."""
     rng = np.random.default_rng(5)
     lens_k = [3000, 700]
-    c, q, batch = random_case(rng, torch.float32, 8, 2, 80, 16, [1, 1], lens_k, "HND")
+    c, q, batch = random_case(rng, torch.float32, 8, 2, 82, 16, [1, 1], lens_k, "HND")
     prep = PreparedAttention.from_batch(batch, DEV)
     lib = _lib.lib()
     max_k = 1000  # smaller than sequence 0's 3,000 keys
@@ -309,14 +309,14 @@ def test_valu_context_past_max_seqlen_k_stays_inside_its_workspace():
     _lib.check(lib.vapi_paged_attention_ex(
         c.pool, 0, q.data_ptr(), out.data_ptr(), prep.seqlens_q.data_ptr(),
         prep.seqlens_k.data_ptr(), prep.block_table.data_ptr(), 2, prep.block_table.shape[1],
-        1, max_k, 8, 80 ** -0.5, -1, 0, 0, ws.data_ptr(), need, stream_handle()))
+        1, max_k, 8, 82 ** -0.5, -1, 0, 0, ws.data_ptr(), need, stream_handle()))
     torch.cuda.synchronize()
     assert bool((ws[need:] == 0xAB).all()), "the call wrote past its workspace"
     trunc = ForwardBatch(cu_seqlens_q=[0, 1, 2], cu_seqlens_k=[0, 1024, 1024 + 700],
                          block_tables=[batch.block_tables[0][:64], batch.block_tables[1]],
                          max_seqlen_q=1, max_seqlen_k=1024)
-    want = oracle_out(q, c, 0, trunc, 80 ** -0.5)
+    want = oracle_out(q, c, 0, trunc, 82 ** -0.5)
     assert max_abs(out[:1], want[:1]) <= 1e-5
     # sequence 1 fits its 1,000-key bound: ordinary attention
-    full = oracle_out(q, c, 0, batch, 80 ** -0.5)
+    full = oracle_out(q, c, 0, batch, 82 ** -0.5)
     assert max_abs(out[1:], full[1:]) <= 1e-5

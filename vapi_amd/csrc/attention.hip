@@ -60,15 +60,24 @@ static bool mfma_ok(const vapi_kv_pool* p, uint32_t num_heads) {
 // else the next of them (elements past head_dim are zeros).
 static uint32_t decode_dim(uint32_t hd) { return hd <= 64 ? 64 : hd <= 128 ? 128 : 256; }
 
-// A 16-bit pure-decode call whose head_dim is not 64, 128 or 256 (a multiple
-// of 8 below 256: Phi-2's 80, Phi-3's 96, ...) runs the decode stream at
-// decode_dim; calls with prefill rows, and other head dims, stay on the VALU
-// kernel.
-static bool pad_decode_ok(const vapi_kv_pool* p, uint32_t num_heads, uint32_t max_seqlen_q) {
-  if (p->dtype != VAPI_KV_BF16 && p->dtype != VAPI_KV_F16) return false;
+// A pure-decode call whose head_dim is not one of the kernels' (a multiple
+// of 8 below 256 in a 16-bit pool: Phi-2's 80, Phi-3's 96, ...; a multiple
+// of 4 below 128 in an f32 pool, except the small calls the VALU kernel
+// takes, see f32_mfma_ok) runs the decode stream at decode_dim; calls with
+// prefill rows, and other head dims, stay on the VALU kernel.
+static bool pad_decode_ok(const vapi_kv_pool* p, uint32_t num_heads, uint32_t max_seqlen_q,
+                          uint32_t max_seqlen_k, uint32_t batch) {
   if (max_seqlen_q > 1) return false;
   const uint32_t hd = p->head_dim;
-  if (hd == 0 || hd % 8 || hd > 256 || hd == 64 || hd == 128 || hd == 256) return false;
+  if (p->dtype == VAPI_KV_F32) {
+    if (hd == 0 || hd % 4 || hd > 128 || hd == 64 || hd == 128) return false;
+    if (max_seqlen_k <= kSmallKeys && (uint64_t)batch * max_seqlen_k <= kSmallBatchKeys)
+      return false;
+  } else if (p->dtype == VAPI_KV_BF16 || p->dtype == VAPI_KV_F16) {
+    if (hd == 0 || hd % 8 || hd > 256 || hd == 64 || hd == 128 || hd == 256) return false;
+  } else {
+    return false;
+  }
   if (p->block_size < 16 || (p->block_size & (p->block_size - 1))) return false;
   if (num_heads == 0 || num_heads % p->num_kv_heads) return false;
   return decode_group_shift(num_heads / p->num_kv_heads) >= 0;
@@ -179,7 +188,7 @@ static size_t required_workspace(const vapi_kv_pool* pool, uint32_t batch, uint3
   const uint32_t group = num_heads / pool->num_kv_heads;
   if (!mfma_ok(pool, num_heads) &&
       !f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch) &&
-      !pad_decode_ok(pool, num_heads, max_seqlen_q))
+      !pad_decode_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch))
     return generic_workspace_bytes(batch, pool->num_kv_heads, group, pool->head_dim,
                                    std::max(max_seqlen_q, 1u), max_seqlen_k);
   return skip_decode ? 0 : decode_ws_for(pool, batch, num_heads);
@@ -382,7 +391,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   if (num_heads > 65535 ||
       (batch > 65535 && !mfma_ok(pool, num_heads) &&
        !f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch) &&
-       !pad_decode_ok(pool, num_heads, max_seqlen_q)))
+       !pad_decode_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch)))
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: batch %u / heads %u too large",
             batch, num_heads);
   // A batch the caller says has no decode rows (and which is not a fused
@@ -503,7 +512,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
       launch_prefill(a, max_seqlen_q, max_seqlen_k, g.d, bf16,
                      room ? (char*)workspace + off : nullptr, room ? workspace_bytes - off : 0, s);
     }
-  } else if (pad_decode_ok(pool, num_heads, max_seqlen_q)) {
+  } else if (pad_decode_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch)) {
     dec.num_waves = decode_num_waves();
     launch_decode(dec, workspace, decode_dim(g.d), pool->dtype, s);
   } else if (f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch)) {

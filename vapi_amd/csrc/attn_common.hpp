@@ -512,7 +512,7 @@ __device__ __forceinline__ floatx4 mfma16x16x4f32(float a, float b, floatx4 c) {
 // K and V of the 16-key tile at s0 + 16 tt (keys past `last` re-read it).
 // kStream: streaming loads (the decode reads each byte once); the prefill's
 // waves share a kv head's K/V through L2 and load them the ordinary way.
-template <int D, bool kStream = true>
+template <int D, bool kStream = true, bool kPad = false>
 __device__ __forceinline__ void load_half_f32(KHalfF32<D>& kt, VHalfF32<D>& vt,
                                               const uint32_t* __restrict__ tab, const float* kb,
                                               const float* vb, const AttnArgs& a, int32_t s0,
@@ -521,9 +521,12 @@ __device__ __forceinline__ void load_half_f32(KHalfF32<D>& kt, VHalfF32<D>& vt,
   const int32_t lim = last - ts;
   const char* kp = tile_base(tab, kb, a, ts) +
                    ((uint32_t)min((int32_t)col, lim) * a.tok_e + 4 * g) * sizeof(float);
+  const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int c = 0; c < D / 16; ++c)
-    kt.k[c] = kStream ? load_stream((const float4*)(kp + 64u * c)) : *(const float4*)(kp + 64u * c);
+    kt.k[c] = kPad && 16 * c + 4 * g >= a.hd ? z
+              : kStream ? load_stream((const float4*)(kp + 64u * c))
+                        : *(const float4*)(kp + 64u * c);
   const char* vp = tile_base(tab, vb, a, ts);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -531,8 +534,9 @@ __device__ __forceinline__ void load_half_f32(KHalfF32<D>& kt, VHalfF32<D>& vt,
         vp + ((uint32_t)min((int32_t)(4 * g + i), lim) * a.tok_e + 4 * col) * sizeof(float);
 #pragma unroll
     for (int h = 0; h < D / 64; ++h)
-      vt.v[i][h] = kStream ? load_stream((const float4*)(row + 256u * h))
-                           : *(const float4*)(row + 256u * h);
+      vt.v[i][h] = kPad && 64 * h + 4 * col >= a.hd ? z
+                   : kStream ? load_stream((const float4*)(row + 256u * h))
+                             : *(const float4*)(row + 256u * h);
   }
 }
 
@@ -573,14 +577,15 @@ __device__ __forceinline__ void attend_half_f32(const KHalfF32<D>& kt, const VHa
 
 // Row `col`'s outputs of o (the f32 layout above), scaled, as float4 runs
 // d = 64h + 16g + 4i .. +3, to `row` (f32 output or partial).
-template <int D>
+template <int D, bool kPad = false>
 __device__ __forceinline__ void store_row_f32(float* row, const floatx4 (&o)[D / 16],
-                                              float scale, uint32_t g) {
+                                              float scale, uint32_t g, uint32_t hd = D) {
 #pragma unroll
   for (int h = 0; h < D / 64; ++h)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      *(float4*)(row + 64 * h + 16 * g + 4 * i) =
+      if (!kPad || 64 * h + 16 * g + 4 * i < hd)
+        *(float4*)(row + 64 * h + 16 * g + 4 * i) =
           make_float4(o[4 * h][i] * scale, o[4 * h + 1][i] * scale, o[4 * h + 2][i] * scale,
                       o[4 * h + 3][i] * scale);
 }

@@ -151,7 +151,10 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t dtyp
     else               \
       VK_DEC(T, DD, false); \
   } while (0)
-    if (a.hd != head_dim) {  // a head dim run at the next D (16-bit, no fused append)
+    if (a.hd != head_dim && dtype == VAPI_KV_F32) {  // an f32 head dim run at the next D
+      if (head_dim == 128) VK_DECP(float, 128, false, true);
+      else VK_DECP(float, 64, false, true);
+    } else if (a.hd != head_dim) {  // a 16-bit head dim run at the next D (no fused append)
       if (head_dim == 256) {
         if (bf16) VK_DECP(bf16_t, 256, false, true);
         else VK_DECP(f16_t, 256, false, true);

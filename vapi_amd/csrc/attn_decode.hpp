@@ -192,7 +192,8 @@ __device__ __forceinline__ void load_q(uint4* qs, const AttnArgs& a, const Decod
     const uint32_t sg = a.q_sign ? 0x80000000u : 0u;
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
-      uint4 x = *(const uint4*)(qrow + 16 * c + 4 * g);
+      uint4 x = !kPad || 16 * c + 4 * g < hd ? *(const uint4*)(qrow + 16 * c + 4 * g)
+                                             : make_uint4(0u, 0u, 0u, 0u);
       x.x ^= sg, x.y ^= sg, x.z ^= sg, x.w ^= sg;
       qs[c * 64 + lane] = x;
     }
@@ -246,8 +247,9 @@ __device__ __forceinline__ void flush_piece(const AttnArgs& a, const DecodePos& 
   if (col >= G) return;  // lanes of padding columns hold no head
   if constexpr (sizeof(T) == 4) {
     if (whole) {
-      float* orow = (float*)a.out + ((uint64_t)p.q0 * a.num_heads + p.kh * G + col) * D;
-      store_row_f32<D>(orow, o, l_tot > 0.f ? 1.f / l_tot : 0.f, g);
+      const uint32_t hd = kPad ? a.hd : (uint32_t)D;
+      float* orow = (float*)a.out + ((uint64_t)p.q0 * a.num_heads + p.kh * G + col) * hd;
+      store_row_f32<D, kPad>(orow, o, l_tot > 0.f ? 1.f / l_tot : 0.f, g, hd);
     } else {
       store_row_f32<D>(a.ws_o + ((uint64_t)slot * G + col) * D, o, 1.f, g);
       if (g == 0) *(float2*)(a.ws_ml + ((uint64_t)slot * G + col) * 2) = make_float2(m_run, l_tot);
@@ -383,7 +385,7 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
   const float* vbf = (const float*)a.v;
   auto load_halves = [&](KTileF32<D>& kt, VTileF32<D>& vt, const DecodePos& p, int tt)
       __attribute__((always_inline)) {
-    load_half_f32<D>(kt.h[tt], vt.h[tt], table + (uint64_t)p.seq * a.max_blocks,
+    load_half_f32<D, true, kPad>(kt.h[tt], vt.h[tt], table + (uint64_t)p.seq * a.max_blocks,
                      kbf + (p.kh >> a.kv_shift) * a.head_e, vbf + (p.kh >> a.kv_shift) * a.head_e,
                      a, p.key0, tt, p.len_k - 1,
                      col, g);
