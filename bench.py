@@ -469,36 +469,46 @@ def bench_head_dim_64(steps, warmup):
 
 
 def bench_decode_other_head_dims(steps, warmup):
-    """Config 2's batch (32 q / 8 kv heads, bf16) at head_dim 80 and 96
-    (Phi-2's and Phi-3's): the decode stream at D = 128 with zeros past the
-    head dim, against the VALU kernel on the same rows (declared with
-    max_seqlen_q = 2, which keeps them off the decode stream)."""
+    """Configs 2 and 3 (32 q / 8 kv heads, bf16) at head_dim 80 and 96
+    (Phi-2's and Phi-3's): the decode stream and the prefill kernel at
+    D = 128 with zeros past the head dim. Bytes and FLOPs are counted at the
+    real head dim (what the padded columns cost shows as a lower rate)."""
     w = workload.config2_decode()
+    p = workload.config3_prefill()
     out = {}
     for d in (80, 96):
         cache = PagedKvCache(2, w.num_blocks, w.block_size, 8, d, torch.bfloat16, "HND")
         workload.fill_normal(cache._slab, workload.seed_for(2))
         q = torch.randn(w.batch, 32, d, device=DEV).to(torch.bfloat16)
         o = torch.empty_like(q)
-        res = {}
-        for name, max_q, n in (("stream", 1, steps), ("valu", 2, max(steps // 5, 3))):
-            batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
-                                 block_tables=[t.tolist() for t in w.tables], max_seqlen_q=max_q,
-                                 max_seqlen_k=int(w.lens.max()))
-            prep = PreparedAttention.from_batch(batch, DEV)
-            turn = [0]
+        batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
+                             block_tables=[t.tolist() for t in w.tables], max_seqlen_q=1,
+                             max_seqlen_k=int(w.lens.max()))
+        prep = PreparedAttention.from_batch(batch, DEV)
+        turn = [0]
 
-            def call():
-                paged_attention_prepared(q, cache, turn[0] % 2, prep, d ** -0.5, out=o)
-                turn[0] += 1
+        def call():
+            paged_attention_prepared(q, cache, turn[0] % 2, prep, d ** -0.5, out=o)
+            turn[0] += 1
 
-            res[name] = timed_graph(call, n, 3 if name == "valu" else warmup,
-                                    replays=3 if name == "valu" else 7) * 1e3
+        us = timed_graph(call, steps, warmup) * 1e3
         kv = int(w.lens.sum()) * 8 * d * 2 * 2
-        out[f"d{d}"] = dict(us=res["stream"], gbs=kv / (res["stream"] * 1e-6) / 1e9,
-                            valu_us=res["valu"], kv_bytes=kv)
-        log(f"decode cfg2 batch, head_dim {d}: {res['stream']:.1f} us "
-            f"({kv / (res['stream'] * 1e-6) / 1e9:.0f} GB/s), VALU kernel {res['valu']:.1f} us")
+        del cache, q, o
+        cache = PagedKvCache(1, p.num_blocks, p.block_size, 8, d, torch.bfloat16, "HND")
+        workload.fill_normal(cache._slab, workload.seed_for(3))
+        q = torch.randn(p.batch * p.len_q, 32, d, device=DEV).to(torch.bfloat16)
+        o = torch.empty_like(q)
+        batch = ForwardBatch(cu_seqlens_q=p.cu_q().tolist(), cu_seqlens_k=p.cu_k().tolist(),
+                             block_tables=[t.tolist() for t in p.tables], max_seqlen_q=p.len_q,
+                             max_seqlen_k=p.len_k)
+        prep = PreparedAttention.from_batch(batch, DEV)
+        ms, _ = timed(lambda: paged_attention_prepared(q, cache, 0, prep, d ** -0.5, out=o),
+                      max(steps, 10), 30)
+        flops = p.flops() * d / 128
+        out[f"d{d}"] = dict(us=us, gbs=kv / (us * 1e-6) / 1e9, kv_bytes=kv,
+                            prefill_ms=ms, prefill_tflops=flops / (ms * 1e-3) / 1e12)
+        log(f"head_dim {d}: decode cfg2 {us:.1f} us ({kv / (us * 1e-6) / 1e9:.0f} GB/s), "
+            f"prefill cfg3 {ms:.3f} ms ({flops / (ms * 1e-3) / 1e12:.0f} TFLOP/s at d{d})")
         del cache, q, o
     torch.cuda.empty_cache()
     return out
@@ -1342,7 +1352,7 @@ def main():
         extras["wide_group_g32"] = bench_wide_group(args.steps, args.warmup)
         extras["head_dim_256"] = bench_head_dim_256(args.steps, args.warmup)
         extras["decode_cfg2_block_major"] = bench_decode_block_major(args.steps, args.warmup)
-        extras["decode_other_head_dims"] = bench_decode_other_head_dims(args.steps, args.warmup)
+        extras["other_head_dims"] = bench_decode_other_head_dims(args.steps, args.warmup)
         extras["decode_small_batches"] = bench_small_batches(args.steps, args.warmup)
         extras["prefill_small_batches"] = bench_small_prefill(args.steps, args.warmup)
     extras["blocks_cfg4"] = bench_blocks(max(args.steps // 5, 3), 2, dec)

@@ -214,7 +214,8 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
  *   or ordered streams).
  * max_seqlen_q/k must bound every sequence's len_q/len_k (as in
  *   flash-attention); max_seqlen_q sizes the prefill grid. On the MFMA path
- *   (bf16/f16, head_dim 64, 128 or 256) the decode's part depends on the batch,
+ *   (bf16/f16, head_dim 64, 128 or 256, or any other multiple of 8 below 256,
+ *   run at the next of them with the extra elements read as zeros) the decode's part depends on the batch,
  *   the heads and the GPU's CU count, not on the lengths; a prefill batch
  *   with fewer query tiles than the GPU has CUs asks for more (up to 256
  *   MiB) to split its keys over more workgroups. That part is optional: a
@@ -224,8 +225,10 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
  *   64 or 128 runs the decode stream and an f32 prefill kernel, sized the
  *   same way (the f32 prefill's key split is the optional part; a
  *   pure-decode f32 call over at
- *   most 512 keys per sequence and 8,192 in all runs the VALU kernel). On the VALU path (those calls,
- *   other head dims, groups with no split into parts of at most 16 query
+ *   most 512 keys per sequence and 8,192 in all runs the VALU kernel); so does
+ *   a larger pure-decode f32 call at another multiple of 4 below 128, run
+ *   padded. On the VALU path (those small calls, f32 prefill at other
+ *   head dims, other head dims, groups with no split into parts of at most 16 query
  *   heads, block sizes below 16) it holds the split-context partials and
  *   grows with the batch, max_seqlen_q and max_seqlen_k (0 while
  *   max_seqlen_k <= 64; small batches split their keys into chunks of 64

@@ -379,3 +379,22 @@ def test_f32_decode_and_wide_groups_size_the_decode_workspace():
     # G = 17 has no split: the VALU kernel, which needs no decode workspace
     # for short contexts.
     assert L.vapi_paged_attention_workspace_size(one, 64, 17, 1, 64) == 0
+
+
+def test_padded_head_dims_size_the_workspace_of_the_next_kernel_dim():
+    """A 16-bit pool at a head_dim that is a multiple of 8 below 256 runs the
+    decode stream and the prefill kernel at the next of 64, 128 and 256:
+    decode-only and prefill calls ask for that dim's workspace (the
+    prefill's key-split partials hold its columns), and a head_dim that is
+    not a multiple of 8 stays on the VALU kernel."""
+    L = _lib.lib()
+    for hd, kd in ((80, 128), (96, 128), (48, 64), (160, 256), (248, 256)):
+        padded = pool(dtype=_lib.BF16, num_kv_heads=4, head_dim=hd)
+        full = pool(dtype=_lib.BF16, num_kv_heads=4, head_dim=kd)
+        for q, k in ((1, 4096), (100, 3000), (512, 4096)):
+            assert (L.vapi_paged_attention_workspace_size(padded, 2, 16, q, k) ==
+                    L.vapi_paged_attention_workspace_size(full, 2, 16, q, k)), (hd, q, k)
+    odd = pool(dtype=_lib.BF16, num_kv_heads=4, head_dim=84)
+    assert (L.vapi_paged_attention_workspace_size(odd, 2, 16, 100, 3000) !=
+            L.vapi_paged_attention_workspace_size(
+                pool(dtype=_lib.BF16, num_kv_heads=4, head_dim=128), 2, 16, 100, 3000))

@@ -223,6 +223,16 @@ CASES = [
     (torch.float32, 32, 8, 80, 16, [1, 1, 1, 1], [1, 600, 1500, 4000], None, "HND"),
     (torch.float32, 16, 4, 96, 32, [1, 1, 1], [65, 2100, 31], 40, "NHD"),
     (torch.float32, 8, 8, 40, 16, [1, 1], [900, 1290], None, "HND-bm"),
+    # ... and with prefill rows (16-bit pools): the prefill kernel at the
+    # next D, Q and K chunks past head_dim zero, output columns past it
+    # unstored; padded dims never take the one-launch mixed step.
+    (torch.bfloat16, 32, 8, 80, 16, [1, 37, 1, 64], [700, 37, 33, 300], None, "HND"),
+    (torch.float16, 16, 4, 96, 32, [20, 1, 5], [900, 65, 300], 50, "NHD"),
+    (torch.bfloat16, 8, 8, 48, 16, [1, 100], [900, 100], None, "HND-bm"),
+    (torch.bfloat16, 6, 2, 16, 16, [40, 1], [50, 700], 6, "HND"),
+    (torch.bfloat16, 16, 2, 160, 16, [64, 1], [1000, 300], None, "HND"),
+    (torch.float16, 64, 2, 200, 32, [33, 1, 5], [700, 1200, 5], 100, "NHD"),
+    (torch.bfloat16, 12, 4, 248, 16, [130, 0], [400, 9], None, "HND-bm"),
     # A 16-bit pool the MFMA paths do not take, on the generic kernel:
     # block_size 8.
     (torch.bfloat16, 16, 8, 128, 8, [1, 12], [210, 50], None, "HND"),
@@ -232,9 +242,10 @@ CASES = [
     (torch.float32, 4, 2, 3, 4, [1, 5], [1100, 600], 100, "NHD"),
     (torch.float32, 8, 8, 128, 16, [1, 37], [2100, 1100], 700, "HND"),
     (torch.float32, 16, 4, 256, 16, [1, 9], [2000, 800], None, "HND"),
-    # More head dims the VALU kernel compiles as constants (96, 32), and a
-    # block size that is not a power of two.
-    (torch.bfloat16, 16, 4, 96, 16, [1, 7], [900, 130], None, "HND"),
+    # More head dims the VALU kernel compiles as constants (96, 32; block
+    # sizes below 16 keep a 16-bit pool there), and a block size that is
+    # not a power of two.
+    (torch.bfloat16, 16, 4, 96, 8, [1, 7], [900, 130], None, "HND"),
     (torch.float16, 8, 2, 32, 12, [1, 3, 1], [260, 45, 1300], 40, "NHD"),
 ]
 
@@ -265,7 +276,7 @@ def drawn_case(seed):
     if dtype == torch.float32:
         d = int(rng.choice([64, 128, 128, 80]))
     else:
-        d = int(rng.choice([64, 128, 128, 256]))
+        d = int(rng.choice([64, 128, 128, 256, 80, 96]))
     bs = int(rng.choice([16, 32, 64]))
     layout = "HND" if rng.random() < 0.7 else "NHD"
     window = None if rng.random() < 0.6 else int(rng.integers(1, 600))
@@ -627,6 +638,10 @@ SPLIT_CASES = [
     (torch.bfloat16, 16, 4, 128, 16, [320], [4000], None, "HND"),
     (torch.bfloat16, 16, 4, 256, 16, [100, 1], [3000, 2000], None, "HND"),
     (torch.float16, 8, 8, 256, 32, [48], [2500], 900, "NHD"),
+    # Padded head dims: the split's partials hold D columns, the merge
+    # stores head_dim of them.
+    (torch.bfloat16, 16, 4, 80, 16, [100, 1], [3000, 2000], None, "HND"),
+    (torch.float16, 8, 8, 192, 32, [48], [2500], 900, "NHD"),
     # f32 pools: paged_prefill_f32's split (waves, not workgroups) and its merge.
     (torch.float32, 32, 8, 128, 16, [128], [8192], None, "HND"),
     (torch.float32, 16, 4, 64, 32, [100, 1], [3000, 2000], 500, "NHD"),

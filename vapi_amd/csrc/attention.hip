@@ -60,24 +60,35 @@ static bool mfma_ok(const vapi_kv_pool* p, uint32_t num_heads) {
 // else the next of them (elements past head_dim are zeros).
 static uint32_t decode_dim(uint32_t hd) { return hd <= 64 ? 64 : hd <= 128 ? 128 : 256; }
 
-// A pure-decode call whose head_dim is not one of the kernels' (a multiple
-// of 8 below 256 in a 16-bit pool: Phi-2's 80, Phi-3's 96, ...; a multiple
-// of 4 below 128 in an f32 pool, except the small calls the VALU kernel
-// takes, see f32_mfma_ok) runs the decode stream at decode_dim; calls with
-// prefill rows, and other head dims, stay on the VALU kernel.
+// A 16-bit pool whose head_dim is not one of the kernels' but a multiple of 8
+// below 256 (Phi-2's 80, Phi-3's 96, ...): its calls run the decode stream
+// and the prefill kernel at decode_dim, elements past head_dim read as zeros
+// and never stored (no fused append, no one-launch mixed step).
+static bool pad16_ok(const vapi_kv_pool* p, uint32_t num_heads) {
+  if (p->dtype != VAPI_KV_BF16 && p->dtype != VAPI_KV_F16) return false;
+  const uint32_t hd = p->head_dim;
+  if (hd == 0 || hd % 8 || hd > 256 || hd == 64 || hd == 128 || hd == 256) return false;
+  if (p->block_size < 16 || (p->block_size & (p->block_size - 1))) return false;
+  if (num_heads == 0 || num_heads % p->num_kv_heads) return false;
+  return decode_group_shift(num_heads / p->num_kv_heads) >= 0;
+}
+
+// A 16-bit pool on the MFMA kernels, at its own head_dim or padded.
+static bool mfma16_ok(const vapi_kv_pool* p, uint32_t num_heads) {
+  return mfma_ok(p, num_heads) || pad16_ok(p, num_heads);
+}
+
+// A pure-decode call in an f32 pool whose head_dim is a multiple of 4 below
+// 128 but not 64 (except the small calls the VALU kernel takes, see
+// f32_mfma_ok) runs the decode stream at decode_dim; calls with prefill
+// rows, and other head dims, stay on the VALU kernel.
 static bool pad_decode_ok(const vapi_kv_pool* p, uint32_t num_heads, uint32_t max_seqlen_q,
                           uint32_t max_seqlen_k, uint32_t batch) {
-  if (max_seqlen_q > 1) return false;
+  if (max_seqlen_q > 1 || p->dtype != VAPI_KV_F32) return false;
   const uint32_t hd = p->head_dim;
-  if (p->dtype == VAPI_KV_F32) {
-    if (hd == 0 || hd % 4 || hd > 128 || hd == 64 || hd == 128) return false;
-    if (max_seqlen_k <= kSmallKeys && (uint64_t)batch * max_seqlen_k <= kSmallBatchKeys)
-      return false;
-  } else if (p->dtype == VAPI_KV_BF16 || p->dtype == VAPI_KV_F16) {
-    if (hd == 0 || hd % 8 || hd > 256 || hd == 64 || hd == 128 || hd == 256) return false;
-  } else {
+  if (hd == 0 || hd % 4 || hd > 128 || hd == 64 || hd == 128) return false;
+  if (max_seqlen_k <= kSmallKeys && (uint64_t)batch * max_seqlen_k <= kSmallBatchKeys)
     return false;
-  }
   if (p->block_size < 16 || (p->block_size & (p->block_size - 1))) return false;
   if (num_heads == 0 || num_heads % p->num_kv_heads) return false;
   return decode_group_shift(num_heads / p->num_kv_heads) >= 0;
@@ -186,7 +197,7 @@ static size_t required_workspace(const vapi_kv_pool* pool, uint32_t batch, uint3
       num_heads == 0)
     return 0;
   const uint32_t group = num_heads / pool->num_kv_heads;
-  if (!mfma_ok(pool, num_heads) &&
+  if (!mfma16_ok(pool, num_heads) &&
       !f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch) &&
       !pad_decode_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch))
     return generic_workspace_bytes(batch, pool->num_kv_heads, group, pool->head_dim,
@@ -202,8 +213,8 @@ static size_t split_bytes(const vapi_kv_pool* pool, uint32_t batch, uint32_t num
       num_heads == 0)
     return 0;
   const uint32_t kvh = pool->num_kv_heads, group = num_heads / kvh;
-  if (mfma_ok(pool, num_heads))
-    return prefill_split_bytes(n_prefill, kvh, group, pool->head_dim, max_seqlen_q,
+  if (mfma16_ok(pool, num_heads))
+    return prefill_split_bytes(n_prefill, kvh, group, decode_dim(pool->head_dim), max_seqlen_q,
                                max_seqlen_k);
   if (f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch))
     return prefill_f32_split_bytes(n_prefill, kvh, group, pool->head_dim, max_seqlen_q,
@@ -389,7 +400,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   if (flags & ~(uint32_t)(VAPI_ATTN_DETERMINISTIC | VAPI_ATTN_NO_DECODE_ROWS))
     VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: unknown flags 0x%x", flags);
   if (num_heads > 65535 ||
-      (batch > 65535 && !mfma_ok(pool, num_heads) &&
+      (batch > 65535 && !mfma16_ok(pool, num_heads) &&
        !f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch) &&
        !pad_decode_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch)))
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: batch %u / heads %u too large",
@@ -399,7 +410,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   // len_q == 1 included, so the result does not depend on the hint. It needs
   // no workspace.
   const bool skip_decode = (flags & VAPI_ATTN_NO_DECODE_ROWS) && !fuse && max_seqlen_q > 1 &&
-                           (mfma_ok(pool, num_heads) ||
+                           (mfma16_ok(pool, num_heads) ||
                             f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch));
   // The sequences the prefill grid covers: those the host named (a mixed
   // step's few prefill chunks among many decode rows), else all of them. A
@@ -407,11 +418,11 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   const bool listed = pf && !skip_decode;
   const uint32_t pf_n = listed ? pf->n : batch;
   // Refused before anything is launched (a refused call writes nothing).
-  if (mfma_ok(pool, num_heads) && max_seqlen_q > 1 && pf_n > 65535)
+  if (mfma16_ok(pool, num_heads) && max_seqlen_q > 1 && pf_n > 65535)
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: %u prefill sequences > 65535", pf_n);
-  if (mfma_ok(pool, num_heads) && max_seqlen_q > 1 &&
+  if (mfma16_ok(pool, num_heads) && max_seqlen_q > 1 &&
       prefill_grid(pf_n, pool->num_kv_heads, num_heads / pool->num_kv_heads, max_seqlen_q,
-                   pool->head_dim) >
+                   decode_dim(pool->head_dim)) >
           0xFFFFFFFFull)
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: prefill batch too large for one launch");
   if (f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch) && max_seqlen_q > 1 &&
@@ -479,16 +490,19 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
     dec.kv_shift = (uint32_t)gsh;
   }
 
-  if (mfma_ok(pool, num_heads)) {
+  if (mfma16_ok(pool, num_heads)) {
     const bool bf16 = pool->dtype == VAPI_KV_BF16;
+    const uint32_t D = decode_dim(g.d);
     a.num_waves = decode_num_waves();
     const size_t off = std::max<size_t>((need + 255) & ~(size_t)255, 256);
     const bool room = workspace && workspace_bytes > off;
     // Decode rows and prefill rows in one step: both kernels in one launch.
     // (At most 4,000 sequences: the launch's dynamic LDS, 4 bytes per
     // sequence, then still lets a decode and a prefill workgroup share a CU.
-    // At head_dim 256 neither kernel fits half a CU's registers.)
-    const bool mixed = !skip_decode && !fuse && gsh == 0 && g.d != 256 && max_seqlen_q > 1 &&
+    // At head_dim 256 neither kernel fits half a CU's registers; padded head
+    // dims run the two launches.)
+    const bool mixed = !skip_decode && !fuse && gsh == 0 && (g.d == 64 || g.d == 128) &&
+                       max_seqlen_q > 1 &&
                        pf_n > 0 &&
                        batch <= std::min(decode_max_plan_seqs(), 4000u) &&
                        mixed_prefill_items(pf_n, g.kvh, num_heads / g.kvh, max_seqlen_q) <
@@ -503,13 +517,13 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
       a.pf_min_q = 1;
     } else {
       dec.num_waves = a.num_waves;
-      launch_decode(dec, workspace, g.d, pool->dtype, s);
+      launch_decode(dec, workspace, D, pool->dtype, s);
     }
     if (max_seqlen_q > 1 && pf_n > 0) {
       // The workspace past the decode's part serves the prefill's key split
       // (never its first 256 bytes, which carry the decode's XCD shares
       // from call to call).
-      launch_prefill(a, max_seqlen_q, max_seqlen_k, g.d, bf16,
+      launch_prefill(a, max_seqlen_q, max_seqlen_k, D, bf16,
                      room ? (char*)workspace + off : nullptr, room ? workspace_bytes - off : 0, s);
     }
   } else if (pad_decode_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch)) {

@@ -72,7 +72,11 @@ __device__ __forceinline__ uint32_t pf_chunk(uint32_t r, uint32_t p) {
 // V (D = 128, 256), or with 8 waves one of K or V (D = 64: waves 0-3 K,
 // waves 4-7 V), with 4 waves one of each. LDS slot t of a tensor holds the chunk its swizzled
 // position names; a wave's 64 slots are contiguous, as the load writes them.
-template <typename T, int D, int W>
+// kPad (a head_dim a.hd below D, a multiple of 8): a chunk at or past a.hd
+// lies outside the key's row, so its slot is filled from the row's chunk 0
+// instead (the K fragment reads zero those chunks; the V columns past a.hd
+// only reach output columns that are never stored).
+template <typename T, int D, int W, bool kPad = false>
 __device__ __forceinline__ void pf_dma(uint16_t* kdst, uint16_t* vdst, const uint32_t* __restrict__ tab,
                                        const T* kb, const T* vb, const AttnArgs& a, int32_t s0,
                                        int32_t last, uint32_t tid, uint32_t wave) {
@@ -88,7 +92,8 @@ __device__ __forceinline__ void pf_dma(uint16_t* kdst, uint16_t* vdst, const uin
   auto one = [&](const T* base_t, uint16_t* buf, uint32_t slot, uint32_t wslot0)
                  __attribute__((always_inline)) {
     const uint32_t r = slot / CPR, pos = slot % CPR;
-    const uint32_t p = pos ^ pf_swz<D>(r);
+    uint32_t p = pos ^ pf_swz<D>(r);
+    if (kPad && 8 * p >= a.hd) p = 0;
     // A wave's slots cover 64 / CPR whole rows of one 16-key tile.
     const bool second = __builtin_amdgcn_readfirstlane(r) >= 16;
     const T* base = base_t + (second ? off1 : off0);
@@ -165,7 +170,7 @@ __device__ __forceinline__ void lgkm_wait(uint2 (&r)[4]) {
 // the GPU with query tiles alone); each writes its rows' (m, l, o) to
 // `part` and paged_prefill_merge combines them.
 // Workgroup `bid` of `n_items` (W waves) of a prefill launch.
-template <typename T, int D, int RT, int W, bool kSplit>
+template <typename T, int D, int RT, int W, bool kSplit, bool kPad = false>
 __device__ __forceinline__ void prefill_body(
     const AttnArgs& a, const uint32_t* __restrict__ cu_q, const uint32_t* __restrict__ cu_k,
     const uint32_t* __restrict__ table, uint32_t qtiles, uint32_t n_split_arg,
@@ -234,11 +239,15 @@ __device__ __forceinline__ void prefill_body(
     int32_t hi;
     key_range(offset + (int32_t)j, len_k, a.wl, a.wr, lo[t], hi);
     cnt[t] = max(hi - lo[t] + 1, 0);
-    const T* qrow = (const T*)a.q + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * D;
+    const T* qrow =
+        (const T*)a.q + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * (kPad ? a.hd : D);
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
-      uint4 x = *(const uint4*)(qrow + 32 * c + 8 * g);
-      x.x ^= a.q_sign, x.y ^= a.q_sign, x.z ^= a.q_sign, x.w ^= a.q_sign;
+      uint4 x = make_uint4(0, 0, 0, 0);
+      if (!kPad || 32 * c + 8 * g < a.hd) {
+        x = *(const uint4*)(qrow + 32 * c + 8 * g);
+        x.x ^= a.q_sign, x.y ^= a.q_sign, x.z ^= a.q_sign, x.w ^= a.q_sign;
+      }
       qf[t][c] = x;
     }
   }
@@ -278,8 +287,8 @@ __device__ __forceinline__ void prefill_body(
   int32_t s0_ = klo & ~31;
   const int32_t s_last = khi & ~31;
   if (!kSplit || s0_ <= khi) {  // (uniform) an empty key split issues no loads
-    pf_dma<T, D, W>(k0, v0, tab, kb, vb, a, s0_, last, tid, wave);
-    pf_dma<T, D, W>(k1, v1, tab, kb, vb, a, min(s0_ + 32, s_last), last, tid, wave);
+    pf_dma<T, D, W, kPad>(k0, v0, tab, kb, vb, a, s0_, last, tid, wave);
+    pf_dma<T, D, W, kPad>(k1, v1, tab, kb, vb, a, min(s0_ + 32, s_last), last, tid, wave);
     wait_vmcnt<kLoadsPerStep>();
     ring_barrier();
   }
@@ -291,7 +300,7 @@ __device__ __forceinline__ void prefill_body(
     uint16_t* const knext = B == 0 ? k2 : B == 1 ? k0 : k1;
     uint16_t* const vnext = B == 0 ? v2 : B == 1 ? v0 : v1;
     const int32_t s0 = __builtin_amdgcn_readfirstlane(s0_);
-    pf_dma<T, D, W>(knext, vnext, tab, kb, vb, a, min(s0 + 64, s_last), last, tid, wave);
+    pf_dma<T, D, W, kPad>(knext, vnext, tab, kb, vb, a, min(s0 + 64, s_last), last, tid, wave);
     // Steps inside [full_lo, full_hi] need no mask (a uniform branch).
     const bool masked = !(s0 >= full_lo && s0 + 31 <= full_hi);
     // V^T fragments in batches of two d tiles (four transposing reads): batch
@@ -315,7 +324,10 @@ __device__ __forceinline__ void prefill_body(
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int c = 0; c < KC; ++c) kt.k[tt][c] = *(const uint4*)(kbuf + k_off[tt][c]);
+        for (int c = 0; c < KC; ++c) {
+          kt.k[tt][c] = *(const uint4*)(kbuf + k_off[tt][c]);
+          if (kPad && D < 256 && 32 * c + 8 * g >= a.hd) kt.k[tt][c] = make_uint4(0, 0, 0, 0);
+        }
 #pragma unroll
       for (int t = 0; t < kPfRT; ++t) qk_scores<T, D>(kt, qf[t], acc[t]);
 #pragma unroll
@@ -416,27 +428,30 @@ __device__ __forceinline__ void prefill_body(
     const uint32_t r = row0 + 16 * t + col;
     if (r >= nrows) continue;
     const uint32_t j = r / G, hl = r % G;
-    T* orow = (T*)a.out + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * D;
+    T* orow = (T*)a.out + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * (kPad ? a.hd : D);
     const float sc = lt > 0.f ? 1.f / lt : 0.f;
 #pragma unroll
     for (int k = 0; k < DT; ++k)
-      *(uint2*)(orow + 16 * k + 4 * g) =
+      if (!kPad || 16 * k + 4 * g < a.hd)
+        *(uint2*)(orow + 16 * k + 4 * g) =
           make_uint2(pack2<T>(o[t][k][0] * sc, o[t][k][1] * sc),
                      pack2<T>(o[t][k][2] * sc, o[t][k][3] * sc));
   }
 }
 
-template <typename T, int D, int RT, int OCC, bool kSplit>
+template <typename T, int D, int RT, int OCC, bool kSplit, bool kPad>
 __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
     AttnArgs a, const uint32_t* __restrict__ cu_q, const uint32_t* __restrict__ cu_k,
     const uint32_t* __restrict__ table, uint32_t qtiles, uint32_t n_split_arg,
     float* __restrict__ part) {
-  prefill_body<T, D, RT, kPfWaves, kSplit>(a, cu_q, cu_k, table, qtiles, n_split_arg, part,
+  prefill_body<T, D, RT, kPfWaves, kSplit, kPad>(a, cu_q, cu_k, table, qtiles, n_split_arg, part,
                                            blockIdx.x, gridDim.x);
 }
 
 // Combines the key splits' partials of a prefill launch: thread (row, four
-// consecutive d) over the splits, in split order.
+// consecutive d) over the splits, in split order. Output rows are a.hd
+// elements apart; with a head_dim below D the columns past it are not
+// stored.
 template <typename T, int D>
 __device__ __forceinline__ void prefill_merge_body(const AttnArgs& a, uint32_t qtiles,
                                                    uint32_t rows_per_item, uint32_t n_split,
@@ -456,7 +471,7 @@ __device__ __forceinline__ void prefill_merge_body(const AttnArgs& a, uint32_t q
   if (len_q < a.pf_min_q || len_q == 0) return;
   const uint32_t G = a.group;
   const uint32_t row = qt * rows_per_item + row_in;
-  if (row >= len_q * G) return;
+  if (row >= len_q * G || dq >= a.hd) return;
   const uint64_t stride = pf_part_bytes(rows_per_item, D);  // per split
   const char* p0 = (const char*)part + (uint64_t)base * n_split * stride;
   const uint64_t ml_off = (uint64_t)row_in * 8;
@@ -497,7 +512,7 @@ __device__ __forceinline__ void prefill_merge_body(const AttnArgs& a, uint32_t q
     M = Mn;
   }
   const uint32_t j = row / G, hl = row % G;
-  T* orow = (T*)a.out + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * D + dq;
+  T* orow = (T*)a.out + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * a.hd + dq;
   const float inv = L > 0.f ? 1.f / L : 0.f;
   if constexpr (sizeof(T) == 4)
     *(float4*)orow = make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
@@ -705,30 +720,39 @@ void launch_prefill(const AttnArgs& a_in, uint32_t max_q, uint32_t max_k, uint32
                                : 1;
   float* part = n_split > 1 ? (float*)split_ws : nullptr;
   const dim3 grid((uint32_t)(base * n_split)), block(kPfThreads);
-#define VK_PF(T, DD)                                                                             \
+#define VK_PF(T, DD, PAD)                                                                        \
   do {                                                                                           \
-    constexpr int occ = DD == 64 ? kPfOcc64 : kPfOcc;                                      \
+    constexpr int occ = DD == 64 ? kPfOcc64 : kPfOcc;                                            \
     constexpr int rt = DD == 256 ? kPfRowTiles256 : kPfRowTiles;                                 \
     if (n_split > 1) {                                                                           \
-      hipLaunchKernelGGL((paged_prefill_tiled<T, DD, rt, occ, true>), grid, block, 0, s, a, \
+      hipLaunchKernelGGL((paged_prefill_tiled<T, DD, rt, occ, true, PAD>), grid, block, 0, s, a, \
                          a.cu_q, a.cu_k, a.table, qtiles, n_split, part);                        \
       hipLaunchKernelGGL((paged_prefill_merge<T, DD>),                                           \
                          dim3((uint32_t)(base * (rows / (256 / (DD / 4))))), dim3(256), 0, s, a, \
                          qtiles, rows, n_split, part);                                           \
     } else {                                                                                     \
-      hipLaunchKernelGGL((paged_prefill_tiled<T, DD, rt, occ, false>), grid, block, 0, s,  \
+      hipLaunchKernelGGL((paged_prefill_tiled<T, DD, rt, occ, false, PAD>), grid, block, 0, s,   \
                          a, a.cu_q, a.cu_k, a.table, qtiles, 1u, nullptr);                       \
     }                                                                                            \
   } while (0)
+  // A head_dim below the kernel's D (a multiple of 8) runs the padded
+  // variant: Q and K chunks past it read as zeros, output columns past it
+  // are not stored.
+#define VK_PF_D(T, DD)              \
+  do {                              \
+    if (a.hd != DD) VK_PF(T, DD, true); \
+    else VK_PF(T, DD, false);       \
+  } while (0)
   if (bf16) {
-    if (head_dim == 256) VK_PF(bf16_t, 256);
-    else if (head_dim == 128) VK_PF(bf16_t, 128);
-    else VK_PF(bf16_t, 64);
+    if (head_dim == 256) VK_PF_D(bf16_t, 256);
+    else if (head_dim == 128) VK_PF_D(bf16_t, 128);
+    else VK_PF_D(bf16_t, 64);
   } else {
-    if (head_dim == 256) VK_PF(f16_t, 256);
-    else if (head_dim == 128) VK_PF(f16_t, 128);
-    else VK_PF(f16_t, 64);
+    if (head_dim == 256) VK_PF_D(f16_t, 256);
+    else if (head_dim == 128) VK_PF_D(f16_t, 128);
+    else VK_PF_D(f16_t, 64);
   }
+#undef VK_PF_D
 #undef VK_PF
 }
 
