@@ -311,7 +311,7 @@ def bench_valu(steps, warmup):
     parity case: at most 512 keys, so the VALU kernel in one launch), config
     2's batch over an f32 pool (1.5 GB of K/V, the f32-MFMA decode stream),
     the same batch at head_dim 80 (the stream padded to 128), and config 3
-    on an f32 pool (the f32-MFMA prefill)."""
+    on an f32 pool (the f32-MFMA prefill) at head_dim 128 and 80."""
     out = {}
     for name, w, heads, kvh, d in (("cfg0_f32", workload.config0_decode_small(), 16, 8, None),
                                    ("cfg2_shape_f32", workload.config2_decode(), 32, 8, None),
@@ -337,21 +337,23 @@ def bench_valu(steps, warmup):
         log(f"f32 attention {name}: {ms * 1e3:.1f} us ({gms * 1e3:.1f} us in a graph), "
             f"{kv / 1e6:.1f} MB of K/V, {out[name]['gbs']:.0f} GB/s, {out[name]['path']}")
         del cache
-    # Config 3 (32 x 512-token chunks over 4,096 keys) on an f32 pool.
+    # Config 3 (32 x 512-token chunks over 4,096 keys) on an f32 pool, at
+    # head_dim 128 and 80 (the prefill padded to 128; FLOPs at 80).
     p = workload.config3_prefill()
-    cache = PagedKvCache(1, p.num_blocks, p.block_size, 8, 128, torch.float32, "HND")
-    workload.fill_normal(cache._slab, workload.seed_for(3))
-    q = torch.randn(p.batch * p.len_q, 32, 128, device=DEV)
-    batch = ForwardBatch(cu_seqlens_q=p.cu_q().tolist(), cu_seqlens_k=p.cu_k().tolist(),
-                         block_tables=[t.tolist() for t in p.tables], max_seqlen_q=p.len_q,
-                         max_seqlen_k=p.len_k)
-    prep = PreparedAttention.from_batch(batch, DEV)
-    o = torch.empty_like(q)
-    ms, _ = timed(lambda: paged_attention_prepared(q, cache, 0, prep, 128 ** -0.5, out=o), 3, 2)
-    flops = p.flops()
-    out["cfg3_f32"] = dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12)
-    log(f"f32 attention cfg3_f32: {ms:.2f} ms, {out['cfg3_f32']['tflops']:.1f} TFLOP/s")
-    del cache, q, o
+    for name, d in (("cfg3_f32", 128), ("cfg3_f32_d80", 80)):
+        cache = PagedKvCache(1, p.num_blocks, p.block_size, 8, d, torch.float32, "HND")
+        workload.fill_normal(cache._slab, workload.seed_for(3))
+        q = torch.randn(p.batch * p.len_q, 32, d, device=DEV)
+        batch = ForwardBatch(cu_seqlens_q=p.cu_q().tolist(), cu_seqlens_k=p.cu_k().tolist(),
+                             block_tables=[t.tolist() for t in p.tables], max_seqlen_q=p.len_q,
+                             max_seqlen_k=p.len_k)
+        prep = PreparedAttention.from_batch(batch, DEV)
+        o = torch.empty_like(q)
+        ms, _ = timed(lambda: paged_attention_prepared(q, cache, 0, prep, d ** -0.5, out=o), 3, 2)
+        flops = p.flops() * d / 128
+        out[name] = dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12)
+        log(f"f32 attention {name}: {ms:.2f} ms, {out[name]['tflops']:.1f} TFLOP/s")
+        del cache, q, o
     return out
 
 

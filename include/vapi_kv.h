@@ -222,13 +222,12 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
  *   workspace holding only the decode's part (or none, for a call with
  *   VAPI_ATTN_NO_DECODE_ROWS) runs the prefill unsplit, and a
  *   VAPI_ATTN_DETERMINISTIC call never splits. An f32 pool with head_dim
- *   64 or 128 runs the decode stream and an f32 prefill kernel, sized the
+ *   64 or 128, or another multiple of 4 below 128 run at the next of them,
+ *   runs the decode stream and an f32 prefill kernel, sized the
  *   same way (the f32 prefill's key split is the optional part; a
  *   pure-decode f32 call over at
- *   most 512 keys per sequence and 8,192 in all runs the VALU kernel); so does
- *   a larger pure-decode f32 call at another multiple of 4 below 128, run
- *   padded. On the VALU path (those small calls, f32 prefill at other
- *   head dims, other head dims, groups with no split into parts of at most 16 query
+ *   most 512 keys per sequence and 8,192 in all runs the VALU kernel). On
+ *   the VALU path (those small calls, other head dims, groups with no split into parts of at most 16 query
  *   heads, block sizes below 16) it holds the split-context partials and
  *   grows with the batch, max_seqlen_q and max_seqlen_k (0 while
  *   max_seqlen_k <= 64; small batches split their keys into chunks of 64

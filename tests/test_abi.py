@@ -160,9 +160,9 @@ def test_launches_too_large_for_one_grid_are_refused():
     assert L.vapi_paged_attention_ex(pool(), 0, *args, _lib.ATTN_NO_DECODE_ROWS, None, 0,
                                      None) == _lib.EUNSUP
     assert b"too large" in L.vapi_kv_last_error()
-    # VALU path (head_dim 80): row tiles x kv heads x sequences x key chunks.
+    # VALU path (head_dim 82): row tiles x kv heads x sequences x key chunks.
     args = [16, 16, 16, 16, 16, 60000, 1, 1 << 20, 1 << 20, 8, 0.1, -1, 0]
-    assert L.vapi_paged_attention_ex(pool(dtype=_lib.F32, head_dim=80), 0, *args, 0, 1,
+    assert L.vapi_paged_attention_ex(pool(dtype=_lib.F32, head_dim=82), 0, *args, 0, 1,
                                      1 << 62, None) == _lib.EUNSUP
     assert b"too large" in L.vapi_kv_last_error()
     # f32 MFMA prefill: 32-row tiles x kv heads x sequences waves.

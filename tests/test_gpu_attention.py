@@ -233,12 +233,17 @@ CASES = [
     (torch.bfloat16, 16, 2, 160, 16, [64, 1], [1000, 300], None, "HND"),
     (torch.float16, 64, 2, 200, 32, [33, 1, 5], [700, 1200, 5], 100, "NHD"),
     (torch.bfloat16, 12, 4, 248, 16, [130, 0], [400, 9], None, "HND-bm"),
+    # f32 pools: paged_prefill_f32 at the next of 64 and 128 (multiples of 4).
+    (torch.float32, 16, 4, 96, 16, [20, 1, 5], [900, 65, 300], 50, "NHD"),
+    (torch.float32, 8, 8, 40, 16, [33, 1], [700, 1200], None, "HND-bm"),
+    (torch.float32, 32, 1, 120, 32, [9, 1], [300, 40], None, "HND"),
+    (torch.float32, 6, 2, 4, 16, [12, 1], [40, 300], None, "HND"),
     # A 16-bit pool the MFMA paths do not take, on the generic kernel:
     # block_size 8.
     (torch.bfloat16, 16, 8, 128, 8, [1, 12], [210, 50], None, "HND"),
     # The VALU kernel's split contexts (more than 512 visible keys: chunks
     # combined by its merge), odd head dims on its scalar dot path.
-    (torch.float32, 12, 4, 80, 16, [1, 20, 1], [3000, 1500, 700], None, "HND"),
+    (torch.float32, 12, 4, 80, 8, [1, 20, 1], [3000, 1500, 700], None, "HND"),
     (torch.float32, 4, 2, 3, 4, [1, 5], [1100, 600], 100, "NHD"),
     (torch.float32, 8, 8, 128, 16, [1, 37], [2100, 1100], 700, "HND"),
     (torch.float32, 16, 4, 256, 16, [1, 9], [2000, 800], None, "HND"),
@@ -646,6 +651,7 @@ SPLIT_CASES = [
     (torch.float32, 32, 8, 128, 16, [128], [8192], None, "HND"),
     (torch.float32, 16, 4, 64, 32, [100, 1], [3000, 2000], 500, "NHD"),
     (torch.float32, 32, 8, 128, 16, [512], [4096], None, "HND-bm"),
+    (torch.float32, 16, 4, 80, 16, [100, 1], [3000, 2000], None, "HND"),
 ]
 
 

@@ -42,7 +42,9 @@ static bool f32_mfma_ok(const vapi_kv_pool* p, uint32_t num_heads, uint32_t max_
   if (p->dtype != VAPI_KV_F32) return false;
   if (max_q <= 1 && max_k <= kSmallKeys && (uint64_t)batch * max_k <= kSmallBatchKeys)
     return false;
-  if (p->head_dim != 64 && p->head_dim != 128) return false;
+  // head_dim 64 or 128, or a multiple of 4 below 128 run at the next of
+  // them (elements past head_dim read as zeros and never stored).
+  if (p->head_dim == 0 || p->head_dim % 4 || p->head_dim > 128) return false;
   if (p->block_size < 16 || (p->block_size & (p->block_size - 1))) return false;
   if (num_heads == 0 || num_heads % p->num_kv_heads) return false;
   return decode_group_shift(num_heads / p->num_kv_heads) >= 0;
@@ -76,22 +78,6 @@ static bool pad16_ok(const vapi_kv_pool* p, uint32_t num_heads) {
 // A 16-bit pool on the MFMA kernels, at its own head_dim or padded.
 static bool mfma16_ok(const vapi_kv_pool* p, uint32_t num_heads) {
   return mfma_ok(p, num_heads) || pad16_ok(p, num_heads);
-}
-
-// A pure-decode call in an f32 pool whose head_dim is a multiple of 4 below
-// 128 but not 64 (except the small calls the VALU kernel takes, see
-// f32_mfma_ok) runs the decode stream at decode_dim; calls with prefill
-// rows, and other head dims, stay on the VALU kernel.
-static bool pad_decode_ok(const vapi_kv_pool* p, uint32_t num_heads, uint32_t max_seqlen_q,
-                          uint32_t max_seqlen_k, uint32_t batch) {
-  if (max_seqlen_q > 1 || p->dtype != VAPI_KV_F32) return false;
-  const uint32_t hd = p->head_dim;
-  if (hd == 0 || hd % 4 || hd > 128 || hd == 64 || hd == 128) return false;
-  if (max_seqlen_k <= kSmallKeys && (uint64_t)batch * max_seqlen_k <= kSmallBatchKeys)
-    return false;
-  if (p->block_size < 16 || (p->block_size & (p->block_size - 1))) return false;
-  if (num_heads == 0 || num_heads % p->num_kv_heads) return false;
-  return decode_group_shift(num_heads / p->num_kv_heads) >= 0;
 }
 
 // The decode's view of the kv heads (virtual ones when G > 16).
@@ -198,8 +184,7 @@ static size_t required_workspace(const vapi_kv_pool* pool, uint32_t batch, uint3
     return 0;
   const uint32_t group = num_heads / pool->num_kv_heads;
   if (!mfma16_ok(pool, num_heads) &&
-      !f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch) &&
-      !pad_decode_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch))
+      !f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch))
     return generic_workspace_bytes(batch, pool->num_kv_heads, group, pool->head_dim,
                                    std::max(max_seqlen_q, 1u), max_seqlen_k);
   return skip_decode ? 0 : decode_ws_for(pool, batch, num_heads);
@@ -217,7 +202,7 @@ static size_t split_bytes(const vapi_kv_pool* pool, uint32_t batch, uint32_t num
     return prefill_split_bytes(n_prefill, kvh, group, decode_dim(pool->head_dim), max_seqlen_q,
                                max_seqlen_k);
   if (f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch))
-    return prefill_f32_split_bytes(n_prefill, kvh, group, pool->head_dim, max_seqlen_q,
+    return prefill_f32_split_bytes(n_prefill, kvh, group, decode_dim(pool->head_dim), max_seqlen_q,
                                    max_seqlen_k);
   return 0;
 }
@@ -401,8 +386,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
     VK_FAIL(VAPI_KV_EINVAL, "vapi_paged_attention: unknown flags 0x%x", flags);
   if (num_heads > 65535 ||
       (batch > 65535 && !mfma16_ok(pool, num_heads) &&
-       !f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch) &&
-       !pad_decode_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch)))
+       !f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch)))
     VK_FAIL(VAPI_KV_EUNSUP, "vapi_paged_attention: batch %u / heads %u too large",
             batch, num_heads);
   // A batch the caller says has no decode rows (and which is not a fused
@@ -526,22 +510,19 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
       launch_prefill(a, max_seqlen_q, max_seqlen_k, D, bf16,
                      room ? (char*)workspace + off : nullptr, room ? workspace_bytes - off : 0, s);
     }
-  } else if (pad_decode_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch)) {
-    dec.num_waves = decode_num_waves();
-    launch_decode(dec, workspace, decode_dim(g.d), pool->dtype, s);
   } else if (f32_mfma_ok(pool, num_heads, max_seqlen_q, max_seqlen_k, batch)) {
     if (skip_decode) {
       a.pf_min_q = 1;
     } else {
       dec.num_waves = decode_num_waves();
-      launch_decode(dec, workspace, g.d, pool->dtype, s);
+      launch_decode(dec, workspace, decode_dim(g.d), pool->dtype, s);
     }
     if (max_seqlen_q > 1 && pf_n > 0) {
       // The workspace past the decode's part (never its first 256 bytes,
       // the XCD shares) serves the key split, as for 16-bit pools.
       const size_t off = std::max<size_t>((need + 255) & ~(size_t)255, 256);
       const bool room = workspace && workspace_bytes > off;
-      launch_prefill_f32(a, max_seqlen_q, max_seqlen_k, g.d,
+      launch_prefill_f32(a, max_seqlen_q, max_seqlen_k, decode_dim(g.d),
                          room ? (char*)workspace + off : nullptr,
                          room ? workspace_bytes - off : 0, s);
     }

@@ -17,7 +17,9 @@
 // is small beside its MFMAs and a second wave per SIMD buys little.
 //
 // Rows with len_q < a.pf_min_q are left to the decode stream (pf_min_q 1:
-// every row here). Numerical contract: paged_attention_cpu (vapi
+// every row here). kPad: a head_dim a.hd below D (a multiple of 4); Q, K
+// and V elements past it load as zeros, output rows are a.hd apart and
+// their columns past it are not stored. Numerical contract: paged_attention_cpu (vapi
 // crates/vapi-backend-candle/src/attention.rs:90-163), f32 throughout.
 #include "attn_common.hpp"
 
@@ -29,7 +31,7 @@ constexpr int kPf32Waves = 4;
 // of steps, one wave each (a batch too small to fill the GPU with query
 // tiles alone); each writes its rows' (m, l, o / l) to `part`
 // (pf_part_bytes of 16 * RT rows per (item, split)) for the merge.
-template <int D, int RT, bool kSplit>
+template <int D, int RT, bool kSplit, bool kPad>
 __global__ __launch_bounds__(64 * kPf32Waves, 1) void paged_prefill_f32(
     AttnArgs a, uint32_t qtiles, uint32_t n_items, uint32_t n_split_arg,
     float* __restrict__ part) {
@@ -68,10 +70,12 @@ __global__ __launch_bounds__(64 * kPf32Waves, 1) void paged_prefill_f32(
     int32_t hi;
     key_range(offset + (int32_t)j, len_k, a.wl, a.wr, lo[t], hi);
     cnt[t] = (uint32_t)max(hi - lo[t] + 1, 0);
-    const float* qrow = (const float*)a.q + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * D;
+    const float* qrow =
+        (const float*)a.q + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * (kPad ? a.hd : D);
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
-      uint4 x = *(const uint4*)(qrow + 16 * c + 4 * g);
+      uint4 x = make_uint4(0, 0, 0, 0);
+      if (!kPad || 16 * c + 4 * g < a.hd) x = *(const uint4*)(qrow + 16 * c + 4 * g);
       x.x ^= sg, x.y ^= sg, x.z ^= sg, x.w ^= sg;
       qf[t][c] = make_float4(__uint_as_float(x.x), __uint_as_float(x.y), __uint_as_float(x.z),
                              __uint_as_float(x.w));
@@ -112,7 +116,7 @@ __global__ __launch_bounds__(64 * kPf32Waves, 1) void paged_prefill_f32(
     VTileF32<D> vt;
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
-      load_half_f32<D, false>(kt.h[tt], vt.h[tt], tab, kb, vb, a, s0, tt, khi, col, g);
+      load_half_f32<D, false, kPad>(kt.h[tt], vt.h[tt], tab, kb, vb, a, s0, tt, khi, col, g);
     while (true) {
       // The next step's halves are loaded unconditionally (the last step
       // re-reads its own keys, from L2): a load inside a branch would make
@@ -127,7 +131,7 @@ __global__ __launch_bounds__(64 * kPf32Waves, 1) void paged_prefill_f32(
           attend_half_f32<D>(kt.h[tt], vt.h[tt], qf[t], o[t], m_run[t], l_run[t], a.scale_log2,
                              [&](int i) { return base + (uint32_t)i < n; });
         }
-        load_half_f32<D, false>(kt.h[tt], vt.h[tt], tab, kb, vb, a, s_next, tt, khi, col, g);
+        load_half_f32<D, false, kPad>(kt.h[tt], vt.h[tt], tab, kb, vb, a, s_next, tt, khi, col, g);
       }
       if (s0 >= s_last) break;
       s0 += 32;
@@ -153,8 +157,9 @@ __global__ __launch_bounds__(64 * kPf32Waves, 1) void paged_prefill_f32(
     const uint32_t r = row0 + 16 * t + col;
     if (r >= nrows) continue;
     const uint32_t j = r / G, hl = r % G;
-    float* orow = (float*)a.out + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * D;
-    store_row_f32<D>(orow, o[t], lt > 0.f ? 1.f / lt : 0.f, g);
+    float* orow =
+        (float*)a.out + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * (kPad ? a.hd : D);
+    store_row_f32<D, kPad>(orow, o[t], lt > 0.f ? 1.f / lt : 0.f, g, a.hd);
   }
 }
 
@@ -198,19 +203,25 @@ void launch_prefill_f32(const AttnArgs& a, uint32_t max_q, uint32_t max_k, uint3
   const uint64_t items = base * n_split;
   const uint32_t wgs = (uint32_t)((items + kPf32Waves - 1) / kPf32Waves);
   float* part = n_split > 1 ? (float*)split_ws : nullptr;
-#define VK_PF32(DD)                                                                             \
+#define VK_PF32(DD, PAD)                                                                        \
   do {                                                                                          \
     if (n_split > 1) {                                                                          \
-      hipLaunchKernelGGL((paged_prefill_f32<DD, kPf32RowTiles, true>), dim3(wgs),               \
+      hipLaunchKernelGGL((paged_prefill_f32<DD, kPf32RowTiles, true, PAD>), dim3(wgs),          \
                          dim3(64 * kPf32Waves), 0, s, a, qtiles, (uint32_t)items, n_split, part); \
       launch_prefill_merge_f32(a, qtiles, kPf32Rows, n_split, part, base, DD, s);               \
     } else {                                                                                    \
-      hipLaunchKernelGGL((paged_prefill_f32<DD, kPf32RowTiles, false>), dim3(wgs),              \
+      hipLaunchKernelGGL((paged_prefill_f32<DD, kPf32RowTiles, false, PAD>), dim3(wgs),         \
                          dim3(64 * kPf32Waves), 0, s, a, qtiles, (uint32_t)items, 1u, nullptr); \
     }                                                                                           \
   } while (0)
-  if (head_dim == 128) VK_PF32(128);
-  else VK_PF32(64);
+  // A head_dim below the kernel's D runs the padded variant.
+  if (head_dim == 128) {
+    if (a.hd != 128) VK_PF32(128, true);
+    else VK_PF32(128, false);
+  } else {
+    if (a.hd != 64) VK_PF32(64, true);
+    else VK_PF32(64, false);
+  }
 #undef VK_PF32
 }
 
