@@ -225,7 +225,8 @@ CASES = [
     (torch.float32, 8, 8, 40, 16, [1, 1], [900, 1290], None, "HND-bm"),
     # ... and with prefill rows (16-bit pools): the prefill kernel at the
     # next D, Q and K chunks past head_dim zero, output columns past it
-    # unstored; padded dims never take the one-launch mixed step.
+    # unstored; below 128 a batch with both kinds of rows takes the
+    # one-launch mixed step with the padded kernels, above it two launches.
     (torch.bfloat16, 32, 8, 80, 16, [1, 37, 1, 64], [700, 37, 33, 300], None, "HND"),
     (torch.float16, 16, 4, 96, 32, [20, 1, 5], [900, 65, 300], 50, "NHD"),
     (torch.bfloat16, 8, 8, 48, 16, [1, 100], [900, 100], None, "HND-bm"),

@@ -483,16 +483,16 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
     // Decode rows and prefill rows in one step: both kernels in one launch.
     // (At most 4,000 sequences: the launch's dynamic LDS, 4 bytes per
     // sequence, then still lets a decode and a prefill workgroup share a CU.
-    // At head_dim 256 neither kernel fits half a CU's registers; padded head
-    // dims run the two launches.)
-    const bool mixed = !skip_decode && !fuse && gsh == 0 && (g.d == 64 || g.d == 128) &&
+    // At head_dim 256 neither kernel fits half a CU's registers; a padded
+    // head_dim below 128 runs the padded kernels.)
+    const bool mixed = !skip_decode && !fuse && gsh == 0 && D <= 128 &&
                        max_seqlen_q > 1 &&
                        pf_n > 0 &&
                        batch <= std::min(decode_max_plan_seqs(), 4000u) &&
                        mixed_prefill_items(pf_n, g.kvh, num_heads / g.kvh, max_seqlen_q) <
                            (1ull << 30);
     if (mixed) {
-      launch_mixed(a, workspace, max_seqlen_q, max_seqlen_k, g.d, bf16,
+      launch_mixed(a, workspace, max_seqlen_q, max_seqlen_k, D, bf16,
                    room ? (char*)workspace + off : nullptr, room ? workspace_bytes - off : 0, s);
       VK_LAUNCHED("paged_attention");
       return 0;

@@ -80,24 +80,37 @@ void launch_decode_merge(const AttnArgs& c, uint32_t nwg, uint32_t head_dim, boo
                          hipStream_t s) {
   bool wide = false;
   const uint32_t merge_wgs = decode_merge_wgs(c.batch, c.kvh, &wide);
-#define VK_MRG(T, DD)                                                                        \
+#define VK_MRG(T, DD, PAD)                                                                   \
   do {                                                                                       \
     if (wide && c.batch * c.kvh <= kFewSegs)                                                 \
-      hipLaunchKernelGGL((paged_decode_merge<T, DD, false, 8>), dim3(merge_wgs),             \
+      hipLaunchKernelGGL((paged_decode_merge<T, DD, false, 8, PAD>), dim3(merge_wgs),        \
                          dim3(merge_threads(8)), 0, s, c, nwg, merge_wgs);                   \
     else if (wide)                                                                           \
-      hipLaunchKernelGGL((paged_decode_merge<T, DD, false, kMergeWaves>), dim3(merge_wgs),   \
-                         dim3(merge_threads(kMergeWaves)), 0, s, c, nwg, merge_wgs);         \
+      hipLaunchKernelGGL((paged_decode_merge<T, DD, false, kMergeWaves, PAD>),               \
+                         dim3(merge_wgs), dim3(merge_threads(kMergeWaves)), 0, s, c, nwg,    \
+                         merge_wgs);                                                         \
     else                                                                                     \
-      hipLaunchKernelGGL((paged_decode_merge<T, DD, false, 1>), dim3(merge_wgs),             \
+      hipLaunchKernelGGL((paged_decode_merge<T, DD, false, 1, PAD>), dim3(merge_wgs),        \
                          dim3(64 * kMergeWaves), 0, s, c, nwg, merge_wgs);                   \
   } while (0)
+  // A head_dim below the kernel's D: the padded merge.
+  const bool pad = c.hd != head_dim;
   if (bf16) {
-    if (head_dim == 128) VK_MRG(bf16_t, 128);
-    else VK_MRG(bf16_t, 64);
+    if (head_dim == 128) {
+      if (pad) VK_MRG(bf16_t, 128, true);
+      else VK_MRG(bf16_t, 128, false);
+    } else {
+      if (pad) VK_MRG(bf16_t, 64, true);
+      else VK_MRG(bf16_t, 64, false);
+    }
   } else {
-    if (head_dim == 128) VK_MRG(f16_t, 128);
-    else VK_MRG(f16_t, 64);
+    if (head_dim == 128) {
+      if (pad) VK_MRG(f16_t, 128, true);
+      else VK_MRG(f16_t, 128, false);
+    } else {
+      if (pad) VK_MRG(f16_t, 64, true);
+      else VK_MRG(f16_t, 64, false);
+    }
   }
 #undef VK_MRG
 }

@@ -594,16 +594,16 @@ constexpr int kMixRowTiles = 2;
 constexpr int kMixPfWaves = 4;
 constexpr uint32_t kMixRows = 16 * kMixRowTiles * kMixPfWaves;
 
-template <typename T, int D, bool kSplit>
+template <typename T, int D, bool kSplit, bool kPad>
 __global__ __launch_bounds__(256, 2) void paged_mixed_stream(AttnArgs a, uint32_t nwg,
                                                              uint32_t qtiles, uint32_t n_split,
                                                              float* __restrict__ part) {
   static_assert(64 * kDecodeWavesPerWG == 256 && 64 * kMixPfWaves == 256, "256 threads");
   extern __shared__ uint32_t P[];
   if (blockIdx.x < nwg)
-    decode_stream_body<T, D, false>(a, a.cu_q, a.cu_k, a.table, P, blockIdx.x, nwg);
+    decode_stream_body<T, D, false, kPad>(a, a.cu_q, a.cu_k, a.table, P, blockIdx.x, nwg);
   else {
-    prefill_body<T, D, kMixRowTiles, kMixPfWaves, kSplit>(a, a.cu_q, a.cu_k, a.table, qtiles,
+    prefill_body<T, D, kMixRowTiles, kMixPfWaves, kSplit, kPad>(a, a.cu_q, a.cu_k, a.table, qtiles,
                                                           n_split, part, blockIdx.x - nwg,
                                                           gridDim.x - nwg);
   }
@@ -611,13 +611,13 @@ __global__ __launch_bounds__(256, 2) void paged_mixed_stream(AttnArgs a, uint32_
 
 // The mixed step's merges in one launch: the decode's (workgroups 0 ..
 // merge_wgs - 1) and the prefill key split's (the rest).
-template <typename T, int D, int WPS>
+template <typename T, int D, int WPS, bool kPad>
 __global__ __launch_bounds__(256) void paged_mixed_merge(AttnArgs a, uint32_t nwg,
                                                          uint32_t merge_wgs, uint32_t qtiles,
                                                          uint32_t n_split,
                                                          const float* __restrict__ part) {
   if (blockIdx.x < merge_wgs)
-    decode_merge_body<T, D, false, WPS>(a, nwg, merge_wgs, blockIdx.x, merge_wgs);
+    decode_merge_body<T, D, false, WPS, kPad>(a, nwg, merge_wgs, blockIdx.x, merge_wgs);
   else
     prefill_merge_body<T, D>(a, qtiles, kMixRows, n_split, part, blockIdx.x - merge_wgs);
 }
@@ -652,33 +652,41 @@ void launch_mixed(const AttnArgs& a_in, void* workspace, uint32_t max_q, uint32_
   const size_t lds = (c.batch + 1) * sizeof(uint32_t);
   bool wide = false;
   const uint32_t merge_wgs = decode_merge_wgs(c.batch, c.kvh, &wide);
-#define VK_MIX(T, DD)                                                                         \
+#define VK_MIX(T, DD, PAD)                                                                    \
   do {                                                                                        \
     if (n_split > 1)                                                                          \
-      hipLaunchKernelGGL((paged_mixed_stream<T, DD, true>), grid, block, lds, s, c, nwg,      \
+      hipLaunchKernelGGL((paged_mixed_stream<T, DD, true, PAD>), grid, block, lds, s, c, nwg, \
                          qtiles, n_split, part);                                              \
     else                                                                                      \
-      hipLaunchKernelGGL((paged_mixed_stream<T, DD, false>), grid, block, lds, s, c, nwg,     \
-                         qtiles, 1u, nullptr);                                                \
+      hipLaunchKernelGGL((paged_mixed_stream<T, DD, false, PAD>), grid, block, lds, s, c,     \
+                         nwg, qtiles, 1u, nullptr);                                           \
     if (n_split == 1) {                                                                       \
       launch_decode_merge(c, nwg, DD, bf16, s);                                               \
     } else {                                                                                  \
       const uint32_t pf_wgs = (uint32_t)(base * (kMixRows / (256 / (DD / 4))));               \
       if (wide)                                                                               \
-        hipLaunchKernelGGL((paged_mixed_merge<T, DD, kMergeWaves>), dim3(merge_wgs + pf_wgs), \
-                           dim3(256), 0, s, c, nwg, merge_wgs, qtiles, n_split, part);        \
+        hipLaunchKernelGGL((paged_mixed_merge<T, DD, kMergeWaves, PAD>),                      \
+                           dim3(merge_wgs + pf_wgs), dim3(256), 0, s, c, nwg, merge_wgs,      \
+                           qtiles, n_split, part);                                            \
       else                                                                                    \
-        hipLaunchKernelGGL((paged_mixed_merge<T, DD, 1>), dim3(merge_wgs + pf_wgs), dim3(256), \
-                           0, s, c, nwg, merge_wgs, qtiles, n_split, part);                   \
+        hipLaunchKernelGGL((paged_mixed_merge<T, DD, 1, PAD>), dim3(merge_wgs + pf_wgs),      \
+                           dim3(256), 0, s, c, nwg, merge_wgs, qtiles, n_split, part);        \
     }                                                                                         \
   } while (0)
+  // A head_dim below the kernel's D (a multiple of 8): the padded kernels.
+#define VK_MIX_D(T, DD)                 \
+  do {                                  \
+    if (c.hd != DD) VK_MIX(T, DD, true); \
+    else VK_MIX(T, DD, false);          \
+  } while (0)
   if (bf16) {
-    if (head_dim == 128) VK_MIX(bf16_t, 128);
-    else VK_MIX(bf16_t, 64);
+    if (head_dim == 128) VK_MIX_D(bf16_t, 128);
+    else VK_MIX_D(bf16_t, 64);
   } else {
-    if (head_dim == 128) VK_MIX(f16_t, 128);
-    else VK_MIX(f16_t, 64);
+    if (head_dim == 128) VK_MIX_D(f16_t, 128);
+    else VK_MIX_D(f16_t, 64);
   }
+#undef VK_MIX_D
 #undef VK_MIX
 }
 
