@@ -328,10 +328,11 @@ __device__ __forceinline__ void load_kv_step(KVStep<D>& st, const uint32_t* __re
 
 // Scores S^T = K Q^T of a 32-key step for 16 query rows: acc[tt][i] is key
 // 16 tt + 4 g + i of this lane's row.
-template <typename T, int D>
+// KC: the 32-column chunks of d that take part (fewer than D / 32 when the
+// rest are padding).
+template <typename T, int D, int KC = D / 32>
 __device__ __forceinline__ void qk_scores(const KTile<D>& kt, const uint4 (&qf)[D / 32],
                                           floatx4 (&acc)[2]) {
-  constexpr int KC = D / 32;
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     acc[tt] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -343,10 +344,11 @@ __device__ __forceinline__ void qk_scores(const KTile<D>& kt, const uint4 (&qf)[
 // Lazy rescale of 16 rows given each lane's max mx over its keys (scaled
 // log2 units): rows whose max grew by more than 2^kRescaleSlack take the row
 // max across the four lane groups and rescale O and l to it.
-template <int D>
+// DPL: the 16-column d tiles of O that are live (fewer than D / 16 when the
+// rest are padding).
+template <int D, int DPL = D / 16>
 __device__ __forceinline__ void rescale_rows(float mx, floatx4 (&o)[D / 16], float& m_run,
                                              float& l_run) {
-  constexpr int DPL = D / 16;
   if (__any(mx > m_run + kRescaleSlack)) {
     const float m_new = fmaxf(m_run, wave_max_g(mx));
     const float alpha = fast_exp2(m_run - m_new);

@@ -170,7 +170,10 @@ __device__ __forceinline__ void lgkm_wait(uint2 (&r)[4]) {
 // the GPU with query tiles alone); each writes its rows' (m, l, o) to
 // `part` and paged_prefill_merge combines them.
 // Workgroup `bid` of `n_items` (W waves) of a prefill launch.
-template <typename T, int D, int RT, int W, bool kSplit, bool kPad = false>
+// DL: the 16-column d tiles that hold head_dim (kPad; D / 16 otherwise):
+// the score MFMAs, V^T reads, PV MFMAs and stores of the tiles past them
+// are left out.
+template <typename T, int D, int RT, int W, bool kSplit, bool kPad = false, int DL = D / 16>
 __device__ __forceinline__ void prefill_body(
     const AttnArgs& a, const uint32_t* __restrict__ cu_q, const uint32_t* __restrict__ cu_k,
     const uint32_t* __restrict__ table, uint32_t qtiles, uint32_t n_split_arg,
@@ -180,6 +183,8 @@ __device__ __forceinline__ void prefill_body(
   static_assert(W == 8 || W == 4, "a step's K and V are loaded by 8 or 4 waves");
   constexpr int KC = D / 32;
   constexpr int DT = D / 16;  // 16-column d tiles
+  static_assert(DL >= 1 && DL <= DT && (kPad || DL == DT), "live d tiles");
+  constexpr int KCL = (DL + 1) / 2;  // live 32-column chunks of d
   constexpr int kPfRT = RT;
   constexpr uint32_t kPfRows = 16 * RT * W;
   // Direct loads per thread per step (the ring's vmcnt waits count them).
@@ -244,7 +249,7 @@ __device__ __forceinline__ void prefill_body(
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
       uint4 x = make_uint4(0, 0, 0, 0);
-      if (!kPad || 32 * c + 8 * g < a.hd) {
+      if (c < KCL && (!kPad || 32 * c + 8 * g < a.hd)) {
         x = *(const uint4*)(qrow + 32 * c + 8 * g);
         x.x ^= a.q_sign, x.y ^= a.q_sign, x.z ^= a.q_sign, x.w ^= a.q_sign;
       }
@@ -307,7 +312,7 @@ __device__ __forceinline__ void prefill_body(
     // b + 1 is issued before batch b's MFMAs, and batch 0 right after the
     // score MFMAs, so its reads land during the softmax.
     const uint32_t vbase = lds_addr(vbuf);
-    constexpr int NB = DT / 2;
+    constexpr int NB = (DL + 1) / 2;
     uint2 r[NB][4];
     auto issue = [&](int b) __attribute__((always_inline)) {
       uint32_t ad[4];
@@ -324,12 +329,12 @@ __device__ __forceinline__ void prefill_body(
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int c = 0; c < KC; ++c) {
+        for (int c = 0; c < KCL; ++c) {
           kt.k[tt][c] = *(const uint4*)(kbuf + k_off[tt][c]);
           if (kPad && D < 256 && 32 * c + 8 * g >= a.hd) kt.k[tt][c] = make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
-      for (int t = 0; t < kPfRT; ++t) qk_scores<T, D>(kt, qf[t], acc[t]);
+      for (int t = 0; t < kPfRT; ++t) qk_scores<T, D, KCL>(kt, qf[t], acc[t]);
 #pragma unroll
       for (int t = 0; t < kPfRT; ++t) {
         const uint32_t base = (uint32_t)(s0 + 4 * (int32_t)g - lo[t]), n = (uint32_t)cnt[t];
@@ -357,7 +362,7 @@ __device__ __forceinline__ void prefill_body(
     }
     if (__any(grow)) {
 #pragma unroll
-      for (int t = 0; t < kPfRT; ++t) rescale_rows<D>(mx[t], o[t], m_run[t], l_run[t]);
+      for (int t = 0; t < kPfRT; ++t) rescale_rows<D, DL>(mx[t], o[t], m_run[t], l_run[t]);
     }
     uint4 pf[kPfRT];
 #pragma unroll
@@ -379,9 +384,11 @@ __device__ __forceinline__ void prefill_body(
       for (int k = 0; k < 2; ++k) {
         const uint4 vf = make_uint4(r[b][2 * k].x, r[b][2 * k].y, r[b][2 * k + 1].x,
                                     r[b][2 * k + 1].y);
+        if (2 * b + k < DL) {
 #pragma unroll
-        for (int t = 0; t < kPfRT; ++t)
-          o[t][2 * b + k] = mfma16x16x32<T>(vf, pf[t], o[t][2 * b + k]);
+          for (int t = 0; t < kPfRT; ++t)
+            o[t][2 * b + k] = mfma16x16x32<T>(vf, pf[t], o[t][2 * b + k]);
+        }
       }
     }
     // Step s + 1's chunks (issued a step ago) are in LDS once this wave's
@@ -416,7 +423,7 @@ __device__ __forceinline__ void prefill_body(
       float* po = (float*)(pb + (uint64_t)kPfRows * 8) + (uint64_t)row * D;
       const float sc = lt > 0.f ? 1.f / lt : 0.f;
 #pragma unroll
-      for (int k = 0; k < DT; ++k)
+      for (int k = 0; k < DL; ++k)
         *(float4*)(po + 16 * k + 4 * g) = make_float4(o[t][k][0] * sc, o[t][k][1] * sc,
                                                       o[t][k][2] * sc, o[t][k][3] * sc);
     }
@@ -431,7 +438,7 @@ __device__ __forceinline__ void prefill_body(
     T* orow = (T*)a.out + ((uint64_t)(q0 + j) * a.num_heads + kh * G + hl) * (kPad ? a.hd : D);
     const float sc = lt > 0.f ? 1.f / lt : 0.f;
 #pragma unroll
-    for (int k = 0; k < DT; ++k)
+    for (int k = 0; k < DL; ++k)
       if (!kPad || 16 * k + 4 * g < a.hd)
         *(uint2*)(orow + 16 * k + 4 * g) =
           make_uint2(pack2<T>(o[t][k][0] * sc, o[t][k][1] * sc),
@@ -439,12 +446,12 @@ __device__ __forceinline__ void prefill_body(
   }
 }
 
-template <typename T, int D, int RT, int OCC, bool kSplit, bool kPad>
+template <typename T, int D, int RT, int OCC, bool kSplit, bool kPad, int DL = D / 16>
 __global__ __launch_bounds__(kPfThreads, OCC) void paged_prefill_tiled(
     AttnArgs a, const uint32_t* __restrict__ cu_q, const uint32_t* __restrict__ cu_k,
     const uint32_t* __restrict__ table, uint32_t qtiles, uint32_t n_split_arg,
     float* __restrict__ part) {
-  prefill_body<T, D, RT, kPfWaves, kSplit, kPad>(a, cu_q, cu_k, table, qtiles, n_split_arg, part,
+  prefill_body<T, D, RT, kPfWaves, kSplit, kPad, DL>(a, cu_q, cu_k, table, qtiles, n_split_arg, part,
                                            blockIdx.x, gridDim.x);
 }
 
@@ -728,28 +735,36 @@ void launch_prefill(const AttnArgs& a_in, uint32_t max_q, uint32_t max_k, uint32
                                : 1;
   float* part = n_split > 1 ? (float*)split_ws : nullptr;
   const dim3 grid((uint32_t)(base * n_split)), block(kPfThreads);
-#define VK_PF(T, DD, PAD)                                                                        \
+#define VK_PF(T, DD, PAD, DL)                                                                    \
   do {                                                                                           \
     constexpr int occ = DD == 64 ? kPfOcc64 : kPfOcc;                                            \
     constexpr int rt = DD == 256 ? kPfRowTiles256 : kPfRowTiles;                                 \
     if (n_split > 1) {                                                                           \
-      hipLaunchKernelGGL((paged_prefill_tiled<T, DD, rt, occ, true, PAD>), grid, block, 0, s, a, \
-                         a.cu_q, a.cu_k, a.table, qtiles, n_split, part);                        \
+      hipLaunchKernelGGL((paged_prefill_tiled<T, DD, rt, occ, true, PAD, DL>), grid, block, 0,   \
+                         s, a, a.cu_q, a.cu_k, a.table, qtiles, n_split, part);                  \
       hipLaunchKernelGGL((paged_prefill_merge<T, DD>),                                           \
                          dim3((uint32_t)(base * (rows / (256 / (DD / 4))))), dim3(256), 0, s, a, \
                          qtiles, rows, n_split, part);                                           \
     } else {                                                                                     \
-      hipLaunchKernelGGL((paged_prefill_tiled<T, DD, rt, occ, false, PAD>), grid, block, 0, s,   \
-                         a, a.cu_q, a.cu_k, a.table, qtiles, 1u, nullptr);                       \
+      hipLaunchKernelGGL((paged_prefill_tiled<T, DD, rt, occ, false, PAD, DL>), grid, block, 0,  \
+                         s, a, a.cu_q, a.cu_k, a.table, qtiles, 1u, nullptr);                    \
     }                                                                                            \
   } while (0)
   // A head_dim below the kernel's D (a multiple of 8) runs the padded
   // variant: Q and K chunks past it read as zeros, output columns past it
-  // are not stored.
-#define VK_PF_D(T, DD)              \
-  do {                              \
-    if (a.hd != DD) VK_PF(T, DD, true); \
-    else VK_PF(T, DD, false);       \
+  // are not stored, and the d tiles wholly past it are skipped where the
+  // launch has a variant that stops at fewer tiles (64: 32 columns; 128:
+  // 80 or 96; 256: 160 or 192).
+  const uint32_t live = (a.hd + 15) / 16;
+#define VK_PF_D(T, DD)                                   \
+  do {                                                   \
+    if (a.hd == DD) VK_PF(T, DD, false, DD / 16);        \
+    else if (DD == 64 && live <= 2) VK_PF(T, 64, true, 2); \
+    else if (DD == 128 && live <= 5) VK_PF(T, 128, true, 5); \
+    else if (DD == 128 && live <= 6) VK_PF(T, 128, true, 6); \
+    else if (DD == 256 && live <= 10) VK_PF(T, 256, true, 10); \
+    else if (DD == 256 && live <= 12) VK_PF(T, 256, true, 12); \
+    else VK_PF(T, DD, true, DD / 16);                    \
   } while (0)
   if (bf16) {
     if (head_dim == 256) VK_PF_D(bf16_t, 256);
