@@ -243,11 +243,12 @@ __device__ __forceinline__ const char* tile_base(const uint32_t* __restrict__ ta
 // K and V tiles of the 32-key step at s0 (keys past `last` re-read it). With
 // `knew` / `vnew` (the row's new key, D contiguous elements) key `last` is
 // read from there instead of the pool: a per-lane address select, no branch.
-template <typename T, int D, bool kPad = false>
+// KCL: the 32-column chunks of K that are loaded (the rest, padding, are
+// left as they were; fewer than D / 32 only with kPad).
+template <typename T, int D, bool kPad = false, int KCL = D / 32>
 __device__ __forceinline__ void load_k(KTile<D>& st, const uint32_t* __restrict__ tab,
                                        const T* kb, const AttnArgs& a, int32_t s0, int32_t last,
                                        uint32_t col, uint32_t g, const char* knew = nullptr) {
-  constexpr int KC = D / 32;
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     const int32_t ts = min(s0 + 16 * tt, last & ~15);
@@ -256,7 +257,7 @@ __device__ __forceinline__ void load_k(KTile<D>& st, const uint32_t* __restrict_
     const char* src = kt + kr;
     if (knew != nullptr && (int32_t)col >= last - ts) src = knew + 8 * g * sizeof(T);
 #pragma unroll
-    for (int c = 0; c < KC; ++c) {
+    for (int c = 0; c < KCL; ++c) {
       if constexpr (kPad)
         st.k[tt][c] = 32 * c + 8 * g < a.hd ? load_stream((const uint4*)(src + 64u * c))
                                              : make_uint4(0u, 0u, 0u, 0u);
@@ -383,11 +384,13 @@ __device__ __forceinline__ uint4 exp_pack(const float (&s)[8], float m_run, floa
 // `visible(i_tile, i)` masks key slot (tt, 4g+i). m_run is kept in scaled
 // log2 units; scale_log2 >= 0, so the max is taken on the raw scores and the
 // scale folds into one FMA per score: p = exp2(s * c - m).
-template <typename T, int D, typename Mask>
+// KC: the 32-column chunks of d in the scores (fewer than D / 32 when the
+// rest are padding).
+template <typename T, int D, int KC = D / 32, typename Mask>
 __device__ __forceinline__ uint4 attend_qk(const KTile<D>& kt, const uint4 (&qf)[D / 32],
                                            floatx4 (&o)[D / 16], float& m_run, float& l_run,
                                            float scale_log2, uint32_t g, Mask visible) {
-  constexpr int KC = D / 32, DPL = D / 16;
+  constexpr int DPL = D / 16;
   float s[8];
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
@@ -514,7 +517,9 @@ __device__ __forceinline__ floatx4 mfma16x16x4f32(float a, float b, floatx4 c) {
 // K and V of the 16-key tile at s0 + 16 tt (keys past `last` re-read it).
 // kStream: streaming loads (the decode reads each byte once); the prefill's
 // waves share a kv head's K/V through L2 and load them the ordinary way.
-template <int D, bool kStream = true, bool kPad = false>
+// CL: the 16-column chunks of K that are loaded (fewer than D / 16 when the
+// rest are padding; those stay as they were).
+template <int D, bool kStream = true, bool kPad = false, int CL = D / 16>
 __device__ __forceinline__ void load_half_f32(KHalfF32<D>& kt, VHalfF32<D>& vt,
                                               const uint32_t* __restrict__ tab, const float* kb,
                                               const float* vb, const AttnArgs& a, int32_t s0,
@@ -525,7 +530,7 @@ __device__ __forceinline__ void load_half_f32(KHalfF32<D>& kt, VHalfF32<D>& vt,
                    ((uint32_t)min((int32_t)col, lim) * a.tok_e + 4 * g) * sizeof(float);
   const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int c = 0; c < D / 16; ++c)
+  for (int c = 0; c < CL; ++c)
     kt.k[c] = kPad && 16 * c + 4 * g >= a.hd ? z
               : kStream ? load_stream((const float4*)(kp + 64u * c))
                         : *(const float4*)(kp + 64u * c);
@@ -548,15 +553,16 @@ __device__ __forceinline__ float f4(const float4& x, int j) {
 
 // Online softmax over one 16-key tile for 16 query columns: S^T, lazy
 // rescale, P = exp2(s c - m) in f32, O^T += V^T P^T. visible(i): key 4g + i
-// of the tile.
-template <int D, typename Mask>
+// of the tile. CL: the 16-column chunks of d in the scores (fewer than
+// D / 16 when the rest are padding).
+template <int D, int CL = D / 16, typename Mask>
 __device__ __forceinline__ void attend_half_f32(const KHalfF32<D>& kt, const VHalfF32<D>& vt,
                                                 const float4 (&qf)[D / 16],
                                                 floatx4 (&o)[D / 16], float& m_run,
                                                 float& l_run, float scale_log2, Mask visible) {
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int c = 0; c < D / 16; ++c)
+  for (int c = 0; c < CL; ++c)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc = mfma16x16x4f32(f4(kt.k[c], j), f4(qf[c], j), acc);
   float s[4];

@@ -3,12 +3,12 @@
 
 namespace vk {
 
-template <typename T, int D, bool kFuse, bool kPad = false>
+template <typename T, int D, bool kFuse, bool kPad = false, int DL = D / 16>
 __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged_decode_stream(
     AttnArgs a, const uint32_t* __restrict__ cu_q, const uint32_t* __restrict__ cu_k,
     const uint32_t* __restrict__ table) {
   extern __shared__ uint32_t P[];
-  decode_stream_body<T, D, kFuse, kPad>(a, cu_q, cu_k, table, P, blockIdx.x, gridDim.x);
+  decode_stream_body<T, D, kFuse, kPad, DL>(a, cu_q, cu_k, table, P, blockIdx.x, gridDim.x);
 }
 
 // Waves per segment of a merge with a workgroup per segment: 8 for at most
@@ -141,9 +141,9 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t dtyp
       copy_wgs = (uint32_t)std::min<uint64_t>((chunks + 64 * kMergeWaves - 1) / (64 * kMergeWaves), 1024);
     }
     const size_t lds = (nb + 1 + (fuse ? nb : 0)) * sizeof(uint32_t);
-#define VK_DECP(T, DD, F, PAD)                                                                  \
+#define VK_DECL(T, DD, F, PAD, DL)                                                              \
   do {                                                                                          \
-    hipLaunchKernelGGL((paged_decode_stream<T, DD, F, PAD>), dim3(nwg),                         \
+    hipLaunchKernelGGL((paged_decode_stream<T, DD, F, PAD, DL>), dim3(nwg),                     \
                        dim3(64 * kDecodeWavesPerWG), lds, s, c, c.cu_q, c.cu_k, c.table);      \
     if (wide && nb * c.kvh <= kFewSegs)                                                        \
       hipLaunchKernelGGL((paged_decode_merge<T, DD, F, 8, PAD>), dim3(merge_wgs + copy_wgs),    \
@@ -156,7 +156,21 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t dtyp
       hipLaunchKernelGGL((paged_decode_merge<T, DD, F, 1, PAD>), dim3(merge_wgs + copy_wgs),    \
                          dim3(64 * kMergeWaves), 0, s, c, nwg, merge_wgs);                      \
   } while (0)
+#define VK_DECP(T, DD, F, PAD) VK_DECL(T, DD, F, PAD, DD / 16)
 #define VK_DEC(T, DD, F) VK_DECP(T, DD, F, false)
+    // A padded head_dim: the stream variant that loads and multiplies only
+    // the K chunks holding it, where there is one (64: 32 columns; 128: 80
+    // or 96; 256: 160 or 192).
+    const uint32_t live = (a.hd + 15) / 16;
+#define VK_DEC_PAD(T, DD)                                    \
+  do {                                                       \
+    if (DD == 64 && live <= 2) VK_DECL(T, 64, false, true, 2);      \
+    else if (DD == 128 && live <= 5) VK_DECL(T, 128, false, true, 5); \
+    else if (DD == 128 && live <= 6) VK_DECL(T, 128, false, true, 6); \
+    else if (DD == 256 && live <= 10) VK_DECL(T, 256, false, true, 10); \
+    else if (DD == 256 && live <= 12) VK_DECL(T, 256, false, true, 12); \
+    else VK_DECP(T, DD, false, true);                        \
+  } while (0)
 #define VK_DEC2(T, DD) \
   do {                 \
     if (fuse)          \
@@ -165,18 +179,24 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t dtyp
       VK_DEC(T, DD, false); \
   } while (0)
     if (a.hd != head_dim && dtype == VAPI_KV_F32) {  // an f32 head dim run at the next D
-      if (head_dim == 128) VK_DECP(float, 128, false, true);
-      else VK_DECP(float, 64, false, true);
+      if (head_dim == 128) {
+        if (live <= 5) VK_DECL(float, 128, false, true, 5);
+        else if (live <= 6) VK_DECL(float, 128, false, true, 6);
+        else VK_DECP(float, 128, false, true);
+      } else {
+        if (live <= 2) VK_DECL(float, 64, false, true, 2);
+        else VK_DECP(float, 64, false, true);
+      }
     } else if (a.hd != head_dim) {  // a 16-bit head dim run at the next D (no fused append)
       if (head_dim == 256) {
-        if (bf16) VK_DECP(bf16_t, 256, false, true);
-        else VK_DECP(f16_t, 256, false, true);
+        if (bf16) VK_DEC_PAD(bf16_t, 256);
+        else VK_DEC_PAD(f16_t, 256);
       } else if (head_dim == 128) {
-        if (bf16) VK_DECP(bf16_t, 128, false, true);
-        else VK_DECP(f16_t, 128, false, true);
+        if (bf16) VK_DEC_PAD(bf16_t, 128);
+        else VK_DEC_PAD(f16_t, 128);
       } else {
-        if (bf16) VK_DECP(bf16_t, 64, false, true);
-        else VK_DECP(f16_t, 64, false, true);
+        if (bf16) VK_DEC_PAD(bf16_t, 64);
+        else VK_DEC_PAD(f16_t, 64);
       }
     } else if (dtype == VAPI_KV_F32) {  // no fused append on f32 pools
       if (head_dim == 128) VK_DEC(float, 128, false);
@@ -193,6 +213,8 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t dtyp
 #undef VK_DEC2
 #undef VK_DEC
 #undef VK_DECP
+#undef VK_DECL
+#undef VK_DEC_PAD
   }
 }
 

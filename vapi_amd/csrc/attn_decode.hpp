@@ -208,7 +208,7 @@ __device__ __forceinline__ void load_q(uint4* qs, const AttnArgs& a, const Decod
   }
 }
 
-template <typename T, int D, bool kPad = false>
+template <typename T, int D, bool kPad = false, int KCL = D / 32>
 __device__ __forceinline__ void load_step_k(KTile<D>& st, const AttnArgs& a,
                                             const uint32_t* __restrict__ table,
                                             const DecodePos& p, uint32_t col, uint32_t g) {
@@ -216,7 +216,7 @@ __device__ __forceinline__ void load_step_k(KTile<D>& st, const AttnArgs& a,
   const T* kb = (const T*)a.k + (p.kh >> a.kv_shift) * a.head_e;
   const char* knew =
       p.fuse ? a.k_new + ((uint64_t)p.q0 * a.kvh + p.kh) * D * sizeof(T) : nullptr;
-  load_k<T, D, kPad>(st, tab, kb, a, p.key0, p.len_k - 1, col, g, knew);
+  load_k<T, D, kPad, KCL>(st, tab, kb, a, p.key0, p.len_k - 1, col, g, knew);
 }
 
 template <typename T, int D, bool kPad = false>
@@ -275,7 +275,10 @@ __device__ __forceinline__ void flush_piece(const AttnArgs& a, const DecodePos& 
 // The persistent stream of workgroup `bid` of `nwg` (4 waves). P: the
 // launch's dynamic LDS, step prefix sums (batch + 1), then with kFuse the
 // per-sequence fused-append flags FZ (batch).
-template <typename T, int D, bool kFuse, bool kPad = false>
+// DL: the 16-column d tiles that hold head_dim (kPad; D / 16 otherwise):
+// K chunks past them are neither loaded nor multiplied (V and O keep D: a
+// lane's V values spread over every d tile).
+template <typename T, int D, bool kFuse, bool kPad = false, int DL = D / 16>
 __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
                                                    const uint32_t* __restrict__ cu_q,
                                                    const uint32_t* __restrict__ cu_k,
@@ -365,6 +368,7 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
   // The Q^T operand of the current segment lives in LDS (read back every
   // step) to keep the K/V buffers in registers.
   constexpr bool kF32 = sizeof(T) == 4;
+  constexpr int KCL = (DL + 1) / 2;  // live 32-column K chunks (16-bit)
   __shared__ uint4 q_lds[kDecodeWavesPerWG][D / 32 * 64 * sizeof(T) / 2];
   uint4* qs = q_lds[wave];
   load_q<T, D, kPad>(qs, a, pos, lane, col, g);
@@ -385,7 +389,7 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
   const float* vbf = (const float*)a.v;
   auto load_halves = [&](KTileF32<D>& kt, VTileF32<D>& vt, const DecodePos& p, int tt)
       __attribute__((always_inline)) {
-    load_half_f32<D, true, kPad>(kt.h[tt], vt.h[tt], table + (uint64_t)p.seq * a.max_blocks,
+    load_half_f32<D, true, kPad, DL>(kt.h[tt], vt.h[tt], table + (uint64_t)p.seq * a.max_blocks,
                      kbf + (p.kh >> a.kv_shift) * a.head_e, vbf + (p.kh >> a.kv_shift) * a.head_e,
                      a, p.key0, tt, p.len_k - 1,
                      col, g);
@@ -394,7 +398,7 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
     load_halves(kA, vA, pos, 0);
     load_halves(kA, vA, pos, 1);
   } else {
-    load_step_k<T, D, kPad>(kA, a, table, pos, col, g);
+    load_step_k<T, D, kPad, KCL>(kA, a, table, pos, col, g);
     load_step_v<T, D, kPad>(vA, a, table, pos, col, g);
   }
 
@@ -437,19 +441,19 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
       }
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
-        attend_half_f32<D>(kc.h[tt], vc.h[tt], qf, o, m_run, l_run, a.scale_log2, [&](int i) {
+        attend_half_f32<D, DL>(kc.h[tt], vc.h[tt], qf, o, m_run, l_run, a.scale_log2, [&](int i) {
           const int32_t key = key0 + 16 * tt + 4 * (int32_t)g + i;
           return key >= lo && key < len_k;
         });
         load_halves(kn, vn, nxt, tt);
       }
     } else {
-      load_step_k<T, D, kPad>(kn, a, table, nxt, col, g);
+      load_step_k<T, D, kPad, KCL>(kn, a, table, nxt, col, g);
       load_step_v<T, D, kPad>(vn, a, table, nxt, col, g);
       uint4 qf[D / 32];
 #pragma unroll
       for (int c = 0; c < D / 32; ++c) qf[c] = qs[c * 64 + lane];
-      const uint4 pf = attend_qk<T, D>(kc, qf, o, m_run, l_run, a.scale_log2, g, [&](int tt, int i) {
+      const uint4 pf = attend_qk<T, D, KCL>(kc, qf, o, m_run, l_run, a.scale_log2, g, [&](int tt, int i) {
         const int32_t key = key0 + 16 * tt + 4 * (int32_t)g + i;
         return key >= lo && key < len_k;
       });

@@ -31,7 +31,9 @@ constexpr int kPf32Waves = 4;
 // of steps, one wave each (a batch too small to fill the GPU with query
 // tiles alone); each writes its rows' (m, l, o / l) to `part`
 // (pf_part_bytes of 16 * RT rows per (item, split)) for the merge.
-template <int D, int RT, bool kSplit, bool kPad>
+// CL: the 16-column chunks of d that hold head_dim (kPad; D / 16
+// otherwise): K chunks past them are neither loaded nor multiplied.
+template <int D, int RT, bool kSplit, bool kPad, int CL = D / 16>
 __global__ __launch_bounds__(64 * kPf32Waves, 1) void paged_prefill_f32(
     AttnArgs a, uint32_t qtiles, uint32_t n_items, uint32_t n_split_arg,
     float* __restrict__ part) {
@@ -116,7 +118,7 @@ __global__ __launch_bounds__(64 * kPf32Waves, 1) void paged_prefill_f32(
     VTileF32<D> vt;
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
-      load_half_f32<D, false, kPad>(kt.h[tt], vt.h[tt], tab, kb, vb, a, s0, tt, khi, col, g);
+      load_half_f32<D, false, kPad, CL>(kt.h[tt], vt.h[tt], tab, kb, vb, a, s0, tt, khi, col, g);
     while (true) {
       // The next step's halves are loaded unconditionally (the last step
       // re-reads its own keys, from L2): a load inside a branch would make
@@ -128,10 +130,10 @@ __global__ __launch_bounds__(64 * kPf32Waves, 1) void paged_prefill_f32(
         for (int t = 0; t < RT; ++t) {
           const uint32_t base = (uint32_t)(s0 + 16 * tt + 4 * (int32_t)g - lo[t]);
           const uint32_t n = cnt[t];
-          attend_half_f32<D>(kt.h[tt], vt.h[tt], qf[t], o[t], m_run[t], l_run[t], a.scale_log2,
+          attend_half_f32<D, CL>(kt.h[tt], vt.h[tt], qf[t], o[t], m_run[t], l_run[t], a.scale_log2,
                              [&](int i) { return base + (uint32_t)i < n; });
         }
-        load_half_f32<D, false, kPad>(kt.h[tt], vt.h[tt], tab, kb, vb, a, s_next, tt, khi, col, g);
+        load_half_f32<D, false, kPad, CL>(kt.h[tt], vt.h[tt], tab, kb, vb, a, s_next, tt, khi, col, g);
       }
       if (s0 >= s_last) break;
       s0 += 32;
@@ -203,24 +205,30 @@ void launch_prefill_f32(const AttnArgs& a, uint32_t max_q, uint32_t max_k, uint3
   const uint64_t items = base * n_split;
   const uint32_t wgs = (uint32_t)((items + kPf32Waves - 1) / kPf32Waves);
   float* part = n_split > 1 ? (float*)split_ws : nullptr;
-#define VK_PF32(DD, PAD)                                                                        \
+#define VK_PF32(DD, PAD, CL)                                                                    \
   do {                                                                                          \
     if (n_split > 1) {                                                                          \
-      hipLaunchKernelGGL((paged_prefill_f32<DD, kPf32RowTiles, true, PAD>), dim3(wgs),          \
+      hipLaunchKernelGGL((paged_prefill_f32<DD, kPf32RowTiles, true, PAD, CL>), dim3(wgs),      \
                          dim3(64 * kPf32Waves), 0, s, a, qtiles, (uint32_t)items, n_split, part); \
       launch_prefill_merge_f32(a, qtiles, kPf32Rows, n_split, part, base, DD, s);               \
     } else {                                                                                    \
-      hipLaunchKernelGGL((paged_prefill_f32<DD, kPf32RowTiles, false, PAD>), dim3(wgs),         \
+      hipLaunchKernelGGL((paged_prefill_f32<DD, kPf32RowTiles, false, PAD, CL>), dim3(wgs),     \
                          dim3(64 * kPf32Waves), 0, s, a, qtiles, (uint32_t)items, 1u, nullptr); \
     }                                                                                           \
   } while (0)
-  // A head_dim below the kernel's D runs the padded variant.
+  // A head_dim below the kernel's D runs the padded variant, which skips the
+  // K chunks wholly past it where the launch has a variant that stops there
+  // (64: 32 columns; 128: 80 or 96).
+  const uint32_t live = (a.hd + 15) / 16;
   if (head_dim == 128) {
-    if (a.hd != 128) VK_PF32(128, true);
-    else VK_PF32(128, false);
+    if (a.hd == 128) VK_PF32(128, false, 8);
+    else if (live <= 5) VK_PF32(128, true, 5);
+    else if (live <= 6) VK_PF32(128, true, 6);
+    else VK_PF32(128, true, 8);
   } else {
-    if (a.hd != 64) VK_PF32(64, true);
-    else VK_PF32(64, false);
+    if (a.hd == 64) VK_PF32(64, false, 4);
+    else if (live <= 2) VK_PF32(64, true, 2);
+    else VK_PF32(64, true, 4);
   }
 #undef VK_PF32
 }
