@@ -545,6 +545,41 @@ def bench_decode_block_major(steps, warmup):
     return dict(us=gms * 1e3, gbs=kv / (gms * 1e-3) / 1e9)
 
 
+def bench_decode_block_size_32(steps, warmup):
+    """Config 2's batch (the same contexts and heads) over a pool of 32-key
+    blocks, the reference's own block size (vapi_core::config::BLOCK_SIZE),
+    16,384 blocks in random order, rotating over 4 layers as the headline."""
+    w = workload.config2_decode()
+    bs, nb = 32, 16384
+    rng = np.random.default_rng(workload.seed_for(2))
+    perm = rng.permutation(nb)
+    tables, at = [], 0
+    for l in w.lens:
+        n = (int(l) + bs - 1) // bs
+        tables.append(perm[at:at + n].tolist())
+        at += n
+    cache = PagedKvCache(DECODE_LAYERS, nb, bs, w.num_kv_heads, w.head_dim, torch.bfloat16, "HND")
+    workload.fill_normal(cache._slab, workload.seed_for(2))
+    q = torch.randn(w.batch, w.num_heads, w.head_dim, device=DEV).to(torch.bfloat16)
+    batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
+                         block_tables=tables, max_seqlen_q=1, max_seqlen_k=int(w.lens.max()))
+    prep = PreparedAttention.from_batch(batch, DEV)
+    out = torch.empty_like(q)
+    turn = [0]
+
+    def call():
+        paged_attention_prepared(q, cache, turn[0] % DECODE_LAYERS, prep, 128 ** -0.5, out=out)
+        turn[0] += 1
+
+    gms = timed_graph(call, steps, warmup)
+    kv = int(w.lens.sum()) * 2 * 8 * 128 * 2
+    log(f"decode cfg2 over 32-key blocks: {gms * 1e3:.1f} us, "
+        f"{kv / (gms * 1e-3) / 1e9:.0f} GB/s of K/V")
+    del cache, q, out
+    torch.cuda.empty_cache()
+    return dict(us=gms * 1e3, gbs=kv / (gms * 1e-3) / 1e9)
+
+
 def bench_wide_group(steps, warmup):
     """Config 2's batch with 64 query heads over 2 kv heads (32 query heads
     per kv head: the decode runs each group as two virtual kv heads of 16,
@@ -1335,6 +1370,7 @@ def main():
         bench_wide_group(args.steps, args.warmup)
         bench_head_dim_256(args.steps, args.warmup)
         bench_decode_block_major(args.steps, args.warmup)
+        bench_decode_block_size_32(args.steps, args.warmup)
         bench_decode_other_head_dims(args.steps, args.warmup)
         return
     if args.only == "mixed":
@@ -1359,6 +1395,7 @@ def main():
         extras["wide_group_g32"] = bench_wide_group(args.steps, args.warmup)
         extras["head_dim_256"] = bench_head_dim_256(args.steps, args.warmup)
         extras["decode_cfg2_block_major"] = bench_decode_block_major(args.steps, args.warmup)
+        extras["decode_cfg2_block_size_32"] = bench_decode_block_size_32(args.steps, args.warmup)
         extras["other_head_dims"] = bench_decode_other_head_dims(args.steps, args.warmup)
         extras["decode_small_batches"] = bench_small_batches(args.steps, args.warmup)
         extras["prefill_small_batches"] = bench_small_prefill(args.steps, args.warmup)
