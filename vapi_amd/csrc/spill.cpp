@@ -10,12 +10,15 @@
 // head_dim]), so spill files are interchangeable with the reference's.
 #include <hip/hip_runtime.h>
 
+#include <sys/mman.h>
+
 #include <cstdio>
 #include <cstring>
 #include <deque>
 #include <filesystem>
 #include <fstream>
 #include <list>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <unordered_map>
@@ -111,6 +114,94 @@ struct Lru {
   }
 };
 
+// Blob memory. A fresh 0.9 MB blob in ordinary heap memory takes a page
+// fault per 4 KiB on first touch (~220 per block), which cost more than the
+// copy itself; blobs of at least kArenaMin bytes are carved instead from
+// 64 MiB chunks aligned to 2 MiB with transparent huge pages asked for
+// (madvise), so a chunk faults in 2 MiB at a time. A freed blob goes to a
+// free list of its size and is reused by the next blob of that size;
+// chunks stay mapped until the process ends, but past kKeepFree bytes of
+// free blobs (a store closed, or shrunk) a freed blob's pages are given back
+// to the system (MADV_DONTNEED: its next use faults them in again).
+class BlobArena {
+ public:
+  static constexpr size_t kArenaMin = 256 << 10;
+  static constexpr size_t kChunk = 64ull << 20;
+  static constexpr size_t kHuge = 2ull << 20;
+  static constexpr size_t kKeepFree = 1ull << 30;
+
+  static BlobArena& get() {
+    static BlobArena* a = new BlobArena();  // never destroyed: blobs may outlive statics
+    return *a;
+  }
+  void* allocate(size_t n) {
+    const size_t sz = round_up(n, 4096);
+    std::lock_guard<std::mutex> lk(mu_);
+    auto it = free_.find(sz);
+    if (it != free_.end() && !it->second.empty()) {
+      void* p = it->second.back();
+      it->second.pop_back();
+      free_bytes_ -= sz;
+      return p;
+    }
+    if (left_ < sz) {
+      const size_t want = std::max(kChunk, round_up(sz, kHuge));
+      // Over-map by one huge page and align the start to it.
+      void* m = mmap(nullptr, want + kHuge, PROT_READ | PROT_WRITE,
+                     MAP_PRIVATE | MAP_ANONYMOUS, -1, 0);
+      if (m == MAP_FAILED) throw std::bad_alloc();
+      char* base = (char*)round_up((size_t)(uintptr_t)m, kHuge);
+      (void)madvise(base, want, MADV_HUGEPAGE);
+      cur_ = base;
+      left_ = want;
+    }
+    void* p = cur_;
+    cur_ += sz;
+    left_ -= sz;
+    return p;
+  }
+  void deallocate(void* p, size_t n) {
+    const size_t sz = round_up(n, 4096);
+    std::lock_guard<std::mutex> lk(mu_);
+    if (free_bytes_ + sz > kKeepFree) (void)madvise(p, sz, MADV_DONTNEED);
+    free_[sz].push_back(p);
+    free_bytes_ += sz;
+  }
+
+ private:
+  static size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+  std::mutex mu_;
+  std::unordered_map<size_t, std::vector<void*>> free_;
+  char* cur_ = nullptr;
+  size_t left_ = 0;
+  size_t free_bytes_ = 0;
+};
+
+template <typename T>
+struct BlobAlloc {
+  using value_type = T;
+  BlobAlloc() = default;
+  template <typename U>
+  BlobAlloc(const BlobAlloc<U>&) {}
+  T* allocate(size_t n) {
+    const size_t bytes = n * sizeof(T);
+    if (bytes < BlobArena::kArenaMin) return (T*)::operator new(bytes);
+    return (T*)BlobArena::get().allocate(bytes);
+  }
+  void deallocate(T* p, size_t n) {
+    const size_t bytes = n * sizeof(T);
+    if (bytes < BlobArena::kArenaMin) ::operator delete(p);
+    else BlobArena::get().deallocate(p, bytes);
+  }
+  template <typename U>
+  bool operator==(const BlobAlloc<U>&) const { return true; }
+  template <typename U>
+  bool operator!=(const BlobAlloc<U>&) const { return false; }
+};
+
+// A stored blob's bytes.
+using Bytes = std::vector<uint8_t, BlobAlloc<uint8_t>>;
+
 // f(i) for i in [0, n) on up to 8 threads: the blob copies of a batch
 // (page faults of fresh host memory and the copy itself) cost ~150 us per
 // 0.9 MB block on one thread, several times the PCIe transfer.
@@ -143,7 +234,7 @@ static int check_ids(const vapi_kv_pool* pool, const uint32_t* ids, uint32_t n, 
 constexpr size_t kMaxInflight = 16;  // asynchronous exports in flight per store
 
 struct vapi_spill_store {
-  Lru<std::vector<uint8_t>> ram;
+  Lru<Bytes> ram;
   uint64_t ram_max = 0, ram_bytes = 0;
   bool has_dir = false;
   fs::path dir;
@@ -190,18 +281,18 @@ struct vapi_spill_store {
   // store recycles its evictions instead). Bounded by kSpareMax bytes and
   // by the host-memory cap.
   static constexpr uint64_t kSpareMax = 256ull << 20;
-  std::vector<std::vector<uint8_t>> spare;
+  std::vector<Bytes> spare;
   uint64_t spare_bytes = 0;
 
-  void recycle(std::vector<uint8_t>&& b) {
+  void recycle(Bytes&& b) {
     if (spare_bytes + b.capacity() > std::min(kSpareMax, ram_max)) return;
     spare_bytes += b.capacity();
     spare.push_back(std::move(b));
   }
 
   // `n` buffers of `len` bytes (contents undefined): recycled ones first.
-  std::vector<std::vector<uint8_t>> buffers(uint32_t n, size_t len) {
-    std::vector<std::vector<uint8_t>> out(n);
+  std::vector<Bytes> buffers(uint32_t n, size_t len) {
+    std::vector<Bytes> out(n);
     for (uint32_t j = 0; j < n && !spare.empty(); ++j) {
       if (spare.back().capacity() < len) break;
       spare_bytes -= spare.back().capacity();
@@ -215,7 +306,7 @@ struct vapi_spill_store {
   // Push host-memory entries out to disk until the cap is met.
   void evict_ram() {
     Hash h;
-    std::vector<uint8_t> bytes;
+    Bytes bytes;
     while (ram_bytes > ram_max && ram.pop_front(h, bytes)) {
       ram_bytes -= bytes.size();
       if (!has_dir || bytes.size() > disk_max) {
@@ -240,7 +331,7 @@ struct vapi_spill_store {
   bool holds(const Hash& h) const { return ram.contains(h) || disk.contains(h); }
 
   // SpillStore::put (spill.rs:128-146), taking the blob's buffer.
-  void put(const Hash& h, std::vector<uint8_t>&& bytes) {
+  void put(const Hash& h, Bytes&& bytes) {
     if (holds(h)) return;
     const uint64_t len = bytes.size();
     if (len > ram_max && len > disk_max) {
@@ -254,7 +345,7 @@ struct vapi_spill_store {
   }
   void put(const Hash& h, const uint8_t* p, size_t len) {
     if (holds(h)) return;
-    put(h, std::vector<uint8_t>(p, p + len));
+    put(h, Bytes(p, p + len));
   }
 
   // The entry's bytes into `out` (capacity `cap`): its length, -1 if not
@@ -302,7 +393,7 @@ struct vapi_spill_store {
       }
       if (force) --force;
       const uint32_t m = (uint32_t)e.hashes.size();
-      std::vector<std::vector<uint8_t>> copies = buffers(m, e.bb);
+      std::vector<Bytes> copies = buffers(m, e.bb);
       parallel_for(m, [&](uint32_t j) {
         if (copies[j].size() == e.bb) std::memcpy(copies[j].data(), e.blobs + (size_t)j * e.bb, e.bb);
         else copies[j].assign(e.blobs + (size_t)j * e.bb, e.blobs + (size_t)(j + 1) * e.bb);
@@ -502,7 +593,7 @@ int64_t vapi_spill_evicted(vapi_spill_store* s, const vapi_kv_pool* pool, const 
     const size_t at = r * per;
     const uint32_t m = (uint32_t)std::min<size_t>(per, todo.size() - at);
     const uint8_t* blobs = stage_blobs(half);
-    std::vector<std::vector<uint8_t>> copies = s->buffers(m, bb);
+    std::vector<Bytes> copies = s->buffers(m, bb);
     parallel_for(m, [&](uint32_t j) {
       if (copies[j].size() == bb) std::memcpy(copies[j].data(), blobs + (size_t)j * bb, bb);
       else copies[j].assign(blobs + (size_t)j * bb, blobs + (size_t)(j + 1) * bb);
@@ -662,14 +753,14 @@ int64_t vapi_spill_promote(vapi_spill_store* s, const vapi_kv_pool* pool, const 
     // the chain there. A hash the store does not hold ends it too (a miss).
     struct Src {
       Hash h;
-      const std::vector<uint8_t>* ram;  // else on disk
+      const Bytes* ram;  // else on disk
       bool ok;
     };
     std::vector<Src> src;
     bool absent = false;
     while (src.size() < per && done + src.size() < n) {
       const Hash h = to_hash(hashes + 32ull * (done + src.size()));
-      const std::vector<uint8_t>* r = s->ram.find(h);
+      const Bytes* r = s->ram.find(h);
       const uint64_t* d = r ? nullptr : s->disk.find(h);
       if (!r && !d) {
         absent = true;
