@@ -239,6 +239,12 @@ CASES = [
     (torch.float32, 8, 8, 40, 16, [33, 1], [700, 1200], None, "HND-bm"),
     (torch.float32, 32, 1, 120, 32, [9, 1], [300, 40], None, "HND"),
     (torch.float32, 6, 2, 4, 16, [12, 1], [40, 300], None, "HND"),
+    # Head dims that end inside the last live d tile of a variant (72 and
+    # 88: tiles 5 and 6 of D = 128 partly zero; f32 68 and 20).
+    (torch.bfloat16, 16, 4, 72, 16, [1, 33, 1], [900, 300, 2000], None, "HND"),
+    (torch.float16, 8, 2, 88, 32, [50, 1], [600, 1500], 200, "NHD-bm"),
+    (torch.float32, 8, 2, 68, 16, [1, 40, 1], [2000, 500, 3000], None, "HND"),
+    (torch.float32, 12, 4, 20, 16, [1, 25], [1800, 400], None, "NHD"),
     # A 16-bit pool the MFMA paths do not take, on the generic kernel:
     # block_size 8.
     (torch.bfloat16, 16, 8, 128, 8, [1, 12], [210, 50], None, "HND"),
