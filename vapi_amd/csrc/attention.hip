@@ -20,10 +20,11 @@ namespace vk {
 
 // The decode's MFMA tile has 16 query-head columns: a group of G > 16
 // query heads per kv head runs as 2^s virtual kv heads of G / 2^s heads
-// each (each reading its pool head's K/V). The shift s, or -1 when G has
-// no such split (G > 64, or not a multiple of 2^s).
+// each (each reading its pool head's K/V). The shift s (at most 3: 8
+// virtual heads, G up to 128), or -1 when G has no such split (G > 128, or
+// not a multiple of 2^s).
 static int decode_group_shift(uint32_t G) {
-  for (int s = 0; s <= 2; ++s)
+  for (int s = 0; s <= 3; ++s)
     if ((G >> s) <= 16 && (G & ((1u << s) - 1)) == 0 && (G >> s) >= 1) return s;
   return -1;
 }
