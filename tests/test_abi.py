@@ -376,6 +376,11 @@ def test_f32_decode_and_wide_groups_size_the_decode_workspace():
     # workspace as 32 heads over two kv heads.
     assert (L.vapi_paged_attention_workspace_size(one, 64, 32, 1, 4096) ==
             L.vapi_paged_attention_workspace_size(two, 64, 32, 1, 4096))
+    # G = 128 on one kv head is decoded as eight kv heads of 16: the same
+    # workspace as 128 heads over eight kv heads.
+    eight = pool(dtype=_lib.BF16, num_kv_heads=8, head_dim=128)
+    assert (L.vapi_paged_attention_workspace_size(one, 64, 128, 1, 4096) ==
+            L.vapi_paged_attention_workspace_size(eight, 64, 128, 1, 4096))
     # G = 17 has no split: the VALU kernel, which needs no decode workspace
     # for short contexts.
     assert L.vapi_paged_attention_workspace_size(one, 64, 17, 1, 64) == 0
