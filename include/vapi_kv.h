@@ -227,8 +227,8 @@ int vapi_kv_gather(const vapi_kv_pool* pool, uint32_t layer,
  *   same way (the f32 prefill's key split is the optional part; a
  *   pure-decode f32 call over at
  *   most 512 keys per sequence and 8,192 in all runs the VALU kernel). On
- *   the VALU path (those small calls, other head dims, groups with no split into parts of at most 16 query
- *   heads, block sizes below 16) it holds the split-context partials and
+ *   the VALU path (those small calls, other head dims, groups of more than 256
+ *   query heads per kv head, block sizes below 16) it holds the split-context partials and
  *   grows with the batch, max_seqlen_q and max_seqlen_k (0 while
  *   max_seqlen_k <= 64; small batches split their keys into chunks of 64
  *   to 512 keys to fill the GPU).

@@ -381,9 +381,15 @@ def test_f32_decode_and_wide_groups_size_the_decode_workspace():
     eight = pool(dtype=_lib.BF16, num_kv_heads=8, head_dim=128)
     assert (L.vapi_paged_attention_workspace_size(one, 64, 128, 1, 4096) ==
             L.vapi_paged_attention_workspace_size(eight, 64, 128, 1, 4096))
-    # G = 17 has no split: the VALU kernel, which needs no decode workspace
-    # for short contexts.
-    assert L.vapi_paged_attention_workspace_size(one, 64, 17, 1, 64) == 0
+    # G = 71 (Falcon-7B's 71 query heads over one kv head) is decoded as five
+    # kv heads of 15 (the last serving 11): the workspace of 75 heads over
+    # five kv heads.
+    five = pool(dtype=_lib.BF16, num_kv_heads=5, head_dim=128)
+    assert (L.vapi_paged_attention_workspace_size(one, 64, 71, 1, 4096) ==
+            L.vapi_paged_attention_workspace_size(five, 64, 75, 1, 4096))
+    # G = 257 has no split into at most 16 parts: the VALU kernel, which
+    # needs no decode workspace for short contexts.
+    assert L.vapi_paged_attention_workspace_size(one, 64, 257, 1, 64) == 0
 
 
 def test_padded_head_dims_size_the_workspace_of_the_next_kernel_dim():

@@ -185,9 +185,9 @@ CASES = [
     (torch.float16, 16, 4, 64, 128, [1, 33, 1], [700, 300, 129], 50, "NHD"),
     (torch.bfloat16, 8, 8, 128, 256, [1, 1, 17], [2000, 257, 600], None, "HND"),
     # More than 16 query heads per kv head: the decode splits each group
-    # into 2, 4 or 8 virtual kv heads of at most 16 (G = 32, 24, 48, 64,
-    # 128, 80, 96); the prefill rows take them as they are. G = 17 has no
-    # such split and runs the generic kernel.
+    # into ceil(G / 16) virtual kv heads of at most 16 (G = 32, 24, 48, 64,
+    # 128, 80, 96; uneven: 17 as 9 + 8, Falcon-7B's 71 as 4 x 15 + 11, 33);
+    # the prefill rows take them as they are.
     (torch.bfloat16, 32, 1, 128, 16, [1, 9, 1], [300, 40, 77], None, "HND"),
     (torch.float16, 48, 2, 64, 16, [1, 1, 20, 1], [700, 2000, 200, 33], 100, "NHD"),
     (torch.bfloat16, 48, 1, 128, 32, [1, 1, 1], [4000, 1, 650], None, "HND"),
@@ -197,6 +197,10 @@ CASES = [
     (torch.float16, 160, 2, 64, 32, [1, 1, 1], [900, 2000, 40], 200, "NHD"),
     (torch.float32, 96, 1, 128, 16, [1, 12], [700, 150], None, "HND"),
     (torch.bfloat16, 80, 1, 80, 16, [1, 1], [1000, 3000], None, "HND-bm"),
+    (torch.bfloat16, 71, 1, 64, 32, [1, 1, 7, 1], [2500, 40, 300, 900], None, "HND"),
+    (torch.float16, 66, 2, 128, 16, [1, 1], [700, 1800], 250, "NHD"),
+    (torch.float32, 71, 1, 64, 16, [1, 1], [600, 1300], None, "HND"),
+    (torch.bfloat16, 200, 1, 96, 16, [1, 3, 1], [900, 50, 2100], None, "HND-bm"),
     # head_dim 256 on the MFMA kernels (one 16-row tile per prefill wave):
     # decode-only batches (G = 4, 1, 8, and 32 as two virtual kv heads) and
     # batches with prefill rows (decode and prefill launched separately).

@@ -19,14 +19,13 @@
 namespace vk {
 
 // The decode's MFMA tile has 16 query-head columns: a group of G > 16
-// query heads per kv head runs as 2^s virtual kv heads of G / 2^s heads
-// each (each reading its pool head's K/V). The shift s (at most 3: 8
-// virtual heads, G up to 128), or -1 when G has no such split (G > 128, or
-// not a multiple of 2^s).
-static int decode_group_shift(uint32_t G) {
-  for (int s = 0; s <= 3; ++s)
-    if ((G >> s) <= 16 && (G & ((1u << s) - 1)) == 0 && (G >> s) >= 1) return s;
-  return -1;
+// query heads per kv head runs as n = ceil(G / 16) virtual kv heads of
+// ceil(G / n) query heads each (the last one may serve fewer), each reading
+// its pool head's K/V. The part count n, or 0 past 16 parts (G > 256).
+static uint32_t decode_group_parts(uint32_t G) {
+  if (G == 0) return 0;
+  const uint32_t n = (G + 15) / 16;
+  return n <= 16 ? n : 0;
 }
 
 // An f32 pool whose calls run on v_mfma_f32_16x16x4_f32: decode rows on the
@@ -48,7 +47,7 @@ static bool f32_mfma_ok(const vapi_kv_pool* p, uint32_t num_heads, uint32_t max_
   if (p->head_dim == 0 || p->head_dim % 4 || p->head_dim > 128) return false;
   if (p->block_size < 16 || (p->block_size & (p->block_size - 1))) return false;
   if (num_heads == 0 || num_heads % p->num_kv_heads) return false;
-  return decode_group_shift(num_heads / p->num_kv_heads) >= 0;
+  return decode_group_parts(num_heads / p->num_kv_heads) > 0;
 }
 
 static bool mfma_ok(const vapi_kv_pool* p, uint32_t num_heads) {
@@ -56,7 +55,7 @@ static bool mfma_ok(const vapi_kv_pool* p, uint32_t num_heads) {
   if (p->head_dim != 64 && p->head_dim != 128 && p->head_dim != 256) return false;
   if (p->block_size < 16 || (p->block_size & (p->block_size - 1))) return false;
   if (num_heads == 0 || num_heads % p->num_kv_heads) return false;
-  return decode_group_shift(num_heads / p->num_kv_heads) >= 0;
+  return decode_group_parts(num_heads / p->num_kv_heads) > 0;
 }
 
 // The decode kernel's D for a pool's head_dim: itself for 64, 128 and 256,
@@ -73,7 +72,7 @@ static bool pad16_ok(const vapi_kv_pool* p, uint32_t num_heads) {
   if (hd == 0 || hd % 8 || hd > 256 || hd == 64 || hd == 128 || hd == 256) return false;
   if (p->block_size < 16 || (p->block_size & (p->block_size - 1))) return false;
   if (num_heads == 0 || num_heads % p->num_kv_heads) return false;
-  return decode_group_shift(num_heads / p->num_kv_heads) >= 0;
+  return decode_group_parts(num_heads / p->num_kv_heads) > 0;
 }
 
 // A 16-bit pool on the MFMA kernels, at its own head_dim or padded.
@@ -84,8 +83,8 @@ static bool mfma16_ok(const vapi_kv_pool* p, uint32_t num_heads) {
 // The decode's view of the kv heads (virtual ones when G > 16).
 static size_t decode_ws_for(const vapi_kv_pool* p, uint32_t batch, uint32_t num_heads) {
   const uint32_t G = num_heads / p->num_kv_heads;
-  const int sh = decode_group_shift(G);
-  return decode_workspace_bytes(batch, p->num_kv_heads << sh, G >> sh, decode_dim(p->head_dim),
+  const uint32_t n = decode_group_parts(G);
+  return decode_workspace_bytes(batch, p->num_kv_heads * n, (G + n - 1) / n, decode_dim(p->head_dim),
                                 decode_num_waves());
 }
 
@@ -462,17 +461,18 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
   a.pf_min_q = 2;
   a.pf_seqs = listed ? pf->seqs : nullptr;
   a.pf_seqs_n = pf_n;
-  a.kv_shift = 0;
+  a.kv_parts = FastDiv(1);
+  a.g_real = a.group;
   a.hd = g.d;
   const hipStream_t s = hs(stream);
   // The decode kernels' arguments: with G > 16 query heads per kv head, the
   // virtual kv heads of at most 16 query heads each.
-  const int gsh = decode_group_shift(a.group);
+  const uint32_t parts = decode_group_parts(a.group);
   AttnArgs dec = a;
-  if (gsh > 0) {
-    dec.kvh = a.kvh << gsh;
-    dec.group = a.group >> gsh;
-    dec.kv_shift = (uint32_t)gsh;
+  if (parts > 1) {
+    dec.kvh = a.kvh * parts;
+    dec.group = (a.group + parts - 1) / parts;
+    dec.kv_parts = FastDiv(parts);
   }
 
   if (mfma16_ok(pool, num_heads)) {
@@ -486,7 +486,7 @@ static int paged_attention_impl(const vapi_kv_pool* pool, uint32_t layer, const 
     // sequence, then still lets a decode and a prefill workgroup share a CU.
     // At head_dim 256 neither kernel fits half a CU's registers; a padded
     // head_dim below 128 runs the padded kernels.)
-    const bool mixed = !skip_decode && !fuse && gsh == 0 && D <= 128 &&
+    const bool mixed = !skip_decode && !fuse && parts == 1 && D <= 128 &&
                        max_seqlen_q > 1 &&
                        pf_n > 0 &&
                        batch <= std::min(decode_max_plan_seqs(), 4000u) &&

@@ -70,10 +70,14 @@ struct AttnArgs {
   // batch - 1); the host names the sequences with prefill rows.
   const uint32_t* pf_seqs;
   uint32_t pf_seqs_n;
-  // decode: more than 16 query heads per kv head run as 2^kv_shift virtual
-  // kv heads of G / 2^kv_shift query heads each (kvh and group then count
-  // the virtual ones); virtual head v reads the K/V of pool head v >> kv_shift.
-  uint32_t kv_shift;
+  // decode: a group of G > 16 query heads per kv head runs as n = kv_parts
+  // virtual kv heads of P = group = ceil(G / n) query heads each (kvh and
+  // group then count the virtual ones; the last part of a group may hold
+  // fewer): virtual head v reads the K/V of pool head v / n and serves query
+  // heads (v / n) G + (v % n) P + c for c < min(P, G - (v % n) P). g_real
+  // is G (n = 1: group).
+  FastDiv kv_parts;
+  uint32_t g_real;
   // The pool's head_dim. The decode also runs head dims that are not a
   // kernel's D (a multiple of 8 up to 256) at the next of 64, 128 or 256:
   // elements d >= hd are loaded as zeros and not stored.

@@ -175,6 +175,17 @@ __device__ __forceinline__ DecodePos next_segment(const AttnArgs& a,
   return p;
 }
 
+// The first query head of virtual kv head v, and how many it serves (the
+// last part of a split group may serve fewer than a.group).
+__device__ __forceinline__ uint32_t vhead_base(const AttnArgs& a, uint32_t v) {
+  const uint32_t kp = a.kv_parts.div(v);
+  return kp * a.g_real + (v - kp * a.kv_parts.d) * a.group;
+}
+__device__ __forceinline__ uint32_t vhead_count(const AttnArgs& a, uint32_t v) {
+  const uint32_t part = v - a.kv_parts.div(v) * a.kv_parts.d;
+  return min(a.group, a.g_real - part * a.group);
+}
+
 // kPad: the pool's head_dim a.hd is below D (its rows are a.hd apart);
 // elements d >= a.hd are zeros.
 template <typename T, int D, bool kPad = false>
@@ -183,9 +194,10 @@ __device__ __forceinline__ void load_q(uint4* qs, const AttnArgs& a, const Decod
   asm volatile("" : "+v"(lane), "+v"(col), "+v"(g));  // see flush_piece
   // MFMA columns past the group carry a copy of the group's first head: their
   // results are computed and never stored.
-  const uint32_t h = col < a.group ? col : 0;
+  const uint32_t h = col < vhead_count(a, p.kh) ? col : 0;
   const uint32_t hd = kPad ? a.hd : (uint32_t)D;
-  const T* qrow = (const T*)a.q + ((uint64_t)p.q0 * a.num_heads + p.kh * a.group + h) * hd;
+  const T* qrow =
+      (const T*)a.q + ((uint64_t)p.q0 * a.num_heads + vhead_base(a, p.kh) + h) * hd;
   if constexpr (sizeof(T) == 4) {
     // f32: D / 16 float4 per lane, Q[h][16c + 4g .. +3] (the f32 MFMA's k
     // order); a negative scale flips the sign bit of every element.
@@ -213,7 +225,7 @@ __device__ __forceinline__ void load_step_k(KTile<D>& st, const AttnArgs& a,
                                             const uint32_t* __restrict__ table,
                                             const DecodePos& p, uint32_t col, uint32_t g) {
   const uint32_t* __restrict__ tab = table + (uint64_t)p.seq * a.max_blocks;
-  const T* kb = (const T*)a.k + (p.kh >> a.kv_shift) * a.head_e;
+  const T* kb = (const T*)a.k + a.kv_parts.div(p.kh) * a.head_e;
   const char* knew =
       p.fuse ? a.k_new + ((uint64_t)p.q0 * a.kvh + p.kh) * D * sizeof(T) : nullptr;
   load_k<T, D, kPad, KCL>(st, tab, kb, a, p.key0, p.len_k - 1, col, g, knew);
@@ -224,7 +236,7 @@ __device__ __forceinline__ void load_step_v(VTile<D>& st, const AttnArgs& a,
                                             const uint32_t* __restrict__ table,
                                             const DecodePos& p, uint32_t col, uint32_t g) {
   const uint32_t* __restrict__ tab = table + (uint64_t)p.seq * a.max_blocks;
-  const T* vb = (const T*)a.v + (p.kh >> a.kv_shift) * a.head_e;
+  const T* vb = (const T*)a.v + a.kv_parts.div(p.kh) * a.head_e;
   const char* vnew =
       p.fuse ? a.v_new + ((uint64_t)p.q0 * a.kvh + p.kh) * D * sizeof(T) : nullptr;
   load_v<T, D, kPad>(st, tab, vb, a, p.key0, p.len_k - 1, col, g, vnew);
@@ -244,11 +256,12 @@ __device__ __forceinline__ void flush_piece(const AttnArgs& a, const DecodePos& 
   // this rarely-taken path's per-lane addresses out of the step loop, where
   // they would pin registers the K/V buffers need.
   asm volatile("" : "+v"(col), "+v"(g));
-  if (col >= G) return;  // lanes of padding columns hold no head
+  if (col >= vhead_count(a, p.kh)) return;  // lanes of padding columns hold no head
+  const uint32_t h0 = vhead_base(a, p.kh);
   if constexpr (sizeof(T) == 4) {
     if (whole) {
       const uint32_t hd = kPad ? a.hd : (uint32_t)D;
-      float* orow = (float*)a.out + ((uint64_t)p.q0 * a.num_heads + p.kh * G + col) * hd;
+      float* orow = (float*)a.out + ((uint64_t)p.q0 * a.num_heads + h0 + col) * hd;
       store_row_f32<D, kPad>(orow, o, l_tot > 0.f ? 1.f / l_tot : 0.f, g, hd);
     } else {
       store_row_f32<D>(a.ws_o + ((uint64_t)slot * G + col) * D, o, 1.f, g);
@@ -258,7 +271,7 @@ __device__ __forceinline__ void flush_piece(const AttnArgs& a, const DecodePos& 
   }
   if (whole) {
     const uint32_t hd = kPad ? a.hd : (uint32_t)D;
-    T* orow = (T*)a.out + ((uint64_t)p.q0 * a.num_heads + p.kh * G + col) * hd;
+    T* orow = (T*)a.out + ((uint64_t)p.q0 * a.num_heads + h0 + col) * hd;
     store_row<T, D, kPad>(orow, o, l_tot > 0.f ? 1.f / l_tot : 0.f, g, hd);
   } else {
     float* po = a.ws_o + ((uint64_t)slot * G + col) * D;
@@ -390,7 +403,7 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
   auto load_halves = [&](KTileF32<D>& kt, VTileF32<D>& vt, const DecodePos& p, int tt)
       __attribute__((always_inline)) {
     load_half_f32<D, true, kPad, DL>(kt.h[tt], vt.h[tt], table + (uint64_t)p.seq * a.max_blocks,
-                     kbf + (p.kh >> a.kv_shift) * a.head_e, vbf + (p.kh >> a.kv_shift) * a.head_e,
+                     kbf + a.kv_parts.div(p.kh) * a.head_e, vbf + a.kv_parts.div(p.kh) * a.head_e,
                      a, p.key0, tt, p.len_k - 1,
                      col, g);
   };
@@ -662,8 +675,13 @@ __device__ __forceinline__ void decode_merge_body(const AttnArgs& a, uint32_t nw
   // not stored; the n outputs from index e of the [G][D] partials are
   // stored one by one (they may span two heads).
   const uint32_t hd = kPad ? a.hd : (uint32_t)D;
-  T* orow = (T*)a.out + ((uint64_t)q0 * a.num_heads + kh * G) * hd;
-  auto store = [&](uint32_t e, uint32_t n, const float (&O)[8], const float (&L)[8]) {
+  T* orow = (T*)a.out + ((uint64_t)q0 * a.num_heads + vhead_base(a, kh)) * hd;
+  // The last part of a split group serves fewer heads: outputs past them
+  // are not stored.
+  const uint32_t e_end = vhead_count(a, kh) * D;
+  auto store = [&](uint32_t e, uint32_t n_all, const float (&O)[8], const float (&L)[8]) {
+    if (e >= e_end) return;
+    const uint32_t n = min(n_all, e_end - e);
     if constexpr (kPad) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
