@@ -581,33 +581,43 @@ def bench_decode_block_size_32(steps, warmup):
 
 
 def bench_wide_group(steps, warmup):
-    """Config 2's batch with 64 query heads over 2 kv heads (32 query heads
-    per kv head: the decode runs each group as two virtual kv heads of 16,
-    each reading the group's K/V) on a bf16 pool: K/V bytes are a quarter of
-    config 2's."""
+    """Config 2's batch with more than 16 query heads per kv head on bf16
+    pools: 64 q over 2 kv heads (G = 32: two virtual kv heads of 16 per
+    group), 48 q over 1 (G = 48: three of 16) and 71 q over 1 (Falcon-7B's
+    G = 71: four of 15 and one of 11). Each virtual kv head reads its
+    group's K/V, so K/V are read ceil(G / 16) times; GB/s count them once."""
     w = workload.config2_decode()
-    cache = PagedKvCache(DECODE_LAYERS, w.num_blocks, w.block_size, 2, 128, torch.bfloat16,
-                         "HND")
-    workload.fill_normal(cache._slab, workload.seed_for(2))
-    q = torch.randn(w.batch, 64, 128, device=DEV).to(torch.bfloat16)
-    batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
-                         block_tables=[t.tolist() for t in w.tables], max_seqlen_q=1,
-                         max_seqlen_k=int(w.lens.max()))
-    prep = PreparedAttention.from_batch(batch, DEV)
-    out = torch.empty_like(q)
-    turn = [0]
+    res = {}
+    for hq, kvh in ((64, 2), (48, 1), (71, 1)):
+        G = hq // kvh
+        parts = (G + 15) // 16
+        cache = PagedKvCache(DECODE_LAYERS, w.num_blocks, w.block_size, kvh, 128, torch.bfloat16,
+                             "HND")
+        workload.fill_normal(cache._slab, workload.seed_for(2))
+        q = torch.randn(w.batch, hq, 128, device=DEV).to(torch.bfloat16)
+        batch = ForwardBatch(cu_seqlens_q=w.cu_q().tolist(), cu_seqlens_k=w.cu_k().tolist(),
+                             block_tables=[t.tolist() for t in w.tables], max_seqlen_q=1,
+                             max_seqlen_k=int(w.lens.max()))
+        prep = PreparedAttention.from_batch(batch, DEV)
+        out = torch.empty_like(q)
+        turn = [0]
 
-    def call():
-        paged_attention_prepared(q, cache, turn[0] % DECODE_LAYERS, prep, 128 ** -0.5, out=out)
-        turn[0] += 1
+        def call():
+            paged_attention_prepared(q, cache, turn[0] % DECODE_LAYERS, prep, 128 ** -0.5,
+                                     out=out)
+            turn[0] += 1
 
-    gms = timed_graph(call, steps, warmup)
-    kv = int(w.lens.sum()) * 2 * 2 * 128 * 2
-    log(f"decode cfg2 batch, 64 q / 2 kv heads (G = 32): {gms * 1e3:.1f} us, "
-        f"{kv / (gms * 1e-3) / 1e9:.0f} GB/s of unique K/V (each group's K/V read twice)")
-    del cache, q, out
-    return dict(us=gms * 1e3, kv_bytes=kv, gbs_unique_kv=kv / (gms * 1e-3) / 1e9,
-                gbs_read=2 * kv / (gms * 1e-3) / 1e9)
+        gms = timed_graph(call, steps, warmup)
+        kv = int(w.lens.sum()) * kvh * 2 * 128 * 2
+        log(f"decode cfg2 batch, {hq} q / {kvh} kv heads (G = {G}, {parts} parts): "
+            f"{gms * 1e3:.1f} us, {kv / (gms * 1e-3) / 1e9:.0f} GB/s of unique K/V "
+            f"({parts * kv / (gms * 1e-3) / 1e9:.0f} GB/s read)")
+        res[f"g{G}"] = dict(us=gms * 1e3, kv_bytes=kv, parts=parts,
+                            gbs_unique_kv=kv / (gms * 1e-3) / 1e9,
+                            gbs_read=parts * kv / (gms * 1e-3) / 1e9)
+        del cache, q, out
+    torch.cuda.empty_cache()
+    return res
 
 
 def bench_head_dim_256(steps, warmup):
