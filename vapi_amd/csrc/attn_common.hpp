@@ -148,16 +148,16 @@ template <int DPL>
 struct VRow {
   uint32_t w[DPL / 2];
 };
-template <int DPL>
+template <int DPL, bool kNt = true>
 __device__ __forceinline__ VRow<DPL> load_vrow(const void* p) {
   VRow<DPL> r;
   if constexpr (DPL == 4) {
-    const uint2 x = load_stream((const uint2*)p);
+    const uint2 x = load_kv<kNt>((const uint2*)p);
     r.w[0] = x.x; r.w[1] = x.y;
   } else {
 #pragma unroll
     for (int i = 0; i < DPL / 8; ++i) {
-      const uint4 x = load_stream((const uint4*)p + i);
+      const uint4 x = load_kv<kNt>((const uint4*)p + i);
       r.w[4 * i] = x.x; r.w[4 * i + 1] = x.y; r.w[4 * i + 2] = x.z; r.w[4 * i + 3] = x.w;
     }
   }
@@ -249,7 +249,9 @@ __device__ __forceinline__ const char* tile_base(const uint32_t* __restrict__ ta
 // read from there instead of the pool: a per-lane address select, no branch.
 // KCL: the 32-column chunks of K that are loaded (the rest, padding, are
 // left as they were; fewer than D / 32 only with kPad).
-template <typename T, int D, bool kPad = false, int KCL = D / 32>
+// kNt: streaming loads (each tile is read once per call); ordinary ones
+// when the virtual kv heads of a split group read the same tiles.
+template <typename T, int D, bool kPad = false, int KCL = D / 32, bool kNt = true>
 __device__ __forceinline__ void load_k(KTile<D>& st, const uint32_t* __restrict__ tab,
                                        const T* kb, const AttnArgs& a, int32_t s0, int32_t last,
                                        uint32_t col, uint32_t g, const char* knew = nullptr) {
@@ -263,10 +265,10 @@ __device__ __forceinline__ void load_k(KTile<D>& st, const uint32_t* __restrict_
 #pragma unroll
     for (int c = 0; c < KCL; ++c) {
       if constexpr (kPad)
-        st.k[tt][c] = 32 * c + 8 * g < a.hd ? load_stream((const uint4*)(src + 64u * c))
+        st.k[tt][c] = 32 * c + 8 * g < a.hd ? load_kv<kNt>((const uint4*)(src + 64u * c))
                                              : make_uint4(0u, 0u, 0u, 0u);
       else
-        st.k[tt][c] = load_stream((const uint4*)(src + 64u * c));
+        st.k[tt][c] = load_kv<kNt>((const uint4*)(src + 64u * c));
     }
   }
 }
@@ -282,7 +284,7 @@ __host__ __device__ constexpr uint32_t v_d(uint32_t m, int k) {
 template <int D>
 __host__ __device__ constexpr uint32_t v_col0(uint32_t m) { return v_d<D>(m, 0); }
 
-template <typename T, int D, bool kPad = false>
+template <typename T, int D, bool kPad = false, bool kNt = true>
 __device__ __forceinline__ void load_v(VTile<D>& st, const uint32_t* __restrict__ tab,
                                        const T* vb, const AttnArgs& a, int32_t s0, int32_t last,
                                        uint32_t col, uint32_t g, const char* vnew = nullptr) {
@@ -302,21 +304,21 @@ __device__ __forceinline__ void load_v(VTile<D>& st, const uint32_t* __restrict_
         // Two 16-byte runs, d = 8 col .. +7 and 128 + 8 col .. +7: each load
         // instruction then reads whole 256-byte rows across the 16 lanes.
         const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-        const uint4 x0 = !kPad || v_d<D>(col, 0) < a.hd ? load_stream((const uint4*)src) : z;
+        const uint4 x0 = !kPad || v_d<D>(col, 0) < a.hd ? load_kv<kNt>((const uint4*)src) : z;
         const uint4 x1 = !kPad || v_d<D>(col, 8) < a.hd
-                             ? load_stream((const uint4*)(src + 128 * sizeof(T))) : z;
+                             ? load_kv<kNt>((const uint4*)(src + 128 * sizeof(T))) : z;
         VRow<DPL>& w = st.v[4 * tt + i];
         w.w[0] = x0.x, w.w[1] = x0.y, w.w[2] = x0.z, w.w[3] = x0.w;
         w.w[4] = x1.x, w.w[5] = x1.y, w.w[6] = x1.z, w.w[7] = x1.w;
       } else if constexpr (kPad) {
         if (v_col0<D>(col) < a.hd) {
-          st.v[4 * tt + i] = load_vrow<DPL>(src);
+          st.v[4 * tt + i] = load_vrow<DPL, kNt>(src);
         } else {
 #pragma unroll
           for (int w = 0; w < DPL / 2; ++w) st.v[4 * tt + i].w[w] = 0u;
         }
       } else {
-        st.v[4 * tt + i] = load_vrow<DPL>(src);
+        st.v[4 * tt + i] = load_vrow<DPL, kNt>(src);
       }
     }
   }

@@ -3,12 +3,30 @@
 
 namespace vk {
 
-template <typename T, int D, bool kFuse, bool kPad = false, int DL = D / 16>
+template <typename T, int D, bool kFuse, bool kPad = false, int DL = D / 16, bool kNt = true>
 __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged_decode_stream(
     AttnArgs a, const uint32_t* __restrict__ cu_q, const uint32_t* __restrict__ cu_k,
     const uint32_t* __restrict__ table) {
   extern __shared__ uint32_t P[];
-  decode_stream_body<T, D, kFuse, kPad, DL>(a, cu_q, cu_k, table, P, blockIdx.x, gridDim.x);
+  decode_stream_body<T, D, kFuse, kPad, DL, kNt>(a, cu_q, cu_k, table, P, blockIdx.x,
+                                                 gridDim.x);
+}
+
+// The stream launch: a group split into virtual kv heads (no fused append,
+// all d tiles live) reads K/V with ordinary loads, its parts sharing the
+// tiles through L2 (config 2's batch at G = 48: 67.5 -> 56.7 us; G = 71:
+// 102.2 -> 85.7 us); every other call with streaming loads.
+template <typename T, int D, bool F, bool PAD, int DL>
+static void launch_stream(const AttnArgs& c, uint32_t nwg, size_t lds, hipStream_t s) {
+  if constexpr (!F && DL == D / 16) {
+    if (c.kv_parts.d > 1) {
+      hipLaunchKernelGGL((paged_decode_stream<T, D, F, PAD, DL, false>), dim3(nwg),
+                         dim3(64 * kDecodeWavesPerWG), lds, s, c, c.cu_q, c.cu_k, c.table);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((paged_decode_stream<T, D, F, PAD, DL, true>), dim3(nwg),
+                     dim3(64 * kDecodeWavesPerWG), lds, s, c, c.cu_q, c.cu_k, c.table);
 }
 
 // Waves per segment of a merge with a workgroup per segment: 8 for at most
@@ -143,8 +161,7 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t dtyp
     const size_t lds = (nb + 1 + (fuse ? nb : 0)) * sizeof(uint32_t);
 #define VK_DECL(T, DD, F, PAD, DL)                                                              \
   do {                                                                                          \
-    hipLaunchKernelGGL((paged_decode_stream<T, DD, F, PAD, DL>), dim3(nwg),                     \
-                       dim3(64 * kDecodeWavesPerWG), lds, s, c, c.cu_q, c.cu_k, c.table);      \
+    launch_stream<T, DD, F, PAD, DL>(c, nwg, lds, s);                                           \
     if (wide && nb * c.kvh <= kFewSegs)                                                        \
       hipLaunchKernelGGL((paged_decode_merge<T, DD, F, 8, PAD>), dim3(merge_wgs + copy_wgs),    \
                          dim3(merge_threads(8)), 0, s, c, nwg, merge_wgs);                      \

@@ -220,7 +220,7 @@ __device__ __forceinline__ void load_q(uint4* qs, const AttnArgs& a, const Decod
   }
 }
 
-template <typename T, int D, bool kPad = false, int KCL = D / 32>
+template <typename T, int D, bool kPad = false, int KCL = D / 32, bool kNt = true>
 __device__ __forceinline__ void load_step_k(KTile<D>& st, const AttnArgs& a,
                                             const uint32_t* __restrict__ table,
                                             const DecodePos& p, uint32_t col, uint32_t g) {
@@ -228,10 +228,10 @@ __device__ __forceinline__ void load_step_k(KTile<D>& st, const AttnArgs& a,
   const T* kb = (const T*)a.k + a.kv_parts.div(p.kh) * a.head_e;
   const char* knew =
       p.fuse ? a.k_new + ((uint64_t)p.q0 * a.kvh + p.kh) * D * sizeof(T) : nullptr;
-  load_k<T, D, kPad, KCL>(st, tab, kb, a, p.key0, p.len_k - 1, col, g, knew);
+  load_k<T, D, kPad, KCL, kNt>(st, tab, kb, a, p.key0, p.len_k - 1, col, g, knew);
 }
 
-template <typename T, int D, bool kPad = false>
+template <typename T, int D, bool kPad = false, bool kNt = true>
 __device__ __forceinline__ void load_step_v(VTile<D>& st, const AttnArgs& a,
                                             const uint32_t* __restrict__ table,
                                             const DecodePos& p, uint32_t col, uint32_t g) {
@@ -239,7 +239,7 @@ __device__ __forceinline__ void load_step_v(VTile<D>& st, const AttnArgs& a,
   const T* vb = (const T*)a.v + a.kv_parts.div(p.kh) * a.head_e;
   const char* vnew =
       p.fuse ? a.v_new + ((uint64_t)p.q0 * a.kvh + p.kh) * D * sizeof(T) : nullptr;
-  load_v<T, D, kPad>(st, tab, vb, a, p.key0, p.len_k - 1, col, g, vnew);
+  load_v<T, D, kPad, kNt>(st, tab, vb, a, p.key0, p.len_k - 1, col, g, vnew);
 }
 
 
@@ -290,8 +290,11 @@ __device__ __forceinline__ void flush_piece(const AttnArgs& a, const DecodePos& 
 // per-sequence fused-append flags FZ (batch).
 // DL: the 16-column d tiles that hold head_dim (kPad; D / 16 otherwise):
 // K chunks past them are neither loaded nor multiplied (V and O keep D: a
-// lane's V values spread over every d tile).
-template <typename T, int D, bool kFuse, bool kPad = false, int DL = D / 16>
+// lane's V values spread over every d tile). kNt: K/V read with streaming
+// loads; ordinary ones for a group split into virtual kv heads, whose
+// parts read the same tiles at about the same time on one XCD (the plan
+// puts a pool head's parts side by side), so all but the first hit in L2.
+template <typename T, int D, bool kFuse, bool kPad = false, int DL = D / 16, bool kNt = true>
 __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
                                                    const uint32_t* __restrict__ cu_q,
                                                    const uint32_t* __restrict__ cu_k,
@@ -402,7 +405,7 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
   const float* vbf = (const float*)a.v;
   auto load_halves = [&](KTileF32<D>& kt, VTileF32<D>& vt, const DecodePos& p, int tt)
       __attribute__((always_inline)) {
-    load_half_f32<D, true, kPad, DL>(kt.h[tt], vt.h[tt], table + (uint64_t)p.seq * a.max_blocks,
+    load_half_f32<D, kNt, kPad, DL>(kt.h[tt], vt.h[tt], table + (uint64_t)p.seq * a.max_blocks,
                      kbf + a.kv_parts.div(p.kh) * a.head_e, vbf + a.kv_parts.div(p.kh) * a.head_e,
                      a, p.key0, tt, p.len_k - 1,
                      col, g);
@@ -411,8 +414,8 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
     load_halves(kA, vA, pos, 0);
     load_halves(kA, vA, pos, 1);
   } else {
-    load_step_k<T, D, kPad, KCL>(kA, a, table, pos, col, g);
-    load_step_v<T, D, kPad>(vA, a, table, pos, col, g);
+    load_step_k<T, D, kPad, KCL, kNt>(kA, a, table, pos, col, g);
+    load_step_v<T, D, kPad, kNt>(vA, a, table, pos, col, g);
   }
 
   // One step: find the next step, issue its K and V, attend over the current
@@ -461,8 +464,8 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
         load_halves(kn, vn, nxt, tt);
       }
     } else {
-      load_step_k<T, D, kPad, KCL>(kn, a, table, nxt, col, g);
-      load_step_v<T, D, kPad>(vn, a, table, nxt, col, g);
+      load_step_k<T, D, kPad, KCL, kNt>(kn, a, table, nxt, col, g);
+      load_step_v<T, D, kPad, kNt>(vn, a, table, nxt, col, g);
       uint4 qf[D / 32];
 #pragma unroll
       for (int c = 0; c < D / 32; ++c) qf[c] = qs[c * 64 + lane];

@@ -156,6 +156,14 @@ __device__ __forceinline__ V load_stream(const V* p) {
   }
 }
 
+// load_stream when kNt, else an ordinary (cached) load: data that other
+// waves on the same XCD read again at about the same time.
+template <bool kNt, typename V>
+__device__ __forceinline__ V load_kv(const V* p) {
+  if constexpr (kNt) return load_stream(p);
+  else return *p;
+}
+
 // 16-bit float storage types as raw bits.
 struct bf16_t { uint16_t x; };
 struct f16_t { uint16_t x; };
