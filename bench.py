@@ -1401,8 +1401,9 @@ def main():
     extras["mixed_step_cfg2"] = bench_mixed_step(dec, args.steps, args.warmup)
     # Block copy, swap and spill run before the other extras: run after
     # them in one process, the swap's host-to-device rate fell to ~31 GB/s
-    # (55.6 alone or first), while a 1 GiB pinned probe allocated after the
-    # swap's 3.76 GB source still read at 57 GB/s; the cause was not found.
+    # (55.6 alone or first; some full runs still read ~31), while a 1 GiB
+    # pinned probe allocated after the swap's 3.76 GB source read at 57
+    # GB/s; the cause was not found.
     extras["blocks_cfg4"] = bench_blocks(max(args.steps // 5, 3), 2, dec)
     if args.only in (None,):
         extras["append_cfg1"] = bench_append(args.steps, args.warmup)
