@@ -13,9 +13,10 @@ __global__ __launch_bounds__(64 * kDecodeWavesPerWG, kDecodeWGsPerCU) void paged
 }
 
 // The stream launch: a group split into virtual kv heads (no fused append,
-// all d tiles live) reads K/V with ordinary loads, its parts sharing the
-// tiles through L2 (config 2's batch at G = 48: 67.5 -> 56.7 us; G = 71:
-// 102.2 -> 85.7 us); every other call with streaming loads.
+// all d tiles live) reads K/V with ordinary loads, its parts (neighbouring
+// waves on one range of steps) sharing the tiles through L2 (config 2's
+// batch at G = 48: 67.5 us with streaming loads, 51.5 us so; G = 71: 102.2
+// and 74.0 us); every other call with streaming loads.
 template <typename T, int D, bool F, bool PAD, int DL>
 static void launch_stream(const AttnArgs& c, uint32_t nwg, size_t lds, hipStream_t s) {
   if constexpr (!F && DL == D / 16) {

@@ -121,9 +121,13 @@ struct DecodePos {
   uint32_t fuse;       // fused append: key len_k - 1 is read from the new rows
 };
 
+// kvh_plan: the kv heads the step order counts (a.kvh, or with a split
+// group's parts side by side the pool heads: then the position is part
+// `part` of pool head kp, virtual head kp * n + part).
 __device__ __forceinline__ DecodePos locate(const AttnArgs& a, const uint32_t* __restrict__ cu_q,
                                             const uint32_t* __restrict__ cu_k, const uint32_t* P,
-                                            const uint32_t* FZ, uint32_t t) {
+                                            const uint32_t* FZ, uint32_t t,
+                                            uint32_t kvh_plan, uint32_t n, uint32_t part) {
   uint32_t lo_i = 0, hi_i = a.batch;  // P[lo_i] <= t < P[hi_i]
   while (hi_i - lo_i > 1) {
     const uint32_t mid = (lo_i + hi_i) >> 1;
@@ -133,10 +137,11 @@ __device__ __forceinline__ DecodePos locate(const AttnArgs& a, const uint32_t* _
   DecodePos p;
   p.seq = lo_i;
   const uint32_t p0 = __builtin_amdgcn_readfirstlane(P[lo_i]);
-  const uint32_t nst = (__builtin_amdgcn_readfirstlane(P[lo_i + 1]) - p0) / a.kvh;
+  const uint32_t nst = (__builtin_amdgcn_readfirstlane(P[lo_i + 1]) - p0) / kvh_plan;
   const uint32_t local = t - p0;
-  p.kh = local / nst;
-  const uint32_t ks = local - p.kh * nst;
+  const uint32_t kp = local / nst;
+  p.kh = kp * n + part;
+  const uint32_t ks = local - kp * nst;
   p.q0 = cu_q[p.seq];
   p.len_k = (int32_t)(cu_k[p.seq + 1] - cu_k[p.seq]);
   p.lo = a.wl >= 0 ? max(0, p.len_k - 1 - a.wl) : 0;
@@ -154,17 +159,18 @@ __device__ __forceinline__ DecodePos next_segment(const AttnArgs& a,
                                                   const uint32_t* __restrict__ cu_q,
                                                   const uint32_t* __restrict__ cu_k,
                                                   const uint32_t* P, const uint32_t* FZ,
-                                                  const DecodePos& cur) {
+                                                  const DecodePos& cur, uint32_t n) {
+  // With n > 1 a wave walks one part of each pool head: kh steps by n.
   DecodePos p = cur;
-  if (cur.kh + 1 < a.kvh) {
-    p.kh = cur.kh + 1;
+  if (cur.kh + n < a.kvh) {
+    p.kh = cur.kh + n;
   } else {
     uint32_t s = cur.seq + 1;
     while (s + 1 < a.batch && __builtin_amdgcn_readfirstlane(P[s + 1]) ==
                                   __builtin_amdgcn_readfirstlane(P[s]))
       ++s;  // sequences without decode steps
     p.seq = s;
-    p.kh = 0;
+    p.kh = cur.kh % n;
     p.q0 = cu_q[s];
     p.len_k = (int32_t)(cu_k[s + 1] - cu_k[s]);
     p.lo = a.wl >= 0 ? max(0, p.len_k - 1 - a.wl) : 0;
@@ -307,6 +313,11 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
   const uint32_t lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t B = a.batch;
+  // A group split into n virtual kv heads: steps are counted per pool
+  // head, each of n neighbouring waves walking one part (n = 1: the
+  // virtual heads are the pool's).
+  const uint32_t n_parts = a.kv_parts.d;
+  const uint32_t kvh_plan = a.kvh / n_parts;
   // The shared 100 MHz clock at entry: XCDs start the grid up to ~2.5 us
   // apart, and the shares account for it.
   const uint32_t t_entry = (uint32_t)__builtin_amdgcn_s_memrealtime();
@@ -317,7 +328,7 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
     const uint32_t per = (B + NT - 1) / NT;
     const uint32_t b0 = min(tid * per, B), b1 = min(b0 + per, B);
     uint32_t sum = 0;
-    for (uint32_t s = b0; s < b1; ++s) sum += decode_steps(a, cu_q, cu_k, s) * a.kvh;
+    for (uint32_t s = b0; s < b1; ++s) sum += decode_steps(a, cu_q, cu_k, s) * kvh_plan;
     uint32_t inc = sum;  // inclusive scan within the wave
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -331,7 +342,7 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
     for (uint32_t s = b0; s < b1; ++s) {
       P[s] = run;
       const uint32_t ns = decode_steps(a, cu_q, cu_k, s);
-      run += ns * a.kvh;
+      run += ns * kvh_plan;
       if (kFuse) {
         // The row's new key (position len_k - 1) comes from token cu_q[s]
         // of the new rows if that token's slot is the one the block table
@@ -361,9 +372,18 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
   const uint32_t x = bid % kGroups;
   const uint32_t j = (bid / kGroups) * kDecodeWavesPerWG + wave;
   const uint32_t len = F[x + 1] - F[x], nw = group_waves(nwg, x);
-  const uint32_t t_begin = F[x] + (uint32_t)(((uint64_t)j * len) / nw);
-  const uint32_t t_end = F[x] + (uint32_t)(((uint64_t)(j + 1) * len) / nw);
-  const uint32_t r = group_offset(nwg, x) + j;
+  // The group's waves form ranges of n consecutive waves, wave j taking
+  // part j % n of range j / n (waves past the last whole range idle), so
+  // the parts of a pool head's steps are read at once, by neighbouring
+  // waves of one XCD. A piece's partial slot is r n + (virtual segment):
+  // r + (pool segment) is distinct for every piece of one part, as in the
+  // unsplit order, so the slots of all parts are too.
+  const uint32_t nr = nw / n_parts;
+  const uint32_t jr = j / n_parts;
+  const uint32_t part = j - jr * n_parts;
+  const uint32_t t_begin = jr < nr ? F[x] + (uint32_t)(((uint64_t)jr * len) / nr) : S;
+  const uint32_t t_end = jr < nr ? F[x] + (uint32_t)(((uint64_t)(jr + 1) * len) / nr) : S;
+  const uint32_t r = group_offset(nwg, x) / n_parts + jr;
   const uint32_t gw = bid * kDecodeWavesPerWG + wave;
   uint32_t* stat = a.bal + kBalStats + kStatWords * gw;
   if (t_begin >= t_end) {
@@ -371,8 +391,8 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
     // An empty slice between the first and last range of a segment: its
     // partial slot is marked empty (l = 0) for the merge.
     if (t_begin < S) {
-      const DecodePos p = locate(a, cu_q, cu_k, P, FZ, t_begin);
-      const uint64_t slot = r + p.seq * a.kvh + p.kh;
+      const DecodePos p = locate(a, cu_q, cu_k, P, FZ, t_begin, kvh_plan, n_parts, part);
+      const uint64_t slot = (uint64_t)r * n_parts + p.seq * a.kvh + p.kh;
       if (lane < a.group) *(float2*)(a.ws_ml + (slot * a.group + lane) * 2) = make_float2(kNegBig, 0.f);
     }
     return;
@@ -380,7 +400,7 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
 
   uint32_t t = t_begin;
   const uint32_t col = lane & 15, g = lane >> 4;
-  DecodePos pos = locate(a, cu_q, cu_k, P, FZ, t);
+  DecodePos pos = locate(a, cu_q, cu_k, P, FZ, t, kvh_plan, n_parts, part);
   // The Q^T operand of the current segment lives in LDS (read back every
   // step) to keep the K/V buffers in registers.
   constexpr bool kF32 = sizeof(T) == 4;
@@ -437,7 +457,7 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
       nxt.key0 += 32;
       nxt.seg_first = false;
     } else if (more) {
-      nxt = next_segment(a, cu_q, cu_k, P, FZ, pos);
+      nxt = next_segment(a, cu_q, cu_k, P, FZ, pos, n_parts);
     } else {
       nxt.seq = 0;
       nxt.key0 = 0;
@@ -481,7 +501,8 @@ __device__ __forceinline__ void decode_stream_body(const AttnArgs& a,
         if (piece_first) a.seg_ranges[2 * seg] = r;
         if (seg_ends) a.seg_ranges[2 * seg + 1] = r;
       }
-      flush_piece<T, D, kPad>(a, pos, piece_first && seg_ends, r + seg, o, m_run, l_run, col, g);
+      flush_piece<T, D, kPad>(a, pos, piece_first && seg_ends, r * n_parts + seg, o, m_run, l_run,
+                              col, g);
       if (!more) return false;
       m_run = kNegBig;
       l_run = 0.f;
@@ -715,7 +736,7 @@ __device__ __forceinline__ void decode_merge_body(const AttnArgs& a, uint32_t nw
       for (int u = 0; u < R; ++u) {
         const uint32_t pc = w + u * WPS;
         const bool in = pc <= r1;
-        const uint64_t sl = (uint64_t)(pc + seg) * G;
+        const uint64_t sl = ((uint64_t)pc * a.kv_parts.d + seg) * G;
         const float* po = a.ws_o + sl * D + e_lane + j0;
         if (in && n == 8) {
           const float4 v0 = *(const float4*)po, v1 = *(const float4*)(po + 4);
