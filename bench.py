@@ -1413,7 +1413,7 @@ def main():
         extras["prefill_cfg3"] = bench_prefill(max(args.steps, 10), 30)
         extras["f32_attention"] = bench_valu(args.steps, args.warmup)
         extras["head_dim_64"] = bench_head_dim_64(args.steps, args.warmup)
-        extras["wide_group_g32"] = bench_wide_group(args.steps, args.warmup)
+        extras["wide_groups"] = bench_wide_group(args.steps, args.warmup)
         extras["head_dim_256"] = bench_head_dim_256(args.steps, args.warmup)
         extras["decode_cfg2_block_major"] = bench_decode_block_major(args.steps, args.warmup)
         extras["decode_cfg2_block_size_32"] = bench_decode_block_size_32(args.steps, args.warmup)
