@@ -22,7 +22,8 @@
 // A wave's run of steps within one segment is a piece. A piece covering a
 // whole segment writes the normalised output; the first and last piece of a
 // slice may be partial and write (m, l, o) to slot range + segment (ranges
-// and segments are both numbered in step order, so slots are unique), and
+// and segments are both numbered in step order, so slots are unique; with a
+// group split into n parts, range x n + virtual segment), and
 // paged_decode_merge combines them: one wave per split segment, or, when a
 // launch has at most 256 segments (each then split into many pieces), one
 // workgroup per segment whose waves share its pieces. Each
