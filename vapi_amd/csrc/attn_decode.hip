@@ -40,8 +40,9 @@ constexpr uint32_t merge_threads(int wps) { return 64u * (wps > (int)kMergeWaves
 
 template <typename T, int D, bool kFuse, int WPS, bool kPad = false>
 __global__ __launch_bounds__(merge_threads(WPS)) void paged_decode_merge(AttnArgs a, uint32_t nwg,
-                                                                      uint32_t merge_wgs) {
-  decode_merge_body<T, D, kFuse, WPS, kPad>(a, nwg, merge_wgs, blockIdx.x, gridDim.x);
+                                                                      uint32_t merge_wgs,
+                                                                      uint32_t ns) {
+  decode_merge_body<T, D, kFuse, WPS, kPad>(a, nwg, merge_wgs, blockIdx.x, gridDim.x, ns);
 }
 
 uint32_t decode_num_waves() {
@@ -103,14 +104,14 @@ void launch_decode_merge(const AttnArgs& c, uint32_t nwg, uint32_t head_dim, boo
   do {                                                                                       \
     if (wide && c.batch * c.kvh <= kFewSegs)                                                 \
       hipLaunchKernelGGL((paged_decode_merge<T, DD, false, 8, PAD>), dim3(merge_wgs),        \
-                         dim3(merge_threads(8)), 0, s, c, nwg, merge_wgs);                   \
+                         dim3(merge_threads(8)), 0, s, c, nwg, merge_wgs, 1u);               \
     else if (wide)                                                                           \
       hipLaunchKernelGGL((paged_decode_merge<T, DD, false, kMergeWaves, PAD>),               \
                          dim3(merge_wgs), dim3(merge_threads(kMergeWaves)), 0, s, c, nwg,    \
-                         merge_wgs);                                                         \
+                         merge_wgs, 1u);                                                     \
     else                                                                                     \
       hipLaunchKernelGGL((paged_decode_merge<T, DD, false, 1, PAD>), dim3(merge_wgs),        \
-                         dim3(64 * kMergeWaves), 0, s, c, nwg, merge_wgs);                   \
+                         dim3(64 * kMergeWaves), 0, s, c, nwg, merge_wgs, 1u);               \
   } while (0)
   // A head_dim below the kernel's D: the padded merge.
   const bool pad = c.hd != head_dim;
@@ -153,7 +154,12 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t dtyp
     const bool fuse = a.k_new != nullptr;
     // Few segments (each split over many waves): a workgroup per segment.
     bool wide = false;
-    const uint32_t merge_wgs = decode_merge_wgs(nb, a.kvh, &wide);
+    // Wide groups merge in slices of at most 8 outputs per lane: config 2's
+    // batch at G = 32 (two parts of 16) 66.3 -> 58.5 us per call, G = 48
+    // 51.5 -> 41.0, G = 71 74.0 -> 54.4; at head_dim 256 (G = 4, two slices)
+    // 251.8 -> 248.6; config 2 itself (8 outputs per lane) unchanged.
+    const uint32_t ns = decode_merge_slices(a.group, head_dim);
+    const uint32_t merge_wgs = decode_merge_wgs(nb, a.kvh, &wide, ns);
     uint32_t copy_wgs = 0;
     if (fuse && b0 == 0) {
       const uint64_t chunks = 2ull * a.n_new * a.kvh * (head_dim / 8);
@@ -165,14 +171,14 @@ void launch_decode(AttnArgs a, void* workspace, uint32_t head_dim, uint32_t dtyp
     launch_stream<T, DD, F, PAD, DL>(c, nwg, lds, s);                                           \
     if (wide && nb * c.kvh <= kFewSegs)                                                        \
       hipLaunchKernelGGL((paged_decode_merge<T, DD, F, 8, PAD>), dim3(merge_wgs + copy_wgs),    \
-                         dim3(merge_threads(8)), 0, s, c, nwg, merge_wgs);                      \
+                         dim3(merge_threads(8)), 0, s, c, nwg, merge_wgs, ns);                  \
     else if (wide)                                                                              \
       hipLaunchKernelGGL((paged_decode_merge<T, DD, F, kMergeWaves, PAD>),                      \
                          dim3(merge_wgs + copy_wgs), dim3(merge_threads(kMergeWaves)), 0, s, c, \
-                         nwg, merge_wgs);                                                       \
+                         nwg, merge_wgs, ns);                                                   \
     else                                                                                        \
       hipLaunchKernelGGL((paged_decode_merge<T, DD, F, 1, PAD>), dim3(merge_wgs + copy_wgs),    \
-                         dim3(64 * kMergeWaves), 0, s, c, nwg, merge_wgs);                      \
+                         dim3(64 * kMergeWaves), 0, s, c, nwg, merge_wgs, ns);                  \
   } while (0)
 #define VK_DECP(T, DD, F, PAD) VK_DECL(T, DD, F, PAD, DD / 16)
 #define VK_DEC(T, DD, F) VK_DECP(T, DD, F, false)

@@ -660,7 +660,7 @@ __device__ __forceinline__ void store_outputs(T* dst, uint32_t n, const float (&
 template <typename T, int D, bool kFuse, int WPS, bool kPad = false>
 __device__ __forceinline__ void decode_merge_body(const AttnArgs& a, uint32_t nwg,
                                                   uint32_t merge_wgs, uint32_t bid,
-                                                  uint32_t nbid) {
+                                                  uint32_t nbid, uint32_t ns = 1) {
   static_assert(WPS == 1 || WPS >= (int)kMergeWaves, "a wave or a workgroup per segment");
   if constexpr (kFuse) {
     if (bid >= merge_wgs) {
@@ -672,13 +672,17 @@ __device__ __forceinline__ void decode_merge_body(const AttnArgs& a, uint32_t nw
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t nseg = a.batch * a.kvh;
   constexpr uint32_t kSegsPerWG = WPS >= (int)kMergeWaves ? 1 : kMergeWaves / WPS;
-  const uint32_t segi = bid * kSegsPerWG + wave / WPS;
+  // Items are (segment, slice): ns slices of a segment's G x D outputs
+  // (ns > 1 for wide groups, so that a lane combines at most 8 outputs in
+  // one pass over the pieces).
+  const uint32_t item = bid * kSegsPerWG + wave / WPS;
   const uint32_t v = wave % WPS;
-  if (segi == nseg) {
+  if (item == nseg * ns) {
     if (v == 0 && !a.deterministic) update_shares(a, nwg, lane);
     return;
   }
-  if (segi > nseg) return;
+  if (item > nseg * ns) return;
+  const uint32_t segi = item / ns, slice = item - segi * ns;
   const uint32_t seq = segi / a.kvh, kh = segi - seq * a.kvh;
   // One round trip: the row's extents and the segment's ranges (stale for
   // rows that are not decode rows, which return here; the same for all the
@@ -693,8 +697,8 @@ __device__ __forceinline__ void decode_merge_body(const AttnArgs& a, uint32_t nw
                     (r1 >= nwg * kDecodeWavesPerWG);
   if (skip) return;
   const uint32_t G = a.group, seg = segi;
-  const uint32_t E = G * D / 64;
-  const uint32_t e_lane = lane * E;
+  const uint32_t E = G * D / 64 / ns;
+  const uint32_t e_lane = (slice * 64 + lane) * E;
   const uint32_t h0 = e_lane / D, h1 = (e_lane + E - 1) / D;
   // kPad: output rows are a.hd apart and elements d >= a.hd (padding) are
   // not stored; the n outputs from index e of the [G][D] partials are
@@ -823,9 +827,20 @@ __device__ __forceinline__ void decode_merge_body(const AttnArgs& a, uint32_t nw
 
 // Workgroups of a decode's merge launch for `batch` sequences (without a
 // fused append's copy); *wide: one workgroup per segment (few segments).
-inline uint32_t decode_merge_wgs(uint32_t batch, uint32_t kvh, bool* wide) {
+inline uint32_t decode_merge_wgs(uint32_t batch, uint32_t kvh, bool* wide, uint32_t ns = 1) {
   *wide = batch * kvh <= 256;
-  return *wide ? batch * kvh + 1 : (batch * kvh + kMergeWaves) / kMergeWaves;
+  const uint32_t items = batch * kvh * ns;
+  return *wide ? items + 1 : (items + kMergeWaves) / kMergeWaves;
+}
+
+// Slices per segment in the merge: the fewest that leave a lane at most 8
+// of the segment's G x D outputs (G * D / 64 per lane unsliced), a divisor
+// of G * D / 64. 1 for groups of up to 4 at head_dim 128.
+inline uint32_t decode_merge_slices(uint32_t group, uint32_t head_dim) {
+  const uint32_t e = group * head_dim / 64;
+  for (uint32_t ns = 1; ns <= e; ++ns)
+    if (e % ns == 0 && e / ns <= 8) return ns;
+  return 1;
 }
 
 // Workspace layout of one decode launch: the balance block (shares and
